@@ -1,0 +1,59 @@
+/* ref_harness.c -- TEST INFRASTRUCTURE: a thin driver linked into
+ * oracle/_ref/libspref.so (the compiled reference) so tests can run the
+ * reference's own session decode on a given .sp-model.  Calls only the
+ * reference's public API (include/sp/sp_l1.h, sp_model.h, qwen3_fixture.h). */
+#include "sp/sp_l1.h"
+#include "sp/sp_model.h"
+#include "sp/sp_hash.h"
+#include "qwen3_fixture.h"
+#include <stdlib.h>
+#include <string.h>
+
+static int argmax_lowest(const float *v, int n) {
+    int a = 0;
+    for (int j = 1; j < n; j++) if (v[j] > v[a]) a = j;
+    return a;
+}
+
+/* prefill `prompt`, then n_gen decode steps; step k feeds forced[k] when forced
+ * is non-NULL, else the greedy argmax of the previous logits.  Writes the
+ * prefill logits (V), every decode step's logits (n_gen x V) and the fed tokens. */
+int refh_decode(const char *spm, const char *spt, const int32_t *prompt, int n_prompt,
+                int n_gen, const int32_t *forced, float *prefill_logits, float *logits,
+                int32_t *fed) {
+    sp_model *m = NULL;
+    if (sp_model_load(spm, spt, &m) != SP_OK) return -1;
+    sp_arch_info ai; sp_model_arch(m, &ai);
+    const int V = (int)ai.vocab_size;
+    sp_session_config cfg; memset(&cfg, 0, sizeof cfg);
+    cfg.deterministic = 1; cfg.max_context = (size_t)(n_prompt + n_gen + 1);
+    sp_session *s = NULL;
+    int rc = -2;
+    if (sp_session_create(m, &cfg, NULL, &s) != SP_OK) goto out;
+    rc = -3;
+    if (sp_prefill_chunk(s, prompt, (size_t)n_prompt, prefill_logits, (size_t)V) != SP_OK) goto out;
+    int t = argmax_lowest(prefill_logits, V);
+    for (int k = 0; k < n_gen; k++) {
+        if (forced) t = forced[k];
+        fed[k] = t;
+        rc = -4 - k;
+        if (sp_decode_step(s, t, logits + (size_t)k * V, (size_t)V) != SP_OK) goto out;
+        t = argmax_lowest(logits + (size_t)k * V, V);
+    }
+    rc = 0;
+out:
+    if (s) sp_session_destroy(s);
+    sp_model_unload(m);
+    return rc;
+}
+
+/* the reference's own qwen3 session fixture: SHA-256 of the .sp-model bytes */
+int refh_qwen3_fixture_sha(uint8_t out[32], size_t *len) {
+    uint8_t *mb = NULL, *tb = NULL;
+    sp_qwen3_fixture_info info;
+    if (sp_qwen3_fixture_build(&mb, &tb, &info)) return 1;
+    sp_sha256(mb, info.model_len, out);
+    *len = info.model_len;
+    free(mb); free(tb);
+    return 0;
+}

@@ -1,0 +1,68 @@
+/* sp_oracle.h -- TEST INFRASTRUCTURE ONLY.  A scalar CPU restatement of the
+ * reference's session-resident KV decode, used as the checker by tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg.  Nothing in the
+ * product library links, loads or calls this code.
+ *
+ * Float mode restates core/session/sp_session.c kv_step (:274-363) and
+ * kv_step_gemma3 (:380-464) with the OK_Q4B arena matmul
+ * (core/forward_dispatch/forward_dispatch.c:59-98) and the scalar kernels
+ * (core/forward_kernels/forward_kernels.c:11-81), in the same operation order,
+ * so that it is bit-identical to the compiled reference on the same inputs.
+ *
+ * Exact mode is the build-defined integer decode (islands restated from
+ * core/exact_islands/exact_islands.c:21-124 plus the integer GEMV, CORDIC RoPE
+ * and integer attention specified in oracle/sp_oracle.c). */
+#ifndef SP_ORACLE_H
+#define SP_ORACLE_H
+#include <stddef.h>
+#include <stdint.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct orc_model orc_model;
+typedef struct orc_sess  orc_sess;
+
+enum { ORC_FLOAT = 0, ORC_EXACT = 1 };
+
+orc_model *orc_model_load(const char *spm_path);
+void       orc_model_free(orc_model *m);
+/* arch_id, vocab, hidden, n_layers, n_heads, n_kv_heads, head_dim, n_ff, swa */
+void       orc_model_dims(const orc_model *m, uint32_t out[9]);
+
+orc_sess *orc_sess_new(orc_model *m, int max_ctx, int mode);
+void      orc_sess_free(orc_sess *s);
+/* one token at the session position (kv_step semantics); logits may be NULL */
+int       orc_step(orc_sess *s, int32_t tok, float *logits);
+int       orc_rewind(orc_sess *s, int n);
+int       orc_pos(const orc_sess *s);
+orc_sess *orc_clone(const orc_sess *s);
+/* K/V rows of one layer for positions [p0, p0+n): KVD floats per position */
+int       orc_kv_get(const orc_sess *s, int layer, int p0, int n, float *k, float *v);
+int       orc_kv_set(orc_sess *s, int layer, int p0, int n, const float *k, const float *v);
+int       orc_set_pos(orc_sess *s, int pos);
+
+/* ---- unit kernels (float mode: reference order) ---- */
+float orc_f16_to_f32(uint16_t h);
+void  orc_rmsnorm(const float *x, const float *w, int n, float eps, float *out);
+void  orc_rope_neox(float *v, int d, int p, float base);
+void  orc_attn_head(const float *qh, const float *KC, const float *VC, int pos, int KVD,
+                    int kvh, int HD, float ascale, int win, float *sc, float *out);
+int   orc_q4b_gemv(const uint8_t *codes, const uint16_t *bscale, int rows, int cols,
+                   const float *x, float *y);
+/* ---- exact islands (reference arithmetic) ---- */
+void  orc_rmsnorm_exact(const float *x, const float *w, int n, float *out);
+void  orc_softmax_exact(const float *z, int m, double *p);
+void  orc_gelu_exact(const float *x, int n, float *out);
+/* ---- build-defined exact primitives ---- */
+void  orc_cordic_sincos(int64_t theta_q60, int32_t *cos_q30, int32_t *sin_q30);
+void  orc_rope_exact(float *v, int d, int p, float base);
+int   orc_q4b_gemv_exact(const uint8_t *codes, const uint16_t *bscale, int rows, int cols,
+                         const float *x, float *y);
+void  orc_silu_exact(const float *x, int n, float *out);
+int64_t orc_rope_freq_q60(float base, int i, int d);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
