@@ -1,0 +1,79 @@
+/* sp_hipkv.h -- C ABI of the MI355X (gfx950) persistent-KV decode backend.
+ *
+ * The drop-in is `sp_hipkv_dispatch`: a section-6b dispatch table that an L2
+ * registrant hands to sp_session_register_kvdecode_backend
+ * (include/sp/sp_l1.h:403-423).  Its six entry points are also exported by name.
+ * All pointers are plain host pointers; logits are caller-allocated host memory
+ * of vocab floats.  Every failing call returns non-zero and sets sp_last_error().
+ */
+#ifndef SP_HIPKV_H
+#define SP_HIPKV_H
+#include <stddef.h>
+#include <stdint.h>
+#include "sp_l1_abi.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* The section-6b table (replaces the engine's registered gemma4_kv_* table,
+ * include/sp/sp_l1.h:381-402; layout sp_l1.h:403-410). */
+extern const sp_kvdecode_dispatch_fn sp_hipkv_dispatch;
+
+/* open: sp_l1.h:390 -- qm_opaque is the session's `const qwen3_model *`
+ * (sp_session_qwen3_model, sp_l1.h:354); uploads the OK_Q4B arena to HBM once
+ * per model and reserves page tables for pmax positions (dpos = 0). */
+int  sp_hipkv_open(const void *qm_opaque, int pmax, sp_kvdecode_handle **out);
+/* prefill: sp_l1.h:392 -- store K/V for n_tok tokens at dpos.., dpos += n_tok */
+int  sp_hipkv_prefill(sp_kvdecode_handle *h, const int32_t *tokens, int n_tok);
+/* decode_step: sp_l1.h:393-395 -- one token at dpos, logits[vocab] of the next
+ * position into caller memory, dpos += 1 */
+int  sp_hipkv_decode_step(sp_kvdecode_handle *h, int32_t token, float *logits);
+/* rewind: sp_l1.h:396 -- O(1): dpos -= n (n <= dpos) */
+int  sp_hipkv_rewind(sp_kvdecode_handle *h, int n);
+/* position: sp_l1.h:397 -- dpos, -1 on NULL */
+int  sp_hipkv_position(const sp_kvdecode_handle *h);
+/* close: sp_l1.h:398 -- NULL-safe */
+void sp_hipkv_close(sp_kvdecode_handle *h);
+
+/* ---- backend knobs (the section-6c/6d pattern: backend symbols, not session verbs) ---- */
+/* Exact-integer decode on/off (replaces gemma4_kv_byteexact_set, sp_l1.h:440-455):
+ * 0 = float mode (reference float semantics, tolerance-equal), 1 = exact mode
+ * (integer islands + CORDIC RoPE + integer attention/GEMV, bit-reproducible).
+ * Changing the mode invalidates the resident cache (dpos must be 0). */
+int  sp_hipkv_set_mode(sp_kvdecode_handle *h, int exact);
+/* Sliding-window layers keep a ring of window + max_rewind positions instead of a
+ * full table (the SWA W-ring knob, sp_l1.h:466-479).  Rewinds beyond max_rewind
+ * then fail.  Only before the first token (dpos == 0).  0 = full table (default). */
+int  sp_hipkv_set_max_rewind(sp_kvdecode_handle *h, int max_rewind);
+/* Copy-on-write fork of the resident cache (no counterpart in sp_l1.h: the
+ * table has no fork row; sp_session_clone uses it through spx_register_fork). */
+int  sp_hipkv_fork(const sp_kvdecode_handle *parent, sp_kvdecode_handle **child);
+/* Register the backend on a session: open(sp_session_qwen3_model(s), pmax) +
+ * sp_session_register_kvdecode_backend + ownership (closed with the session). */
+sp_status sp_hipkv_attach(sp_session *s, int pmax, int exact);
+
+/* ---- device-resident driver entry points (bench / tests) ---- */
+/* n greedy steps entirely on the device (argmax feeds the next token, no host
+ * round trip), starting with `first_token` at dpos; writes the n generated
+ * tokens and the device time of the n steps (HIP events on the backend's stream). */
+int  sp_hipkv_greedy(sp_kvdecode_handle *h, int32_t first_token, int n, int32_t *out_tokens,
+                     double *device_ms);
+/* Per-kernel-class device times over n greedy steps, each launch bracketed by HIP
+ * events on the backend's stream.  Classes: 0 layer GEMV, 1 LM-head GEMV,
+ * 2 attention (global layers), 3 attention (window layers), 4 q/k prep + append,
+ * 5 embed + argmax.  ms[6], launches[6]; bytes[6] = algorithmic HBM bytes. */
+int  sp_hipkv_kernel_times(sp_kvdecode_handle *h, int32_t first_token, int n,
+                           double ms[6], long long launches[6], double bytes[6]);
+/* Read K/V of one layer for positions [p0, p0+n) in the reference slab layout
+ * ([n][n_kv_heads*head_dim] floats, or int32 grid values in exact mode). */
+int  sp_hipkv_read_kv(const sp_kvdecode_handle *h, int layer, int p0, int n, float *k, float *v);
+/* Use a captured HIP graph for each step body (1, default) or plain launches (0). */
+int  sp_hipkv_set_graph(sp_kvdecode_handle *h, int on);
+/* Bytes of model weights resident in HBM and KV bytes per token per layer. */
+int  sp_hipkv_info(const sp_kvdecode_handle *h, long long out[8]);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

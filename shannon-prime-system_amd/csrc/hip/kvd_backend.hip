@@ -1,0 +1,860 @@
+// kvd_backend.hip -- host side of the HIP section-6b kvdecode backend: model
+// upload, the paged KV pool (page tables, copy-on-write forks, O(1) rewind,
+// optional window ring), the per-step kernel sequence (eager or one captured
+// HIP graph per step shape) and the C ABI of include/sp_hipkv.h.
+//
+// Reference boundary: include/sp/sp_l1.h:384-427 (dispatch table semantics),
+// core/session/sp_session.c:737-746 (how sp_decode_step drives decode_step).
+// Model access goes through the frozen model ABI only: qwen3_model fields,
+// sp_arena_find (include/sp/arena.h:52) and sp_as_f32 (forward_dispatch.h:44).
+#include "sp_l1_abi.h"
+#include "sp_model_abi.h"
+#include "sp_hipkv.h"
+#include "kvd_internal.h"
+#include <hip/hip_runtime.h>
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <tuple>
+#include <vector>
+
+using namespace kvd;
+
+namespace {
+
+typedef __int128 i128;
+typedef unsigned __int128 u128;
+
+std::mutex g_mu;
+
+int fail(const char *fmt, const char *a = nullptr, long long b = 0) {
+    char buf[400];
+    snprintf(buf, sizeof buf, fmt, a ? a : "", b);
+    sp_set_error(buf);
+    return 1;
+}
+#define HIPCHK(call, what) do { hipError_t e_ = (call); if (e_ != hipSuccess) { \
+        char b_[300]; snprintf(b_, sizeof b_, "sp_hipkv: %s: %s", (what), hipGetErrorString(e_)); \
+        sp_set_error(b_); return 1; } } while (0)
+
+// ------------------------------------------------------------ integer RoPE constants
+// Host computation of the exact-mode RoPE tables: atan(2^-i) (Q60), the CORDIC
+// gain inverse (Q62) and base^(-2i/d) (Q60), all by integer arithmetic.
+constexpr int64_t HALF_PI_Q60 = 1811004864519280711LL;
+u128 isqrt128(u128 v) {
+    u128 x = 0, b = (u128)1 << 126;
+    while (b > v) b >>= 2;
+    while (b) {
+        if (v >= x + b) { v -= x + b; x = (x >> 1) + b; } else x >>= 1;
+        b >>= 2;
+    }
+    return x;
+}
+struct RopeConst { int64_t atan_q60[64]; int64_t kinv_q62; int64_t exp2neg_q62[64]; };
+const RopeConst &rope_const() {
+    static RopeConst rc;
+    static bool ready = false;
+    if (ready) return rc;
+    rc.atan_q60[0] = HALF_PI_Q60 / 2;                      // atan(1) = pi/4
+    for (int i = 1; i < 64; i++) {                         // atan(2^-i) = sum (-1)^k 2^-i(2k+1)/(2k+1)
+        i128 sum = 0; int sgn = 1;
+        for (int k = 0;; k++) {
+            const int pw = i * (2 * k + 1);
+            if (pw >= 120) break;
+            const i128 term = ((i128)1 << (120 - pw)) / (2 * k + 1);
+            sum += sgn > 0 ? term : -term; sgn = -sgn;
+        }
+        rc.atan_q60[i] = (int64_t)((sum + ((i128)1 << 59)) >> 60);
+    }
+    u128 k = (u128)1 << 62;                                // prod 1/sqrt(1 + 4^-i)
+    for (int i = 0; i < 62; i++) {
+        const u128 r = isqrt128(((u128)1 << 124) + ((u128)1 << (124 - 2 * i)));
+        k = (k * (((u128)1 << 124) / r)) >> 62;
+    }
+    rc.kinv_q62 = (int64_t)k;
+    u128 c = (u128)1 << 61;                                // 2^(-2^-j) by repeated sqrt of 1/2
+    rc.exp2neg_q62[0] = 0;
+    for (int j = 1; j < 64; j++) { c = isqrt128(c << 62); rc.exp2neg_q62[j] = (int64_t)c; }
+    ready = true;
+    return rc;
+}
+i128 log2_q62(float v) {                                   // normal positive floats
+    uint32_t bits; memcpy(&bits, &v, 4);
+    const int e = (int)((bits >> 23) & 255u) - 127;
+    u128 y = (u128)((bits & 0x7FFFFFu) | 0x800000u) << (62 - 23);
+    i128 frac = 0;
+    for (int b = 61; b >= 0; b--) {
+        y = (y * y) >> 62;
+        if (y >= ((u128)2 << 62)) { y >>= 1; frac |= (i128)1 << b; }
+    }
+    return ((i128)e << 62) + frac;
+}
+int64_t rope_freq_q60(float base, int i, int d) {
+    const RopeConst &rc = rope_const();
+    if (i == 0) return (int64_t)1 << 60;
+    i128 t = (log2_q62(base) * (i128)(2 * i)) / (i128)d;
+    if (t < 0) t = 0;
+    const int64_t n = (int64_t)(t >> 62);
+    const uint64_t r = (uint64_t)(t & (((i128)1 << 62) - 1));
+    u128 acc = (u128)1 << 62;
+    for (int j = 1; j <= 62; j++)
+        if ((r >> (62 - j)) & 1u) acc = (acc * (u128)rc.exp2neg_q62[j]) >> 62;
+    if (n >= 62) return 0;
+    return (int64_t)((acc >> 2) >> n);
+}
+
+// ------------------------------------------------------------ device model
+struct DevLayer {
+    DevW q, k, v, o, gate, up, down;
+    const float *attn_norm, *q_norm, *k_norm, *ffn_norm, *post_attn, *post_ffw;
+};
+struct DevModel {
+    const qwen3_model *qm = nullptr;
+    int refs = 0, gemma = 0;
+    int E = 0, FF = 0, NH = 0, NKV = 0, HD = 0, V = 0, NL = 0, SW = 0;
+    float base = 0, eps = 0;
+    DevW embd{}, out{};
+    const float *out_norm = nullptr;
+    std::vector<DevLayer> L;
+    void *buf = nullptr;
+    size_t bytes = 0, weight_bytes = 0, lm_bytes = 0, layer_bytes = 0, embd_bytes = 0;
+    int64_t *freq_global = nullptr, *freq_local = nullptr;
+};
+std::map<const qwen3_model *, DevModel *> g_models;
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+struct Uploader {                         // one allocation, arrays carved at 256 B
+    std::vector<std::pair<const void *, size_t>> src;
+    std::vector<size_t> off;
+    size_t total = 0;
+    size_t add(const void *p, size_t n) { off.push_back(total); src.push_back({p, n}); size_t o = total; total = align_up(total + n, 256); return o; }
+};
+
+int load_weight(const qwen3_model *qm, const gguf_tensor *t, int rows, int cols, Uploader &up,
+                std::vector<std::vector<int8_t>> &ebase_store, DevW &w, size_t offs[3]) {
+    if (!t) return fail("sp_hipkv_open: model lacks a weight tensor%s", "");
+    const sp_arena_tensor *at = sp_arena_find(qm->arena, t->name);
+    if (!at) return fail("sp_hipkv_open: weight %s not in the packed arena", t->name);
+    const sp_frob_packed_tensor &p = at->pt;
+    if (!p.bscale || p.bs_nblk != (cols + 31) / 32)
+        return fail("sp_hipkv_open: %s is not OK_Q4B (block-scaled 4-bit); only OK_Q4B is served", t->name);
+    if (p.rows != rows || p.cols != cols) return fail("sp_hipkv_open: %s has unexpected shape", t->name);
+    const size_t rb = (size_t)(cols + 1) / 2, nb = (size_t)p.bs_nblk;
+    for (int r = 0; r < rows; r++)
+        if (p.row_prec[r] == 8u || p.row_off[r] != (size_t)r * rb)
+            return fail("sp_hipkv_open: %s has Q8-promoted or non-contiguous rows", t->name);
+    if (cols % 32 != 0) return fail("sp_hipkv_open: %s: cols must be a multiple of 32", t->name);
+    // per-row smallest block exponent; rows whose exponent spread could overflow
+    // the int64 accumulator (see kvd_gemv.hip) switch the tensor to int128
+    ebase_store.emplace_back(rows);
+    std::vector<int8_t> &eb = ebase_store.back();
+    int lg = 0; while ((1 << lg) < (int)nb) lg++;
+    const int max_spread = 21 - lg;
+    int wide = 0;
+    for (int r = 0; r < rows; r++) {
+        int emin = 127, emax = -127;
+        const uint16_t *bs = p.bscale + (size_t)r * nb;
+        for (size_t b = 0; b < nb; b++) {
+            const int E5 = (bs[b] >> 10) & 31, mant = bs[b] & 1023;
+            if (E5 == 31) return fail("sp_hipkv_open: %s has a non-finite block scale", t->name);
+            if (!E5 && !mant) continue;
+            const int e = E5 ? E5 - 25 : -24;
+            emin = std::min(emin, e); emax = std::max(emax, e);
+        }
+        if (emin > emax) emin = emax = 0;
+        eb[r] = (int8_t)emin;
+        if (emax - emin > max_spread) wide = 1;
+    }
+    offs[0] = up.add(p.codes, rb * rows);
+    offs[1] = up.add(p.bscale, nb * 2 * rows);
+    offs[2] = up.add(eb.data(), (size_t)rows);
+    w.rows = rows; w.cols = cols; w.nblk = (int)nb; w.wide = wide;
+    return 0;
+}
+
+DevModel *model_get(const qwen3_model *qm) {
+    auto it = g_models.find(qm);
+    if (it != g_models.end()) { it->second->refs++; return it->second; }
+    const qwen3_config &c = qm->cfg;
+    if (c.arch != SP_ARCH_QWEN3 && c.arch != SP_ARCH_GEMMA3) { fail("sp_hipkv_open: architecture %s not served (Qwen3 / Gemma3 only)", ""); return nullptr; }
+    if (!qm->arena) { fail("sp_hipkv_open: model has no packed arena%s", ""); return nullptr; }
+    if (c.head_dim % 64 || c.head_dim > 512 || !c.n_head_kv || c.n_head % c.n_head_kv) {
+        fail("sp_hipkv_open: unsupported head geometry (head_dim %s%lld)", "", (long long)c.head_dim); return nullptr;
+    }
+    const int G = (int)(c.n_head / c.n_head_kv), HD = (int)c.head_dim;
+    if (!((HD == 256 && (G == 2 || G == 4)) || (HD == 128 && (G == 2 || G == 4)) || (HD == 64 && (G == 2 || G == 4)))) {
+        fail("sp_hipkv_open: unsupported (head_dim, group) combination%s", ""); return nullptr;
+    }
+    std::unique_ptr<DevModel> m(new DevModel);
+    m->qm = qm; m->gemma = c.arch == SP_ARCH_GEMMA3;
+    m->E = (int)c.n_embd; m->FF = (int)c.n_ff; m->NH = (int)c.n_head; m->NKV = (int)c.n_head_kv;
+    m->HD = HD; m->V = (int)c.n_vocab; m->NL = (int)c.n_layers; m->SW = (int)c.sliding_window;
+    m->base = c.rope_freq_base; m->eps = c.rms_eps;
+    const int QD = m->NH * HD, KVD = m->NKV * HD;
+    Uploader up;
+    std::vector<std::vector<int8_t>> ebs;
+    ebs.reserve((size_t)m->NL * 7 + 2);
+    struct Pending { DevW *w; size_t o[3]; };
+    std::vector<Pending> pend;
+    auto addw = [&](const gguf_tensor *t, int rows, int cols, DevW &w) -> int {
+        Pending pd; pd.w = &w;
+        if (load_weight(qm, t, rows, cols, up, ebs, w, pd.o)) return 1;
+        pend.push_back(pd);
+        return 0;
+    };
+    std::vector<std::pair<const float *, size_t>> norms;   // (host src, len)
+    std::vector<const float **> norm_slots;
+    std::vector<size_t> norm_off;
+    auto addn = [&](const gguf_tensor *t, int n, const float **slot) -> int {
+        const float *src = t ? sp_as_f32(qm, t) : nullptr;
+        if (!src) return fail("sp_hipkv_open: missing norm tensor %s", t ? t->name : "(null)");
+        norm_off.push_back(up.add(src, (size_t)n * 4));
+        norm_slots.push_back(slot);
+        return 0;
+    };
+    m->L.resize(m->NL);
+    if (addw(qm->token_embd, m->V, m->E, m->embd)) return nullptr;
+    if (qm->output != qm->token_embd) { if (addw(qm->output, m->V, m->E, m->out)) return nullptr; }
+    if (addn(qm->output_norm, m->E, &m->out_norm)) return nullptr;
+    for (int l = 0; l < m->NL; l++) {
+        const qwen3_layer &y = qm->layers[l];
+        DevLayer &d = m->L[l];
+        if (addw(y.attn_q, QD, m->E, d.q) || addw(y.attn_k, KVD, m->E, d.k) || addw(y.attn_v, KVD, m->E, d.v) ||
+            addw(y.attn_output, m->E, QD, d.o) || addw(y.ffn_gate, m->FF, m->E, d.gate) ||
+            addw(y.ffn_up, m->FF, m->E, d.up) || addw(y.ffn_down, m->E, m->FF, d.down)) return nullptr;
+        if (addn(y.attn_norm, m->E, &d.attn_norm) || addn(y.attn_q_norm, HD, &d.q_norm) ||
+            addn(y.attn_k_norm, HD, &d.k_norm) || addn(y.ffn_norm, m->E, &d.ffn_norm)) return nullptr;
+        d.post_attn = d.post_ffw = nullptr;
+        if (m->gemma && (addn(y.post_attn_norm, m->E, &d.post_attn) || addn(y.post_ffw_norm, m->E, &d.post_ffw))) return nullptr;
+    }
+    // exact-mode RoPE frequency tables (global base, and 1e4 for Gemma window layers)
+    std::vector<int64_t> fg(HD / 2), fl(HD / 2);
+    for (int i = 0; i < HD / 2; i++) { fg[i] = rope_freq_q60(m->base, i, HD); fl[i] = rope_freq_q60(10000.0f, i, HD); }
+    const size_t o_fg = up.add(fg.data(), fg.size() * 8), o_fl = up.add(fl.data(), fl.size() * 8);
+
+    if (hipMalloc(&m->buf, up.total) != hipSuccess) {
+        fail("sp_hipkv_open: hipMalloc of %s%lld weight bytes failed", "", (long long)up.total); return nullptr;
+    }
+    m->bytes = up.total;
+    uint8_t *base = (uint8_t *)m->buf;
+    for (size_t i = 0; i < up.src.size(); i++)
+        if (hipMemcpy(base + up.off[i], up.src[i].first, up.src[i].second, hipMemcpyHostToDevice) != hipSuccess) {
+            hipFree(m->buf); fail("sp_hipkv_open: weight upload failed%s", ""); return nullptr;
+        }
+    for (auto &pd : pend) {
+        pd.w->codes = base + pd.o[0];
+        pd.w->bs = (const uint16_t *)(base + pd.o[1]);
+        pd.w->ebase = (const int8_t *)(base + pd.o[2]);
+        const size_t wb = (size_t)pd.w->rows * (pd.w->cols / 2) + (size_t)pd.w->rows * pd.w->nblk * 2;
+        m->weight_bytes += wb;
+    }
+    for (size_t i = 0; i < norm_slots.size(); i++) *norm_slots[i] = (const float *)(base + norm_off[i]);
+    const bool tied = qm->output == qm->token_embd;
+    if (tied) m->out = m->embd;
+    m->embd_bytes = (size_t)m->embd.rows * (m->embd.cols / 2) + (size_t)m->embd.rows * m->embd.nblk * 2;
+    m->lm_bytes = (size_t)m->out.rows * (m->out.cols / 2) + (size_t)m->out.rows * m->out.nblk * 2;
+    m->layer_bytes = m->weight_bytes - m->embd_bytes - (tied ? 0 : m->lm_bytes);
+    m->freq_global = (int64_t *)(base + o_fg);
+    m->freq_local = (int64_t *)(base + o_fl);
+    const RopeConst &rc = rope_const();
+    set_rope_tables(rc.atan_q60, rc.kinv_q62);
+    m->refs = 1;
+    DevModel *raw = m.release();
+    g_models[qm] = raw;
+    return raw;
+}
+void model_put(DevModel *m) {
+    if (!m || --m->refs > 0) return;
+    g_models.erase(m->qm);
+    hipFree(m->buf);
+    delete m;
+}
+
+// ------------------------------------------------------------ KV page pool
+struct KvPool {
+    std::mutex mu;                            // shared by a handle and its forks
+    size_t page_bytes = 0;
+    std::vector<void *> chunks;
+    std::vector<float *> ptr;
+    std::vector<int> refc, free_ids;
+    int pages_per_chunk = 0;
+    ~KvPool() { for (void *c : chunks) hipFree(c); }
+    int grow(int min_pages) {
+        const int n = std::max(min_pages, pages_per_chunk);
+        void *c = nullptr;
+        if (hipMalloc(&c, (size_t)n * page_bytes) != hipSuccess) return 1;
+        chunks.push_back(c);
+        for (int i = 0; i < n; i++) {
+            ptr.push_back((float *)((uint8_t *)c + (size_t)i * page_bytes));
+            refc.push_back(0);
+            free_ids.push_back((int)ptr.size() - 1);
+        }
+        std::reverse(free_ids.end() - n, free_ids.end());
+        return 0;
+    }
+    int alloc() {
+        if (free_ids.empty() && grow(1)) return -1;
+        const int id = free_ids.back(); free_ids.pop_back();
+        refc[id] = 1;
+        return id;
+    }
+    void unref(int id) { if (id >= 0 && --refc[id] == 0) free_ids.push_back(id); }
+};
+
+}  // namespace
+
+// ------------------------------------------------------------ the handle
+struct sp_kvdecode_handle {
+    DevModel *m = nullptr;
+    std::shared_ptr<KvPool> pool;
+    int mode = FLOAT, pmax = 0, dpos = 0, use_graph = 1, hwm = 0;
+    int max_rewind = 0;                      // 0: full tables for window layers
+    int full_pages = 0, ring_pages = 0;
+    std::vector<std::vector<int>> pt;        // [NL][slots] page ids (-1 = unmapped)
+    std::vector<int> slots;                  // per layer: number of slots
+    float **d_pt = nullptr;                  // device: concatenated per-layer pointer tables
+    float **h_pt = nullptr;                  // pinned mirror
+    std::vector<size_t> pt_off;              // per layer offset into d_pt
+    hipStream_t stream = nullptr;
+    DState *d_st = nullptr;
+    DState *h_st = nullptr;                  // pinned
+    float *x0 = nullptr, *x1 = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *qr = nullptr,
+          *ao = nullptr, *ap = nullptr, *gg = nullptr, *uu = nullptr, *hh = nullptr, *dn = nullptr,
+          *logits = nullptr, *part = nullptr, *part_ml = nullptr, *am_v = nullptr;
+    int *counter = nullptr, *zscratch = nullptr, *am_i = nullptr, *am_cnt = nullptr, *gen_log = nullptr;
+    float *h_logits = nullptr;               // pinned staging
+    int max_chunks = 0;
+    void *scratch = nullptr;
+    // graph cache: key (logits?, argmax?, grid_global, grid_local, chunk_global)
+    struct GKey { int lg, am, gg, gl, cg; bool operator<(const GKey &o) const {
+        return std::tie(lg, am, gg, gl, cg) < std::tie(o.lg, o.am, o.gg, o.gl, o.cg); } };
+    std::map<GKey, hipGraphExec_t> graphs;
+};
+
+namespace {
+
+bool is_global(const DevModel *m, int l) { return !m->gemma || (l % 6) == 5; }
+
+void free_graphs(sp_kvdecode_handle *h) {
+    for (auto &g : h->graphs) hipGraphExecDestroy(g.second);
+    h->graphs.clear();
+}
+
+int layer_slots(const sp_kvdecode_handle *h, int l) {
+    if (!is_global(h->m, l) && h->max_rewind > 0 && h->m->SW > 0) return h->ring_pages;
+    return h->full_pages;
+}
+
+int build_tables(sp_kvdecode_handle *h) {
+    const DevModel *m = h->m;
+    h->full_pages = (h->pmax + PAGE - 1) / PAGE;
+    h->ring_pages = h->max_rewind > 0 ? std::min(h->full_pages, (m->SW + h->max_rewind + PAGE - 1) / PAGE + 1) : 0;
+    h->pt.assign(m->NL, {});
+    h->slots.assign(m->NL, 0);
+    h->pt_off.assign(m->NL, 0);
+    size_t tot = 0;
+    for (int l = 0; l < m->NL; l++) {
+        h->slots[l] = layer_slots(h, l);
+        h->pt[l].assign(h->slots[l], -1);
+        h->pt_off[l] = tot; tot += (size_t)h->slots[l];
+    }
+    if (h->d_pt) { hipFree(h->d_pt); h->d_pt = nullptr; }
+    if (h->h_pt) { hipHostFree(h->h_pt); h->h_pt = nullptr; }
+    HIPCHK(hipMalloc(&h->d_pt, tot * sizeof(float *)), "page table alloc");
+    HIPCHK(hipHostMalloc(&h->h_pt, tot * sizeof(float *), hipHostMallocDefault), "page table mirror alloc");
+    for (size_t i = 0; i < tot; i++) h->h_pt[i] = nullptr;
+    HIPCHK(hipMemcpy(h->d_pt, h->h_pt, tot * sizeof(float *), hipMemcpyHostToDevice), "page table init");
+    return 0;
+}
+
+// Make the pages holding positions [p0, p1) present and exclusively owned in
+// every layer (allocate on first touch, copy-on-write when shared by a fork).
+int ensure_pages(sp_kvdecode_handle *h, int p0, int p1) {
+    const DevModel *m = h->m;
+    if (p1 <= p0) return 0;
+    std::lock_guard<std::mutex> lk(h->pool->mu);
+    for (int l = 0; l < m->NL; l++) {
+        const int S = h->slots[l];
+        bool dirty = false;
+        const int lp0 = p0 / PAGE, lp1 = (p1 - 1) / PAGE;
+        for (int lp = lp0; lp <= lp1; lp++) {
+            const int slot = (S == h->full_pages) ? lp : lp % S;
+            int &id = h->pt[l][slot];
+            if (id < 0) {
+                id = h->pool->alloc();
+                if (id < 0) return fail("sp_hipkv: KV pool exhausted (hipMalloc failed)%s");
+                dirty = true;
+            } else if (h->pool->refc[id] > 1) {
+                const int nid = h->pool->alloc();
+                if (nid < 0) return fail("sp_hipkv: KV pool exhausted during copy-on-write%s");
+                HIPCHK(hipMemcpyAsync(h->pool->ptr[nid], h->pool->ptr[id], h->pool->page_bytes,
+                                      hipMemcpyDeviceToDevice, h->stream), "copy-on-write page copy");
+                h->pool->unref(id);
+                id = nid;
+                dirty = true;
+            }
+            h->h_pt[h->pt_off[l] + slot] = h->pool->ptr[id];
+        }
+        if (dirty) {
+            // whole-layer refresh keeps the pinned mirror authoritative
+            HIPCHK(hipMemcpyAsync(h->d_pt + h->pt_off[l], h->h_pt + h->pt_off[l], (size_t)S * sizeof(float *),
+                                  hipMemcpyHostToDevice, h->stream), "page table update");
+            HIPCHK(hipStreamSynchronize(h->stream), "page table update sync");
+        }
+    }
+    return 0;
+}
+
+int alloc_scratch(sp_kvdecode_handle *h) {
+    const DevModel *m = h->m;
+    const int QD = m->NH * m->HD, KVD = m->NKV * m->HD;
+    h->max_chunks = (h->pmax + 15) / 16 + 2;
+    struct Item { void **p; size_t n; };
+    const size_t part_bytes = (size_t)m->NH * h->max_chunks * m->HD * 8;
+    const size_t ml_bytes = (size_t)m->NH * h->max_chunks * 16;
+    const size_t z_bytes = (size_t)m->NH * h->max_chunks * 64 * 4;
+    const int amb = argmax_blocks(m->V);
+    Item items[] = {
+        {(void **)&h->x0, (size_t)m->E * 4}, {(void **)&h->x1, (size_t)m->E * 4}, {(void **)&h->q, (size_t)QD * 4},
+        {(void **)&h->k, (size_t)KVD * 4}, {(void **)&h->v, (size_t)KVD * 4}, {(void **)&h->qr, (size_t)QD * 4},
+        {(void **)&h->ao, (size_t)QD * 4}, {(void **)&h->ap, (size_t)m->E * 4}, {(void **)&h->gg, (size_t)m->FF * 4},
+        {(void **)&h->uu, (size_t)m->FF * 4}, {(void **)&h->hh, (size_t)m->FF * 4}, {(void **)&h->dn, (size_t)m->E * 4},
+        {(void **)&h->logits, (size_t)m->V * 4}, {(void **)&h->part, part_bytes}, {(void **)&h->part_ml, ml_bytes},
+        {(void **)&h->zscratch, z_bytes}, {(void **)&h->counter, 64 * 4}, {(void **)&h->am_v, (size_t)amb * 4},
+        {(void **)&h->am_i, (size_t)amb * 4}, {(void **)&h->am_cnt, 64}, {(void **)&h->gen_log, (size_t)h->pmax * 4 + 64},
+        {(void **)&h->d_st, sizeof(DState) * 4},
+    };
+    size_t tot = 0;
+    for (auto &it : items) tot = align_up(tot + it.n, 256);
+    HIPCHK(hipMalloc(&h->scratch, tot), "scratch alloc");
+    HIPCHK(hipMemset(h->scratch, 0, tot), "scratch clear");
+    size_t off = 0;
+    for (auto &it : items) { *it.p = (uint8_t *)h->scratch + off; off = align_up(off + it.n, 256); }
+    HIPCHK(hipHostMalloc(&h->h_st, sizeof(DState) * 4, hipHostMallocDefault), "pinned state alloc");
+    HIPCHK(hipHostMalloc(&h->h_logits, (size_t)m->V * 4, hipHostMallocDefault), "pinned logits alloc");
+    return 0;
+}
+
+// ------------------------------------------------------------ one step body
+struct StepShape { int logits, argmax, grid_global, grid_local, chunk_global, chunk_local; };
+
+int attn_chunks(const sp_kvdecode_handle *h, int pos_hi, StepShape &sh) {
+    const DevModel *m = h->m;
+    // global layers: chunk 64 (one page) unless that leaves the GPU under-filled
+    int cg = 64;
+    while (cg > 16 && (long long)((pos_hi + 1) / cg + 1) * m->NKV < 1024) cg /= 2;
+    sh.chunk_global = cg;
+    sh.grid_global = pos_hi / cg + 1;
+    sh.chunk_local = 16;
+    const int span = m->SW > 0 ? std::min(m->SW, pos_hi + 1) : pos_hi + 1;
+    sh.grid_local = span / 16 + 2;
+    sh.grid_local = std::min(sh.grid_local, pos_hi / 16 + 1);
+    return 0;
+}
+
+typedef void (*TimeCb)(void *ctx, int cls, bool begin);
+
+void enqueue_body(sp_kvdecode_handle *h, const StepShape &sh, TimeCb cb, void *ctx) {
+    const DevModel *m = h->m;
+    hipStream_t s = h->stream;
+    const int QD = m->NH * m->HD, KVD = m->NKV * m->HD;
+    auto T = [&](int cls, bool b) { if (cb) cb(ctx, cls, b); };
+    T(5, true);
+    launch_embed(m->embd, h->d_st, h->x1, m->gemma ? sqrtf((float)m->E) : 0.0f, s);
+    T(5, false);
+    for (int l = 0; l < m->NL; l++) {
+        const DevLayer &d = m->L[l];
+        const bool glob = is_global(m, l);
+        GemvArgs g{};
+        g.mode = h->mode; g.cols = m->E; g.act = ACT_NONE; g.nseg = 3;
+        if (l == 0) { g.pro.kind = PRO_NORM; g.pro.x = h->x1; }
+        else {
+            g.pro.kind = PRO_RESID; g.pro.x = h->x0; g.pro.delta = h->dn; g.pro.x_out = h->x1;
+            g.pro.post_w = m->gemma ? m->L[l - 1].post_ffw : nullptr;
+        }
+        g.pro.norm_w = d.attn_norm; g.pro.n = m->E; g.pro.eps = m->eps;
+        g.seg[0] = {d.q, h->q}; g.seg[1] = {d.k, h->k}; g.seg[2] = {d.v, h->v};
+        T(0, true); launch_gemv(g, QD + 2 * KVD, s); T(0, false);
+
+        AttnArgs a{};
+        a.q = h->q; a.k = h->k; a.v = h->v; a.q_norm = d.q_norm; a.k_norm = d.k_norm; a.qr = h->qr;
+        a.pages = h->d_pt + h->pt_off[l];
+        a.ring_pages = h->slots[l] == h->full_pages ? 0 : h->slots[l];
+        a.ao = h->ao; a.part = h->part; a.part_ml = h->part_ml; a.counter = h->counter; a.zscratch = h->zscratch;
+        a.st = h->d_st; a.freq_q60 = (m->gemma && !glob) ? m->freq_local : m->freq_global;
+        a.NH = m->NH; a.NKV = m->NKV; a.HD = m->HD;
+        a.win = (m->gemma && !glob) ? m->SW : -1;
+        a.max_chunks = h->max_chunks; a.mode = h->mode; a.eps = m->eps;
+        a.base = (m->gemma && !glob) ? 10000.0f : m->base;
+        a.ascale = 1.0f / sqrtf((float)m->HD);
+        a.chunk = glob ? sh.chunk_global : sh.chunk_local;
+        T(4, true); launch_qk_prep(a, s); T(4, false);
+        const int cls = (glob || a.win < 0) ? 2 : 3;
+        T(cls, true); launch_attention(a, glob ? sh.grid_global : sh.grid_local, s); T(cls, false);
+
+        GemvArgs o{};
+        o.mode = h->mode; o.cols = QD; o.act = ACT_NONE; o.nseg = 1;
+        o.pro.kind = PRO_PLAIN; o.pro.x = h->ao; o.pro.n = QD;
+        o.seg[0] = {d.o, h->ap};
+        T(0, true); launch_gemv(o, m->E, s); T(0, false);
+
+        GemvArgs f{};
+        f.mode = h->mode; f.cols = m->E; f.act = m->gemma ? ACT_GELU : ACT_SILU; f.nseg = 2;
+        f.pro.kind = PRO_RESID; f.pro.x = h->x1; f.pro.delta = h->ap; f.pro.post_w = d.post_attn;
+        f.pro.norm_w = d.ffn_norm; f.pro.x_out = h->x0; f.pro.n = m->E; f.pro.eps = m->eps;
+        f.seg[0] = {d.gate, h->gg}; f.seg[1] = {d.up, h->uu}; f.act_out = h->hh;
+        T(0, true); launch_gemv(f, m->FF, s); T(0, false);
+
+        GemvArgs dd{};
+        dd.mode = h->mode; dd.cols = m->FF; dd.act = ACT_NONE; dd.nseg = 1;
+        dd.pro.kind = PRO_PLAIN; dd.pro.x = h->hh; dd.pro.n = m->FF;
+        dd.seg[0] = {d.down, h->dn};
+        T(0, true); launch_gemv(dd, m->E, s); T(0, false);
+    }
+    if (sh.logits) {
+        GemvArgs lm{};
+        lm.mode = h->mode; lm.cols = m->E; lm.act = ACT_NONE; lm.nseg = 1;
+        lm.pro.kind = PRO_RESID; lm.pro.x = h->x0; lm.pro.delta = h->dn;
+        lm.pro.post_w = m->gemma ? m->L[m->NL - 1].post_ffw : nullptr;
+        lm.pro.norm_w = m->out_norm; lm.pro.x_out = nullptr; lm.pro.n = m->E; lm.pro.eps = m->eps;
+        lm.seg[0] = {m->out, h->logits};
+        T(1, true); launch_gemv(lm, m->V, s); T(1, false);
+        if (sh.argmax) {
+            T(5, true);
+            launch_argmax(h->logits, m->V, h->am_v, h->am_i, h->am_cnt, h->d_st, h->gen_log, argmax_blocks(m->V), s);
+            T(5, false);
+        }
+    }
+}
+
+int run_body(sp_kvdecode_handle *h, const StepShape &sh) {
+    if (!h->use_graph) {
+        enqueue_body(h, sh, nullptr, nullptr);
+        HIPCHK(hipGetLastError(), "kernel launch");
+        return 0;
+    }
+    sp_kvdecode_handle::GKey key{sh.logits, sh.argmax, sh.grid_global, sh.grid_local, sh.chunk_global};
+    auto it = h->graphs.find(key);
+    if (it == h->graphs.end()) {
+        hipGraph_t g;
+        HIPCHK(hipStreamBeginCapture(h->stream, hipStreamCaptureModeThreadLocal), "graph capture begin");
+        enqueue_body(h, sh, nullptr, nullptr);
+        HIPCHK(hipStreamEndCapture(h->stream, &g), "graph capture end");
+        hipGraphExec_t ge;
+        hipError_t e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+        hipGraphDestroy(g);
+        HIPCHK(e, "graph instantiate");
+        if (h->graphs.size() > 64) free_graphs(h);
+        it = h->graphs.insert({key, ge}).first;
+    }
+    HIPCHK(hipGraphLaunch(it->second, h->stream), "graph launch");
+    return 0;
+}
+
+// round the attention grids up so one captured graph serves a run of positions
+StepShape shape_for(const sp_kvdecode_handle *h, int pos, int logits, int argmax) {
+    StepShape sh{};
+    sh.logits = logits; sh.argmax = argmax;
+    const int hi = std::min(h->pmax - 1, ((pos / 256) + 1) * 256 - 1);
+    attn_chunks(h, h->use_graph ? hi : pos, sh);
+    return sh;
+}
+
+int set_state(sp_kvdecode_handle *h, int pos, int tok, int greedy) {
+    // one pinned slot per in-flight step: callers synchronize before reusing it
+    h->h_st->pos = pos; h->h_st->tok = tok; h->h_st->greedy = greedy; h->h_st->pad = 0;
+    HIPCHK(hipMemcpyAsync(h->d_st, h->h_st, sizeof(DState), hipMemcpyHostToDevice, h->stream), "state upload");
+    return 0;
+}
+
+int check_tok(const sp_kvdecode_handle *h, int32_t tok) {
+    if (tok < 0 || tok >= h->m->V) return fail("sp_hipkv: token %s%lld out of vocabulary range", "", (long long)tok);
+    return 0;
+}
+
+int step_one(sp_kvdecode_handle *h, int32_t tok, int want_logits) {
+    if (check_tok(h, tok)) return 1;
+    if (h->dpos >= h->pmax) return fail("sp_hipkv: context full (dpos == pmax %s%lld)", "", (long long)h->pmax);
+    if (ensure_pages(h, h->dpos, h->dpos + 1)) return 1;
+    if (set_state(h, h->dpos, tok, 0)) return 1;
+    StepShape sh = shape_for(h, h->dpos, want_logits, 0);
+    if (run_body(h, sh)) return 1;
+    return 0;
+}
+
+}  // namespace
+
+// ================================================================ C ABI
+extern "C" {
+
+int sp_hipkv_open(const void *qm_opaque, int pmax, sp_kvdecode_handle **out) {
+    if (!out) return fail("sp_hipkv_open: null out%s");
+    *out = nullptr;
+    if (!qm_opaque || pmax <= 0) return fail("sp_hipkv_open: null model or pmax <= 0%s");
+    std::lock_guard<std::mutex> lk(g_mu);
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0)
+        return fail("sp_hipkv_open: no HIP device visible (this backend runs on MI355X / gfx950)%s");
+    DevModel *m = model_get((const qwen3_model *)qm_opaque);
+    if (!m) return 1;
+    std::unique_ptr<sp_kvdecode_handle> h(new sp_kvdecode_handle);
+    h->m = m; h->pmax = pmax;
+    h->pool = std::make_shared<KvPool>();
+    h->pool->page_bytes = (size_t)2 * m->NKV * PAGE * m->HD * 4;
+    h->pool->pages_per_chunk = (int)std::max<size_t>(16, ((size_t)1 << 30) / h->pool->page_bytes);
+    if (hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking) != hipSuccess) { model_put(m); return fail("sp_hipkv_open: stream creation failed%s"); }
+    if (build_tables(h.get()) || alloc_scratch(h.get())) { sp_hipkv_close(h.release()); return 1; }
+    *out = h.release();
+    return 0;
+}
+
+void sp_hipkv_close(sp_kvdecode_handle *h) {
+    if (!h) return;
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (h->stream) hipStreamSynchronize(h->stream);
+    free_graphs(h);
+    if (h->pool) { std::lock_guard<std::mutex> pl(h->pool->mu); for (auto &v : h->pt) for (int id : v) h->pool->unref(id); }
+    h->pool.reset();
+    if (h->d_pt) hipFree(h->d_pt);
+    if (h->h_pt) hipHostFree(h->h_pt);
+    if (h->scratch) hipFree(h->scratch);
+    if (h->h_st) hipHostFree(h->h_st);
+    if (h->h_logits) hipHostFree(h->h_logits);
+    if (h->stream) hipStreamDestroy(h->stream);
+    model_put(h->m);
+    delete h;
+}
+
+int sp_hipkv_position(const sp_kvdecode_handle *h) { return h ? h->dpos : -1; }
+
+int sp_hipkv_rewind(sp_kvdecode_handle *h, int n) {
+    if (!h) return fail("sp_hipkv_rewind: null handle%s");
+    if (n < 0 || n > h->dpos) return fail("sp_hipkv_rewind: n %s%lld exceeds the resident position", "", (long long)n);
+    if (h->ring_pages > 0) {
+        // window layers keep ring_pages*PAGE positions: the window of the new
+        // position must not have been overwritten by a later position
+        const int cap = h->ring_pages * PAGE - h->m->SW;
+        if (h->hwm - (h->dpos - n) > cap)
+            return fail("sp_hipkv_rewind: rewinding %s%lld positions leaves the window ring (set a larger max_rewind)", "", (long long)n);
+    }
+    h->dpos -= n;          // stale slots past dpos are overwritten by the next steps
+    return 0;
+}
+
+int sp_hipkv_prefill(sp_kvdecode_handle *h, const int32_t *tokens, int n_tok) {
+    if (!h || (!tokens && n_tok > 0) || n_tok < 0) return fail("sp_hipkv_prefill: bad argument%s");
+    if (n_tok > h->pmax - h->dpos) return fail("sp_hipkv_prefill: context full%s");
+    for (int i = 0; i < n_tok; i++) if (check_tok(h, tokens[i])) return 1;
+    for (int i = 0; i < n_tok; i++) {
+        if (step_one(h, tokens[i], 0)) return 1;
+        HIPCHK(hipStreamSynchronize(h->stream), "prefill step");   // pinned state slot reuse
+        h->dpos++;
+        h->hwm = std::max(h->hwm, h->dpos);
+    }
+    return 0;
+}
+
+int sp_hipkv_decode_step(sp_kvdecode_handle *h, int32_t token, float *logits) {
+    if (!h || !logits) return fail("sp_hipkv_decode_step: null argument%s");
+    if (step_one(h, token, 1)) return 1;
+    HIPCHK(hipMemcpyAsync(h->h_logits, h->logits, (size_t)h->m->V * 4, hipMemcpyDeviceToHost, h->stream), "logits download");
+    HIPCHK(hipStreamSynchronize(h->stream), "decode step");
+    memcpy(logits, h->h_logits, (size_t)h->m->V * 4);
+    h->dpos++;
+    h->hwm = std::max(h->hwm, h->dpos);
+    return 0;
+}
+
+int sp_hipkv_set_mode(sp_kvdecode_handle *h, int exact) {
+    if (!h) return fail("sp_hipkv_set_mode: null handle%s");
+    const int m = exact ? EXACT : FLOAT;
+    if (m == h->mode) return 0;
+    if (h->dpos != 0) return fail("sp_hipkv_set_mode: the mode is fixed once tokens are resident%s");
+    h->mode = m;
+    free_graphs(h);
+    return 0;
+}
+
+int sp_hipkv_set_max_rewind(sp_kvdecode_handle *h, int max_rewind) {
+    if (!h || max_rewind < 0) return fail("sp_hipkv_set_max_rewind: bad argument%s");
+    if (h->dpos != 0) return fail("sp_hipkv_set_max_rewind: only before the first token%s");
+    { std::lock_guard<std::mutex> pl(h->pool->mu); for (auto &v : h->pt) for (int id : v) h->pool->unref(id); }
+    h->max_rewind = max_rewind;
+    free_graphs(h);
+    return build_tables(h);
+}
+
+int sp_hipkv_set_graph(sp_kvdecode_handle *h, int on) {
+    if (!h) return fail("sp_hipkv_set_graph: null handle%s");
+    h->use_graph = on ? 1 : 0;
+    if (!on) free_graphs(h);
+    return 0;
+}
+
+int sp_hipkv_fork(const sp_kvdecode_handle *p, sp_kvdecode_handle **out) {
+    if (!p || !out) return fail("sp_hipkv_fork: null argument%s");
+    *out = nullptr;
+    std::unique_ptr<sp_kvdecode_handle> h(new sp_kvdecode_handle);
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        h->m = p->m; h->m->refs++;
+    }
+    h->pool = p->pool; h->mode = p->mode; h->pmax = p->pmax; h->dpos = p->dpos; h->hwm = p->hwm;
+    h->use_graph = p->use_graph; h->max_rewind = p->max_rewind;
+    if (hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking) != hipSuccess) {
+        std::lock_guard<std::mutex> lk(g_mu); model_put(h->m); return fail("sp_hipkv_fork: stream creation failed%s");
+    }
+    hipStreamSynchronize(p->stream);
+    if (build_tables(h.get()) || alloc_scratch(h.get())) { sp_hipkv_close(h.release()); return 1; }
+    // share every mapped page (copy-on-write on the next append into it)
+    {
+        std::lock_guard<std::mutex> pl(h->pool->mu);
+        for (int l = 0; l < h->m->NL; l++) {
+            for (int s = 0; s < h->slots[l]; s++) {
+                const int id = p->pt[l][s];
+                h->pt[l][s] = id;
+                if (id >= 0) { h->pool->refc[id]++; h->h_pt[h->pt_off[l] + s] = h->pool->ptr[id]; }
+            }
+        }
+    }
+    size_t tot = 0; for (int l = 0; l < h->m->NL; l++) tot += (size_t)h->slots[l];
+    if (hipMemcpy(h->d_pt, h->h_pt, tot * sizeof(float *), hipMemcpyHostToDevice) != hipSuccess) {
+        sp_hipkv_close(h.release()); return fail("sp_hipkv_fork: page table upload failed%s");
+    }
+    *out = h.release();
+    return 0;
+}
+
+sp_status sp_hipkv_attach(sp_session *s, int pmax, int exact) {
+    if (!s || pmax <= 0) { sp_set_error("sp_hipkv_attach: bad argument"); return SP_EBADARG; }
+    sp_kvdecode_handle *h = nullptr;
+    if (sp_hipkv_open(sp_session_qwen3_model(s), pmax, &h)) return SP_EBACKEND_OOM;
+    if (exact && sp_hipkv_set_mode(h, 1)) { sp_hipkv_close(h); return SP_EBADSTATE; }
+    sp_status st = sp_session_register_kvdecode_backend(s, h, &sp_hipkv_dispatch);
+    if (st != SP_OK) { sp_hipkv_close(h); return st; }
+    return spx_session_own_kvdecode(s, 1);
+}
+
+int sp_hipkv_greedy(sp_kvdecode_handle *h, int32_t first_token, int n, int32_t *out_tokens, double *device_ms) {
+    if (!h || n < 0) return fail("sp_hipkv_greedy: bad argument%s");
+    if (check_tok(h, first_token)) return 1;
+    if (n > h->pmax - h->dpos) return fail("sp_hipkv_greedy: context full%s");
+    if (n == 0) { if (device_ms) *device_ms = 0; return 0; }
+    if (ensure_pages(h, h->dpos, h->dpos + n)) return 1;
+    if (set_state(h, h->dpos, first_token, 1)) return 1;
+    hipEvent_t e0, e1;
+    HIPCHK(hipEventCreate(&e0), "event"); HIPCHK(hipEventCreate(&e1), "event");
+    // pre-instantiate the graphs this run needs so capture is outside the timed region
+    for (int w = h->dpos / 256; w <= (h->dpos + n - 1) / 256; w++) {
+        StepShape sh = shape_for(h, std::max(h->dpos, w * 256), 1, 1);
+        if (h->use_graph) {
+            sp_kvdecode_handle::GKey key{sh.logits, sh.argmax, sh.grid_global, sh.grid_local, sh.chunk_global};
+            if (!h->graphs.count(key)) {
+                hipGraph_t g; hipGraphExec_t ge;
+                HIPCHK(hipStreamBeginCapture(h->stream, hipStreamCaptureModeThreadLocal), "capture");
+                enqueue_body(h, sh, nullptr, nullptr);
+                HIPCHK(hipStreamEndCapture(h->stream, &g), "capture end");
+                hipError_t er = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+                hipGraphDestroy(g);
+                HIPCHK(er, "instantiate");
+                h->graphs[key] = ge;
+            }
+        }
+    }
+    // the argmax kernel logs each position's token into gen_log[pos]
+    HIPCHK(hipEventRecord(e0, h->stream), "event record");
+    for (int i = 0; i < n; i++) {
+        StepShape sh = shape_for(h, h->dpos + i, 1, 1);
+        if (run_body(h, sh)) return 1;
+    }
+    HIPCHK(hipEventRecord(e1, h->stream), "event record");
+    HIPCHK(hipStreamSynchronize(h->stream), "greedy run");
+    float ms = 0; hipEventElapsedTime(&ms, e0, e1);
+    if (device_ms) *device_ms = ms;
+    hipEventDestroy(e0); hipEventDestroy(e1);
+    if (out_tokens)
+        HIPCHK(hipMemcpy(out_tokens, h->gen_log + h->dpos, (size_t)n * 4, hipMemcpyDeviceToHost), "token log read");
+    h->dpos += n;
+    h->hwm = std::max(h->hwm, h->dpos);
+    return 0;
+}
+
+int sp_hipkv_kernel_times(sp_kvdecode_handle *h, int32_t first_token, int n, double ms[6],
+                          long long launches[6], double bytes[6]) {
+    if (!h || n <= 0 || !ms || !launches || !bytes) return fail("sp_hipkv_kernel_times: bad argument%s");
+    if (check_tok(h, first_token)) return 1;
+    if (n > h->pmax - h->dpos) return fail("sp_hipkv_kernel_times: context full%s");
+    if (ensure_pages(h, h->dpos, h->dpos + n)) return 1;
+    if (set_state(h, h->dpos, first_token, 1)) return 1;
+    struct Ctx { hipStream_t s; std::vector<std::pair<int, std::pair<hipEvent_t, hipEvent_t>>> ev; hipEvent_t cur; };
+    Ctx c; c.s = h->stream;
+    auto cb = [](void *vp, int cls, bool begin) {
+        Ctx *cc = (Ctx *)vp;
+        hipEvent_t e; hipEventCreate(&e); hipEventRecord(e, cc->s);
+        if (begin) cc->cur = e; else cc->ev.push_back({cls, {cc->cur, e}});
+    };
+    for (int i = 0; i < 6; i++) { ms[i] = 0; launches[i] = 0; bytes[i] = 0; }
+    const DevModel *m = h->m;
+    const double kvb = (double)m->NKV * m->HD * 4 * 2;     // K+V bytes per position per layer
+    for (int i = 0; i < n; i++) {
+        const int pos = h->dpos + i;
+        StepShape sh = shape_for(h, pos, 1, 1);
+        enqueue_body(h, sh, cb, &c);
+        bytes[0] += (double)m->layer_bytes;
+        bytes[1] += (double)m->lm_bytes;
+        bytes[5] += (double)(m->embd.cols / 2 + m->embd.nblk * 2) + 4.0 * m->V;   // one embedding row + logits read by argmax
+        for (int l = 0; l < m->NL; l++) {
+            const bool glob = is_global(m, l);
+            const int s0 = (!glob && m->SW > 0 && pos - m->SW + 1 > 0) ? pos - m->SW + 1 : 0;
+            bytes[(glob || m->SW <= 0) ? 2 : 3] += kvb * (pos - s0 + 1);
+        }
+    }
+    HIPCHK(hipStreamSynchronize(h->stream), "timed run");
+    for (auto &e : c.ev) {
+        float t = 0; hipEventElapsedTime(&t, e.second.first, e.second.second);
+        ms[e.first] += t; launches[e.first]++;
+        hipEventDestroy(e.second.first); hipEventDestroy(e.second.second);
+    }
+    h->dpos += n;
+    h->hwm = std::max(h->hwm, h->dpos);
+    return 0;
+}
+
+int sp_hipkv_read_kv(const sp_kvdecode_handle *h, int layer, int p0, int n, float *k, float *v) {
+    if (!h || !k || !v || layer < 0 || layer >= h->m->NL || p0 < 0 || n < 0 || p0 + n > h->dpos)
+        return fail("sp_hipkv_read_kv: bad argument%s");
+    const DevModel *m = h->m;
+    const int HD = m->HD, NKV = m->NKV, S = h->slots[layer];
+    hipStreamSynchronize(h->stream);
+    for (int p = p0; p < p0 + n; p++) {
+        const int lp = p / PAGE, slot = S == h->full_pages ? lp : lp % S;
+        const int id = h->pt[layer][slot];
+        if (id < 0) return fail("sp_hipkv_read_kv: position not resident%s");
+        const float *page = h->pool->ptr[id];
+        for (int hh = 0; hh < NKV; hh++) {
+            const float *ks = page + ((size_t)hh * PAGE + p % PAGE) * HD;
+            const float *vs = page + (size_t)NKV * PAGE * HD + ((size_t)hh * PAGE + p % PAGE) * HD;
+            HIPCHK(hipMemcpy(k + (size_t)(p - p0) * NKV * HD + (size_t)hh * HD, ks, (size_t)HD * 4, hipMemcpyDeviceToHost), "kv read");
+            HIPCHK(hipMemcpy(v + (size_t)(p - p0) * NKV * HD + (size_t)hh * HD, vs, (size_t)HD * 4, hipMemcpyDeviceToHost), "kv read");
+        }
+    }
+    return 0;
+}
+
+int sp_hipkv_info(const sp_kvdecode_handle *h, long long out[8]) {
+    if (!h || !out) return fail("sp_hipkv_info: bad argument%s");
+    out[0] = (long long)h->m->weight_bytes; out[1] = (long long)h->m->lm_bytes;
+    out[2] = (long long)h->m->NKV * h->m->HD * 8; out[3] = h->mode; out[4] = h->dpos;
+    out[5] = (long long)h->pool->ptr.size(); out[6] = (long long)h->pool->page_bytes; out[7] = h->pmax;
+    return 0;
+}
+
+}  // extern "C"
+

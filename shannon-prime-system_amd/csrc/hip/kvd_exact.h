@@ -1,0 +1,123 @@
+// kvd_exact.h -- integer building blocks shared by the exact-mode kernels.
+// Same integer arithmetic as the exact islands (core/exact_islands/exact_islands.c:21-124);
+// every function here is a deterministic integer map, so device results are
+// bit-identical to the CPU arithmetic that defines them.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kvd {
+typedef __int128 i128;
+typedef unsigned __int128 u128;
+
+constexpr int FB = 30;
+constexpr int64_t ONE = (int64_t)1 << FB;
+constexpr int64_t LOG2E = 1549082005LL;                    // round(log2(e) * 2^30)
+__device__ constexpr int64_t EXPC[7] = {1073741824LL, 744261118LL, 257941248LL, 59597083LL,
+                                        10327387LL, 1431680LL, 165394LL};   // round((ln2)^k/k! * 2^30)
+constexpr int64_t GK = 856722024LL;                        // round(sqrt(2/pi) * 2^30)
+constexpr int64_t GA = 48012366LL;                         // round(0.044715 * 2^30)
+
+__device__ __forceinline__ int64_t exp2_frac(int64_t r) {
+    int64_t acc = EXPC[6];
+    #pragma unroll
+    for (int k = 5; k >= 0; k--) acc = ((acc * r) >> FB) + EXPC[k];
+    return acc;
+}
+// e^d for d <= 0, Q30 in and out
+__device__ __forceinline__ int64_t exp_fixed(int64_t d) {
+    int64_t g = (int64_t)(-(((i128)d * LOG2E) >> FB));
+    int64_t n = g >> FB, r = g - (n << FB);
+    if (n >= 32) return 0;
+    if (r) return exp2_frac(ONE - r) >> (n + 1);
+    return ONE >> n;
+}
+__device__ __forceinline__ uint64_t isqrt_u64(uint64_t v) {
+    uint64_t x = 0, b = 1ULL << 62;
+    while (b > v) b >>= 2;
+    while (b) {
+        if (v >= x + b) { v -= x + b; x = (x >> 1) + b; } else x >>= 1;
+        b >>= 2;
+    }
+    return x;
+}
+__device__ __forceinline__ int64_t tanh_fixed(int64_t t) {
+    int s = (t >= 0) ? 1 : -1;
+    int64_t a = (t >= 0) ? t : -t;
+    int64_t e2 = exp_fixed(-(2 * a));
+    int64_t num = (2 * e2) << FB;
+    return (int64_t)s * (ONE - num / (ONE + e2));
+}
+// round half away from zero of a double to int64 (llround)
+__device__ __forceinline__ int64_t llround_d(double d) { return (int64_t)round(d); }
+
+__device__ __forceinline__ float gelu_exact1(float x) {
+    int64_t xq = llround_d((double)x * 65536.0);
+    int64_t X = (xq * ONE) >> 16;
+    i128 X2 = ((i128)X * X) >> FB;
+    int64_t x3 = (int64_t)((X2 * X) >> FB);
+    i128 inner = ((i128)GK * (X + (int64_t)(((i128)GA * x3) >> FB))) >> FB;
+    int64_t t = tanh_fixed((int64_t)inner);
+    int64_t g = (int64_t)(((i128)(X >> 1) * (ONE + t)) >> FB);
+    return (float)((double)g / (double)ONE);
+}
+__device__ __forceinline__ float silu_exact1(float x) {
+    int64_t xq = llround_d((double)x * 65536.0);
+    int64_t X = (xq * ONE) >> 16;
+    int64_t e = exp_fixed(X >= 0 ? -X : X);
+    int64_t sg = X >= 0 ? (int64_t)(((i128)ONE << FB) / (ONE + e))
+                        : (int64_t)(((i128)e << FB) / (ONE + e));
+    int64_t g = (int64_t)(((i128)X * sg) >> FB);
+    return (float)((double)g / (double)ONE);
+}
+
+// Round-to-nearest-even of (mag * 2^k) to float, mag > 0.  Exact for every
+// input (normal, subnormal, overflow to inf): the one rounding primitive of
+// exact mode.  Any correct RNE gives the same bits, so this matches the CPU.
+__device__ __forceinline__ float rne_u128_scaled(u128 mag, int k) {
+    if (!mag) return 0.0f;
+    uint64_t hi = (uint64_t)(mag >> 64), lo = (uint64_t)mag;
+    int msb = hi ? 127 - __builtin_clzll(hi) : 63 - __builtin_clzll(lo);
+    int e = msb + k;
+    int keep = 24;
+    if (e < -126) keep = 24 - (-126 - e);
+    if (keep <= 0) {
+        if (keep == 0) return (mag == ((u128)1 << msb)) ? 0.0f : 0x1.0p-149f;
+        return 0.0f;
+    }
+    int drop = msb + 1 - keep;
+    uint32_t q;
+    if (drop > 0) {
+        u128 qq = mag >> drop;
+        u128 rem = mag & (((u128)1 << drop) - 1u), half = (u128)1 << (drop - 1);
+        if (rem > half || (rem == half && (qq & 1u))) qq++;
+        q = (uint32_t)qq;
+    } else {
+        q = (uint32_t)(mag << (-drop));
+    }
+    return ldexpf((float)q, k + drop);
+}
+__device__ __forceinline__ float rne_i128_scaled(i128 v, int k) {
+    return v >= 0 ? rne_u128_scaled((u128)v, k) : -rne_u128_scaled((u128)(-v), k);
+}
+__device__ __forceinline__ float rne_i64_scaled(int64_t v, int k) {
+    return v >= 0 ? rne_u128_scaled((u128)(uint64_t)v, k) : -rne_u128_scaled((u128)(uint64_t)(-v), k);
+}
+// RNE of num / (den * 2^k), den > 0
+__device__ __forceinline__ int bitlen128(u128 v) {
+    uint64_t hi = (uint64_t)(v >> 64), lo = (uint64_t)v;
+    return hi ? 128 - __builtin_clzll(hi) : (lo ? 64 - __builtin_clzll(lo) : 0);
+}
+__device__ __forceinline__ float rne_div_to_float(i128 num, int64_t den, int k) {
+    if (!num) return 0.0f;
+    bool neg = num < 0;
+    u128 n = neg ? (u128)(-num) : (u128)num, d = (u128)(uint64_t)den;
+    int sh = 28 + bitlen128(d) - bitlen128(n);
+    if (sh < 0) sh = 0;
+    n <<= sh;
+    u128 q = n / d, r = n % d;
+    q = (q << 1) | (r ? 1u : 0u);
+    float f = rne_u128_scaled(q, -(k + sh + 1));
+    return neg ? -f : f;
+}
+}  // namespace kvd

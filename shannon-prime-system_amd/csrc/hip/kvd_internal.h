@@ -1,0 +1,88 @@
+// kvd_internal.h -- shared definitions of the HIP kvdecode backend (device
+// layouts, kernel argument blocks, launchers).  Not part of the C ABI.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kvd {
+
+constexpr int PAGE = 64;            // positions per KV page
+constexpr int GEMV_WAVES = 4;       // waves per GEMV workgroup
+constexpr int GEMV_R = 4;           // rows per wave pass
+constexpr int NDIG = 6;             // balanced base-16 digit planes of an activation (|xq| < 2^22)
+
+enum Mode { FLOAT = 0, EXACT = 1 };
+
+// One OK_Q4B weight tensor on the device, reference row layout:
+// codes [rows][cols/2] nibbles (low = even column), scales [rows][cols/32] f16,
+// plus ebase[rows] = smallest block exponent of the row (for the int64 fast path).
+struct DevW {
+    const uint8_t  *codes;
+    const uint16_t *bs;
+    const int8_t   *ebase;
+    int rows, cols, nblk, wide;   // wide: a row's exponent spread needs the int128 path
+};
+
+// Input transform run by every GEMV workgroup before the matrix pass.
+enum ProKind { PRO_PLAIN = 0, PRO_NORM = 1, PRO_RESID = 2 };
+struct ProArgs {
+    const float *x;        // residual stream (or plain input)
+    const float *delta;    // PRO_RESID: branch output added into x
+    const float *post_w;   // PRO_RESID: sandwich norm weight on delta (NULL = add raw)
+    const float *norm_w;   // PRO_NORM / PRO_RESID: pre-norm weight
+    float       *x_out;    // PRO_RESID: updated residual (written by workgroup 0)
+    int   kind, n;
+    float eps;
+};
+
+struct Seg { DevW w; float *out; };
+enum Act { ACT_NONE = 0, ACT_GELU = 1, ACT_SILU = 2 };
+struct GemvArgs {
+    ProArgs pro;
+    Seg  seg[3];
+    int  nseg;
+    int  cols;
+    int  act;          // paired gate/up with activation: seg[0] = gate, seg[1] = up
+    float *act_out;    // h = act(gate) * up
+    int  mode;
+};
+
+// Per-session device-side step state (graph-replay friendly: kernels read it).
+struct DState {
+    int pos;           // position of the token being processed
+    int tok;           // token id being processed
+    int greedy;        // argmax kernel writes tok = argmax and advances pos
+    int pad;
+};
+
+struct AttnArgs {
+    const float *q;          // un-rotated q [NH*HD] (GEMV output)
+    const float *k;          // new k [KVD]
+    const float *v;          // new v [KVD]
+    const float *q_norm, *k_norm;
+    float *qr;               // rotated+normed q [NH*HD]
+    float *const *pages;     // page table of this layer: device page pointers
+    int   ring_pages;        // 0 = full table, else number of ring slots
+    float *ao;               // output [NH*HD]
+    float *part;             // partials [NKV*G][max_chunks][HD]
+    float *part_ml;          // [NKV*G][max_chunks][2] (max, sum) or exact (max, S lo/hi)
+    int   *counter;          // [NKV] arrival counters (self-resetting)
+    int   *zscratch;         // exact mode: int32 score grid per (head, position)
+    const DState *st;
+    const int64_t *freq_q60; // exact-mode RoPE frequencies base^(-2i/HD) in Q60 [HD/2]
+    int NH, NKV, HD, win, max_chunks, chunk, mode;
+    float eps, base, ascale;
+};
+
+// launchers (kvd_kernels.hip)
+void launch_embed(const DevW &embd, const DState *st, float *x, float scale, hipStream_t s);
+void launch_gemv(const GemvArgs &a, int nrows_total, hipStream_t s);
+void launch_qk_prep(const AttnArgs &a, hipStream_t s);
+void launch_attention(const AttnArgs &a, int grid_chunks, hipStream_t s);
+void set_rope_tables(const int64_t atan_q60[64], int64_t kinv_q62);
+void launch_argmax(const float *logits, int V, float *pval, int *pidx, int *counter,
+                   DState *st, int *gen_log, int nblocks, hipStream_t s);
+int  argmax_blocks(int V);
+int  gemv_grid(int nrows_total, int cols, int paired);
+
+}  // namespace kvd

@@ -1,0 +1,294 @@
+"""spkv -- Python host mirror of the C ABI (include/sp_l1_abi.h, sp_model_abi.h,
+sp_hipkv.h) through ctypes.
+
+The product is the two in-tree shared libraries:
+  lib/libsp_l1.so     .sp-model loader / bridge / session verbs / OK_Q4B producer (C11)
+  lib/libsp_hipkv.so  the section-6b kvdecode backend on MI355X (HIP, gfx950)
+This module only declares their signatures and wraps handles; it computes
+nothing itself.  Loading libsp_hipkv.so fails loudly when it has not been built.
+"""
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_DIR = os.path.join(HERE, "lib")
+
+SP_OK, SP_EBADARG, SP_EBADSTATE, SP_EUNSUPPORTED = 0, -3, -4, -5
+SP_ECANCEL, SP_ECONTEXT_FULL, SP_EBACKEND_OOM = -2, -33, -43
+ARCH_QWEN3, ARCH_GEMMA3 = 2, 3
+
+c_void_p, c_int, c_int32, c_size_t, c_float, c_double = (
+    ctypes.c_void_p, ctypes.c_int, ctypes.c_int32, ctypes.c_size_t, ctypes.c_float, ctypes.c_double)
+c_char_p, c_uint32, c_uint64, c_longlong = ctypes.c_char_p, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_longlong
+
+
+class SynthSpec(ctypes.Structure):
+    """sp_synth_spec (include/sp_model_abi.h)."""
+    _fields_ = [("arch_id", c_uint32), ("n_layers", c_uint32), ("hidden", c_uint32),
+                ("n_heads", c_uint32), ("n_kv_heads", c_uint32), ("head_dim", c_uint32),
+                ("n_ff", c_uint32), ("vocab", c_uint32), ("max_context", c_uint32),
+                ("swa_window", c_uint32), ("rope_base", c_float), ("rms_eps", c_float),
+                ("untied", c_int), ("seed", c_uint64)]
+
+
+class SessionConfig(ctypes.Structure):
+    """sp_session_config (include/sp/sp_l1.h:160-169)."""
+    _fields_ = [("max_context", c_size_t), ("deterministic", c_int), ("arm_bank_kb", c_uint32),
+                ("sieve_capacity", c_uint32), ("flags", c_uint32), ("precision_override", c_uint32)]
+
+
+class DispatchTable(ctypes.Structure):
+    """sp_kvdecode_dispatch_fn (include/sp/sp_l1.h:403-410)."""
+    _fields_ = [("open", c_void_p), ("prefill", c_void_p), ("decode_step", c_void_p),
+                ("rewind", c_void_p), ("position", c_void_p), ("close", c_void_p)]
+
+
+_l1 = None
+_kv = None
+
+
+def _sig(lib, name, res, args):
+    f = getattr(lib, name)
+    f.restype = res
+    f.argtypes = args
+    return f
+
+
+def l1():
+    """libsp_l1.so: host C library (no GPU needed)."""
+    global _l1
+    if _l1 is None:
+        path = os.path.join(LIB_DIR, "libsp_l1.so")
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} is not built: run __graft_entry__.build()")
+        lib = ctypes.CDLL(path, mode=ctypes.RTLD_GLOBAL)
+        _sig(lib, "sp_last_error", c_char_p, [])
+        _sig(lib, "sp_crc32", c_uint32, [c_void_p, c_size_t])
+        _sig(lib, "sp_sha256", None, [c_void_p, c_size_t, c_void_p])
+        _sig(lib, "sp_xxh64", c_uint64, [c_void_p, c_size_t, c_uint64])
+        _sig(lib, "sp_f16_to_f32", c_float, [ctypes.c_uint16])
+        _sig(lib, "sp_f32_to_f16", ctypes.c_uint16, [c_float])
+        _sig(lib, "sp_q4b_quantize_row", None, [c_void_p, c_int, c_void_p, c_void_p])
+        _sig(lib, "sp_write_synthetic_q4b", c_int, [ctypes.POINTER(SynthSpec), c_char_p, c_char_p, c_int])
+        _sig(lib, "sp_model_load", c_int, [c_char_p, c_char_p, ctypes.POINTER(c_void_p)])
+        _sig(lib, "sp_model_unload", None, [c_void_p])
+        _sig(lib, "sp_model_find_tensor", c_void_p, [c_void_p, c_char_p])
+        _sig(lib, "sp_model_tensor_count", c_uint32, [c_void_p])
+        _sig(lib, "sp_model_arch", c_int, [c_void_p, c_void_p])
+        _sig(lib, "sp_session_create", c_int, [c_void_p, ctypes.POINTER(SessionConfig), c_void_p, ctypes.POINTER(c_void_p)])
+        _sig(lib, "sp_session_destroy", None, [c_void_p])
+        _sig(lib, "sp_prefill_chunk", c_int, [c_void_p, c_void_p, c_size_t, c_void_p, c_size_t])
+        _sig(lib, "sp_decode_step", c_int, [c_void_p, c_int32, c_void_p, c_size_t])
+        _sig(lib, "sp_session_clone", c_int, [c_void_p, c_void_p, ctypes.POINTER(c_void_p)])
+        _sig(lib, "sp_session_rewind", c_int, [c_void_p, c_size_t])
+        _sig(lib, "sp_session_position", c_int, [c_void_p, ctypes.POINTER(c_size_t)])
+        _sig(lib, "sp_session_qwen3_model", c_void_p, [c_void_p])
+        _sig(lib, "sp_session_register_kvdecode_backend", c_int, [c_void_p, c_void_p, c_void_p])
+        _sig(lib, "sp_session_kvdecode_backend_handle", c_void_p, [c_void_p])
+        _sig(lib, "sp_session_kvdecode_backend_dt", c_void_p, [c_void_p])
+        _sig(lib, "spx_session_own_kvdecode", c_int, [c_void_p, c_int])
+        _l1 = lib
+    return _l1
+
+
+def kv():
+    """libsp_hipkv.so: the HIP backend.  Raises if not built (no fallback)."""
+    global _kv
+    if _kv is None:
+        l1()
+        path = os.path.join(LIB_DIR, "libsp_hipkv.so")
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} is not built: the HIP kvdecode backend is required")
+        lib = ctypes.CDLL(path, mode=ctypes.RTLD_GLOBAL)
+        _sig(lib, "sp_hipkv_open", c_int, [c_void_p, c_int, ctypes.POINTER(c_void_p)])
+        _sig(lib, "sp_hipkv_prefill", c_int, [c_void_p, c_void_p, c_int])
+        _sig(lib, "sp_hipkv_decode_step", c_int, [c_void_p, c_int32, c_void_p])
+        _sig(lib, "sp_hipkv_rewind", c_int, [c_void_p, c_int])
+        _sig(lib, "sp_hipkv_position", c_int, [c_void_p])
+        _sig(lib, "sp_hipkv_close", None, [c_void_p])
+        _sig(lib, "sp_hipkv_set_mode", c_int, [c_void_p, c_int])
+        _sig(lib, "sp_hipkv_set_max_rewind", c_int, [c_void_p, c_int])
+        _sig(lib, "sp_hipkv_set_graph", c_int, [c_void_p, c_int])
+        _sig(lib, "sp_hipkv_fork", c_int, [c_void_p, ctypes.POINTER(c_void_p)])
+        _sig(lib, "sp_hipkv_attach", c_int, [c_void_p, c_int, c_int])
+        _sig(lib, "sp_hipkv_greedy", c_int, [c_void_p, c_int32, c_int, c_void_p, ctypes.POINTER(c_double)])
+        _sig(lib, "sp_hipkv_kernel_times", c_int, [c_void_p, c_int32, c_int, c_void_p, c_void_p, c_void_p])
+        _sig(lib, "sp_hipkv_read_kv", c_int, [c_void_p, c_int, c_int, c_int, c_void_p, c_void_p])
+        _sig(lib, "sp_hipkv_info", c_int, [c_void_p, c_void_p])
+        _kv = lib
+    return _kv
+
+
+def last_error():
+    e = l1().sp_last_error()
+    return e.decode(errors="replace") if e else ""
+
+
+def ptr(a):
+    """numpy array -> void* (ctypes would otherwise truncate the address to int)."""
+    return c_void_p(a.ctypes.data)
+
+
+def check(rc, what):
+    if rc != 0:
+        raise RuntimeError(f"{what} failed ({rc}): {last_error()}")
+
+
+# ---------------------------------------------------------------- shapes
+SHAPES = {
+    # hidden, layers, heads, kv_heads, head_dim, ffn, vocab, arch, rope_base, swa
+    "qwen3-0.6b-1layer": dict(arch_id=ARCH_QWEN3, n_layers=1, hidden=1024, n_heads=16, n_kv_heads=8,
+                              head_dim=128, n_ff=3072, vocab=151936, rope_base=1e6, swa_window=0),
+    "qwen3-0.6b": dict(arch_id=ARCH_QWEN3, n_layers=28, hidden=1024, n_heads=16, n_kv_heads=8,
+                       head_dim=128, n_ff=3072, vocab=151936, rope_base=1e6, swa_window=0),
+    "gemma3-12b": dict(arch_id=ARCH_GEMMA3, n_layers=48, hidden=3840, n_heads=16, n_kv_heads=8,
+                       head_dim=256, n_ff=15360, vocab=262144, rope_base=1e6, swa_window=1024),
+    "qwen3-8b": dict(arch_id=ARCH_QWEN3, n_layers=36, hidden=4096, n_heads=32, n_kv_heads=8,
+                     head_dim=128, n_ff=12288, vocab=151936, rope_base=1e6, swa_window=0, untied=1),
+}
+
+
+def write_model(path_prefix, shape=None, seed=0, max_context=4096, threads=0, **kw):
+    """Write <prefix>.spm/.spt with the seeded OK_Q4B generator (sp_write_synthetic_q4b)."""
+    d = dict(SHAPES[shape]) if shape else {}
+    d.update(kw)
+    spec = SynthSpec(d["arch_id"], d["n_layers"], d["hidden"], d["n_heads"], d["n_kv_heads"],
+                     d["head_dim"], d["n_ff"], d["vocab"], max_context, d.get("swa_window", 0),
+                     d.get("rope_base", 1e6), d.get("rms_eps", 1e-6), d.get("untied", 0), seed)
+    spm, spt = path_prefix + ".spm", path_prefix + ".spt"
+    check(l1().sp_write_synthetic_q4b(ctypes.byref(spec), spm.encode(), spt.encode(), threads),
+          "sp_write_synthetic_q4b")
+    return spm, spt
+
+
+class Model:
+    def __init__(self, spm, spt):
+        h = c_void_p()
+        check(l1().sp_model_load(spm.encode(), spt.encode(), ctypes.byref(h)), "sp_model_load")
+        self.h = h
+
+    def close(self):
+        if self.h:
+            l1().sp_model_unload(self.h)
+            self.h = None
+
+
+class Session:
+    """sp_session over a Model; attach() registers the HIP backend (owned)."""
+
+    def __init__(self, model, max_context=0, cancel=None):
+        cfg = SessionConfig(max_context, 1, 0, 0, 0, 0)
+        h = c_void_p()
+        self.cancel = cancel
+        check(l1().sp_session_create(model.h, ctypes.byref(cfg),
+                                     ctypes.addressof(cancel) if cancel is not None else None,
+                                     ctypes.byref(h)), "sp_session_create")
+        self.h = h
+
+    def attach(self, pmax, exact=False):
+        check(kv().sp_hipkv_attach(self.h, pmax, 1 if exact else 0), "sp_hipkv_attach")
+
+    def prefill(self, toks, logits):
+        import numpy as np
+        t = np.ascontiguousarray(toks, dtype=np.int32)
+        return l1().sp_prefill_chunk(self.h, ptr(t), len(t), ptr(logits), logits.size)
+
+    def decode(self, tok, logits):
+        return l1().sp_decode_step(self.h, int(tok), ptr(logits), logits.size)
+
+    def position(self):
+        p = c_size_t()
+        check(l1().sp_session_position(self.h, ctypes.byref(p)), "sp_session_position")
+        return p.value
+
+    def rewind(self, n):
+        return l1().sp_session_rewind(self.h, n)
+
+    def clone(self):
+        c = Session.__new__(Session)
+        h = c_void_p()
+        rc = l1().sp_session_clone(self.h, None, ctypes.byref(h))
+        check(rc, "sp_session_clone")
+        c.h = h
+        c.cancel = None
+        return c
+
+    def backend_handle(self):
+        return l1().sp_session_kvdecode_backend_handle(self.h)
+
+    def close(self):
+        if self.h:
+            l1().sp_session_destroy(self.h)
+            self.h = None
+
+
+class Backend:
+    """A bare section-6b handle driven through the dispatch functions directly."""
+
+    def __init__(self, qm, pmax, exact=False, graph=True):
+        h = c_void_p()
+        check(kv().sp_hipkv_open(qm, pmax, ctypes.byref(h)), "sp_hipkv_open")
+        self.h = h
+        if exact:
+            check(kv().sp_hipkv_set_mode(h, 1), "sp_hipkv_set_mode")
+        if not graph:
+            check(kv().sp_hipkv_set_graph(h, 0), "sp_hipkv_set_graph")
+
+    @classmethod
+    def wrap(cls, h):
+        b = cls.__new__(cls)
+        b.h = c_void_p(h) if not isinstance(h, c_void_p) else h
+        return b
+
+    def prefill(self, toks):
+        import numpy as np
+        t = np.ascontiguousarray(toks, dtype=np.int32)
+        check(kv().sp_hipkv_prefill(self.h, ptr(t), len(t)), "sp_hipkv_prefill")
+
+    def decode(self, tok, logits):
+        check(kv().sp_hipkv_decode_step(self.h, int(tok), ptr(logits)), "sp_hipkv_decode_step")
+
+    def rewind(self, n):
+        return kv().sp_hipkv_rewind(self.h, n)
+
+    def position(self):
+        return kv().sp_hipkv_position(self.h)
+
+    def fork(self):
+        c = c_void_p()
+        check(kv().sp_hipkv_fork(self.h, ctypes.byref(c)), "sp_hipkv_fork")
+        return Backend.wrap(c)
+
+    def greedy(self, first_tok, n):
+        import numpy as np
+        out = np.zeros(n, dtype=np.int32)
+        ms = c_double()
+        check(kv().sp_hipkv_greedy(self.h, int(first_tok), n, ptr(out), ctypes.byref(ms)), "sp_hipkv_greedy")
+        return out, ms.value
+
+    def kernel_times(self, first_tok, n):
+        import numpy as np
+        ms = np.zeros(6, np.float64)
+        nl = np.zeros(6, np.int64)
+        by = np.zeros(6, np.float64)
+        check(kv().sp_hipkv_kernel_times(self.h, int(first_tok), n, ptr(ms), ptr(nl), ptr(by)),
+              "sp_hipkv_kernel_times")
+        return ms, nl, by
+
+    def read_kv(self, layer, p0, n, kvd):
+        import numpy as np
+        k = np.zeros((n, kvd), np.float32)
+        v = np.zeros((n, kvd), np.float32)
+        check(kv().sp_hipkv_read_kv(self.h, layer, p0, n, ptr(k), ptr(v)), "sp_hipkv_read_kv")
+        return k, v
+
+    def info(self):
+        import numpy as np
+        o = np.zeros(8, np.int64)
+        check(kv().sp_hipkv_info(self.h, ptr(o)), "sp_hipkv_info")
+        return o
+
+    def close(self):
+        if self.h:
+            kv().sp_hipkv_close(self.h)
+            self.h = None
