@@ -24,7 +24,7 @@ OBJ := $(patsubst %.c,$(OUT)/obj/%.o,$(SRC))
 CFLAGS := -std=gnu11 -O2 -fPIC -w -I$(REF)/include -I$(REF)/core/session
 
 $(OUT)/libspref.so: $(OBJ) $(ORC)/ref_harness.c
-	$(CC) $(CFLAGS) -shared -o $@ $(OBJ) $(ORC)/ref_harness.c -lm -lpthread
+	$(CC) $(CFLAGS) -shared -Wl,-Bsymbolic -o $@ $(OBJ) $(ORC)/ref_harness.c -lm -lpthread
 
 $(OUT)/obj/%.o: $(REF)/%.c
 	@mkdir -p $(dir $@)

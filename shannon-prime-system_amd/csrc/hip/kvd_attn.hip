@@ -118,11 +118,10 @@ __global__ __launch_bounds__(64) void k_qk_prep(AttnArgs a) {
         ss = wsuml(ss);
         if (ss == 0) { for (int j = 0; j < per; j++) v[j] = 0.0f; }
         else {
-            const int64_t inv = (int64_t)isqrt_u64((uint64_t)(((i128)HD << 72) / (i128)ss));
+            const int64_t inv = (int64_t)isqrt_u64(udiv128_64((u128)HD << 72, (uint64_t)ss));
             for (int j = 0; j < per; j++) {
                 int64_t xi = llround_d((double)v[j] * 65536.0), wi = llround_d((double)nw[lane + 64 * j] * 65536.0);
-                i128 yi = (i128)xi * inv * wi;
-                v[j] = (float)((double)(int64_t)yi / 4503599627370496.0);
+                v[j] = (float)((double)mul3_lo64(xi, inv, wi) / 4503599627370496.0);
             }
         }
     }
@@ -142,7 +141,7 @@ __global__ __launch_bounds__(64) void k_qk_prep(AttnArgs a) {
             rot[i + half] = x0 * s + x1 * c;
         } else {
             const i128 th = (i128)pos * freq_q60[i];
-            const int64_t r = (int64_t)(th % (i128)TWO_PI_Q60);
+            const int64_t r = umod128_64(th, TWO_PI_Q60);
             int64_t co, si; cordic_q62(r, co, si);
             c = rne_i64_scaled(co, -62); s = rne_i64_scaled(si, -62);
             const float ac = x0 * c, bs = x1 * s, as = x0 * s, bc = x1 * c;
@@ -277,16 +276,14 @@ __global__ __launch_bounds__(256) void k_attn_float(AttnArgs a) {
     for (int i = threadIdx.x; i < G * HD; i += 256) {
         const int g = i / HD, d = i % HD;
         const size_t base = (size_t)(h * G + g) * a.max_chunks;
+        // plain loads: the acquire fence above invalidated this CU's L1
+        const float *pml = a.part_ml + base * 2, *po = a.part + base * HD + d;
         float M = -INFINITY;
-        for (int k = 0; k < nch; k++)
-            M = fmaxf(M, __hip_atomic_load(&a.part_ml[(base + k) * 2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        for (int k = 0; k < nch; k++) M = fmaxf(M, pml[k * 2]);
         float L = 0.0f, acc = 0.0f;
         for (int k = 0; k < nch; k++) {
-            const float mk = __hip_atomic_load(&a.part_ml[(base + k) * 2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const float lk = __hip_atomic_load(&a.part_ml[(base + k) * 2 + 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const float ok = __hip_atomic_load(&a.part[(base + k) * HD + d], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const float w = expf(mk - M);
-            L += lk * w; acc += ok * w;
+            const float w = expf(pml[k * 2] - M);
+            L += pml[k * 2 + 1] * w; acc += po[(size_t)k * HD] * w;
         }
         a.ao[(size_t)(h * G + g) * HD + d] = acc / L;
     }
@@ -414,9 +411,9 @@ __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a) {
         const int g = i / HD, d = i % HD;
         const size_t base = (size_t)(h * G + g) * a.max_chunks;
         i128 acc = 0; int64_t S = 0;
-        for (int k = 0; k < nch; k++) {
-            acc += (i128)__hip_atomic_load(&part[(base + k) * HD + d], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            S += __hip_atomic_load((int64_t *)&pml[(base + k) * 4 + 2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int k = 0; k < nch; k++) {          // plain loads after the acquire fence
+            acc += (i128)part[(base + k) * HD + d];
+            S += *(const int64_t *)&pml[(base + k) * 4 + 2];
         }
         a.ao[(size_t)(h * G + g) * HD + d] = rne_div_to_float(acc, S, 16);
     }
@@ -443,8 +440,8 @@ void launch_attention(const AttnArgs &a, int grid_chunks, hipStream_t s) {
 }
 
 // ------------------------------------------------------------------ embedding
-__global__ __launch_bounds__(256) void k_embed(DevW w, const DState *st, float *x, float scale) {
-    const int tok = st->tok, E = w.cols;
+__global__ __launch_bounds__(256) void k_embed(DevW w, const DState *st, const int *tokbuf, float *x, float scale) {
+    const int tok = st->drive == DRIVE_STREAM ? tokbuf[st->pos] : st->tok, E = w.cols;
     const uint8_t *rc = w.codes + (size_t)tok * ((E + 1) / 2);
     const uint16_t *bs = w.bs + (size_t)tok * w.nblk;
     for (int i = threadIdx.x; i < E; i += blockDim.x) {
@@ -457,9 +454,13 @@ __global__ __launch_bounds__(256) void k_embed(DevW w, const DState *st, float *
         x[i] = v;
     }
 }
-void launch_embed(const DevW &embd, const DState *st, float *x, float scale, hipStream_t s) {
-    hipLaunchKernelGGL(k_embed, dim3(1), dim3(256), 0, s, embd, st, x, scale);
+void launch_embed(const DevW &embd, const DState *st, const int *tokbuf, float *x, float scale, hipStream_t s) {
+    hipLaunchKernelGGL(k_embed, dim3(1), dim3(256), 0, s, embd, st, tokbuf, x, scale);
 }
+__global__ void k_advance(DState *st) {
+    if (threadIdx.x == 0 && st->drive == DRIVE_STREAM) st->pos = st->pos + 1;
+}
+void launch_advance(DState *st, hipStream_t s) { hipLaunchKernelGGL(k_advance, dim3(1), dim3(64), 0, s, st); }
 
 // ------------------------------------------------------------------ argmax
 // lowest index among the maxima (strict '>' scan order of the reference callers)
@@ -484,13 +485,11 @@ __global__ __launch_bounds__(256) void k_argmax(const float *lg, int V, float *p
     if (!is_last || threadIdx.x != 0) return;
     __threadfence();
     float bv = -INFINITY; int bi = 0x7FFFFFFF;
-    for (int b = 0; b < (int)gridDim.x; b++)
-        amax_merge(bv, bi, __hip_atomic_load(&pv[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
-                   __hip_atomic_load(&pi[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    for (int b = 0; b < (int)gridDim.x; b++) amax_merge(bv, bi, pv[b], pi[b]);
     if (bi == 0x7FFFFFFF) bi = 0;
     st->tok = bi;
     if (gen_log) gen_log[st->pos] = bi;
-    if (st->greedy) st->pos = st->pos + 1;
+    if (st->drive == DRIVE_GREEDY) st->pos = st->pos + 1;
     *counter = 0;
 }
 int argmax_blocks(int V) { int b = (V + 2047) / 2048; return b < 1 ? 1 : (b > 256 ? 256 : b); }

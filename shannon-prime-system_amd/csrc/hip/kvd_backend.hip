@@ -329,6 +329,7 @@ struct sp_kvdecode_handle {
           *ao = nullptr, *ap = nullptr, *gg = nullptr, *uu = nullptr, *hh = nullptr, *dn = nullptr,
           *logits = nullptr, *part = nullptr, *part_ml = nullptr, *am_v = nullptr;
     int *counter = nullptr, *zscratch = nullptr, *am_i = nullptr, *am_cnt = nullptr, *gen_log = nullptr;
+    int *tokbuf = nullptr;                   // DRIVE_STREAM tokens by absolute position
     float *h_logits = nullptr;               // pinned staging
     int max_chunks = 0;
     void *scratch = nullptr;
@@ -429,6 +430,7 @@ int alloc_scratch(sp_kvdecode_handle *h) {
         {(void **)&h->logits, (size_t)m->V * 4}, {(void **)&h->part, part_bytes}, {(void **)&h->part_ml, ml_bytes},
         {(void **)&h->zscratch, z_bytes}, {(void **)&h->counter, 64 * 4}, {(void **)&h->am_v, (size_t)amb * 4},
         {(void **)&h->am_i, (size_t)amb * 4}, {(void **)&h->am_cnt, 64}, {(void **)&h->gen_log, (size_t)h->pmax * 4 + 64},
+        {(void **)&h->tokbuf, (size_t)h->pmax * 4 + 64},
         {(void **)&h->d_st, sizeof(DState) * 4},
     };
     size_t tot = 0;
@@ -467,7 +469,7 @@ void enqueue_body(sp_kvdecode_handle *h, const StepShape &sh, TimeCb cb, void *c
     const int QD = m->NH * m->HD, KVD = m->NKV * m->HD;
     auto T = [&](int cls, bool b) { if (cb) cb(ctx, cls, b); };
     T(5, true);
-    launch_embed(m->embd, h->d_st, h->x1, m->gemma ? sqrtf((float)m->E) : 0.0f, s);
+    launch_embed(m->embd, h->d_st, h->tokbuf, h->x1, m->gemma ? sqrtf((float)m->E) : 0.0f, s);
     T(5, false);
     for (int l = 0; l < m->NL; l++) {
         const DevLayer &d = m->L[l];
@@ -531,6 +533,8 @@ void enqueue_body(sp_kvdecode_handle *h, const StepShape &sh, TimeCb cb, void *c
             launch_argmax(h->logits, m->V, h->am_v, h->am_i, h->am_cnt, h->d_st, h->gen_log, argmax_blocks(m->V), s);
             T(5, false);
         }
+    } else {
+        launch_advance(h->d_st, s);
     }
 }
 
@@ -567,9 +571,9 @@ StepShape shape_for(const sp_kvdecode_handle *h, int pos, int logits, int argmax
     return sh;
 }
 
-int set_state(sp_kvdecode_handle *h, int pos, int tok, int greedy) {
+int set_state(sp_kvdecode_handle *h, int pos, int tok, int drive) {
     // one pinned slot per in-flight step: callers synchronize before reusing it
-    h->h_st->pos = pos; h->h_st->tok = tok; h->h_st->greedy = greedy; h->h_st->pad = 0;
+    h->h_st->pos = pos; h->h_st->tok = tok; h->h_st->drive = drive; h->h_st->pad = 0;
     HIPCHK(hipMemcpyAsync(h->d_st, h->h_st, sizeof(DState), hipMemcpyHostToDevice, h->stream), "state upload");
     return 0;
 }
@@ -583,7 +587,7 @@ int step_one(sp_kvdecode_handle *h, int32_t tok, int want_logits) {
     if (check_tok(h, tok)) return 1;
     if (h->dpos >= h->pmax) return fail("sp_hipkv: context full (dpos == pmax %s%lld)", "", (long long)h->pmax);
     if (ensure_pages(h, h->dpos, h->dpos + 1)) return 1;
-    if (set_state(h, h->dpos, tok, 0)) return 1;
+    if (set_state(h, h->dpos, tok, DRIVE_HOST)) return 1;
     StepShape sh = shape_for(h, h->dpos, want_logits, 0);
     if (run_body(h, sh)) return 1;
     return 0;
@@ -651,13 +655,19 @@ int sp_hipkv_rewind(sp_kvdecode_handle *h, int n) {
 int sp_hipkv_prefill(sp_kvdecode_handle *h, const int32_t *tokens, int n_tok) {
     if (!h || (!tokens && n_tok > 0) || n_tok < 0) return fail("sp_hipkv_prefill: bad argument%s");
     if (n_tok > h->pmax - h->dpos) return fail("sp_hipkv_prefill: context full%s");
+    if (n_tok == 0) return 0;
     for (int i = 0; i < n_tok; i++) if (check_tok(h, tokens[i])) return 1;
+    if (ensure_pages(h, h->dpos, h->dpos + n_tok)) return 1;
+    HIPCHK(hipStreamSynchronize(h->stream), "prefill staging");
+    HIPCHK(hipMemcpy(h->tokbuf + h->dpos, tokens, (size_t)n_tok * 4, hipMemcpyHostToDevice), "prefill tokens");
+    if (set_state(h, h->dpos, 0, DRIVE_STREAM)) return 1;
     for (int i = 0; i < n_tok; i++) {
-        if (step_one(h, tokens[i], 0)) return 1;
-        HIPCHK(hipStreamSynchronize(h->stream), "prefill step");   // pinned state slot reuse
-        h->dpos++;
-        h->hwm = std::max(h->hwm, h->dpos);
+        StepShape sh = shape_for(h, h->dpos + i, 0, 0);
+        if (run_body(h, sh)) return 1;
     }
+    HIPCHK(hipStreamSynchronize(h->stream), "prefill");
+    h->dpos += n_tok;
+    h->hwm = std::max(h->hwm, h->dpos);
     return 0;
 }
 
@@ -748,7 +758,7 @@ int sp_hipkv_greedy(sp_kvdecode_handle *h, int32_t first_token, int n, int32_t *
     if (n > h->pmax - h->dpos) return fail("sp_hipkv_greedy: context full%s");
     if (n == 0) { if (device_ms) *device_ms = 0; return 0; }
     if (ensure_pages(h, h->dpos, h->dpos + n)) return 1;
-    if (set_state(h, h->dpos, first_token, 1)) return 1;
+    if (set_state(h, h->dpos, first_token, DRIVE_GREEDY)) return 1;
     hipEvent_t e0, e1;
     HIPCHK(hipEventCreate(&e0), "event"); HIPCHK(hipEventCreate(&e1), "event");
     // pre-instantiate the graphs this run needs so capture is outside the timed region
@@ -792,7 +802,7 @@ int sp_hipkv_kernel_times(sp_kvdecode_handle *h, int32_t first_token, int n, dou
     if (check_tok(h, first_token)) return 1;
     if (n > h->pmax - h->dpos) return fail("sp_hipkv_kernel_times: context full%s");
     if (ensure_pages(h, h->dpos, h->dpos + n)) return 1;
-    if (set_state(h, h->dpos, first_token, 1)) return 1;
+    if (set_state(h, h->dpos, first_token, DRIVE_GREEDY)) return 1;
     struct Ctx { hipStream_t s; std::vector<std::pair<int, std::pair<hipEvent_t, hipEvent_t>>> ev; hipEvent_t cur; };
     Ctx c; c.s = h->stream;
     auto cb = [](void *vp, int cls, bool begin) {
@@ -831,19 +841,22 @@ int sp_hipkv_read_kv(const sp_kvdecode_handle *h, int layer, int p0, int n, floa
     if (!h || !k || !v || layer < 0 || layer >= h->m->NL || p0 < 0 || n < 0 || p0 + n > h->dpos)
         return fail("sp_hipkv_read_kv: bad argument%s");
     const DevModel *m = h->m;
-    const int HD = m->HD, NKV = m->NKV, S = h->slots[layer];
-    hipStreamSynchronize(h->stream);
-    for (int p = p0; p < p0 + n; p++) {
-        const int lp = p / PAGE, slot = S == h->full_pages ? lp : lp % S;
+    const int HD = m->HD, NKV = m->NKV, S = h->slots[layer], KVD = NKV * HD;
+    HIPCHK(hipStreamSynchronize(h->stream), "kv read sync");
+    std::vector<float> page(h->pool->page_bytes / 4);
+    for (int lp = p0 / PAGE; lp <= (p0 + n - 1) / PAGE && n > 0; lp++) {
+        const int slot = S == h->full_pages ? lp : lp % S;
         const int id = h->pt[layer][slot];
         if (id < 0) return fail("sp_hipkv_read_kv: position not resident%s");
-        const float *page = h->pool->ptr[id];
-        for (int hh = 0; hh < NKV; hh++) {
-            const float *ks = page + ((size_t)hh * PAGE + p % PAGE) * HD;
-            const float *vs = page + (size_t)NKV * PAGE * HD + ((size_t)hh * PAGE + p % PAGE) * HD;
-            HIPCHK(hipMemcpy(k + (size_t)(p - p0) * NKV * HD + (size_t)hh * HD, ks, (size_t)HD * 4, hipMemcpyDeviceToHost), "kv read");
-            HIPCHK(hipMemcpy(v + (size_t)(p - p0) * NKV * HD + (size_t)hh * HD, vs, (size_t)HD * 4, hipMemcpyDeviceToHost), "kv read");
-        }
+        HIPCHK(hipMemcpy(page.data(), h->pool->ptr[id], h->pool->page_bytes, hipMemcpyDeviceToHost), "kv page read");
+        const int a = std::max(p0, lp * PAGE), b = std::min(p0 + n, (lp + 1) * PAGE);
+        for (int p = a; p < b; p++)
+            for (int hh = 0; hh < NKV; hh++) {
+                memcpy(k + (size_t)(p - p0) * KVD + (size_t)hh * HD,
+                       page.data() + ((size_t)hh * PAGE + p % PAGE) * HD, (size_t)HD * 4);
+                memcpy(v + (size_t)(p - p0) * KVD + (size_t)hh * HD,
+                       page.data() + (size_t)NKV * PAGE * HD + ((size_t)hh * PAGE + p % PAGE) * HD, (size_t)HD * 4);
+            }
     }
     return 0;
 }

@@ -32,14 +32,44 @@ __device__ __forceinline__ int64_t exp_fixed(int64_t d) {
     if (r) return exp2_frac(ONE - r) >> (n + 1);
     return ONE >> n;
 }
+// floor(sqrt(v)): double estimate, then exact integer correction (the result
+// is the unique floor, identical to the bit-serial isqrt of the islands)
 __device__ __forceinline__ uint64_t isqrt_u64(uint64_t v) {
-    uint64_t x = 0, b = 1ULL << 62;
-    while (b > v) b >>= 2;
-    while (b) {
-        if (v >= x + b) { v -= x + b; x = (x >> 1) + b; } else x >>= 1;
-        b >>= 2;
-    }
+    uint64_t x = (uint64_t)sqrt((double)v);
+    if (x > 0xFFFFFFFFull) x = 0xFFFFFFFFull;
+    while (x * x > v) x--;
+    while ((x + 1) * (x + 1) <= v && x < 0xFFFFFFFFull) x++;
     return x;
+}
+// floor(num / den) for 0 <= num < 2^127, 0 < den < 2^63 with a quotient below
+// 2^64: double estimate refined twice, then exact +-1 correction
+__device__ __forceinline__ uint64_t udiv128_64(u128 num, uint64_t den) {
+    if ((uint64_t)(num >> 64) >= den) return (uint64_t)(num / (u128)den);   // quotient >= 2^64: wraps like the cast
+    const double dd = (double)den;
+    uint64_t q = (uint64_t)fmin((double)num / dd, 1.8446744073709550e19);
+    for (int it = 0; it < 2; it++) {
+        const i128 r = (i128)num - (i128)((u128)q * den);
+        const double adj = (double)r / dd;
+        q = (uint64_t)((i128)q + (i128)adj);
+    }
+    i128 r = (i128)num - (i128)((u128)q * den);
+    while (r < 0) { q--; r += den; }
+    while (r >= (i128)den) { q++; r -= den; }
+    return q;
+}
+// v mod m for v >= 0 (v < 2^100), 0 < m < 2^63: estimate the quotient in
+// double, correct exactly
+__device__ __forceinline__ int64_t umod128_64(i128 v, int64_t m) {
+    const int64_t q = (int64_t)((double)v / (double)m);
+    i128 r = v - (i128)q * m;
+    while (r < 0) r += m;
+    while (r >= m) r -= m;
+    return (int64_t)r;
+}
+// low 64 bits of xi * inv * wi -- the island converts its 128-bit product with
+// (int64_t), i.e. exactly this wrap-around value
+__device__ __forceinline__ int64_t mul3_lo64(int64_t a, int64_t b, int64_t c) {
+    return (int64_t)((uint64_t)a * (uint64_t)b * (uint64_t)c);
 }
 __device__ __forceinline__ int64_t tanh_fixed(int64_t t) {
     int s = (t >= 0) ? 1 : -1;
@@ -115,7 +145,10 @@ __device__ __forceinline__ float rne_div_to_float(i128 num, int64_t den, int k) 
     int sh = 28 + bitlen128(d) - bitlen128(n);
     if (sh < 0) sh = 0;
     n <<= sh;
-    u128 q = n / d, r = n % d;
+    u128 q, r;
+    if ((uint64_t)(n >> 64) < (uint64_t)den) {            // quotient fits 64 bits: fast path
+        q = udiv128_64(n, (uint64_t)den); r = n - q * d;
+    } else { q = n / d; r = n % d; }
     q = (q << 1) | (r ? 1u : 0u);
     float f = rne_u128_scaled(q, -(k + sh + 1));
     return neg ? -f : f;

@@ -22,6 +22,8 @@
 // and one 16 B LDS read per digit plane, shared by the wave's rows.
 #include "kvd_internal.h"
 #include "kvd_exact.h"
+#include <cstdio>
+#include <cstdlib>
 
 namespace kvd {
 
@@ -46,7 +48,7 @@ __device__ __forceinline__ i128 wave_sum128(i128 v) {
     return v;
 }
 // block-wide reductions for 256 threads through a small LDS scratch
-template <typename T> __device__ T block_sum(T v, T *red) {
+template <typename T> __device__ T block_sum(T v, T *red) {   // red: blockDim/64 slots
     v = wave_sum(v);
     const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
     __syncthreads();
@@ -88,7 +90,7 @@ __device__ NormScale norm_scale(const float *v, int n, float eps, int mode, void
         }
         ss = block_sum<int64_t>(ss, (int64_t *)red);
         if (ss == 0) { s.zero = 1; return s; }
-        uint64_t q = (uint64_t)(((i128)n << 72) / (i128)ss);
+        const uint64_t q = udiv128_64((u128)n << 72, (uint64_t)ss);
         s.inv = (int64_t)isqrt_u64(q);
     }
     return s;
@@ -96,9 +98,8 @@ __device__ NormScale norm_scale(const float *v, int n, float eps, int mode, void
 __device__ __forceinline__ float norm_apply(float x, float w, const NormScale &s, int mode) {
     if (mode == FLOAT) return x * s.f * w;
     if (s.zero) return 0.0f;
-    int64_t xi = llround_d((double)x * 65536.0), wi = llround_d((double)w * 65536.0);
-    i128 yi = (i128)xi * s.inv * wi;
-    return (float)((double)(int64_t)yi / 4503599627370496.0);   // 2^52
+    const int64_t xi = llround_d((double)x * 65536.0), wi = llround_d((double)w * 65536.0);
+    return (float)((double)mul3_lo64(xi, s.inv, wi) / 4503599627370496.0);   // 2^52
 }
 
 // ------------------------------------------------------- prologue
@@ -191,21 +192,47 @@ __device__ __forceinline__ float act_apply(float g, float u, int act, int mode) 
     return g / (1.0f + expf(-g)) * u;                              // sp_session.c:354
 }
 
+// Sum GEMV_R = 8 per-lane int64 partials over the wave with 10 exchanges
+// instead of 48: each step halves the rows a lane carries.  Afterwards lane l
+// holds the total of row ((l>>5)&1)*4 + ((l>>4)&1)*2 + ((l>>3)&1) (all lanes
+// of an aligned group of 8 agree).
+__device__ __forceinline__ int64_t transpose_reduce8(const int64_t v[8], int lane) {
+    const bool hi32 = lane & 32, hi16 = lane & 16, hi8 = lane & 8;
+    int64_t w[4], x[2];
+    #pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int64_t send = hi32 ? v[r] : v[r + 4];
+        w[r] = (hi32 ? v[r + 4] : v[r]) + __shfl_xor(send, 32, 64);
+    }
+    #pragma unroll
+    for (int r = 0; r < 2; r++) {
+        const int64_t send = hi16 ? w[r] : w[r + 2];
+        x[r] = (hi16 ? w[r + 2] : w[r]) + __shfl_xor(send, 16, 64);
+    }
+    const int64_t send = hi8 ? x[0] : x[1];
+    int64_t y = (hi8 ? x[1] : x[0]) + __shfl_xor(send, 8, 64);
+    y += __shfl_xor(y, 4, 64);
+    y += __shfl_xor(y, 2, 64);
+    y += __shfl_xor(y, 1, 64);
+    return y;
+}
+
 template <bool WIDE>
-__global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
+__global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
     extern __shared__ uint4 smem4[];
     const int cols = a.cols, nblk = (cols + 31) / 32;
     uint4 *dig = smem4;                                   // NDIG * nblk
-    float *xf = (float *)(dig + NDIG * nblk);             // cols
-    __shared__ double red[8];
+    float *xf = (float *)(dig + NDIG * nblk);             // pro.n floats (norm prologues only)
+    __shared__ double red[GEMV_WAVES];
 
     const int sh = gemv_prologue(a.pro, a.mode, xf, dig, nblk, red);
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int rows0 = a.seg[0].w.rows;
     const int paired = a.act != ACT_NONE;
+    const int HR = GEMV_R / 2;                            // paired: HR gate rows + HR up rows
     int total_groups;
-    if (paired) total_groups = (rows0 + 1) / 2;
+    if (paired) total_groups = (rows0 + HR - 1) / HR;
     else {
         int tr = 0;
         for (int s = 0; s < a.nseg; s++) tr += a.seg[s].w.rows;
@@ -214,29 +241,33 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
     const size_t rb = (size_t)(cols + 1) / 2;
 
     for (int grp = blockIdx.x * GEMV_WAVES + wave; grp < total_groups; grp += gridDim.x * GEMV_WAVES) {
-        // resolve the wave's GEMV_R row slots to (segment, row)
-        int sseg[GEMV_R], srow[GEMV_R];
-        #pragma unroll
-        for (int r = 0; r < GEMV_R; r++) {
-            if (paired) {
-                sseg[r] = r >> 1; srow[r] = grp * 2 + (r & 1);
-                if (srow[r] >= rows0) sseg[r] = -1;
-            } else {
-                int g = grp * GEMV_R + r, s = 0;
-                while (s < a.nseg && g >= a.seg[s].w.rows) { g -= a.seg[s].w.rows; s++; }
-                sseg[r] = s < a.nseg ? s : -1; srow[r] = g;
-            }
+        // A group never straddles segments (segment row counts are multiples of
+        // the group size, checked by the host), so its rows are consecutive and
+        // addressed from one wave-uniform base per half.
+        int seg0, row0, nvalid;
+        if (paired) {
+            seg0 = 0; row0 = grp * HR;
+            nvalid = rows0 - row0 < HR ? rows0 - row0 : HR;
+        } else {
+            int g = grp * GEMV_R, s = 0;
+            while (s < a.nseg - 1 && g >= a.seg[s].w.rows) { g -= a.seg[s].w.rows; s++; }
+            seg0 = s; row0 = g;
+            nvalid = a.seg[s].w.rows - g < GEMV_R ? a.seg[s].w.rows - g : GEMV_R;
         }
-        const uint8_t *cp[GEMV_R];
-        const uint16_t *sp[GEMV_R];
+        seg0 = __builtin_amdgcn_readfirstlane(seg0);
+        row0 = __builtin_amdgcn_readfirstlane(row0);
+        nvalid = __builtin_amdgcn_readfirstlane(nvalid);
+        const DevW &wa = a.seg[seg0].w;
+        const DevW &wb = a.seg[paired ? 1 : seg0].w;
+        const uint8_t *cba = wa.codes + (size_t)row0 * rb, *cbb = wb.codes + (size_t)row0 * rb;
+        const uint16_t *sba = wa.bs + (size_t)row0 * nblk, *sbb = wb.bs + (size_t)row0 * nblk;
+        const int per = paired ? HR : GEMV_R;             // rows taken from each base
         int eb[GEMV_R];
         #pragma unroll
         for (int r = 0; r < GEMV_R; r++) {
-            const int s = sseg[r] < 0 ? 0 : sseg[r], row = sseg[r] < 0 ? 0 : srow[r];
-            const DevW &w = a.seg[s].w;
-            cp[r] = w.codes + (size_t)row * rb;
-            sp[r] = w.bs + (size_t)row * nblk;
-            eb[r] = WIDE ? -24 : (int)w.ebase[row];
+            const int rr = r % per;
+            const DevW &w = (paired && r >= HR) ? wb : wa;
+            eb[r] = WIDE ? -24 : (rr < nvalid ? (int)w.ebase[row0 + rr] : 0);
         }
         typedef typename std::conditional<WIDE, i128, int64_t>::type acc_t;
         acc_t acc[GEMV_R];
@@ -245,18 +276,23 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
 
         if (sh != SH_ZERO) {
             for (int b = lane; b < nblk; b += 64) {
-                uint4 D[NDIG];
-                #pragma unroll
-                for (int k = 0; k < NDIG; k++) D[k] = dig[k * nblk + b];
                 uint4 c[GEMV_R];
                 uint32_t h[GEMV_R];
                 #pragma unroll
                 for (int r = 0; r < GEMV_R; r++) {
-                    if (sseg[r] >= 0) {
-                        c[r] = *(const uint4 *)(cp[r] + (size_t)b * 16);
-                        h[r] = sp[r][b];
+                    const int rr = r % per;
+                    const bool second = paired && r >= HR;
+                    if (rr < nvalid) {
+                        typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+                        const uint8_t *cp = (second ? cbb : cba) + (size_t)rr * rb + (size_t)b * 16;
+                        const u32x4 t = __builtin_nontemporal_load((const u32x4 *)cp);
+                        c[r] = make_uint4(t.x, t.y, t.z, t.w);
+                        h[r] = (second ? sbb : sba)[(size_t)rr * nblk + b];
                     } else { c[r] = make_uint4(0, 0, 0, 0); h[r] = 0; }
                 }
+                uint4 D[NDIG];
+                #pragma unroll
+                for (int k = 0; k < NDIG; k++) D[k] = dig[k * nblk + b];
                 #pragma unroll
                 for (int r = 0; r < GEMV_R; r++) {
                     const int32_t d = dot_digits(c[r], D);
@@ -271,49 +307,79 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
             }
         }
         float y[GEMV_R];
-        #pragma unroll
-        for (int r = 0; r < GEMV_R; r++) {
-            acc_t t;
-            if constexpr (WIDE) t = wave_sum128(acc[r]); else t = wave_sum<int64_t>(acc[r]);
-            if (sh == SH_ZERO) y[r] = 0.0f;
-            else if constexpr (WIDE) y[r] = rne_i128_scaled(t, -24 - sh);
-            else y[r] = rne_i64_scaled(t, eb[r] - sh);
+        int myrow = 0;
+        if constexpr (WIDE) {
+            #pragma unroll
+            for (int r = 0; r < GEMV_R; r++) {
+                const i128 t = wave_sum128(acc[r]);
+                y[r] = sh == SH_ZERO ? 0.0f : rne_i128_scaled(t, -24 - sh);
+            }
+        } else {
+            const int64_t t = transpose_reduce8(acc, lane);
+            myrow = ((lane >> 5) & 1) * 4 + ((lane >> 4) & 1) * 2 + ((lane >> 3) & 1);
+            int ebm = eb[0];
+            #pragma unroll
+            for (int r = 1; r < GEMV_R; r++) if (myrow == r) ebm = eb[r];
+            y[0] = sh == SH_ZERO ? 0.0f : rne_i64_scaled(t, ebm - sh);
         }
-        if (lane == 0) {
-            if (paired) {
-                #pragma unroll
-                for (int r = 0; r < 2; r++) {
-                    if (sseg[r] < 0) continue;
-                    const int j = srow[r];
-                    a.seg[0].out[j] = y[r];
-                    a.seg[1].out[j] = y[r + 2];
-                    a.act_out[j] = act_apply(y[r], y[r + 2], a.act, a.mode);
+        if constexpr (WIDE) {
+            if (lane == 0) {
+                if (paired) {
+                    for (int r = 0; r < nvalid; r++) {
+                        const int j = row0 + r;
+                        a.seg[0].out[j] = y[r]; a.seg[1].out[j] = y[r + HR];
+                        a.act_out[j] = act_apply(y[r], y[r + HR], a.act, a.mode);
+                    }
+                } else {
+                    for (int r = 0; r < nvalid; r++) a.seg[seg0].out[row0 + r] = y[r];
                 }
-            } else {
-                #pragma unroll
-                for (int r = 0; r < GEMV_R; r++)
-                    if (sseg[r] >= 0) a.seg[sseg[r]].out[srow[r]] = y[r];
+            }
+        } else {
+            // lane (myrow*8) owns row myrow's total; paired rows fetch their up partner
+            const float partner = __shfl_xor(y[0], 32, 64);          // row myrow^4
+            if ((lane & 7) == 0) {
+                if (paired) {
+                    if (myrow < HR && myrow < nvalid) {
+                        const int j = row0 + myrow;
+                        a.seg[0].out[j] = y[0]; a.seg[1].out[j] = partner;
+                        a.act_out[j] = act_apply(y[0], partner, a.act, a.mode);
+                    }
+                } else if (myrow < nvalid) {
+                    a.seg[seg0].out[row0 + myrow] = y[0];
+                }
             }
         }
     }
 }
 
+static int g_num_cu = 0;
 int gemv_grid(int nrows_total, int cols, int paired) {
-    const int groups = paired ? (nrows_total + 1) / 2 : (nrows_total + GEMV_R - 1) / GEMV_R;
-    int blocks = (groups + GEMV_WAVES - 1) / GEMV_WAVES;
-    const int cap = cols >= 8192 ? 512 : 2048;     // bound the per-workgroup prologue re-reads
+    if (!g_num_cu) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+            g_num_cu = n;
+        else
+            g_num_cu = 256;
+    }
+    const int groups = paired ? (nrows_total + GEMV_R / 2 - 1) / (GEMV_R / 2) : (nrows_total + GEMV_R - 1) / GEMV_R;
+    const int blocks = (groups + GEMV_WAVES - 1) / GEMV_WAVES;
+    const int cap = 2 * g_num_cu;                      // every workgroup pays the input prologue once
+    (void)cols;
     return blocks < cap ? blocks : cap;
 }
 
 void launch_gemv(const GemvArgs &a, int nrows_total, hipStream_t s) {
     const int nblk = (a.cols + 31) / 32;
+    // a wave's row group must not straddle segments
+    for (int i = 0; i + 1 < a.nseg; i++)
+        if (a.seg[i].w.rows % GEMV_R) { fprintf(stderr, "kvd: GEMV segment rows %d not a multiple of %d\n", a.seg[i].w.rows, GEMV_R); abort(); }
     const size_t lds = (size_t)NDIG * nblk * sizeof(uint4) +
                        (a.pro.kind == PRO_PLAIN ? 0 : (size_t)a.pro.n * sizeof(float));
     const int grid = gemv_grid(nrows_total, a.cols, a.act != ACT_NONE);
     bool wide = false;
     for (int i = 0; i < a.nseg; i++) wide |= a.seg[i].w.wide != 0;
-    if (wide) hipLaunchKernelGGL(k_gemv<true>, dim3(grid), dim3(256), lds, s, a);
-    else      hipLaunchKernelGGL(k_gemv<false>, dim3(grid), dim3(256), lds, s, a);
+    if (wide) hipLaunchKernelGGL(k_gemv<true>, dim3(grid), dim3(GEMV_WAVES * 64), lds, s, a);
+    else      hipLaunchKernelGGL(k_gemv<false>, dim3(grid), dim3(GEMV_WAVES * 64), lds, s, a);
 }
 
 }  // namespace kvd

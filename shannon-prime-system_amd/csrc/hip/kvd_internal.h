@@ -7,8 +7,8 @@
 namespace kvd {
 
 constexpr int PAGE = 64;            // positions per KV page
-constexpr int GEMV_WAVES = 4;       // waves per GEMV workgroup
-constexpr int GEMV_R = 4;           // rows per wave pass
+constexpr int GEMV_WAVES = 8;       // waves per GEMV workgroup (512 threads)
+constexpr int GEMV_R = 8;           // rows per wave pass
 constexpr int NDIG = 6;             // balanced base-16 digit planes of an activation (|xq| < 2^22)
 
 enum Mode { FLOAT = 0, EXACT = 1 };
@@ -50,9 +50,14 @@ struct GemvArgs {
 // Per-session device-side step state (graph-replay friendly: kernels read it).
 struct DState {
     int pos;           // position of the token being processed
-    int tok;           // token id being processed
-    int greedy;        // argmax kernel writes tok = argmax and advances pos
+    int tok;           // token id being processed (DRIVE_HOST)
+    int drive;         // DRIVE_HOST / DRIVE_GREEDY / DRIVE_STREAM
     int pad;
+};
+enum Drive {
+    DRIVE_HOST = 0,    // host sets pos/tok before every step
+    DRIVE_GREEDY = 1,  // argmax writes the next tok and advances pos
+    DRIVE_STREAM = 2,  // embed reads tokbuf[pos]; the advance kernel moves pos on
 };
 
 struct AttnArgs {
@@ -75,7 +80,8 @@ struct AttnArgs {
 };
 
 // launchers (kvd_kernels.hip)
-void launch_embed(const DevW &embd, const DState *st, float *x, float scale, hipStream_t s);
+void launch_embed(const DevW &embd, const DState *st, const int *tokbuf, float *x, float scale, hipStream_t s);
+void launch_advance(DState *st, hipStream_t s);
 void launch_gemv(const GemvArgs &a, int nrows_total, hipStream_t s);
 void launch_qk_prep(const AttnArgs &a, hipStream_t s);
 void launch_attention(const AttnArgs &a, int grid_chunks, hipStream_t s);

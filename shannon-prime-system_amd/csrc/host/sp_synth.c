@@ -98,7 +98,18 @@ static void *gen_rows(void *arg) {
         if (r0 >= pc->rows) break;
         for (uint64_t r = r0; r < r1; r++) {
             const uint64_t e0 = pc->elem0 + r * cols;
-            for (uint64_t c = 0; c < cols; c++) row[c] = synth_normal(g->sp->seed, e0 + c);
+            if (!(e0 & 1u) && !(cols & 1u)) {          /* whole Box-Muller pairs: one log/sincos each */
+                for (uint64_t c = 0; c < cols; c += 2) {
+                    const uint64_t j = (e0 + c) >> 1;
+                    const double u1 = ((double)(sm64_out(g->sp->seed, 2u * j) >> 11) + 1.0) * 0x1.0p-53;
+                    const double u2 = (double)(sm64_out(g->sp->seed, 2u * j + 1u) >> 11) * 0x1.0p-53;
+                    const double rr = sqrt(-2.0 * log(u1)), a = 6.283185307179586476925 * u2;
+                    row[c] = (float)(0.02 * rr * cos(a));
+                    row[c + 1] = (float)(0.02 * rr * sin(a));
+                }
+            } else {
+                for (uint64_t c = 0; c < cols; c++) row[c] = synth_normal(g->sp->seed, e0 + c);
+            }
             sp_q4b_quantize_row(row, (int)cols, g->data + pc->offset + r * rb,
                                 (uint16_t *)(g->data + ps->offset) + r * nb);
         }

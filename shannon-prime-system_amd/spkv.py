@@ -61,7 +61,7 @@ def l1():
         path = os.path.join(LIB_DIR, "libsp_l1.so")
         if not os.path.exists(path):
             raise RuntimeError(f"{path} is not built: run __graft_entry__.build()")
-        lib = ctypes.CDLL(path, mode=ctypes.RTLD_GLOBAL)
+        lib = ctypes.CDLL(path)
         _sig(lib, "sp_last_error", c_char_p, [])
         _sig(lib, "sp_crc32", c_uint32, [c_void_p, c_size_t])
         _sig(lib, "sp_sha256", None, [c_void_p, c_size_t, c_void_p])
@@ -99,7 +99,7 @@ def kv():
         path = os.path.join(LIB_DIR, "libsp_hipkv.so")
         if not os.path.exists(path):
             raise RuntimeError(f"{path} is not built: the HIP kvdecode backend is required")
-        lib = ctypes.CDLL(path, mode=ctypes.RTLD_GLOBAL)
+        lib = ctypes.CDLL(path)
         _sig(lib, "sp_hipkv_open", c_int, [c_void_p, c_int, ctypes.POINTER(c_void_p)])
         _sig(lib, "sp_hipkv_prefill", c_int, [c_void_p, c_void_p, c_int])
         _sig(lib, "sp_hipkv_decode_step", c_int, [c_void_p, c_int32, c_void_p])

@@ -1,0 +1,251 @@
+"""Pinning the oracle (the CPU restatement that the GPU path is checked against).
+
+Float mode:  bit-identical to the compiled reference (oracle/_ref, built from the
+             reference's own C sources) on Qwen3 and Gemma3 models with a
+             clipping sliding window -- prefill logits and every decode step.
+Islands:     bit-identical to the reference's exact islands on the inputs of
+             core/exact_islands/exact_islands_test.c:32-97, plus that test's own
+             properties (fidelity, order immunity, determinism) and the closed
+             forms of every integer constant.
+Build-defined exact primitives (CORDIC RoPE, integer GEMV, SiLU, V-sum
+rounding) are pinned by closed forms and exact rational arithmetic in Python.
+"""
+import ctypes
+import math
+from decimal import Decimal, getcontext
+from fractions import Fraction
+
+import numpy as np
+import pytest
+
+import orc
+import spkv
+from helpers import model_files, prompt
+
+P = orc.ptr
+
+
+def _ref():
+    R = orc.ref_lib()
+    if R is None:
+        pytest.skip("oracle/_ref (the compiled reference) not built")
+    return R
+
+
+# ---------------------------------------------------------------- float mode vs reference
+@pytest.mark.parametrize("name", ["qwen3-tiny", "gemma3-tiny", "qwen3-g4"])
+def test_float_decode_bitexact_vs_reference(tmpdir_models, name):
+    R = _ref()
+    spm, spt = model_files(tmpdir_models, name)
+    o = orc.Oracle(spm, 64, orc.FLOAT)
+    V = o.V
+    n_prompt, n_gen = 24, 16
+    pr = prompt(n_prompt, V)
+    pre = np.zeros(V, np.float32); lg = np.zeros((n_gen, V), np.float32); fed = np.zeros(n_gen, np.int32)
+    assert R.refh_decode(spm.encode(), spt.encode(), P(pr), n_prompt, n_gen, None, P(pre), P(lg), P(fed)) == 0
+    for i, t in enumerate(pr):
+        ol = o.step(int(t), i == n_prompt - 1)
+    assert np.array_equal(ol.view(np.uint32), pre.view(np.uint32)), "prefill logits"
+    for k in range(n_gen):
+        ol = o.step(int(fed[k]))
+        assert np.array_equal(ol.view(np.uint32), lg[k].view(np.uint32)), f"decode step {k}"
+    o.close()
+
+
+def test_float_clone_rewind_semantics(tmpdir_models):
+    """core/session/session_test.c:171-206 semantics on the oracle: clone decodes
+    bit-identically; rewind then re-decode reproduces the original logits."""
+    spm, _ = model_files(tmpdir_models, "qwen3-tiny")
+    o = orc.Oracle(spm, 64)
+    for t in prompt(9, o.V):
+        last = o.step(int(t))
+    c = o.clone()
+    a = o.step(7); b = c.step(7)
+    assert np.array_equal(a, b)
+    assert o.rewind(2) == 0 and o.pos() == 8
+    assert o.rewind(999) != 0
+    o.step(int(prompt(9, o.V)[-1]))          # re-decode position 8 with the same token
+    again = o.step(7)
+    assert np.array_equal(again, a)
+    c.close(); o.close()
+
+
+# ---------------------------------------------------------------- islands
+def _udev(state, rng):
+    """core/exact_islands/exact_islands_test.c:196-201 LCG uniform in [-rng, rng]."""
+    state[0] = (state[0] * 6364136223846793005 + 1442695040888963407) & ((1 << 64) - 1)
+    u = (state[0] >> 11) / float(1 << 53)
+    return (2.0 * u - 1.0) * rng
+
+
+def _island_inputs():
+    E, M, G = 3840, 256, 512
+    st = [1]
+    x = np.zeros(E, np.float32); w = np.zeros(E, np.float32)
+    for i in range(E):
+        x[i] = _udev(st, 2.0); w[i] = 1.0 + _udev(st, 0.1)
+    st = [7]; z = np.array([_udev(st, 8.0) for _ in range(M)], np.float32)
+    st = [11]; g = np.array([_udev(st, 3.0) for _ in range(G)], np.float32)
+    return x, w, z, g
+
+
+def test_islands_bitexact_vs_reference():
+    R = _ref()
+    L = orc.lib()
+    x, w, z, g = _island_inputs()
+    a = np.zeros_like(x); b = np.zeros_like(x)
+    L.orc_rmsnorm_exact(P(x), P(w), x.size, P(a)); R.sp_rmsnorm_exact(P(x), P(w), x.size, P(b))
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    pa = np.zeros(z.size); pb = np.zeros(z.size)
+    L.orc_softmax_exact(P(z), z.size, P(pa)); R.sp_softmax_exact(P(z), z.size, P(pb))
+    assert np.array_equal(pa.view(np.uint64), pb.view(np.uint64))
+    ga = np.zeros_like(g); gb = np.zeros_like(g)
+    L.orc_gelu_exact(P(g), g.size, P(ga)); R.sp_gelu_exact(P(g), g.size, P(gb))
+    assert np.array_equal(ga.view(np.uint32), gb.view(np.uint32))
+
+
+def test_islands_properties():
+    """exact_islands_test.c:32-97 gates, run on the oracle without the reference."""
+    L = orc.lib()
+    x, w, z, g = _island_inputs()
+    out = np.zeros_like(x)
+    L.orc_rmsnorm_exact(P(x), P(w), x.size, P(out))
+    yf = x.astype(np.float64) / np.sqrt(np.mean(x.astype(np.float64) ** 2)) * w
+    assert np.linalg.norm(out - yf) / np.linalg.norm(yf) < 1e-4
+    one = np.ones_like(x); oa = np.zeros_like(x); orr = np.zeros_like(x)
+    L.orc_rmsnorm_exact(P(x), P(one), x.size, P(oa))
+    xr = np.ascontiguousarray(x[::-1])
+    L.orc_rmsnorm_exact(P(xr), P(one), x.size, P(orr))
+    assert np.array_equal(orr, oa[::-1])                      # order immunity
+    p = np.zeros(z.size); pr = np.zeros(z.size)
+    L.orc_softmax_exact(P(z), z.size, P(p))
+    e = np.exp(z.astype(np.float64) - z.max()); e /= e.sum()
+    assert np.abs(p - e).max() < 1e-5
+    zr = np.ascontiguousarray(z[::-1])
+    L.orc_softmax_exact(P(zr), z.size, P(pr))
+    assert np.array_equal(pr, p[::-1])
+    go = np.zeros_like(g); go2 = np.zeros_like(g)
+    L.orc_gelu_exact(P(g), g.size, P(go)); L.orc_gelu_exact(P(g), g.size, P(go2))
+    gd = g.astype(np.float64)
+    gf = 0.5 * gd * (1 + np.tanh(math.sqrt(2 / math.pi) * (gd + 0.044715 * gd ** 3)))
+    assert np.linalg.norm(go - gf) / np.linalg.norm(gf) < 1e-4
+    assert np.array_equal(go, go2)
+
+
+def test_island_constants_closed_form():
+    """Every integer constant of the islands equals round(closed form * 2^30)."""
+    getcontext().prec = 60
+    ln2 = Decimal(2).ln()
+    S = Decimal(2) ** 30
+    assert int((Decimal(1) / ln2 * S).to_integral_value()) == 1549082005        # log2(e)
+    fact = 1
+    expc = [1073741824, 744261118, 257941248, 59597083, 10327387, 1431680, 165394]
+    for k in range(7):
+        fact *= max(k, 1)
+        assert int((ln2 ** k / fact * S).to_integral_value()) == expc[k]
+    pi = Decimal("3.14159265358979323846264338327950288419716939937510582097494459")
+    assert int(((2 / pi).sqrt() * S).to_integral_value()) == 856722024
+    assert int((Decimal("0.044715") * S).to_integral_value()) == 48012366
+
+
+# ---------------------------------------------------------------- build-defined exact primitives
+PI = Fraction(314159265358979323846264338327950288419716939937510582097494459, 10 ** 62)
+
+
+def test_cordic_sincos():
+    L = orc.lib()
+    co = ctypes.c_int32(); si = ctypes.c_int32()
+    two_pi_q60 = 7244019458077122842
+    assert two_pi_q60 == round(2 * PI * 2 ** 60) and 1811004864519280711 == round(PI / 2 * 2 ** 60)
+    rng = np.random.default_rng(0)
+    worst = 0.0
+    for th in list(rng.integers(0, two_pi_q60, 400)) + [0, two_pi_q60 // 4, two_pi_q60 // 2, two_pi_q60 - 1]:
+        L.orc_cordic_sincos(int(th), ctypes.byref(co), ctypes.byref(si))
+        t = int(th) / 2 ** 60
+        worst = max(worst, abs(co.value / 2 ** 30 - math.cos(t)), abs(si.value / 2 ** 30 - math.sin(t)))
+    assert worst < 4e-9                      # Q30 output resolution is ~1e-9
+
+
+def test_rope_freq_table():
+    L = orc.lib()
+    for base in (1e6, 1e4):
+        for d in (64, 128, 256):
+            for i in range(0, d // 2, 7):
+                f = L.orc_rope_freq_q60(base, i, d) / 2 ** 60
+                exact = float(base) ** (-2.0 * i / d)
+                assert abs(f - exact) <= 1e-15 + 2e-14 * exact, (base, d, i)
+
+
+def test_rope_exact_vs_libm():
+    """CORDIC RoPE agrees with the mathematically exact rotation (angle computed in
+    double) to float rounding, and preserves pair norms (forward_kernels_test.c)."""
+    L = orc.lib()
+    rng = np.random.default_rng(2)
+    for p in (0, 1, 17, 1000, 32768, 131071):
+        v = rng.standard_normal(256).astype(np.float32)
+        out = v.copy()
+        L.orc_rope_exact(P(out), 256, p, 1e6)
+        half = 128
+        i = np.arange(half)
+        th = p * np.power(1e6, -2.0 * i / 256)
+        c, s = np.cos(th), np.sin(th)
+        a, b = v[:half].astype(np.float64), v[half:].astype(np.float64)
+        ref = np.concatenate([a * c - b * s, a * s + b * c])
+        assert np.abs(out - ref).max() < 1e-5 * max(1.0, np.abs(ref).max())
+        n0 = a * a + b * b; n1 = out[:half].astype(np.float64) ** 2 + out[half:].astype(np.float64) ** 2
+        assert np.abs(n0 - n1).max() < 1e-5 * n0.max()
+
+
+def _q4b_tensor(rows, cols, seed):
+    rng = np.random.default_rng(seed)
+    w = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
+    codes = np.zeros((rows, cols // 2), np.uint8); bs = np.zeros((rows, cols // 32), np.uint16)
+    for r in range(rows):
+        spkv.l1().sp_q4b_quantize_row(P(w[r]), cols, P(codes[r]), P(bs[r]))
+    return codes, bs
+
+
+def _codes_int(codes):
+    q = np.empty((codes.shape[0], codes.shape[1] * 2), np.int64)
+    q[:, 0::2] = codes & 15; q[:, 1::2] = codes >> 4
+    return np.where(q >= 8, q - 16, q)
+
+
+def _f16_frac(h):
+    h = int(h); E5 = (h >> 10) & 31; m = h & 1023
+    v = Fraction(1024 + m, 1) * Fraction(2) ** (E5 - 25) if E5 else Fraction(m) * Fraction(2) ** -24
+    return -v if h & 0x8000 else v
+
+
+@pytest.mark.parametrize("cols", [64, 256, 1024])
+def test_exact_gemv_is_rne_of_rational(cols):
+    """y = RNE( sum_b f16(s_b) sum_i code_i * xq_i / 2^sh ) exactly, with xq the
+    per-vector power-of-two grid of x (max |xq| < 2^22)."""
+    rows = 24
+    codes, bs = _q4b_tensor(rows, cols, cols)
+    x = (np.random.default_rng(9).standard_normal(cols) * np.float32(0.7)).astype(np.float32)
+    x[3] = 0.0
+    y = np.zeros(rows, np.float32)
+    orc.lib().orc_q4b_gemv_exact(P(codes), P(bs), rows, cols, P(x), P(y))
+    e = math.frexp(float(np.abs(x).max()))[1]
+    sh = 22 - e
+    xq = [int(np.rint(math.ldexp(float(v), sh))) for v in x]
+    assert max(abs(v) for v in xq) < 2 ** 22
+    q = _codes_int(codes)
+    for r in range(rows):
+        acc = Fraction(0)
+        for b in range(cols // 32):
+            acc += _f16_frac(bs[r, b]) * sum(int(q[r, i]) * xq[i] for i in range(b * 32, b * 32 + 32))
+        exact = acc / 2 ** sh
+        assert y[r] == np.float32(float(exact)) or abs(Fraction(float(y[r])) - exact) <= abs(exact) * Fraction(1, 2 ** 24)
+    yf = np.zeros(rows, np.float32)
+    orc.lib().orc_q4b_gemv(P(codes), P(bs), rows, cols, P(x), P(yf))
+    assert np.abs(y - yf).max() <= 1e-5 * np.abs(yf).max()
+
+
+def test_exact_silu_fidelity():
+    g = np.linspace(-12, 12, 2001).astype(np.float32)
+    out = np.zeros_like(g)
+    orc.lib().orc_silu_exact(P(g), g.size, P(out))
+    ref = g.astype(np.float64) / (1 + np.exp(-g.astype(np.float64)))
+    assert np.abs(out - ref).max() < 2e-5 * 12

@@ -1,0 +1,196 @@
+"""Section-6b routing and the session verbs' control semantics, on the CPU with a
+counting mock dispatch table (the pattern of core/session/arm_genkv_gate.c:200-233).
+
+Pins the reference's guards and commit points (core/session/sp_session.c
+:154-212, :725-770, :773-824, :909-925): argument errors, context full, cancel
+before any mutation, backend failure -> SP_EBADSTATE with the position unchanged,
+rewind > position -> SP_EBADARG; plus this library's routing extensions (prefill
+= dt->prefill(n-1) + dt->decode_step(last), rewind -> dt->rewind, clone without a
+registered fork drops the registration as the reference does)."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+import spkv
+from helpers import model_files
+
+OPEN = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.POINTER(ctypes.c_void_p))
+PREFILL = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p, ctypes.POINTER(ctypes.c_int32), ctypes.c_int)
+STEP = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p, ctypes.c_int32, ctypes.POINTER(ctypes.c_float))
+REWIND = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p, ctypes.c_int)
+POSN = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p)
+CLOSE = ctypes.CFUNCTYPE(None, ctypes.c_void_p)
+
+
+class Mock:
+    def __init__(self, vocab, fail_step=False):
+        self.calls = []
+        self.dpos = 0
+        self.vocab = vocab
+        self.fail_step = fail_step
+        self.closed = 0
+        self._fns = [OPEN(lambda qm, p, out: 0), PREFILL(self.prefill), STEP(self.step),
+                     REWIND(self.rewind), POSN(lambda h: self.dpos), CLOSE(self.close)]
+        self.table = spkv.DispatchTable(*[ctypes.cast(f, ctypes.c_void_p) for f in self._fns])
+
+    def prefill(self, h, toks, n):
+        self.calls.append(("prefill", [toks[i] for i in range(n)]))
+        self.dpos += n
+        return 0
+
+    def step(self, h, tok, logits):
+        self.calls.append(("step", tok))
+        if self.fail_step:
+            return 1
+        for i in range(self.vocab):
+            logits[i] = float(i == (tok + self.dpos) % self.vocab)
+        self.dpos += 1
+        return 0
+
+    def rewind(self, h, n):
+        self.calls.append(("rewind", n))
+        self.dpos -= n
+        return 0
+
+    def close(self, h):
+        self.closed += 1
+
+
+@pytest.fixture
+def session(tmpdir_models):
+    spm, spt = model_files(tmpdir_models, "qwen3-tiny", max_context=32)
+    m = spkv.Model(spm, spt)
+    flag = ctypes.c_int(0)
+    s = spkv.Session(m, 0, cancel=flag)          # max_context 0 -> arch default (32)
+    yield s, flag
+    s.close(); m.close()
+
+
+def register(s, mock):
+    L = spkv.l1()
+    assert L.sp_session_register_kvdecode_backend(s.h, ctypes.c_void_p(0x1234), ctypes.byref(mock.table)) == 0
+    assert L.sp_session_kvdecode_backend_handle(s.h) == 0x1234
+
+
+def test_unregistered_session_has_no_host_decode(session):
+    s, _ = session
+    lg = np.zeros(1000, np.float32)
+    assert s.decode(1, lg) == spkv.SP_EUNSUPPORTED
+    assert "no kvdecode backend" in spkv.last_error()
+    assert s.prefill([1, 2], lg) == spkv.SP_EUNSUPPORTED
+    assert s.position() == 0
+
+
+def test_decode_routes_and_advances(session):
+    s, _ = session
+    mock = Mock(1000); register(s, mock)
+    lg = np.zeros(1000, np.float32)
+    assert s.prefill([5, 6, 7], lg) == 0
+    assert mock.calls == [("prefill", [5, 6]), ("step", 7)]
+    assert lg.argmax() == (7 + 2) % 1000 and s.position() == 3
+    assert s.decode(9, lg) == 0 and s.position() == 4 and mock.calls[-1] == ("step", 9)
+
+
+def test_guards(session):
+    s, flag = session
+    mock = Mock(1000); register(s, mock)
+    lg = np.zeros(1000, np.float32)
+    small = np.zeros(999, np.float32)
+    assert s.decode(1, small) == spkv.SP_EBADARG                         # capacity < vocab
+    assert spkv.l1().sp_decode_step(s.h, 1, None, 1000) == spkv.SP_EBADARG
+    assert s.prefill([], lg) == spkv.SP_EBADARG                          # n_tokens == 0
+    assert s.prefill(list(range(33)), lg) == spkv.SP_ECONTEXT_FULL      # > hist_cap
+    flag.value = 1
+    assert s.decode(1, lg) == spkv.SP_ECANCEL and s.prefill([1], lg) == spkv.SP_ECANCEL
+    assert mock.calls == [] and s.position() == 0                        # no mutation on cancel
+    flag.value = 0
+    for t in range(32):
+        assert s.decode(t, lg) == 0
+    assert s.decode(0, lg) == spkv.SP_ECONTEXT_FULL and s.position() == 32
+
+
+def test_backend_failure_keeps_position(session):
+    s, _ = session
+    mock = Mock(1000, fail_step=True); register(s, mock)
+    lg = np.zeros(1000, np.float32)
+    assert s.decode(3, lg) == spkv.SP_EBADSTATE
+    assert s.position() == 0 and "backend step failed" in spkv.last_error()
+    assert s.prefill([1, 2, 3], lg) == spkv.SP_EBADSTATE
+    assert s.position() == 0
+    assert mock.calls[-1] == ("rewind", 2) and mock.dpos == 0          # backend brought back in step
+
+
+def test_rewind_routes(session):
+    s, _ = session
+    mock = Mock(1000); register(s, mock)
+    lg = np.zeros(1000, np.float32)
+    for t in range(9):
+        s.decode(t, lg)
+    assert s.rewind(2) == 0 and s.position() == 7 and mock.calls[-1] == ("rewind", 2) and mock.dpos == 7
+    assert s.rewind(9999) == spkv.SP_EBADARG and s.position() == 7
+    assert s.rewind(0) == 0 and s.position() == 7
+
+
+def test_clone_without_fork_drops_registration(session):
+    s, _ = session
+    mock = Mock(1000); register(s, mock)
+    lg = np.zeros(1000, np.float32)
+    for t in range(4):
+        s.decode(t, lg)
+    c = s.clone()
+    assert c.position() == 4
+    assert spkv.l1().sp_session_kvdecode_backend_dt(c.h) is None        # reference :792-799
+    assert c.decode(1, lg) == spkv.SP_EUNSUPPORTED
+    c.close()
+
+
+def test_unregister_and_owned_close(session):
+    s, _ = session
+    mock = Mock(1000); register(s, mock)
+    L = spkv.l1()
+    assert L.spx_session_own_kvdecode(s.h, 1) == 0
+    assert L.sp_session_register_kvdecode_backend(s.h, None, None) == 0      # NULL dt unregisters
+    assert mock.closed == 1                                                  # owned handle closed
+    assert L.sp_session_kvdecode_backend_dt(s.h) is None
+    assert L.sp_session_register_kvdecode_backend(None, None, None) == spkv.SP_EBADARG
+
+
+def test_hipkv_library_exports_every_declared_symbol():
+    """libsp_hipkv.so loads on a host without a GPU and exports each symbol of
+    include/sp_hipkv.h; libsp_l1.so exports the session/model ABI headers' symbols."""
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    lib = spkv.kv()
+    hdr = open(os.path.join(root, "include", "sp_hipkv.h")).read()
+    names = set(re.findall(r"\b(sp_hipkv_\w+)\s*\(", hdr)) | {"sp_hipkv_dispatch"}
+    assert len(names) >= 14
+    for n in sorted(names):
+        assert hasattr(lib, n), n
+    l1 = spkv.l1()
+    for h in ("sp_l1_abi.h", "sp_model_abi.h"):
+        txt = open(os.path.join(root, "include", h)).read()
+        for n in set(re.findall(r"^\s*(?:[\w\s\*]+?)\b((?:sp|spx|qwen3)_\w+)\s*\(", txt, re.M)):
+            assert hasattr(l1, n), n
+    # the dispatch table points at the named entry points
+    tab = spkv.DispatchTable.in_dll(lib, "sp_hipkv_dispatch")
+    assert tab.open == ctypes.cast(lib.sp_hipkv_open, ctypes.c_void_p).value
+    assert tab.close == ctypes.cast(lib.sp_hipkv_close, ctypes.c_void_p).value
+
+
+def test_hipkv_open_without_gpu_fails_loudly(session):
+    """No silent fallback: opening the HIP backend without a device is an error."""
+    import subprocess, sys, json
+    s, _ = session
+    if os.environ.get("HIP_VISIBLE_DEVICES") is None:
+        try:
+            import torch
+            if torch.cuda.is_available():
+                pytest.skip("a GPU is visible")
+        except Exception:
+            pass
+    qm = spkv.l1().sp_session_qwen3_model(s.h)
+    h = ctypes.c_void_p()
+    rc = spkv.kv().sp_hipkv_open(qm, 16, ctypes.byref(h))
+    assert rc != 0 and "no HIP device" in spkv.last_error()
