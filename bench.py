@@ -79,6 +79,9 @@ def main():
     ap.add_argument("--kernel-steps", type=int, default=8)
     ap.add_argument("--workdir", default=None)
     ap.add_argument("--ctx", type=int, default=None, help="override the workload's prefill length")
+    ap.add_argument("--no-graph", action="store_true", help="plain kernel launches instead of one HIP graph per step")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="run one device-to-device copy of this many MiB first (HBM counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -104,7 +107,12 @@ def main():
         sess.attach(pmax, exact=exact)
         log(f"backend attached (upload) in {time.time()-t0:.1f}s, mode={args.mode}")
         be = spkv.Backend.wrap(sess.backend_handle())
+        if args.no_graph:
+            spkv.check(spkv.kv().sp_hipkv_set_graph(be.h, 0), "sp_hipkv_set_graph")
         info = be.info()
+
+        if args.calib_copy_mib:
+            calib_copy(args.calib_copy_mib << 20)
 
         prompt = splitmix_tokens(ctx, V, seed=1)
         logits = np.zeros(V, np.float32)
@@ -184,6 +192,24 @@ def main():
     finally:
         if not args.workdir:
             shutil.rmtree(work, ignore_errors=True)
+
+
+def calib_copy(nbytes):
+    """One plain device-to-device copy of nbytes (the HIP runtime's copy kernel):
+    its FETCH_SIZE / WRITE_SIZE counters calibrate the HBM traffic figures."""
+    import ctypes
+    hip = ctypes.CDLL("libamdhip64.so")
+    a, b = ctypes.c_void_p(), ctypes.c_void_p()
+    if hip.hipMalloc(ctypes.byref(a), ctypes.c_size_t(nbytes)) or hip.hipMalloc(ctypes.byref(b), ctypes.c_size_t(nbytes)):
+        raise RuntimeError("calibration copy: hipMalloc failed")
+    hip.hipMemset(a, 1, ctypes.c_size_t(nbytes))
+    hip.hipDeviceSynchronize()
+    rc = hip.hipMemcpy(b, a, ctypes.c_size_t(nbytes), 3)       # hipMemcpyDeviceToDevice
+    hip.hipDeviceSynchronize()
+    hip.hipFree(a); hip.hipFree(b)
+    if rc:
+        raise RuntimeError(f"calibration copy failed ({rc})")
+    log(f"calibration copy of {nbytes >> 20} MiB done")
 
 
 def cpu_baseline(spm, be, info, shape, exact, n_steps, tok, sess):

@@ -27,8 +27,9 @@
  *                  float rotation without contraction
  *   attention      qi = rne(q*2^16), ki = rne(k*2^16), exact int64 dot,
  *                  score = (float)((double)ip/2^32)*ascale (decode.c:141-152 form),
- *                  softmax island exp weights e (Q30), V-sum over e>>7 and
- *                  vq = clamp(rne(v*2^16), +-(2^23-1)) in int128, one RNE division
+ *                  softmax island exp weights e (Q30), V-sum over e>>8 (Q22) and
+ *                  vq = clamp(rne(v*2^16), +-(2^23-1)): every product < 2^45, so the
+ *                  sum fits int64 for contexts below 2^18; one RNE division
  *   SwiGLU         silu via the island exp (sigmoid in Q30); GeGLU = GELU island
  * KV cache in exact mode holds ki and vq as int32 (same 4 bytes per element). */
 #include "sp_oracle.h"
@@ -622,7 +623,7 @@ static void attn_head_exact(const float *qh, const int32_t *KC, const int32_t *V
     i128 acc[1024];
     for (int i = 0; i < HD; i++) acc[i] = 0;
     for (int s = s0; s <= pos; s++) {
-        int64_t e = exp_fixed(((zi[s] - mx) * ONE) >> 14) >> 7;
+        int64_t e = exp_fixed(((zi[s] - mx) * ONE) >> 14) >> 8;
         S += e;
         const int32_t *vh = VC + (size_t)s * KVD + (size_t)kvh * HD;
         for (int i = 0; i < HD; i++) acc[i] += (i128)((int64_t)e * vh[i]);

@@ -22,6 +22,8 @@
 // finish a kv-head merges the chunk partials (arrival counter, self-resetting).
 #include "kvd_internal.h"
 #include "kvd_exact.h"
+#include <cstdio>
+#include <cstdlib>
 
 namespace kvd {
 
@@ -79,7 +81,6 @@ __device__ __forceinline__ float *page_of(float *const *pages, int ring, int pos
 // grid.x = NH (q heads) + NKV (k heads) + NKV (v heads); block = 64 threads
 // (one wave), each lane owning HD/64 pairs-halves.  float/exact by a.mode.
 __global__ __launch_bounds__(64) void k_qk_prep(AttnArgs a) {
-    const int64_t *freq_q60 = a.freq_q60;
     const int HD = a.HD, half = HD / 2, lane = threadIdx.x;
     const int pos = a.st->pos;
     const int hb = blockIdx.x;
@@ -125,25 +126,19 @@ __global__ __launch_bounds__(64) void k_qk_prep(AttnArgs a) {
             }
         }
     }
-    // NEOX RoPE: pairs (i, i+half).  Lane owns columns lane+64j; the partner of a
-    // column in the lower half lives in the same lane (half is a multiple of 64).
+    // NEOX RoPE: pairs (i, i+half), cos/sin from this step's rotation table
+    // (same values the per-pair formula gives; computed once per step).
     __shared__ float rot[512];
     for (int j = 0; j < per; j++) rot[lane + 64 * j] = v[j];
     __syncthreads();
+    const float *cs = a.rope_cs;
     for (int i = lane; i < half; i += 64) {
         const float x0 = rot[i], x1 = rot[i + half];
-        float c, s;
+        const float c = cs[i], s = cs[half + i];
         if (a.mode == FLOAT) {
-            const float freq = powf(a.base, -2.0f * (float)i / (float)HD);
-            const float theta = (float)pos * freq;
-            c = cosf(theta); s = sinf(theta);
             rot[i] = x0 * c - x1 * s;
             rot[i + half] = x0 * s + x1 * c;
         } else {
-            const i128 th = (i128)pos * freq_q60[i];
-            const int64_t r = umod128_64(th, TWO_PI_Q60);
-            int64_t co, si; cordic_q62(r, co, si);
-            c = rne_i64_scaled(co, -62); s = rne_i64_scaled(si, -62);
             const float ac = x0 * c, bs = x1 * s, as = x0 * s, bc = x1 * c;
             rot[i] = ac - bs;
             rot[i + half] = as + bc;
@@ -161,6 +156,33 @@ __global__ __launch_bounds__(64) void k_qk_prep(AttnArgs a) {
     }
 }
 
+// Rotation table of the current position for both RoPE bases:
+// out[t][0..half) = cos, out[t][half..HD) = sin, t = 0 global base, 1 window base.
+// Float mode: freq = powf(base, -2i/d), theta = (float)p*freq, cosf/sinf
+// (forward_kernels.c:31-41); exact mode: p*F_i mod 2*pi (Q60) by CORDIC, RNE.
+__global__ __launch_bounds__(256) void k_rope_table(const DState *st, int HD, int mode, float base_g, float base_l,
+                                                     const int64_t *fq_g, const int64_t *fq_l, float *out) {
+    const int half = HD / 2, pos = st->pos;
+    for (int idx = threadIdx.x; idx < 2 * half; idx += blockDim.x) {
+        const int t = idx / half, i = idx % half;
+        float c, s;
+        if (mode == FLOAT) {
+            const float freq = powf(t ? base_l : base_g, -2.0f * (float)i / (float)HD);
+            const float theta = (float)pos * freq;
+            c = cosf(theta); s = sinf(theta);
+        } else {
+            const i128 th = (i128)pos * (t ? fq_l : fq_g)[i];
+            int64_t co, si; cordic_q62(umod128_64(th, TWO_PI_Q60), co, si);
+            c = rne_i64_scaled(co, -62); s = rne_i64_scaled(si, -62);
+        }
+        out[(size_t)t * HD + i] = c;
+        out[(size_t)t * HD + half + i] = s;
+    }
+}
+void launch_rope_table(const DState *st, int HD, int mode, float base_g, float base_l,
+                       const int64_t *fq_g, const int64_t *fq_l, float *out, hipStream_t s) {
+    hipLaunchKernelGGL(k_rope_table, dim3(1), dim3(256), 0, s, st, HD, mode, base_g, base_l, fq_g, fq_l, out);
+}
 void launch_qk_prep(const AttnArgs &a, hipStream_t s) {
     hipLaunchKernelGGL(k_qk_prep, dim3(a.NH + 2 * a.NKV), dim3(64), 0, s, a);
 }
@@ -170,7 +192,8 @@ void set_rope_tables(const int64_t atan_q60[64], int64_t kinv_q62) {
 }
 
 // ------------------------------------------------------------------ attention
-// chunk geometry for the current position
+// chunk geometry for the current position: chunks are `chunk`-aligned absolute
+// position ranges clipped to the attended window [s0, pos]
 __device__ __forceinline__ void chunk_range(const AttnArgs &a, int pos, int c, int &cs, int &ce, int &nch) {
     const int s0 = (a.win >= 0 && pos - a.win + 1 > 0) ? pos - a.win + 1 : 0;
     const int c0 = s0 / a.chunk;
@@ -180,6 +203,28 @@ __device__ __forceinline__ void chunk_range(const AttnArgs &a, int pos, int c, i
     if (ce > pos + 1) ce = pos + 1;
 }
 
+// 16 B-per-lane row loads of one head's HD elements at absolute position p
+template <int EPL, typename T>
+__device__ __forceinline__ void load_row(const AttnArgs &a, int h, int p, bool vpart, int lane, T out[EPL]) {
+    const float *page = page_of(a.pages, a.ring_pages, p);
+    const int HD = EPL * 64;
+    const T *src = (const T *)(page + (vpart ? (size_t)a.NKV * PAGE * HD : 0) + ((size_t)h * PAGE + p % PAGE) * HD) + lane * EPL;
+    if constexpr (EPL == 4) {
+        typedef T v4 __attribute__((ext_vector_type(4)));
+        const v4 t = *(const v4 *)src; out[0] = t.x; out[1] = t.y; out[2] = t.z; out[3] = t.w;
+    } else if constexpr (EPL == 2) {
+        typedef T v2 __attribute__((ext_vector_type(2)));
+        const v2 t = *(const v2 *)src; out[0] = t.x; out[1] = t.y;
+    } else {
+        #pragma unroll
+        for (int e = 0; e < EPL; e++) out[e] = src[e];
+    }
+}
+
+constexpr int MAXCH = 256;       // positions per chunk (LDS score buffer)
+constexpr int MAXNCH = 4096;     // chunks per kv-head (combine weight buffer)
+constexpr int UNR = 4;           // positions in flight per wave
+
 template <int EPL, int G>
 __global__ __launch_bounds__(256) void k_attn_float(AttnArgs a) {
     const int HD = EPL * 64, c = blockIdx.x, h = blockIdx.y;
@@ -188,33 +233,33 @@ __global__ __launch_bounds__(256) void k_attn_float(AttnArgs a) {
     int cs, ce, nch;
     chunk_range(a, pos, c, cs, ce, nch);
     if (c >= nch) return;
-    __shared__ float sc[G][PAGE];
+    __shared__ float sc[G][MAXCH];
     __shared__ float ored[4][G][EPL * 64];
+    __shared__ float wk[MAXNCH];
+    __shared__ float redf[4];
     __shared__ int is_last;
-
     float q[G][EPL];
     #pragma unroll
     for (int g = 0; g < G; g++)
         #pragma unroll
         for (int e = 0; e < EPL; e++) q[g][e] = a.qr[(size_t)(h * G + g) * HD + lane * EPL + e];
-
-    const float *page = page_of(a.pages, a.ring_pages, cs);
-    const float *K = page + (size_t)h * PAGE * HD;
-    const float *V = page + (size_t)a.NKV * PAGE * HD + (size_t)h * PAGE * HD;
     const int n = ce - cs;
-    for (int j = wave; j < n; j += 4) {
-        const int slot = (cs + j) % PAGE;
-        float kv[EPL];
-        if constexpr (EPL == 4) { float4 t = *(const float4 *)(K + (size_t)slot * HD + lane * 4); kv[0] = t.x; kv[1] = t.y; kv[2] = t.z; kv[3] = t.w; }
-        else if constexpr (EPL == 2) { float2 t = *(const float2 *)(K + (size_t)slot * HD + lane * 2); kv[0] = t.x; kv[1] = t.y; }
-        else { for (int e = 0; e < EPL; e++) kv[e] = K[(size_t)slot * HD + lane * EPL + e]; }
+    // scores: each wave takes UNR consecutive positions per iteration
+    for (int j0 = wave * UNR; j0 < n; j0 += 4 * UNR) {
+        float kv[UNR][EPL];
         #pragma unroll
-        for (int g = 0; g < G; g++) {
-            float d = 0.0f;
+        for (int u = 0; u < UNR; u++) if (j0 + u < n) load_row<EPL>(a, h, cs + j0 + u, false, lane, kv[u]);
+        #pragma unroll
+        for (int u = 0; u < UNR; u++) {
+            if (j0 + u >= n) break;
             #pragma unroll
-            for (int e = 0; e < EPL; e++) d += q[g][e] * kv[e];
-            d = wsum(d);
-            if (lane == 0) sc[g][j] = d * a.ascale;
+            for (int g = 0; g < G; g++) {
+                float d = 0.0f;
+                #pragma unroll
+                for (int e = 0; e < EPL; e++) d += q[g][e] * kv[u][e];
+                d = wsum(d);
+                if (lane == 0) sc[g][j0 + u] = d * a.ascale;
+            }
         }
     }
     __syncthreads();
@@ -224,31 +269,28 @@ __global__ __launch_bounds__(256) void k_attn_float(AttnArgs a) {
         float mv = -INFINITY;
         for (int j = lane; j < n; j += 64) mv = fmaxf(mv, sc[g][j]);
         m[g] = wmax(mv);
-    }
-    __syncthreads();
-    #pragma unroll
-    for (int g = 0; g < G; g++) {
         float lv = 0.0f;
-        for (int j = lane; j < n; j += 64) { const float p = expf(sc[g][j] - m[g]); lv += p; }
+        for (int j = lane; j < n; j += 64) lv += expf(sc[g][j] - m[g]);
         l[g] = wsum(lv);
     }
-    // V-sum with p = exp(s - m) recomputed per position
     float o[G][EPL];
     #pragma unroll
     for (int g = 0; g < G; g++)
         #pragma unroll
         for (int e = 0; e < EPL; e++) o[g][e] = 0.0f;
-    for (int j = wave; j < n; j += 4) {
-        const int slot = (cs + j) % PAGE;
-        float vv[EPL];
-        if constexpr (EPL == 4) { float4 t = *(const float4 *)(V + (size_t)slot * HD + lane * 4); vv[0] = t.x; vv[1] = t.y; vv[2] = t.z; vv[3] = t.w; }
-        else if constexpr (EPL == 2) { float2 t = *(const float2 *)(V + (size_t)slot * HD + lane * 2); vv[0] = t.x; vv[1] = t.y; }
-        else { for (int e = 0; e < EPL; e++) vv[e] = V[(size_t)slot * HD + lane * EPL + e]; }
+    for (int j0 = wave * UNR; j0 < n; j0 += 4 * UNR) {
+        float vv[UNR][EPL];
         #pragma unroll
-        for (int g = 0; g < G; g++) {
-            const float p = expf(sc[g][j] - m[g]);
+        for (int u = 0; u < UNR; u++) if (j0 + u < n) load_row<EPL>(a, h, cs + j0 + u, true, lane, vv[u]);
+        #pragma unroll
+        for (int u = 0; u < UNR; u++) {
+            if (j0 + u >= n) break;
             #pragma unroll
-            for (int e = 0; e < EPL; e++) o[g][e] += p * vv[e];
+            for (int g = 0; g < G; g++) {
+                const float p = expf(sc[g][j0 + u] - m[g]);
+                #pragma unroll
+                for (int e = 0; e < EPL; e++) o[g][e] += p * vv[u][e];
+            }
         }
     }
     #pragma unroll
@@ -258,36 +300,51 @@ __global__ __launch_bounds__(256) void k_attn_float(AttnArgs a) {
     __syncthreads();
     for (int i = threadIdx.x; i < G * HD; i += 256) {
         const int g = i / HD, d = i % HD;
-        const float t = ored[0][g][d] + ored[1][g][d] + ored[2][g][d] + ored[3][g][d];
-        a.part[((size_t)(h * G + g) * a.max_chunks + c) * HD + d] = t;
+        st_agent(&a.part[((size_t)(h * G + g) * a.max_chunks + c) * HD + d], ored[0][g][d] + ored[1][g][d] + ored[2][g][d] + ored[3][g][d]);
     }
     if (threadIdx.x < G) {
         const int g = threadIdx.x;
-        a.part_ml[((size_t)(h * G + g) * a.max_chunks + c) * 2 + 0] = m[g];
-        a.part_ml[((size_t)(h * G + g) * a.max_chunks + c) * 2 + 1] = l[g];
+        st_agent(&a.part_ml[((size_t)(h * G + g) * a.max_chunks + c) * 2 + 0], m[g]);
+        st_agent(&a.part_ml[((size_t)(h * G + g) * a.max_chunks + c) * 2 + 1], l[g]);
     }
-    // ---- last arriving workgroup of this kv-head merges the chunks ----
-    __threadfence();
+    // ---- the last workgroup of this kv-head merges the chunks ----
+    mem_complete();
     __syncthreads();
-    if (threadIdx.x == 0) is_last = (atomicAdd(&a.counter[h], 1) == nch - 1);
+    if (threadIdx.x == 0) is_last = (arrive(&a.counter[h]) == nch - 1);
     __syncthreads();
     if (!is_last) return;
-    __threadfence();
-    for (int i = threadIdx.x; i < G * HD; i += 256) {
-        const int g = i / HD, d = i % HD;
+    for (int g = 0; g < G; g++) {
         const size_t base = (size_t)(h * G + g) * a.max_chunks;
-        // plain loads: the acquire fence above invalidated this CU's L1
-        const float *pml = a.part_ml + base * 2, *po = a.part + base * HD + d;
-        float M = -INFINITY;
-        for (int k = 0; k < nch; k++) M = fmaxf(M, pml[k * 2]);
-        float L = 0.0f, acc = 0.0f;
-        for (int k = 0; k < nch; k++) {
-            const float w = expf(pml[k * 2] - M);
-            L += pml[k * 2 + 1] * w; acc += po[(size_t)k * HD] * w;
+        const float *pml = a.part_ml + base * 2;
+        float mv = -INFINITY;
+        for (int k = threadIdx.x; k < nch; k += 256) mv = fmaxf(mv, ld_agent(&pml[k * 2]));
+        mv = wmax(mv);
+        if (lane == 0) redf[wave] = mv;
+        __syncthreads();
+        const float M = fmaxf(fmaxf(redf[0], redf[1]), fmaxf(redf[2], redf[3]));
+        __syncthreads();
+        float lv = 0.0f;
+        for (int k = threadIdx.x; k < nch; k += 256) { const float w = expf(ld_agent(&pml[k * 2]) - M); wk[k] = w; lv += ld_agent(&pml[k * 2 + 1]) * w; }
+        lv = wsum(lv);
+        if (lane == 0) redf[wave] = lv;
+        __syncthreads();
+        const float L = redf[0] + redf[1] + redf[2] + redf[3];
+        const float *po = a.part + base * HD;
+        for (int d = threadIdx.x; d < HD; d += 256) {
+            float acc0 = 0.0f, acc1 = 0.0f, acc2 = 0.0f, acc3 = 0.0f;
+            int k = 0;
+            for (; k + 4 <= nch; k += 4) {
+                acc0 += ld_agent(&po[(size_t)k * HD + d]) * wk[k];
+                acc1 += ld_agent(&po[(size_t)(k + 1) * HD + d]) * wk[k + 1];
+                acc2 += ld_agent(&po[(size_t)(k + 2) * HD + d]) * wk[k + 2];
+                acc3 += ld_agent(&po[(size_t)(k + 3) * HD + d]) * wk[k + 3];
+            }
+            for (; k < nch; k++) acc0 += ld_agent(&po[(size_t)k * HD + d]) * wk[k];
+            a.ao[(size_t)(h * G + g) * HD + d] = ((acc0 + acc1) + (acc2 + acc3)) / L;
         }
-        a.ao[(size_t)(h * G + g) * HD + d] = acc / L;
+        __syncthreads();
     }
-    if (threadIdx.x == 0) a.counter[h] = 0;
+    if (threadIdx.x == 0) reset_counter(&a.counter[h]);
 }
 
 // ---- exact mode: pass 1, integer scores on the softmax grid + chunk max ----
@@ -305,26 +362,28 @@ __global__ __launch_bounds__(256) void k_attn_exact_scores(AttnArgs a) {
     for (int g = 0; g < G; g++)
         #pragma unroll
         for (int e = 0; e < EPL; e++) qi[g][e] = (int32_t)rintf(a.qr[(size_t)(h * G + g) * HD + lane * EPL + e] * 65536.0f);
-    const int32_t *K = (const int32_t *)(page_of(a.pages, a.ring_pages, cs) + (size_t)h * PAGE * HD);
     int mx[G];
     #pragma unroll
     for (int g = 0; g < G; g++) mx[g] = INT32_MIN;
     const int n = ce - cs;
-    for (int j = wave; j < n; j += 4) {
-        const int slot = (cs + j) % PAGE;
-        int32_t kv[EPL];
+    for (int j0 = wave * UNR; j0 < n; j0 += 4 * UNR) {
+        int32_t kv[UNR][EPL];
         #pragma unroll
-        for (int e = 0; e < EPL; e++) kv[e] = K[(size_t)slot * HD + lane * EPL + e];
+        for (int u = 0; u < UNR; u++) if (j0 + u < n) load_row<EPL>(a, h, cs + j0 + u, false, lane, kv[u]);
         #pragma unroll
-        for (int g = 0; g < G; g++) {
-            int64_t ip = 0;
+        for (int u = 0; u < UNR; u++) {
+            if (j0 + u >= n) break;
             #pragma unroll
-            for (int e = 0; e < EPL; e++) ip += (int64_t)qi[g][e] * kv[e];
-            ip = wsuml(ip);
-            const float sc = (float)((double)ip / 4294967296.0) * a.ascale;
-            const int32_t z = (int32_t)llround_d((double)sc * 16384.0);
-            if (lane == 0) a.zscratch[(size_t)(h * G + g) * a.max_chunks * a.chunk + (size_t)c * a.chunk + j] = z;
-            mx[g] = z > mx[g] ? z : mx[g];
+            for (int g = 0; g < G; g++) {
+                int64_t ip = 0;
+                #pragma unroll
+                for (int e = 0; e < EPL; e++) ip += (int64_t)qi[g][e] * kv[u][e];
+                ip = wsuml(ip);
+                const float scv = (float)((double)ip / 4294967296.0) * a.ascale;
+                const int32_t z = (int32_t)llround_d((double)scv * 16384.0);
+                if (lane == 0) a.zscratch[(size_t)(h * G + g) * a.max_chunks * 16 + (size_t)(cs + j0 + u)] = z;
+                mx[g] = z > mx[g] ? z : mx[g];
+            }
         }
     }
     if (lane == 0) for (int g = 0; g < G; g++) zmax[wave][g] = mx[g];
@@ -346,78 +405,97 @@ __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a) {
     int cs, ce, nch;
     chunk_range(a, pos, c, cs, ce, nch);
     if (c >= nch) return;
-    __shared__ int64_t ew[G][PAGE];
+    __shared__ int64_t ew[G][MAXCH];
     __shared__ int64_t ored[4][G][EPL * 64];
+    __shared__ int redi[4][G];
+    __shared__ int64_t redl[4];
     __shared__ int is_last;
-    int32_t *pml = (int32_t *)a.part_ml;
+    const int32_t *pml = (const int32_t *)a.part_ml;
+    // global max of the attended window over every chunk's maximum
     int M[G];
     #pragma unroll
     for (int g = 0; g < G; g++) {
         int t = INT32_MIN;
-        for (int k = lane; k < nch; k += 64) {
+        for (int k = threadIdx.x; k < nch; k += 256) {
             const int v = pml[((size_t)(h * G + g) * a.max_chunks + k) * 4];
             t = v > t ? v : t;
         }
         #pragma unroll
         for (int o = 32; o > 0; o >>= 1) { const int u = __shfl_xor(t, o, 64); t = u > t ? u : t; }
+        if (lane == 0) redi[wave][g] = t;
+    }
+    __syncthreads();
+    #pragma unroll
+    for (int g = 0; g < G; g++) {
+        int t = redi[0][g];
+        for (int w = 1; w < 4; w++) t = redi[w][g] > t ? redi[w][g] : t;
         M[g] = t;
     }
     const int n = ce - cs;
     for (int i = threadIdx.x; i < G * n; i += 256) {
         const int g = i / n, j = i % n;
-        const int64_t z = a.zscratch[(size_t)(h * G + g) * a.max_chunks * a.chunk + (size_t)c * a.chunk + j];
-        ew[g][j] = exp_fixed(((z - (int64_t)M[g]) * ONE) >> 14) >> 7;
+        const int64_t z = a.zscratch[(size_t)(h * G + g) * a.max_chunks * 16 + (size_t)(cs + j)];
+        ew[g][j] = exp_fixed(((z - (int64_t)M[g]) * ONE) >> 14) >> 8;
     }
     __syncthreads();
-    const int32_t *V = (const int32_t *)(page_of(a.pages, a.ring_pages, cs) + (size_t)a.NKV * PAGE * HD + (size_t)h * PAGE * HD);
     int64_t o[G][EPL];
     #pragma unroll
     for (int g = 0; g < G; g++)
         #pragma unroll
         for (int e = 0; e < EPL; e++) o[g][e] = 0;
-    for (int j = wave; j < n; j += 4) {
-        const int slot = (cs + j) % PAGE;
-        int32_t vv[EPL];
+    for (int j0 = wave * UNR; j0 < n; j0 += 4 * UNR) {
+        int32_t vv[UNR][EPL];
         #pragma unroll
-        for (int e = 0; e < EPL; e++) vv[e] = V[(size_t)slot * HD + lane * EPL + e];
+        for (int u = 0; u < UNR; u++) if (j0 + u < n) load_row<EPL>(a, h, cs + j0 + u, true, lane, vv[u]);
         #pragma unroll
-        for (int g = 0; g < G; g++)
+        for (int u = 0; u < UNR; u++) {
+            if (j0 + u >= n) break;
             #pragma unroll
-            for (int e = 0; e < EPL; e++) o[g][e] += ew[g][j] * (int64_t)vv[e];
+            for (int g = 0; g < G; g++)
+                #pragma unroll
+                for (int e = 0; e < EPL; e++) o[g][e] += ew[g][j0 + u] * (int64_t)vv[u][e];
+        }
     }
     #pragma unroll
     for (int g = 0; g < G; g++)
         #pragma unroll
         for (int e = 0; e < EPL; e++) ored[wave][g][lane * EPL + e] = o[g][e];
     __syncthreads();
-    int64_t *part = (int64_t *)a.part;
+    // exact, order-free accumulation of this chunk into the kv-head's totals
     for (int i = threadIdx.x; i < G * HD; i += 256) {
         const int g = i / HD, d = i % HD;
-        part[((size_t)(h * G + g) * a.max_chunks + c) * HD + d] = ored[0][g][d] + ored[1][g][d] + ored[2][g][d] + ored[3][g][d];
+        const int64_t t = ored[0][g][d] + ored[1][g][d] + ored[2][g][d] + ored[3][g][d];
+        atomicAdd((unsigned long long *)&a.vacc[(size_t)(h * G + g) * HD + d], (unsigned long long)t);
     }
-    if (threadIdx.x < G) {
-        const int g = threadIdx.x;
+    #pragma unroll
+    for (int g = 0; g < G; g++) {
         int64_t S = 0;
-        for (int j = 0; j < n; j++) S += ew[g][j];
-        *(int64_t *)&pml[((size_t)(h * G + g) * a.max_chunks + c) * 4 + 2] = S;
+        for (int j = threadIdx.x; j < n; j += 256) S += ew[g][j];
+        S = wsuml(S);
+        if (lane == 0) redl[wave] = S;
+        __syncthreads();
+        if (threadIdx.x == 0)
+            atomicAdd((unsigned long long *)&a.vacc_s[h * G + g], (unsigned long long)(redl[0] + redl[1] + redl[2] + redl[3]));
+        __syncthreads();
     }
-    __threadfence();
+    mem_complete();
     __syncthreads();
-    if (threadIdx.x == 0) is_last = (atomicAdd(&a.counter[h], 1) == nch - 1);
+    if (threadIdx.x == 0) is_last = (arrive(&a.counter[h]) == nch - 1);
     __syncthreads();
     if (!is_last) return;
-    __threadfence();
+    // the totals are read and cleared for the next launch in one atomic step
     for (int i = threadIdx.x; i < G * HD; i += 256) {
-        const int g = i / HD, d = i % HD;
-        const size_t base = (size_t)(h * G + g) * a.max_chunks;
-        i128 acc = 0; int64_t S = 0;
-        for (int k = 0; k < nch; k++) {          // plain loads after the acquire fence
-            acc += (i128)part[(base + k) * HD + d];
-            S += *(const int64_t *)&pml[(base + k) * 4 + 2];
-        }
-        a.ao[(size_t)(h * G + g) * HD + d] = rne_div_to_float(acc, S, 16);
+        const int g = i / HD;
+        const int64_t acc = (int64_t)__hip_atomic_exchange((unsigned long long *)&a.vacc[(size_t)h * G * HD + i], 0ull,
+                                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int64_t S = (int64_t)__hip_atomic_fetch_add((unsigned long long *)&a.vacc_s[h * G + g], 0ull,
+                                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        a.ao[(size_t)h * G * HD + i] = rne_div_to_float((i128)acc, S, 16);
     }
-    if (threadIdx.x == 0) a.counter[h] = 0;
+    __syncthreads();
+    if (threadIdx.x < G) __hip_atomic_exchange((unsigned long long *)&a.vacc_s[h * G + threadIdx.x], 0ull,
+                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0) reset_counter(&a.counter[h]);
 }
 
 template <int EPL, int G> static void attn_dispatch(const AttnArgs &a, int grid_chunks, hipStream_t s) {
@@ -431,6 +509,10 @@ template <int EPL, int G> static void attn_dispatch(const AttnArgs &a, int grid_
 
 void launch_attention(const AttnArgs &a, int grid_chunks, hipStream_t s) {
     const int G = a.NH / a.NKV;
+    if (a.chunk > MAXCH || a.chunk % 16 || grid_chunks > MAXNCH) {
+        fprintf(stderr, "kvd: attention chunk %d / grid %d outside the kernel's limits\n", a.chunk, grid_chunks);
+        abort();
+    }
     if (a.HD == 256 && G == 2) attn_dispatch<4, 2>(a, grid_chunks, s);
     else if (a.HD == 128 && G == 2) attn_dispatch<2, 2>(a, grid_chunks, s);
     else if (a.HD == 128 && G == 4) attn_dispatch<2, 4>(a, grid_chunks, s);
@@ -477,20 +559,19 @@ __global__ __launch_bounds__(256) void k_argmax(const float *lg, int V, float *p
     __syncthreads();
     if (threadIdx.x == 0) {
         for (int w = 1; w < 4; w++) amax_merge(v, idx, sv[w], si[w]);
-        pv[blockIdx.x] = v; pi[blockIdx.x] = idx;
-        __threadfence();
-        is_last = atomicAdd(counter, 1) == (int)gridDim.x - 1;
+        st_agent(&pv[blockIdx.x], v); st_agent(&pi[blockIdx.x], idx);
+        mem_complete();
+        is_last = arrive(counter) == (int)gridDim.x - 1;
     }
     __syncthreads();
     if (!is_last || threadIdx.x != 0) return;
-    __threadfence();
     float bv = -INFINITY; int bi = 0x7FFFFFFF;
-    for (int b = 0; b < (int)gridDim.x; b++) amax_merge(bv, bi, pv[b], pi[b]);
+    for (int b = 0; b < (int)gridDim.x; b++) amax_merge(bv, bi, ld_agent(&pv[b]), ld_agent(&pi[b]));
     if (bi == 0x7FFFFFFF) bi = 0;
     st->tok = bi;
     if (gen_log) gen_log[st->pos] = bi;
     if (st->drive == DRIVE_GREEDY) st->pos = st->pos + 1;
-    *counter = 0;
+    reset_counter(counter);
 }
 int argmax_blocks(int V) { int b = (V + 2047) / 2048; return b < 1 ? 1 : (b > 256 ? 256 : b); }
 void launch_argmax(const float *logits, int V, float *pval, int *pidx, int *counter, DState *st,

@@ -330,6 +330,11 @@ struct sp_kvdecode_handle {
           *logits = nullptr, *part = nullptr, *part_ml = nullptr, *am_v = nullptr;
     int *counter = nullptr, *zscratch = nullptr, *am_i = nullptr, *am_cnt = nullptr, *gen_log = nullptr;
     int *tokbuf = nullptr;                   // DRIVE_STREAM tokens by absolute position
+    float *rope = nullptr;                   // [2][HD] rotation table of the current step
+    int64_t *vacc = nullptr, *vacc_s = nullptr;
+    int64_t *gacc = nullptr;                 // GEMV split-K row totals (zero between launches)
+    int *gcnt = nullptr;                     // GEMV split arrival counters
+    int acc_rows = 0;
     float *h_logits = nullptr;               // pinned staging
     int max_chunks = 0;
     void *scratch = nullptr;
@@ -420,9 +425,11 @@ int alloc_scratch(sp_kvdecode_handle *h) {
     struct Item { void **p; size_t n; };
     const size_t part_bytes = (size_t)m->NH * h->max_chunks * m->HD * 8;
     const size_t ml_bytes = (size_t)m->NH * h->max_chunks * 16;
-    const size_t z_bytes = (size_t)m->NH * h->max_chunks * 64 * 4;
+    const size_t z_bytes = (size_t)m->NH * h->max_chunks * 16 * 4;   // one int32 per (q-head, position)
     const int amb = argmax_blocks(m->V);
+    h->acc_rows = std::max(std::max(QD + 2 * KVD, 2 * m->FF), std::max(m->E, m->V));
     Item items[] = {
+        {(void **)&h->gacc, (size_t)h->acc_rows * 8}, {(void **)&h->gcnt, (size_t)h->acc_rows * 4},
         {(void **)&h->x0, (size_t)m->E * 4}, {(void **)&h->x1, (size_t)m->E * 4}, {(void **)&h->q, (size_t)QD * 4},
         {(void **)&h->k, (size_t)KVD * 4}, {(void **)&h->v, (size_t)KVD * 4}, {(void **)&h->qr, (size_t)QD * 4},
         {(void **)&h->ao, (size_t)QD * 4}, {(void **)&h->ap, (size_t)m->E * 4}, {(void **)&h->gg, (size_t)m->FF * 4},
@@ -430,7 +437,8 @@ int alloc_scratch(sp_kvdecode_handle *h) {
         {(void **)&h->logits, (size_t)m->V * 4}, {(void **)&h->part, part_bytes}, {(void **)&h->part_ml, ml_bytes},
         {(void **)&h->zscratch, z_bytes}, {(void **)&h->counter, 64 * 4}, {(void **)&h->am_v, (size_t)amb * 4},
         {(void **)&h->am_i, (size_t)amb * 4}, {(void **)&h->am_cnt, 64}, {(void **)&h->gen_log, (size_t)h->pmax * 4 + 64},
-        {(void **)&h->tokbuf, (size_t)h->pmax * 4 + 64},
+        {(void **)&h->tokbuf, (size_t)h->pmax * 4 + 64}, {(void **)&h->rope, (size_t)m->HD * 2 * 4},
+        {(void **)&h->vacc, (size_t)QD * 8}, {(void **)&h->vacc_s, (size_t)m->NH * 8},
         {(void **)&h->d_st, sizeof(DState) * 4},
     };
     size_t tot = 0;
@@ -449,9 +457,11 @@ struct StepShape { int logits, argmax, grid_global, grid_local, chunk_global, ch
 
 int attn_chunks(const sp_kvdecode_handle *h, int pos_hi, StepShape &sh) {
     const DevModel *m = h->m;
-    // global layers: chunk 64 (one page) unless that leaves the GPU under-filled
-    int cg = 64;
-    while (cg > 16 && (long long)((pos_hi + 1) / cg + 1) * m->NKV < 1024) cg /= 2;
+    // global layers: the largest chunk (<= 256 positions) that still gives about
+    // 2048 workgroups; fewer chunks make the merge of the partials cheaper
+    int cg = 256;
+    while (cg > 16 && (long long)((pos_hi + 1) / cg + 1) * m->NKV < 2048) cg /= 2;
+    while ((pos_hi / cg + 1) > 4096) cg *= 2;
     sh.chunk_global = cg;
     sh.grid_global = pos_hi / cg + 1;
     sh.chunk_local = 16;
@@ -470,11 +480,14 @@ void enqueue_body(sp_kvdecode_handle *h, const StepShape &sh, TimeCb cb, void *c
     auto T = [&](int cls, bool b) { if (cb) cb(ctx, cls, b); };
     T(5, true);
     launch_embed(m->embd, h->d_st, h->tokbuf, h->x1, m->gemma ? sqrtf((float)m->E) : 0.0f, s);
+    launch_rope_table(h->d_st, m->HD, h->mode, m->base, m->gemma ? 10000.0f : m->base,
+                      m->freq_global, m->gemma ? m->freq_local : m->freq_global, h->rope, s);
     T(5, false);
     for (int l = 0; l < m->NL; l++) {
         const DevLayer &d = m->L[l];
         const bool glob = is_global(m, l);
         GemvArgs g{};
+        g.accbuf = h->gacc; g.gcnt = h->gcnt; g.acc_rows = h->acc_rows;
         g.mode = h->mode; g.cols = m->E; g.act = ACT_NONE; g.nseg = 3;
         if (l == 0) { g.pro.kind = PRO_NORM; g.pro.x = h->x1; }
         else {
@@ -490,7 +503,8 @@ void enqueue_body(sp_kvdecode_handle *h, const StepShape &sh, TimeCb cb, void *c
         a.pages = h->d_pt + h->pt_off[l];
         a.ring_pages = h->slots[l] == h->full_pages ? 0 : h->slots[l];
         a.ao = h->ao; a.part = h->part; a.part_ml = h->part_ml; a.counter = h->counter; a.zscratch = h->zscratch;
-        a.st = h->d_st; a.freq_q60 = (m->gemma && !glob) ? m->freq_local : m->freq_global;
+        a.vacc = h->vacc; a.vacc_s = h->vacc_s;
+        a.st = h->d_st; a.rope_cs = h->rope + ((m->gemma && !glob) ? m->HD : 0);
         a.NH = m->NH; a.NKV = m->NKV; a.HD = m->HD;
         a.win = (m->gemma && !glob) ? m->SW : -1;
         a.max_chunks = h->max_chunks; a.mode = h->mode; a.eps = m->eps;
@@ -502,12 +516,14 @@ void enqueue_body(sp_kvdecode_handle *h, const StepShape &sh, TimeCb cb, void *c
         T(cls, true); launch_attention(a, glob ? sh.grid_global : sh.grid_local, s); T(cls, false);
 
         GemvArgs o{};
+        o.accbuf = h->gacc; o.gcnt = h->gcnt; o.acc_rows = h->acc_rows;
         o.mode = h->mode; o.cols = QD; o.act = ACT_NONE; o.nseg = 1;
         o.pro.kind = PRO_PLAIN; o.pro.x = h->ao; o.pro.n = QD;
         o.seg[0] = {d.o, h->ap};
         T(0, true); launch_gemv(o, m->E, s); T(0, false);
 
         GemvArgs f{};
+        f.accbuf = h->gacc; f.gcnt = h->gcnt; f.acc_rows = h->acc_rows;
         f.mode = h->mode; f.cols = m->E; f.act = m->gemma ? ACT_GELU : ACT_SILU; f.nseg = 2;
         f.pro.kind = PRO_RESID; f.pro.x = h->x1; f.pro.delta = h->ap; f.pro.post_w = d.post_attn;
         f.pro.norm_w = d.ffn_norm; f.pro.x_out = h->x0; f.pro.n = m->E; f.pro.eps = m->eps;
@@ -515,6 +531,7 @@ void enqueue_body(sp_kvdecode_handle *h, const StepShape &sh, TimeCb cb, void *c
         T(0, true); launch_gemv(f, m->FF, s); T(0, false);
 
         GemvArgs dd{};
+        dd.accbuf = h->gacc; dd.gcnt = h->gcnt; dd.acc_rows = h->acc_rows;
         dd.mode = h->mode; dd.cols = m->FF; dd.act = ACT_NONE; dd.nseg = 1;
         dd.pro.kind = PRO_PLAIN; dd.pro.x = h->hh; dd.pro.n = m->FF;
         dd.seg[0] = {d.down, h->dn};
@@ -522,6 +539,7 @@ void enqueue_body(sp_kvdecode_handle *h, const StepShape &sh, TimeCb cb, void *c
     }
     if (sh.logits) {
         GemvArgs lm{};
+        lm.accbuf = h->gacc; lm.gcnt = h->gcnt; lm.acc_rows = h->acc_rows;
         lm.mode = h->mode; lm.cols = m->E; lm.act = ACT_NONE; lm.nseg = 1;
         lm.pro.kind = PRO_RESID; lm.pro.x = h->x0; lm.pro.delta = h->dn;
         lm.pro.post_w = m->gemma ? m->L[m->NL - 1].post_ffw : nullptr;
@@ -687,6 +705,8 @@ int sp_hipkv_set_mode(sp_kvdecode_handle *h, int exact) {
     const int m = exact ? EXACT : FLOAT;
     if (m == h->mode) return 0;
     if (h->dpos != 0) return fail("sp_hipkv_set_mode: the mode is fixed once tokens are resident%s");
+    // exact V-sum: weights <= 2^22, |vq| < 2^23, so int64 totals hold 2^18 positions
+    if (m == EXACT && h->pmax > (1 << 18)) return fail("sp_hipkv_set_mode: exact mode holds at most %s%lld positions", "", (long long)(1 << 18));
     h->mode = m;
     free_graphs(h);
     return 0;

@@ -103,19 +103,20 @@ __device__ __forceinline__ float norm_apply(float x, float w, const NormScale &s
 }
 
 // ------------------------------------------------------- prologue
-// Builds the GEMV input (float, in xf) and its digit planes (in dig), returns sh
-// (or INT_MIN for an all-zero input).
+// Builds the GEMV input (float, in xf), its grid exponent sh from the whole
+// vector, and the digit planes of the workgroup's column split [b_lo, b_hi)
+// blocks (in dig, indexed from b_lo).  Returns SH_ZERO for an all-zero input.
 constexpr int SH_ZERO = -1000000;
 
-__device__ int gemv_prologue(const ProArgs &p, int mode, float *xf, uint4 *dig, int nblk, void *red) {
+template <int PRO>
+__device__ int gemv_prologue(const ProArgs &p, int mode, float *xf, uint4 *dig, int b_lo, int b_hi, void *red) {
     const int n = p.n;
     // PRO_PLAIN reads its input straight from global memory (two passes: max,
     // then digits); the norm prologues stage the transformed vector in xf.
-    const bool plain = p.kind == PRO_PLAIN;
-    if (p.kind == PRO_NORM) {
+    if constexpr (PRO == PRO_NORM) {
         NormScale s = norm_scale(p.x, n, p.eps, mode, red);
         for (int i = threadIdx.x; i < n; i += blockDim.x) xf[i] = norm_apply(p.x[i], p.norm_w[i], s, mode);
-    } else if (p.kind == PRO_RESID) {
+    } else if constexpr (PRO == PRO_RESID) {
         if (p.post_w) {
             NormScale sd = norm_scale(p.delta, n, p.eps, mode, red);
             for (int i = threadIdx.x; i < n; i += blockDim.x)
@@ -130,7 +131,7 @@ __device__ int gemv_prologue(const ProArgs &p, int mode, float *xf, uint4 *dig, 
         __syncthreads();
         for (int i = threadIdx.x; i < n; i += blockDim.x) xf[i] = norm_apply(xf[i], p.norm_w[i], s, mode);
     }
-    const float *src = plain ? p.x : xf;
+    const float *src = PRO == PRO_PLAIN ? p.x : xf;
     float m = 0.0f;
     for (int i = threadIdx.x; i < n; i += blockDim.x) m = fmaxf(m, fabsf(src[i]));
     m = block_max(m, (float *)red);                      // also orders the xf writes above
@@ -138,8 +139,8 @@ __device__ int gemv_prologue(const ProArgs &p, int mode, float *xf, uint4 *dig, 
     int e; frexpf(m, &e);
     const int sh = 22 - e;
     // digits: one thread per 8 consecutive columns (one nibble-dword per plane)
-    const int ngroups = nblk * 4;
-    for (int g = threadIdx.x; g < ngroups; g += blockDim.x) {
+    const int g_lo = b_lo * 4, g_hi = b_hi * 4, nb = b_hi - b_lo;
+    for (int g = g_lo + threadIdx.x; g < g_hi; g += blockDim.x) {
         uint32_t dw[NDIG] = {0, 0, 0, 0, 0, 0};
         #pragma unroll
         for (int j = 0; j < 8; j++) {
@@ -152,9 +153,9 @@ __device__ int gemv_prologue(const ProArgs &p, int mode, float *xf, uint4 *dig, 
                 dw[k] |= (uint32_t)(d & 15) << (4 * j);
             }
         }
-        const int b = g >> 2, q = g & 3;
+        const int b = (g >> 2) - b_lo, q = g & 3;
         #pragma unroll
-        for (int k = 0; k < NDIG; k++) ((uint32_t *)&dig[k * nblk + b])[q] = dw[k];
+        for (int k = 0; k < NDIG; k++) ((uint32_t *)&dig[k * nb + b])[q] = dw[k];
     }
     __syncthreads();
     return sh;
@@ -217,82 +218,108 @@ __device__ __forceinline__ int64_t transpose_reduce8(const int64_t v[8], int lan
     return y;
 }
 
-template <bool WIDE>
+// One wave task: GEMV_R rows (paired: HR gate + HR up rows) over the
+// workgroup's column split.  All fields are wave-uniform.
+struct Task { int seg, row0, nvalid, grow0; };
+
+template <bool PAIRED>
+__device__ __forceinline__ Task task_of(const GemvArgs &a, int grp) {
+    Task t;
+    if (PAIRED) {
+        const int rows0 = a.seg[0].w.rows;
+        t.seg = 0; t.row0 = grp * (GEMV_R / 2);
+        t.nvalid = rows0 - t.row0 < GEMV_R / 2 ? rows0 - t.row0 : GEMV_R / 2;
+        t.grow0 = t.row0;
+    } else {
+        // a group never straddles segments (segment row counts are multiples
+        // of GEMV_R, checked by the host), so its rows are consecutive
+        int g = grp * GEMV_R, s = 0, off = 0;
+        while (s < a.nseg - 1 && g >= a.seg[s].w.rows) { g -= a.seg[s].w.rows; off += a.seg[s].w.rows; s++; }
+        t.seg = s; t.row0 = g; t.grow0 = off + g;
+        t.nvalid = a.seg[s].w.rows - g < GEMV_R ? a.seg[s].w.rows - g : GEMV_R;
+    }
+    t.seg = __builtin_amdgcn_readfirstlane(t.seg);
+    t.row0 = __builtin_amdgcn_readfirstlane(t.row0);
+    t.nvalid = __builtin_amdgcn_readfirstlane(t.nvalid);
+    t.grow0 = __builtin_amdgcn_readfirstlane(t.grow0);
+    return t;
+}
+
+// 16 B of codes and the f16 scale of block b for each of the task's rows
+// (zeros for rows past the end and for b >= b_hi)
+template <bool PAIRED>
+__device__ __forceinline__ void load_iter(const GemvArgs &a, const Task &t, bool ok, int b, int b_hi,
+                                          uint4 c[GEMV_R], uint32_t h[GEMV_R]) {
+    const int per = PAIRED ? GEMV_R / 2 : GEMV_R;
+    const DevW &wa = a.seg[t.seg].w;
+    const DevW &wb = a.seg[PAIRED ? 1 : t.seg].w;
+    const int nblk = wa.nblk;
+    const size_t rb = (size_t)(wa.cols + 1) / 2;
+    #pragma unroll
+    for (int r = 0; r < GEMV_R; r++) {
+        const int rr = r % per;
+        const bool second = PAIRED && r >= per;
+        if (ok && rr < t.nvalid && b < b_hi) {
+            typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+            const DevW &w = second ? wb : wa;
+            const uint8_t *cp = w.codes + (size_t)(t.row0 + rr) * rb + (size_t)b * 16;
+            const u32x4 v = __builtin_nontemporal_load((const u32x4 *)cp);
+            c[r] = make_uint4(v.x, v.y, v.z, v.w);
+            h[r] = w.bs[(size_t)(t.row0 + rr) * nblk + b];
+        } else { c[r] = make_uint4(0, 0, 0, 0); h[r] = 0; }
+    }
+}
+
+// The matrix pass.  Workgroup w works on column split s = w % nsplit (blocks
+// [s*bps, min(nblk, (s+1)*bps)) ); its waves take row groups in a grid stride.
+// With nsplit > 1 every task adds its exact int64 row partials atomically into
+// accbuf (order-free, so still bit-exact); the wave that completes a group's
+// last split converts the totals, writes the outputs and clears accbuf/gcnt
+// for the next launch.  The first weights are requested before the prologue,
+// and each task requests the next task's weights before its own epilogue.
+template <int PRO, bool PAIRED, bool WIDE>
 __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
     extern __shared__ uint4 smem4[];
-    const int cols = a.cols, nblk = (cols + 31) / 32;
-    uint4 *dig = smem4;                                   // NDIG * nblk
-    float *xf = (float *)(dig + NDIG * nblk);             // pro.n floats (norm prologues only)
+    const int nblk = (a.cols + 31) / 32, nsplit = a.nsplit, bps = a.bps;
+    const int split = blockIdx.x % nsplit;
+    const int b_lo = split * bps, b_hi = b_lo + bps < nblk ? b_lo + bps : nblk, nb = b_hi - b_lo;
+    uint4 *dig = smem4;                                   // NDIG * nb
+    float *xf = (float *)(dig + NDIG * nb);               // pro.n floats (norm prologues only)
     __shared__ double red[GEMV_WAVES];
-
-    const int sh = gemv_prologue(a.pro, a.mode, xf, dig, nblk, red);
-
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int rows0 = a.seg[0].w.rows;
-    const int paired = a.act != ACT_NONE;
-    const int HR = GEMV_R / 2;                            // paired: HR gate rows + HR up rows
-    int total_groups;
-    if (paired) total_groups = (rows0 + HR - 1) / HR;
-    else {
-        int tr = 0;
-        for (int s = 0; s < a.nseg; s++) tr += a.seg[s].w.rows;
-        total_groups = (tr + GEMV_R - 1) / GEMV_R;
-    }
-    const size_t rb = (size_t)(cols + 1) / 2;
+    const int nwaves = blockDim.x >> 6;
+    constexpr int HR = GEMV_R / 2;
+    constexpr int per = PAIRED ? HR : GEMV_R;
+    const int gstride = (gridDim.x / nsplit) * nwaves;
+    int grp = (blockIdx.x / nsplit) * nwaves + wave;
 
-    for (int grp = blockIdx.x * GEMV_WAVES + wave; grp < total_groups; grp += gridDim.x * GEMV_WAVES) {
-        // A group never straddles segments (segment row counts are multiples of
-        // the group size, checked by the host), so its rows are consecutive and
-        // addressed from one wave-uniform base per half.
-        int seg0, row0, nvalid;
-        if (paired) {
-            seg0 = 0; row0 = grp * HR;
-            nvalid = rows0 - row0 < HR ? rows0 - row0 : HR;
-        } else {
-            int g = grp * GEMV_R, s = 0;
-            while (s < a.nseg - 1 && g >= a.seg[s].w.rows) { g -= a.seg[s].w.rows; s++; }
-            seg0 = s; row0 = g;
-            nvalid = a.seg[s].w.rows - g < GEMV_R ? a.seg[s].w.rows - g : GEMV_R;
-        }
-        seg0 = __builtin_amdgcn_readfirstlane(seg0);
-        row0 = __builtin_amdgcn_readfirstlane(row0);
-        nvalid = __builtin_amdgcn_readfirstlane(nvalid);
-        const DevW &wa = a.seg[seg0].w;
-        const DevW &wb = a.seg[paired ? 1 : seg0].w;
-        const uint8_t *cba = wa.codes + (size_t)row0 * rb, *cbb = wb.codes + (size_t)row0 * rb;
-        const uint16_t *sba = wa.bs + (size_t)row0 * nblk, *sbb = wb.bs + (size_t)row0 * nblk;
-        const int per = paired ? HR : GEMV_R;             // rows taken from each base
+    Task t = task_of<PAIRED>(a, grp < a.groups ? grp : 0);
+    uint4 c[GEMV_R];
+    uint32_t h[GEMV_R];
+    load_iter<PAIRED>(a, t, grp < a.groups, b_lo + lane, b_hi, c, h);
+
+    const int sh = gemv_prologue<PRO>(a.pro, a.mode, xf, dig, b_lo, b_hi, red);
+    const int nit = (nb + 63) / 64;
+
+    for (; grp < a.groups; grp += gstride) {
         int eb[GEMV_R];
         #pragma unroll
         for (int r = 0; r < GEMV_R; r++) {
             const int rr = r % per;
-            const DevW &w = (paired && r >= HR) ? wb : wa;
-            eb[r] = WIDE ? -24 : (rr < nvalid ? (int)w.ebase[row0 + rr] : 0);
+            const DevW &w = (PAIRED && r >= HR) ? a.seg[1].w : a.seg[t.seg].w;
+            eb[r] = WIDE ? -24 : (rr < t.nvalid ? (int)w.ebase[t.row0 + rr] : 0);
         }
         typedef typename std::conditional<WIDE, i128, int64_t>::type acc_t;
         acc_t acc[GEMV_R];
         #pragma unroll
         for (int r = 0; r < GEMV_R; r++) acc[r] = 0;
-
-        if (sh != SH_ZERO) {
-            for (int b = lane; b < nblk; b += 64) {
-                uint4 c[GEMV_R];
-                uint32_t h[GEMV_R];
-                #pragma unroll
-                for (int r = 0; r < GEMV_R; r++) {
-                    const int rr = r % per;
-                    const bool second = paired && r >= HR;
-                    if (rr < nvalid) {
-                        typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-                        const uint8_t *cp = (second ? cbb : cba) + (size_t)rr * rb + (size_t)b * 16;
-                        const u32x4 t = __builtin_nontemporal_load((const u32x4 *)cp);
-                        c[r] = make_uint4(t.x, t.y, t.z, t.w);
-                        h[r] = (second ? sbb : sba)[(size_t)rr * nblk + b];
-                    } else { c[r] = make_uint4(0, 0, 0, 0); h[r] = 0; }
-                }
+        for (int it = 0; it < nit; it++) {
+            const int b = b_lo + it * 64 + lane;
+            if (it > 0) load_iter<PAIRED>(a, t, true, b, b_hi, c, h);
+            if (b < b_hi && sh != SH_ZERO) {
                 uint4 D[NDIG];
                 #pragma unroll
-                for (int k = 0; k < NDIG; k++) D[k] = dig[k * nblk + b];
+                for (int k = 0; k < NDIG; k++) D[k] = dig[k * nb + (b - b_lo)];
                 #pragma unroll
                 for (int r = 0; r < GEMV_R; r++) {
                     const int32_t d = dot_digits(c[r], D);
@@ -306,54 +333,75 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
                 }
             }
         }
-        float y[GEMV_R];
-        int myrow = 0;
+        // request the next task's first weights before this task's epilogue
+        const int ngrp = grp + gstride;
+        const Task tn = task_of<PAIRED>(a, ngrp < a.groups ? ngrp : 0);
+        load_iter<PAIRED>(a, tn, ngrp < a.groups, b_lo + lane, b_hi, c, h);
+
         if constexpr (WIDE) {
+            // int128 rows: whole rows per task (nsplit == 1, enforced by the host)
+            float y[GEMV_R];
             #pragma unroll
             for (int r = 0; r < GEMV_R; r++) {
-                const i128 t = wave_sum128(acc[r]);
-                y[r] = sh == SH_ZERO ? 0.0f : rne_i128_scaled(t, -24 - sh);
+                const i128 tt = wave_sum128(acc[r]);
+                y[r] = sh == SH_ZERO ? 0.0f : rne_i128_scaled(tt, -24 - sh);
             }
-        } else {
-            const int64_t t = transpose_reduce8(acc, lane);
-            myrow = ((lane >> 5) & 1) * 4 + ((lane >> 4) & 1) * 2 + ((lane >> 3) & 1);
-            int ebm = eb[0];
-            #pragma unroll
-            for (int r = 1; r < GEMV_R; r++) if (myrow == r) ebm = eb[r];
-            y[0] = sh == SH_ZERO ? 0.0f : rne_i64_scaled(t, ebm - sh);
-        }
-        if constexpr (WIDE) {
             if (lane == 0) {
-                if (paired) {
-                    for (int r = 0; r < nvalid; r++) {
-                        const int j = row0 + r;
+                if (PAIRED) {
+                    for (int r = 0; r < t.nvalid; r++) {
+                        const int j = t.row0 + r;
                         a.seg[0].out[j] = y[r]; a.seg[1].out[j] = y[r + HR];
                         a.act_out[j] = act_apply(y[r], y[r + HR], a.act, a.mode);
                     }
                 } else {
-                    for (int r = 0; r < nvalid; r++) a.seg[seg0].out[row0 + r] = y[r];
+                    for (int r = 0; r < t.nvalid; r++) a.seg[t.seg].out[t.row0 + r] = y[r];
                 }
             }
         } else {
-            // lane (myrow*8) owns row myrow's total; paired rows fetch their up partner
-            const float partner = __shfl_xor(y[0], 32, 64);          // row myrow^4
-            if ((lane & 7) == 0) {
-                if (paired) {
-                    if (myrow < HR && myrow < nvalid) {
-                        const int j = row0 + myrow;
-                        a.seg[0].out[j] = y[0]; a.seg[1].out[j] = partner;
-                        a.act_out[j] = act_apply(y[0], partner, a.act, a.mode);
+            int64_t tot = transpose_reduce8(acc, lane);
+            const int myrow = ((lane >> 5) & 1) * 4 + ((lane >> 4) & 1) * 2 + ((lane >> 3) & 1);
+            const int rr = myrow % per;
+            const bool holder = (lane & 7) == 0 && rr < t.nvalid;
+            bool finish = true;
+            if (nsplit > 1) {
+                int64_t *slot = a.accbuf + (PAIRED ? (myrow >= HR ? a.seg[0].w.rows : 0) + t.row0 + rr : t.grow0 + myrow);
+                if (holder) atomicAdd((unsigned long long *)slot, (unsigned long long)tot);
+                mem_complete();
+                int prev = 0;
+                if (lane == 0) prev = arrive(&a.gcnt[grp]);
+                prev = __shfl(prev, 0, 64);
+                finish = prev == nsplit - 1;
+                if (finish) {
+                    if (holder) tot = (int64_t)__hip_atomic_exchange((unsigned long long *)slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if (lane == 0) reset_counter(&a.gcnt[grp]);
+                }
+            }
+            if (finish) {
+                int ebm = eb[0];
+                #pragma unroll
+                for (int r = 1; r < GEMV_R; r++) if (myrow == r) ebm = eb[r];
+                const float y = sh == SH_ZERO ? 0.0f : rne_i64_scaled(tot, ebm - sh);
+                // lane (myrow*8) owns row myrow's total; paired rows fetch their up partner
+                const float partner = __shfl_xor(y, 32, 64);          // row myrow^4
+                if (holder) {
+                    if (PAIRED) {
+                        if (myrow < HR) {
+                            const int j = t.row0 + myrow;
+                            a.seg[0].out[j] = y; a.seg[1].out[j] = partner;
+                            a.act_out[j] = act_apply(y, partner, a.act, a.mode);
+                        }
+                    } else {
+                        a.seg[t.seg].out[t.row0 + myrow] = y;
                     }
-                } else if (myrow < nvalid) {
-                    a.seg[seg0].out[row0 + myrow] = y[0];
                 }
             }
         }
+        t = tn;
     }
 }
 
 static int g_num_cu = 0;
-int gemv_grid(int nrows_total, int cols, int paired) {
+static int num_cu() {
     if (!g_num_cu) {
         int dev = 0, n = 0;
         if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
@@ -361,25 +409,60 @@ int gemv_grid(int nrows_total, int cols, int paired) {
         else
             g_num_cu = 256;
     }
-    const int groups = paired ? (nrows_total + GEMV_R / 2 - 1) / (GEMV_R / 2) : (nrows_total + GEMV_R - 1) / GEMV_R;
-    const int blocks = (groups + GEMV_WAVES - 1) / GEMV_WAVES;
-    const int cap = 2 * g_num_cu;                      // every workgroup pays the input prologue once
-    (void)cols;
-    return blocks < cap ? blocks : cap;
+    return g_num_cu;
 }
 
-void launch_gemv(const GemvArgs &a, int nrows_total, hipStream_t s) {
-    const int nblk = (a.cols + 31) / 32;
+// Work decomposition: row groups x column splits of 64-block multiples, so
+// that about two 8-wave workgroups per CU have work; the grid is a multiple
+// of nsplit so that a workgroup keeps one split (and builds only its digits).
+GemvPlan gemv_plan(int nrows_total, int cols, int paired, int wide) {
+    GemvPlan p;
+    const int nblk = (cols + 31) / 32;
+    p.groups = paired ? (nrows_total + GEMV_R / 2 - 1) / (GEMV_R / 2) : (nrows_total + GEMV_R - 1) / GEMV_R;
+    const int cap = 2 * num_cu();                       // workgroups
+    const int max_split = (nblk + 63) / 64;
+    int want = (cap * GEMV_WAVES + p.groups - 1) / p.groups;
+    if (wide || want < 1) want = 1;
+    p.nsplit = want < max_split ? want : max_split;
+    p.bps = 64 * ((max_split + p.nsplit - 1) / p.nsplit);
+    p.nsplit = (nblk + p.bps - 1) / p.bps;
+    int per_split = (p.groups + GEMV_WAVES - 1) / GEMV_WAVES;
+    const int lim = cap / p.nsplit > 0 ? cap / p.nsplit : 1;
+    if (per_split > lim) per_split = lim;
+    p.grid = per_split * p.nsplit;
+    return p;
+}
+
+template <int PRO, bool PAIRED>
+static void launch_pro(const GemvArgs &a, bool wide, int grid, size_t lds, hipStream_t s) {
+    if (wide) hipLaunchKernelGGL((k_gemv<PRO, PAIRED, true>), dim3(grid), dim3(GEMV_WAVES * 64), lds, s, a);
+    else      hipLaunchKernelGGL((k_gemv<PRO, PAIRED, false>), dim3(grid), dim3(GEMV_WAVES * 64), lds, s, a);
+}
+
+void launch_gemv(const GemvArgs &a_in, int nrows_total, hipStream_t s) {
+    GemvArgs a = a_in;
     // a wave's row group must not straddle segments
     for (int i = 0; i + 1 < a.nseg; i++)
         if (a.seg[i].w.rows % GEMV_R) { fprintf(stderr, "kvd: GEMV segment rows %d not a multiple of %d\n", a.seg[i].w.rows, GEMV_R); abort(); }
-    const size_t lds = (size_t)NDIG * nblk * sizeof(uint4) +
-                       (a.pro.kind == PRO_PLAIN ? 0 : (size_t)a.pro.n * sizeof(float));
-    const int grid = gemv_grid(nrows_total, a.cols, a.act != ACT_NONE);
     bool wide = false;
     for (int i = 0; i < a.nseg; i++) wide |= a.seg[i].w.wide != 0;
-    if (wide) hipLaunchKernelGGL(k_gemv<true>, dim3(grid), dim3(GEMV_WAVES * 64), lds, s, a);
-    else      hipLaunchKernelGGL(k_gemv<false>, dim3(grid), dim3(GEMV_WAVES * 64), lds, s, a);
+    const bool paired = a.act != ACT_NONE;
+    const GemvPlan p = gemv_plan(nrows_total, a.cols, paired, wide);
+    if (p.nsplit > 1 && (!a.accbuf || !a.gcnt || nrows_total * (paired ? 2 : 1) > a.acc_rows || p.groups > a.acc_rows)) {
+        fprintf(stderr, "kvd: GEMV split accumulators missing or too small\n"); abort();
+    }
+    a.nsplit = p.nsplit; a.bps = p.bps; a.groups = p.groups;
+    const int nb = p.bps < (a.cols + 31) / 32 ? p.bps : (a.cols + 31) / 32;
+    const size_t lds = (size_t)NDIG * nb * sizeof(uint4) +
+                       (a.pro.kind == PRO_PLAIN ? 0 : (size_t)a.pro.n * sizeof(float));
+    switch (a.pro.kind * 2 + (paired ? 1 : 0)) {
+    case PRO_PLAIN * 2:     launch_pro<PRO_PLAIN, false>(a, wide, p.grid, lds, s); break;
+    case PRO_PLAIN * 2 + 1: launch_pro<PRO_PLAIN, true>(a, wide, p.grid, lds, s); break;
+    case PRO_NORM * 2:      launch_pro<PRO_NORM, false>(a, wide, p.grid, lds, s); break;
+    case PRO_NORM * 2 + 1:  launch_pro<PRO_NORM, true>(a, wide, p.grid, lds, s); break;
+    case PRO_RESID * 2:     launch_pro<PRO_RESID, false>(a, wide, p.grid, lds, s); break;
+    default:                launch_pro<PRO_RESID, true>(a, wide, p.grid, lds, s); break;
+    }
 }
 
 }  // namespace kvd

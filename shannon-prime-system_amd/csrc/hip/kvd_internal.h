@@ -45,7 +45,12 @@ struct GemvArgs {
     int  act;          // paired gate/up with activation: seg[0] = gate, seg[1] = up
     float *act_out;    // h = act(gate) * up
     int  mode;
+    int64_t *accbuf;   // split-K row totals [acc_rows] (zero between launches)
+    int  *gcnt;        // split arrival counters per row group [acc_rows] (zero between launches)
+    int  acc_rows;
+    int  nsplit, bps, groups;   // filled in by launch_gemv
 };
+struct GemvPlan { int groups, nsplit, bps, grid; };
 
 // Per-session device-side step state (graph-replay friendly: kernels read it).
 struct DState {
@@ -72,23 +77,51 @@ struct AttnArgs {
     float *part;             // partials [NKV*G][max_chunks][HD]
     float *part_ml;          // [NKV*G][max_chunks][2] (max, sum) or exact (max, S lo/hi)
     int   *counter;          // [NKV] arrival counters (self-resetting)
-    int   *zscratch;         // exact mode: int32 score grid per (head, position)
+    int   *zscratch;         // exact mode: int32 score grid [NH][max_chunks*16] by absolute position
+    int64_t *vacc;           // exact mode: V-sum totals [NH][HD] (atomic, order-free)
+    int64_t *vacc_s;         // exact mode: softmax denominators [NH]
     const DState *st;
-    const int64_t *freq_q60; // exact-mode RoPE frequencies base^(-2i/HD) in Q60 [HD/2]
+    const float *rope_cs;    // this step's rotation table for the layer's base: cos[HD/2], sin[HD/2]
     int NH, NKV, HD, win, max_chunks, chunk, mode;
     float eps, base, ascale;
 };
+
+// Hand-off between workgroups of one launch without cache-wide fences: all data
+// one workgroup passes to another goes through agent-scope atomic operations
+// (coherent across the XCDs' L2s by themselves), and the arrival counter is
+// bumped only after the wave's own memory operations have completed.  An
+// agent-scope release/acquire fence would instead write back / invalidate the
+// whole L2 of the XCD, which costs far more than the hand-off itself.
+__device__ __forceinline__ void mem_complete() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+template <typename T> __device__ __forceinline__ void st_agent(T *p, T v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T> __device__ __forceinline__ T ld_agent(const T *p) {
+    return __hip_atomic_load(const_cast<T *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int arrive(int *counter) {
+    return __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void reset_counter(int *counter) {
+    __hip_atomic_exchange(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // launchers (kvd_kernels.hip)
 void launch_embed(const DevW &embd, const DState *st, const int *tokbuf, float *x, float scale, hipStream_t s);
 void launch_advance(DState *st, hipStream_t s);
 void launch_gemv(const GemvArgs &a, int nrows_total, hipStream_t s);
 void launch_qk_prep(const AttnArgs &a, hipStream_t s);
+void launch_rope_table(const DState *st, int HD, int mode, float base_g, float base_l,
+                       const int64_t *fq_g, const int64_t *fq_l, float *out, hipStream_t s);
 void launch_attention(const AttnArgs &a, int grid_chunks, hipStream_t s);
 void set_rope_tables(const int64_t atan_q60[64], int64_t kinv_q62);
 void launch_argmax(const float *logits, int V, float *pval, int *pidx, int *counter,
                    DState *st, int *gen_log, int nblocks, hipStream_t s);
 int  argmax_blocks(int V);
-int  gemv_grid(int nrows_total, int cols, int paired);
+GemvPlan gemv_plan(int nrows_total, int cols, int paired, int wide);
 
 }  // namespace kvd

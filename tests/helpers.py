@@ -18,6 +18,12 @@ SMALL = {
                          head_dim=256, n_ff=1024, vocab=2048, swa_window=32),
     "qwen3-g4": dict(arch_id=spkv.ARCH_QWEN3, n_layers=2, hidden=512, n_heads=8, n_kv_heads=2,
                      head_dim=128, n_ff=1024, vocab=2048, untied=1),
+    # wide rows: the GEMVs split their columns over workgroups (2-3 splits, the
+    # last one ragged) and combine exact partials atomically
+    "qwen3-wide": dict(arch_id=spkv.ARCH_QWEN3, n_layers=2, hidden=2304, n_heads=8, n_kv_heads=4,
+                       head_dim=128, n_ff=4352, vocab=3000),
+    "gemma3-wide": dict(arch_id=spkv.ARCH_GEMMA3, n_layers=6, hidden=2304, n_heads=8, n_kv_heads=4,
+                        head_dim=256, n_ff=4352, vocab=3000, swa_window=16),
 }
 
 

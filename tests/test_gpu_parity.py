@@ -6,7 +6,7 @@ Bars:
   float mode  -- logits within rel 1e-3 of the oracle's float mode (which is
                  bit-identical to the compiled reference), same greedy trajectory.
 Cases cover both architectures, head_dim 64/128/256, GQA groups 2 and 4, an
-untied head, clipping sliding windows, prefill through sp_prefill_chunk, the
+untied head, GEMVs whose columns are split over workgroups (ragged last split), clipping sliding windows, prefill through sp_prefill_chunk, the
 dispatch table driven directly, HIP-graph and plain launches, copy-on-write
 forks through sp_session_clone, O(1) rewind (full table and window ring), and
 the C1 configuration (Qwen3-0.6B single layer, vocab 151936).
@@ -77,11 +77,13 @@ def close_all(*objs):
         o.close()
 
 
-@pytest.mark.parametrize("name", ["qwen3-tiny", "gemma3-tiny", "qwen3-hd128", "gemma3-hd256", "qwen3-g4"])
+@pytest.mark.parametrize("name", ["qwen3-tiny", "gemma3-tiny", "qwen3-hd128", "gemma3-hd256", "qwen3-g4",
+                                  "qwen3-wide", "gemma3-wide"])
 @pytest.mark.parametrize("exact", [True, False])
 def test_decode_parity(tmpdir_models, name, exact):
     spm, spt = model_files(tmpdir_models, name)
-    m, s, o, be, res = run_pair(spm, spt, exact, n_prompt=40, n_gen=24)
+    wide = name.endswith("-wide")
+    m, s, o, be, res = run_pair(spm, spt, exact, n_prompt=24 if wide else 40, n_gen=12 if wide else 24)
     check(res, exact)
     # resident K/V equals the oracle's slab (exact: bit for bit)
     kvd = o.NKV * o.HD
