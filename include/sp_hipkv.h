@@ -70,6 +70,10 @@ int  sp_hipkv_kernel_times(sp_kvdecode_handle *h, int32_t first_token, int n,
 int  sp_hipkv_read_kv(const sp_kvdecode_handle *h, int layer, int p0, int n, float *k, float *v);
 /* Use a captured HIP graph for each step body (1, default) or plain launches (0). */
 int  sp_hipkv_set_graph(sp_kvdecode_handle *h, int on);
+/* Prefill through the batched path (1, default: 128 tokens per pass, int8-MFMA
+ * GEMMs, token-batched attention) or one decode step per token (0).  Both
+ * leave the same K/V (bit-identical in exact mode). */
+int  sp_hipkv_set_batch_prefill(sp_kvdecode_handle *h, int on);
 /* Bytes of model weights resident in HBM and KV bytes per token per layer. */
 int  sp_hipkv_info(const sp_kvdecode_handle *h, long long out[8]);
 

@@ -77,12 +77,29 @@ __device__ __forceinline__ float *page_of(float *const *pages, int ring, int pos
     return pages[ring ? lp % ring : lp];
 }
 
+// Decode: the position comes from the step state.  Batched prefill: token t of
+// the batch sits at pos0 + t and every per-token buffer is offset to its row.
+__device__ __forceinline__ void tok_select(AttnArgs &a, int t, int &pos) {
+    if (!a.nt) { pos = a.st->pos; return; }
+    pos = a.pos0 + t;
+    const size_t QD = (size_t)a.NH * a.HD, KVD = (size_t)a.NKV * a.HD;
+    a.q += t * QD; a.k += t * KVD; a.v += t * KVD; a.qr += t * QD; a.ao += t * QD;
+    a.part += t * (size_t)a.NH * a.max_chunks * a.HD;
+    a.part_ml += t * (size_t)a.NH * a.max_chunks * 4;
+    a.counter += t * a.NKV;
+    a.zscratch += t * (size_t)a.NH * a.zstride;
+    a.vacc += t * QD; a.vacc_s += t * a.NH;
+    a.rope_cs += t * (size_t)a.rope_stride;
+}
+
 // ------------------------------------------------------------------ qk_prep
 // grid.x = NH (q heads) + NKV (k heads) + NKV (v heads); block = 64 threads
 // (one wave), each lane owning HD/64 pairs-halves.  float/exact by a.mode.
-__global__ __launch_bounds__(64) void k_qk_prep(AttnArgs a) {
+__global__ __launch_bounds__(64) void k_qk_prep(AttnArgs a_in) {
+    AttnArgs a = a_in;
+    int pos;
+    tok_select(a, blockIdx.y, pos);
     const int HD = a.HD, half = HD / 2, lane = threadIdx.x;
-    const int pos = a.st->pos;
     const int hb = blockIdx.x;
     const bool isq = hb < a.NH, isk = !isq && hb < a.NH + a.NKV;
     const int h = isq ? hb : (isk ? hb - a.NH : hb - a.NH - a.NKV);
@@ -115,13 +132,13 @@ __global__ __launch_bounds__(64) void k_qk_prep(AttnArgs a) {
         for (int j = 0; j < per; j++) v[j] = v[j] * sc * nw[lane + 64 * j];
     } else {
         int64_t ss = 0;
-        for (int j = 0; j < per; j++) { int64_t xi = llround_d((double)v[j] * 65536.0); ss += xi * xi; }
+        for (int j = 0; j < per; j++) { int64_t xi = llround_pow2<16>(v[j]); ss += xi * xi; }
         ss = wsuml(ss);
         if (ss == 0) { for (int j = 0; j < per; j++) v[j] = 0.0f; }
         else {
             const int64_t inv = (int64_t)isqrt_u64(udiv128_64((u128)HD << 72, (uint64_t)ss));
             for (int j = 0; j < per; j++) {
-                int64_t xi = llround_d((double)v[j] * 65536.0), wi = llround_d((double)nw[lane + 64 * j] * 65536.0);
+                int64_t xi = llround_pow2<16>(v[j]), wi = llround_pow2<16>(nw[lane + 64 * j]);
                 v[j] = (float)((double)mul3_lo64(xi, inv, wi) / 4503599627370496.0);
             }
         }
@@ -160,9 +177,11 @@ __global__ __launch_bounds__(64) void k_qk_prep(AttnArgs a) {
 // out[t][0..half) = cos, out[t][half..HD) = sin, t = 0 global base, 1 window base.
 // Float mode: freq = powf(base, -2i/d), theta = (float)p*freq, cosf/sinf
 // (forward_kernels.c:31-41); exact mode: p*F_i mod 2*pi (Q60) by CORDIC, RNE.
-__global__ __launch_bounds__(256) void k_rope_table(const DState *st, int HD, int mode, float base_g, float base_l,
+__global__ __launch_bounds__(256) void k_rope_table(const DState *st, int pos0, int HD, int mode, float base_g, float base_l,
                                                      const int64_t *fq_g, const int64_t *fq_l, float *out) {
-    const int half = HD / 2, pos = st->pos;
+    // decode: one workgroup at the step's position; batched: workgroup t at pos0 + t
+    const int half = HD / 2, pos = st ? st->pos : pos0 + (int)blockIdx.x;
+    out += (size_t)blockIdx.x * 2 * HD;
     for (int idx = threadIdx.x; idx < 2 * half; idx += blockDim.x) {
         const int t = idx / half, i = idx % half;
         float c, s;
@@ -181,10 +200,14 @@ __global__ __launch_bounds__(256) void k_rope_table(const DState *st, int HD, in
 }
 void launch_rope_table(const DState *st, int HD, int mode, float base_g, float base_l,
                        const int64_t *fq_g, const int64_t *fq_l, float *out, hipStream_t s) {
-    hipLaunchKernelGGL(k_rope_table, dim3(1), dim3(256), 0, s, st, HD, mode, base_g, base_l, fq_g, fq_l, out);
+    hipLaunchKernelGGL(k_rope_table, dim3(1), dim3(256), 0, s, st, 0, HD, mode, base_g, base_l, fq_g, fq_l, out);
+}
+void launch_rope_table_batch(int pos0, int T, int HD, int mode, float base_g, float base_l,
+                             const int64_t *fq_g, const int64_t *fq_l, float *out, hipStream_t s) {
+    hipLaunchKernelGGL(k_rope_table, dim3(T), dim3(256), 0, s, nullptr, pos0, HD, mode, base_g, base_l, fq_g, fq_l, out);
 }
 void launch_qk_prep(const AttnArgs &a, hipStream_t s) {
-    hipLaunchKernelGGL(k_qk_prep, dim3(a.NH + 2 * a.NKV), dim3(64), 0, s, a);
+    hipLaunchKernelGGL(k_qk_prep, dim3(a.NH + 2 * a.NKV, a.nt ? a.nt : 1), dim3(64), 0, s, a);
 }
 void set_rope_tables(const int64_t atan_q60[64], int64_t kinv_q62) {
     hipMemcpyToSymbol(HIP_SYMBOL(g_atan_q60), atan_q60, 64 * sizeof(int64_t));
@@ -226,10 +249,12 @@ constexpr int MAXNCH = 4096;     // chunks per kv-head (combine weight buffer)
 constexpr int UNR = 4;           // positions in flight per wave
 
 template <int EPL, int G>
-__global__ __launch_bounds__(256) void k_attn_float(AttnArgs a) {
+__global__ __launch_bounds__(256) void k_attn_float(AttnArgs a_in) {
+    AttnArgs a = a_in;
+    int pos;
+    tok_select(a, blockIdx.z, pos);
     const int HD = EPL * 64, c = blockIdx.x, h = blockIdx.y;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int pos = a.st->pos;
     int cs, ce, nch;
     chunk_range(a, pos, c, cs, ce, nch);
     if (c >= nch) return;
@@ -349,10 +374,12 @@ __global__ __launch_bounds__(256) void k_attn_float(AttnArgs a) {
 
 // ---- exact mode: pass 1, integer scores on the softmax grid + chunk max ----
 template <int EPL, int G>
-__global__ __launch_bounds__(256) void k_attn_exact_scores(AttnArgs a) {
+__global__ __launch_bounds__(256) void k_attn_exact_scores(AttnArgs a_in) {
+    AttnArgs a = a_in;
+    int pos;
+    tok_select(a, blockIdx.z, pos);
     const int HD = EPL * 64, c = blockIdx.x, h = blockIdx.y;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int pos = a.st->pos;
     int cs, ce, nch;
     chunk_range(a, pos, c, cs, ce, nch);
     if (c >= nch) return;
@@ -380,8 +407,8 @@ __global__ __launch_bounds__(256) void k_attn_exact_scores(AttnArgs a) {
                 for (int e = 0; e < EPL; e++) ip += (int64_t)qi[g][e] * kv[u][e];
                 ip = wsuml(ip);
                 const float scv = (float)((double)ip / 4294967296.0) * a.ascale;
-                const int32_t z = (int32_t)llround_d((double)scv * 16384.0);
-                if (lane == 0) a.zscratch[(size_t)(h * G + g) * a.max_chunks * 16 + (size_t)(cs + j0 + u)] = z;
+                const int32_t z = (int32_t)llround_pow2<14>(scv);
+                if (lane == 0) a.zscratch[(size_t)(h * G + g) * a.zstride + (size_t)(cs + j0 + u)] = z;
                 mx[g] = z > mx[g] ? z : mx[g];
             }
         }
@@ -398,10 +425,12 @@ __global__ __launch_bounds__(256) void k_attn_exact_scores(AttnArgs a) {
 
 // ---- exact mode: pass 2, exp weights on the island grid, exact V-sum ----
 template <int EPL, int G>
-__global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a) {
+__global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a_in) {
+    AttnArgs a = a_in;
+    int pos;
+    tok_select(a, blockIdx.z, pos);
     const int HD = EPL * 64, c = blockIdx.x, h = blockIdx.y;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int pos = a.st->pos;
     int cs, ce, nch;
     chunk_range(a, pos, c, cs, ce, nch);
     if (c >= nch) return;
@@ -434,7 +463,7 @@ __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a) {
     const int n = ce - cs;
     for (int i = threadIdx.x; i < G * n; i += 256) {
         const int g = i / n, j = i % n;
-        const int64_t z = a.zscratch[(size_t)(h * G + g) * a.max_chunks * 16 + (size_t)(cs + j)];
+        const int64_t z = a.zscratch[(size_t)(h * G + g) * a.zstride + (size_t)(cs + j)];
         ew[g][j] = exp_fixed(((z - (int64_t)M[g]) * ONE) >> 14) >> 8;
     }
     __syncthreads();
@@ -499,7 +528,7 @@ __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a) {
 }
 
 template <int EPL, int G> static void attn_dispatch(const AttnArgs &a, int grid_chunks, hipStream_t s) {
-    dim3 grid(grid_chunks, a.NKV);
+    dim3 grid(grid_chunks, a.NKV, a.nt ? a.nt : 1);
     if (a.mode == FLOAT) hipLaunchKernelGGL((k_attn_float<EPL, G>), grid, dim3(256), 0, s, a);
     else {
         hipLaunchKernelGGL((k_attn_exact_scores<EPL, G>), grid, dim3(256), 0, s, a);
@@ -522,8 +551,10 @@ void launch_attention(const AttnArgs &a, int grid_chunks, hipStream_t s) {
 }
 
 // ------------------------------------------------------------------ embedding
-__global__ __launch_bounds__(256) void k_embed(DevW w, const DState *st, const int *tokbuf, float *x, float scale) {
-    const int tok = st->drive == DRIVE_STREAM ? tokbuf[st->pos] : st->tok, E = w.cols;
+__global__ __launch_bounds__(256) void k_embed(DevW w, const DState *st, const int *tokbuf, int pos0, float *x, float scale) {
+    // decode: the step's token; batched: workgroup t embeds tokbuf[pos0 + t] into row t
+    const int tok = st ? (st->drive == DRIVE_STREAM ? tokbuf[st->pos] : st->tok) : tokbuf[pos0 + blockIdx.x], E = w.cols;
+    x += (size_t)blockIdx.x * E;
     const uint8_t *rc = w.codes + (size_t)tok * ((E + 1) / 2);
     const uint16_t *bs = w.bs + (size_t)tok * w.nblk;
     for (int i = threadIdx.x; i < E; i += blockDim.x) {
@@ -537,7 +568,10 @@ __global__ __launch_bounds__(256) void k_embed(DevW w, const DState *st, const i
     }
 }
 void launch_embed(const DevW &embd, const DState *st, const int *tokbuf, float *x, float scale, hipStream_t s) {
-    hipLaunchKernelGGL(k_embed, dim3(1), dim3(256), 0, s, embd, st, tokbuf, x, scale);
+    hipLaunchKernelGGL(k_embed, dim3(1), dim3(256), 0, s, embd, st, tokbuf, 0, x, scale);
+}
+void launch_embed_batch(const DevW &embd, const int *tokbuf, int pos0, int T, float *x, float scale, hipStream_t s) {
+    hipLaunchKernelGGL(k_embed, dim3(T), dim3(256), 0, s, embd, nullptr, tokbuf, pos0, x, scale);
 }
 __global__ void k_advance(DState *st) {
     if (threadIdx.x == 0 && st->drive == DRIVE_STREAM) st->pos = st->pos + 1;

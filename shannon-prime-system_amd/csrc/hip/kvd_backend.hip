@@ -315,6 +315,7 @@ struct sp_kvdecode_handle {
     DevModel *m = nullptr;
     std::shared_ptr<KvPool> pool;
     int mode = FLOAT, pmax = 0, dpos = 0, use_graph = 1, hwm = 0;
+    int use_batch = 1;                       // batched (MFMA) prefill where the shapes allow it
     int max_rewind = 0;                      // 0: full tables for window layers
     int full_pages = 0, ring_pages = 0;
     std::vector<std::vector<int>> pt;        // [NL][slots] page ids (-1 = unmapped)
@@ -338,6 +339,14 @@ struct sp_kvdecode_handle {
     float *h_logits = nullptr;               // pinned staging
     int max_chunks = 0;
     void *scratch = nullptr;
+    // batched prefill buffers ([TB][...] per token), allocated on first use
+    struct Batch {
+        void *buf = nullptr;
+        int TB = 0, mcb = 0;                 // tokens per batch, chunk capacity per q-head
+        float *x0, *x1, *q, *k, *v, *qr, *ao, *ap, *gg, *uu, *hh, *dn, *rope, *part, *part_ml;
+        int8_t *planes; int *sh, *counter, *zs;
+        int64_t *vacc, *vacc_s;
+    } b;
     // graph cache: key (logits?, argmax?, grid_global, grid_local, chunk_global)
     struct GKey { int lg, am, gg, gl, cg; bool operator<(const GKey &o) const {
         return std::tie(lg, am, gg, gl, cg) < std::tie(o.lg, o.am, o.gg, o.gl, o.cg); } };
@@ -508,6 +517,7 @@ void enqueue_body(sp_kvdecode_handle *h, const StepShape &sh, TimeCb cb, void *c
         a.NH = m->NH; a.NKV = m->NKV; a.HD = m->HD;
         a.win = (m->gemma && !glob) ? m->SW : -1;
         a.max_chunks = h->max_chunks; a.mode = h->mode; a.eps = m->eps;
+        a.zstride = h->max_chunks * 16; a.nt = 0;
         a.base = (m->gemma && !glob) ? 10000.0f : m->base;
         a.ascale = 1.0f / sqrtf((float)m->HD);
         a.chunk = glob ? sh.chunk_global : sh.chunk_local;
@@ -554,6 +564,128 @@ void enqueue_body(sp_kvdecode_handle *h, const StepShape &sh, TimeCb cb, void *c
     } else {
         launch_advance(h->d_st, s);
     }
+}
+
+// ------------------------------------------------------------ batched prefill
+// Tokens go through the model TB at a time: per layer one staging kernel per
+// GEMM input (one workgroup per token), the int8-MFMA GEMMs, and the decode
+// attention kernels with a token grid dimension.  Each token's K/V and every
+// intermediate are the same integers/floats a decode step computes.
+constexpr int PREFILL_TB = 128;
+
+bool batch_supported(const sp_kvdecode_handle *h) {
+    const DevModel *m = h->m;
+    const int G = m->NH / m->NKV;
+    const bool attn_ok = (m->HD == 64 || m->HD == 128 || m->HD == 256) && (G == 2 || G == 4);
+    if (!attn_ok || m->E % 256 || m->FF % 256 || (m->NH * m->HD) % 256) return false;
+    for (const DevLayer &d : m->L)
+        for (const DevW *w : {&d.q, &d.k, &d.v, &d.o, &d.gate, &d.up, &d.down})
+            if (!gemm_supported(*w)) return false;
+    return true;
+}
+
+int alloc_batch(sp_kvdecode_handle *h) {
+    if (h->b.buf) return 0;
+    const DevModel *m = h->m;
+    auto &b = h->b;
+    const size_t TB = PREFILL_TB, QD = (size_t)m->NH * m->HD, KVD = (size_t)m->NKV * m->HD;
+    const size_t E = m->E, FF = m->FF;
+    b.TB = PREFILL_TB;
+    b.mcb = h->pmax / 64 + 2;                // batched attention chunks hold >= 64 positions
+    const size_t nmax = std::max(std::max(E, QD), FF);
+    struct Item { void **p; size_t n; };
+    Item items[] = {
+        {(void **)&b.x0, TB * E * 4}, {(void **)&b.x1, TB * E * 4}, {(void **)&b.q, TB * QD * 4},
+        {(void **)&b.k, TB * KVD * 4}, {(void **)&b.v, TB * KVD * 4}, {(void **)&b.qr, TB * QD * 4},
+        {(void **)&b.ao, TB * QD * 4}, {(void **)&b.ap, TB * E * 4}, {(void **)&b.gg, TB * FF * 4},
+        {(void **)&b.uu, TB * FF * 4}, {(void **)&b.hh, TB * FF * 4}, {(void **)&b.dn, TB * E * 4},
+        {(void **)&b.rope, TB * 2 * m->HD * 4}, {(void **)&b.planes, 3 * (nmax / 32) * TB * 32},
+        {(void **)&b.sh, TB * 4}, {(void **)&b.counter, TB * m->NKV * 4},
+        {(void **)&b.zs, TB * m->NH * (size_t)h->max_chunks * 16 * 4},
+        {(void **)&b.part_ml, TB * m->NH * (size_t)b.mcb * 16},
+        {(void **)&b.part, h->mode == FLOAT ? TB * m->NH * (size_t)b.mcb * m->HD * 4 : 256},
+        {(void **)&b.vacc, TB * QD * 8}, {(void **)&b.vacc_s, TB * m->NH * 8},
+    };
+    size_t tot = 0;
+    for (auto &it : items) tot = align_up(tot + it.n, 256);
+    HIPCHK(hipMalloc(&b.buf, tot), "prefill batch alloc");
+    HIPCHK(hipMemset(b.buf, 0, tot), "prefill batch clear");
+    size_t off = 0;
+    for (auto &it : items) { *it.p = (uint8_t *)b.buf + off; off = align_up(off + it.n, 256); }
+    return 0;
+}
+
+// n tokens at positions pos0.. (tokbuf already holds them), no logits
+int prefill_batch(sp_kvdecode_handle *h, int pos0, int T) {
+    const DevModel *m = h->m;
+    auto &b = h->b;
+    hipStream_t s = h->stream;
+    const int QD = m->NH * m->HD, KVD = m->NKV * m->HD, TP = (T + 31) / 32 * 32;
+    launch_embed_batch(m->embd, h->tokbuf, pos0, T, b.x1, m->gemma ? sqrtf((float)m->E) : 0.0f, s);
+    launch_rope_table_batch(pos0, T, m->HD, h->mode, m->base, m->gemma ? 10000.0f : m->base,
+                            m->freq_global, m->gemma ? m->freq_local : m->freq_global, b.rope, s);
+    auto stage = [&](int kind, const float *x, const float *delta, const float *post_w, const float *norm_w,
+                     float *x_out, int n) {
+        StageArgs a{};
+        a.pro.kind = kind; a.pro.x = x; a.pro.delta = delta; a.pro.post_w = post_w; a.pro.norm_w = norm_w;
+        a.pro.x_out = x_out; a.pro.n = n; a.pro.eps = m->eps;
+        a.planes = b.planes; a.sh = b.sh; a.T = T; a.TP = TP; a.mode = h->mode;
+        launch_stage(a, s);
+    };
+    auto gemm = [&](int cols) {
+        GemmArgs g{};
+        g.cols = cols; g.planes = b.planes; g.sh = b.sh; g.T = T; g.TP = TP; g.mode = h->mode; g.act = ACT_NONE;
+        return g;
+    };
+    const int pos_hi = pos0 + T - 1;
+    for (int l = 0; l < m->NL; l++) {
+        const DevLayer &d = m->L[l];
+        const bool glob = is_global(m, l);
+        if (l == 0) stage(PRO_NORM, b.x1, nullptr, nullptr, d.attn_norm, nullptr, m->E);
+        else stage(PRO_RESID, b.x0, b.dn, m->gemma ? m->L[l - 1].post_ffw : nullptr, d.attn_norm, b.x1, m->E);
+        GemmArgs g = gemm(m->E);
+        g.nseg = 3; g.seg[0] = {d.q, b.q}; g.seg[1] = {d.k, b.k}; g.seg[2] = {d.v, b.v};
+        launch_gemm(g, QD + 2 * KVD, s);
+
+        AttnArgs a{};
+        a.q = b.q; a.k = b.k; a.v = b.v; a.q_norm = d.q_norm; a.k_norm = d.k_norm; a.qr = b.qr;
+        a.pages = h->d_pt + h->pt_off[l];
+        a.ring_pages = h->slots[l] == h->full_pages ? 0 : h->slots[l];
+        a.ao = b.ao; a.part = b.part; a.part_ml = b.part_ml; a.counter = b.counter; a.zscratch = b.zs;
+        a.vacc = b.vacc; a.vacc_s = b.vacc_s;
+        a.st = nullptr; a.rope_cs = b.rope + ((m->gemma && !glob) ? m->HD : 0);
+        a.NH = m->NH; a.NKV = m->NKV; a.HD = m->HD;
+        a.win = (m->gemma && !glob) ? m->SW : -1;
+        a.max_chunks = b.mcb; a.zstride = h->max_chunks * 16; a.mode = h->mode; a.eps = m->eps;
+        a.base = (m->gemma && !glob) ? 10000.0f : m->base;
+        a.ascale = 1.0f / sqrtf((float)m->HD);
+        a.nt = T; a.pos0 = pos0; a.rope_stride = 2 * m->HD;
+        a.chunk = (glob || a.win < 0) ? 256 : 64;
+        launch_qk_prep(a, s);
+        // chunks of the batch's longest span: a window of W positions covers at
+        // most (W-1)/chunk + 2 chunks whatever its alignment
+        int nch = pos_hi / a.chunk + 1;
+        if (a.win >= 0) nch = std::min(nch, (a.win - 1) / a.chunk + 2);
+        launch_attention(a, nch, s);
+
+        stage(PRO_PLAIN, b.ao, nullptr, nullptr, nullptr, nullptr, QD);
+        GemmArgs o = gemm(QD);
+        o.nseg = 1; o.seg[0] = {d.o, b.ap};
+        launch_gemm(o, m->E, s);
+
+        stage(PRO_RESID, b.x1, b.ap, d.post_attn, d.ffn_norm, b.x0, m->E);
+        GemmArgs f = gemm(m->E);
+        f.nseg = 2; f.act = m->gemma ? ACT_GELU : ACT_SILU;
+        f.seg[0] = {d.gate, b.gg}; f.seg[1] = {d.up, b.uu}; f.act_out = b.hh;
+        launch_gemm(f, m->FF, s);
+
+        stage(PRO_PLAIN, b.hh, nullptr, nullptr, nullptr, nullptr, m->FF);
+        GemmArgs dd = gemm(m->FF);
+        dd.nseg = 1; dd.seg[0] = {d.down, b.dn};
+        launch_gemm(dd, m->E, s);
+    }
+    HIPCHK(hipGetLastError(), "prefill batch launch");
+    return 0;
 }
 
 int run_body(sp_kvdecode_handle *h, const StepShape &sh) {
@@ -647,6 +779,7 @@ void sp_hipkv_close(sp_kvdecode_handle *h) {
     if (h->d_pt) hipFree(h->d_pt);
     if (h->h_pt) hipHostFree(h->h_pt);
     if (h->scratch) hipFree(h->scratch);
+    if (h->b.buf) hipFree(h->b.buf);
     if (h->h_st) hipHostFree(h->h_st);
     if (h->h_logits) hipHostFree(h->h_logits);
     if (h->stream) hipStreamDestroy(h->stream);
@@ -678,10 +811,22 @@ int sp_hipkv_prefill(sp_kvdecode_handle *h, const int32_t *tokens, int n_tok) {
     if (ensure_pages(h, h->dpos, h->dpos + n_tok)) return 1;
     HIPCHK(hipStreamSynchronize(h->stream), "prefill staging");
     HIPCHK(hipMemcpy(h->tokbuf + h->dpos, tokens, (size_t)n_tok * 4, hipMemcpyHostToDevice), "prefill tokens");
-    if (set_state(h, h->dpos, 0, DRIVE_STREAM)) return 1;
-    for (int i = 0; i < n_tok; i++) {
-        StepShape sh = shape_for(h, h->dpos + i, 0, 0);
-        if (run_body(h, sh)) return 1;
+    if (h->use_batch && batch_supported(h)) {
+        if (alloc_batch(h)) return 1;
+        // window layers on a ring: writing position q reuses the page slot of
+        // the page ring_pages back, i.e. drops positions up to q - ring*PAGE + PAGE-1;
+        // a batch must not drop positions its first token still attends to
+        int tb = h->b.TB;
+        if (h->ring_pages > 0) tb = std::min(tb, h->ring_pages * PAGE - h->m->SW - (PAGE - 1));
+        if (tb < 1) tb = 1;
+        for (int i = 0; i < n_tok; i += tb)
+            if (prefill_batch(h, h->dpos + i, std::min(tb, n_tok - i))) return 1;
+    } else {
+        if (set_state(h, h->dpos, 0, DRIVE_STREAM)) return 1;
+        for (int i = 0; i < n_tok; i++) {
+            StepShape sh = shape_for(h, h->dpos + i, 0, 0);
+            if (run_body(h, sh)) return 1;
+        }
     }
     HIPCHK(hipStreamSynchronize(h->stream), "prefill");
     h->dpos += n_tok;
@@ -709,6 +854,7 @@ int sp_hipkv_set_mode(sp_kvdecode_handle *h, int exact) {
     if (m == EXACT && h->pmax > (1 << 18)) return fail("sp_hipkv_set_mode: exact mode holds at most %s%lld positions", "", (long long)(1 << 18));
     h->mode = m;
     free_graphs(h);
+    if (h->b.buf) { hipStreamSynchronize(h->stream); hipFree(h->b.buf); h->b = sp_kvdecode_handle::Batch{}; }
     return 0;
 }
 
@@ -728,6 +874,12 @@ int sp_hipkv_set_graph(sp_kvdecode_handle *h, int on) {
     return 0;
 }
 
+int sp_hipkv_set_batch_prefill(sp_kvdecode_handle *h, int on) {
+    if (!h) return fail("sp_hipkv_set_batch_prefill: null handle%s");
+    h->use_batch = on ? 1 : 0;
+    return 0;
+}
+
 int sp_hipkv_fork(const sp_kvdecode_handle *p, sp_kvdecode_handle **out) {
     if (!p || !out) return fail("sp_hipkv_fork: null argument%s");
     *out = nullptr;
@@ -737,6 +889,7 @@ int sp_hipkv_fork(const sp_kvdecode_handle *p, sp_kvdecode_handle **out) {
         h->m = p->m; h->m->refs++;
     }
     h->pool = p->pool; h->mode = p->mode; h->pmax = p->pmax; h->dpos = p->dpos; h->hwm = p->hwm;
+    h->use_batch = p->use_batch; h->use_graph = p->use_graph;
     h->use_graph = p->use_graph; h->max_rewind = p->max_rewind;
     if (hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking) != hipSuccess) {
         std::lock_guard<std::mutex> lk(g_mu); model_put(h->m); return fail("sp_hipkv_fork: stream creation failed%s");

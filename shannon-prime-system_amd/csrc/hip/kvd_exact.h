@@ -80,9 +80,17 @@ __device__ __forceinline__ int64_t tanh_fixed(int64_t t) {
 }
 // round half away from zero of a double to int64 (llround)
 __device__ __forceinline__ int64_t llround_d(double d) { return (int64_t)round(d); }
+// llround(x * 2^SH) of a float: x * 2^SH is exact in float short of overflow,
+// roundf is exact, and results below 2^31 convert in 32 bits; anything else
+// takes the double route.  The same value either way.
+template <int SH> __device__ __forceinline__ int64_t llround_pow2(float x) {
+    const float r = roundf(x * (float)(1 << SH));
+    if (fabsf(r) < 2147483648.0f) return (int64_t)(int32_t)r;
+    return llround_d((double)x * (double)(1 << SH));
+}
 
 __device__ __forceinline__ float gelu_exact1(float x) {
-    int64_t xq = llround_d((double)x * 65536.0);
+    int64_t xq = llround_pow2<16>(x);
     int64_t X = (xq * ONE) >> 16;
     i128 X2 = ((i128)X * X) >> FB;
     int64_t x3 = (int64_t)((X2 * X) >> FB);
@@ -92,7 +100,7 @@ __device__ __forceinline__ float gelu_exact1(float x) {
     return (float)((double)g / (double)ONE);
 }
 __device__ __forceinline__ float silu_exact1(float x) {
-    int64_t xq = llround_d((double)x * 65536.0);
+    int64_t xq = llround_pow2<16>(x);
     int64_t X = (xq * ONE) >> 16;
     int64_t e = exp_fixed(X >= 0 ? -X : X);
     int64_t sg = X >= 0 ? (int64_t)(((i128)ONE << FB) / (ONE + e))

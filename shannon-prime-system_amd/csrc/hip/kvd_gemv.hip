@@ -22,137 +22,47 @@
 // and one 16 B LDS read per digit plane, shared by the wave's rows.
 #include "kvd_internal.h"
 #include "kvd_exact.h"
+#include "kvd_vec.h"
 #include <cstdio>
 #include <cstdlib>
 
 namespace kvd {
 
-// ---------------------------------------------------------------- reductions
-template <typename T> __device__ __forceinline__ T wave_sum(T v) {
-    #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
-__device__ __forceinline__ float wave_max(float v) {
-    #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
-}
-__device__ __forceinline__ i128 wave_sum128(i128 v) {
-    #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        uint64_t lo = (uint64_t)v, hi = (uint64_t)((u128)v >> 64);
-        uint64_t lo2 = __shfl_xor(lo, o, 64), hi2 = __shfl_xor(hi, o, 64);
-        v += (i128)(((u128)hi2 << 64) | lo2);
-    }
-    return v;
-}
-// block-wide reductions for 256 threads through a small LDS scratch
-template <typename T> __device__ T block_sum(T v, T *red) {   // red: blockDim/64 slots
-    v = wave_sum(v);
-    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
-    __syncthreads();
-    if (l == 0) red[w] = v;
-    __syncthreads();
-    T t = red[0];
-    for (int i = 1; i < (int)(blockDim.x >> 6); i++) t += red[i];
-    return t;
-}
-__device__ float block_max(float v, float *red) {
-    v = wave_max(v);
-    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
-    __syncthreads();
-    if (l == 0) red[w] = v;
-    __syncthreads();
-    float t = red[0];
-    for (int i = 1; i < (int)(blockDim.x >> 6); i++) t = fmaxf(t, red[i]);
-    return t;
-}
-
-// ------------------------------------------------------- RMSNorm (both modes)
-// Float mode: core/forward_kernels/forward_kernels.c:17-22 (sum of squares in
-// double, 1/sqrtf((float)(ss/n)+eps), out = x*scale*w).  Exact mode: the
-// integer island core/exact_islands/exact_islands.c:60-79 (no eps).
-struct NormScale { float f; int64_t inv; int zero; };
-
-__device__ NormScale norm_scale(const float *v, int n, float eps, int mode, void *red) {
-    NormScale s; s.f = 0.0f; s.inv = 0; s.zero = 0;
-    if (mode == FLOAT) {
-        double ss = 0.0;
-        for (int i = threadIdx.x; i < n; i += blockDim.x) ss += (double)v[i] * (double)v[i];
-        ss = block_sum<double>(ss, (double *)red);
-        s.f = 1.0f / sqrtf((float)(ss / n) + eps);
-    } else {
-        int64_t ss = 0;
-        for (int i = threadIdx.x; i < n; i += blockDim.x) {
-            int64_t xi = llround_d((double)v[i] * 65536.0);
-            ss += xi * xi;
-        }
-        ss = block_sum<int64_t>(ss, (int64_t *)red);
-        if (ss == 0) { s.zero = 1; return s; }
-        const uint64_t q = udiv128_64((u128)n << 72, (uint64_t)ss);
-        s.inv = (int64_t)isqrt_u64(q);
-    }
-    return s;
-}
-__device__ __forceinline__ float norm_apply(float x, float w, const NormScale &s, int mode) {
-    if (mode == FLOAT) return x * s.f * w;
-    if (s.zero) return 0.0f;
-    const int64_t xi = llround_d((double)x * 65536.0), wi = llround_d((double)w * 65536.0);
-    return (float)((double)mul3_lo64(xi, s.inv, wi) / 4503599627370496.0);   // 2^52
-}
-
 // ------------------------------------------------------- prologue
-// Builds the GEMV input (float, in xf), its grid exponent sh from the whole
-// vector, and the digit planes of the workgroup's column split [b_lo, b_hi)
-// blocks (in dig, indexed from b_lo).  Returns SH_ZERO for an all-zero input.
-constexpr int SH_ZERO = -1000000;
+// Builds the GEMV input (input_transform) and the digit planes of the
+// workgroup's column split [b_lo, b_hi) blocks (in dig, indexed from b_lo).
+// Returns sh, or SH_ZERO for an all-zero input.
+// xq = rne(x * 2^sh) as six balanced base-16 digits, 8 columns per dword and
+// plane.  u = xq + 0x888888 has the digits + 8 as its plain nibbles (|xq| <=
+// 2^22 keeps 0 <= u < 16^6), so digit & 15 = nibble ^ 8.  x * 2^sh is exact in
+// float for every result that can round to a non-zero integer.
+__device__ __forceinline__ void digits8(const float v[8], int sh, uint32_t dw[NDIG]) {
+    #pragma unroll
+    for (int k = 0; k < NDIG; k++) dw[k] = 0;
+    #pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const uint32_t u = (uint32_t)((int32_t)rintf(ldexpf(v[j], sh)) + 0x888888);
+        #pragma unroll
+        for (int k = 0; k < NDIG; k++) dw[k] |= ((u >> (4 * k)) & 15u) << (4 * j);
+    }
+    #pragma unroll
+    for (int k = 0; k < NDIG; k++) dw[k] ^= 0x88888888u;
+}
 
 template <int PRO>
 __device__ int gemv_prologue(const ProArgs &p, int mode, float *xf, uint4 *dig, int b_lo, int b_hi, void *red) {
-    const int n = p.n;
-    // PRO_PLAIN reads its input straight from global memory (two passes: max,
-    // then digits); the norm prologues stage the transformed vector in xf.
-    if constexpr (PRO == PRO_NORM) {
-        NormScale s = norm_scale(p.x, n, p.eps, mode, red);
-        for (int i = threadIdx.x; i < n; i += blockDim.x) xf[i] = norm_apply(p.x[i], p.norm_w[i], s, mode);
-    } else if constexpr (PRO == PRO_RESID) {
-        if (p.post_w) {
-            NormScale sd = norm_scale(p.delta, n, p.eps, mode, red);
-            for (int i = threadIdx.x; i < n; i += blockDim.x)
-                xf[i] = p.x[i] + norm_apply(p.delta[i], p.post_w[i], sd, mode);
-        } else {
-            for (int i = threadIdx.x; i < n; i += blockDim.x) xf[i] = p.x[i] + p.delta[i];
-        }
-        __syncthreads();
-        if (blockIdx.x == 0 && p.x_out)
-            for (int i = threadIdx.x; i < n; i += blockDim.x) p.x_out[i] = xf[i];
-        NormScale s = norm_scale(xf, n, p.eps, mode, red);
-        __syncthreads();
-        for (int i = threadIdx.x; i < n; i += blockDim.x) xf[i] = norm_apply(xf[i], p.norm_w[i], s, mode);
-    }
+    const int T = blockDim.x, tid = threadIdx.x;
+    const int sh = input_transform<PRO>(p, mode, xf, red, blockIdx.x == 0);
+    if (sh == SH_ZERO) return SH_ZERO;
+    // digits: one thread per 8 consecutive columns (one nibble-dword per plane);
+    // the column count is a multiple of 32, so a group never runs past n
     const float *src = PRO == PRO_PLAIN ? p.x : xf;
-    float m = 0.0f;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) m = fmaxf(m, fabsf(src[i]));
-    m = block_max(m, (float *)red);                      // also orders the xf writes above
-    if (m == 0.0f) return SH_ZERO;
-    int e; frexpf(m, &e);
-    const int sh = 22 - e;
-    // digits: one thread per 8 consecutive columns (one nibble-dword per plane)
     const int g_lo = b_lo * 4, g_hi = b_hi * 4, nb = b_hi - b_lo;
-    for (int g = g_lo + threadIdx.x; g < g_hi; g += blockDim.x) {
-        uint32_t dw[NDIG] = {0, 0, 0, 0, 0, 0};
-        #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const int c = g * 8 + j;
-            int32_t v = c < n ? (int32_t)rint(ldexp((double)src[c], sh)) : 0;
-            #pragma unroll
-            for (int k = 0; k < NDIG; k++) {
-                int32_t d = ((v + 8) & 15) - 8;
-                v = (v - d) >> 4;
-                dw[k] |= (uint32_t)(d & 15) << (4 * j);
-            }
-        }
+    for (int g = g_lo + tid; g < g_hi; g += T) {
+        const float4 v0 = *(const float4 *)(src + g * 8), v1 = *(const float4 *)(src + g * 8 + 4);
+        const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+        uint32_t dw[NDIG];
+        digits8(v, sh, dw);
         const int b = (g >> 2) - b_lo, q = g & 3;
         #pragma unroll
         for (int k = 0; k < NDIG; k++) ((uint32_t *)&dig[k * nb + b])[q] = dw[k];
@@ -162,12 +72,6 @@ __device__ int gemv_prologue(const ProArgs &p, int mode, float *xf, uint4 *dig, 
 }
 
 // ------------------------------------------------------- main kernel
-__device__ __forceinline__ void f16_parts(uint32_t h, int32_t &M, int &e) {
-    const int E5 = (h >> 10) & 31, mant = h & 1023;
-    M = E5 ? 1024 + mant : mant;
-    if (h & 0x8000u) M = -M;
-    e = E5 ? E5 - 25 : -24;
-}
 __device__ __forceinline__ int32_t dot_digits(const uint4 c, const uint4 *D) {
     // sum over the 32 codes of code * xq, xq = sum_k 16^k digit_k
     int32_t a = 0;
@@ -181,16 +85,6 @@ __device__ __forceinline__ int32_t dot_digits(const uint4 c, const uint4 *D) {
         a = a * 16 + t;
     }
     return a;
-}
-
-__device__ __forceinline__ float act_apply(float g, float u, int act, int mode) {
-    if (act == ACT_GELU) {
-        if (mode == EXACT) return gelu_exact1(g) * u;
-        const float k = 0.7978845608028654f;                       // sp_session.c:365-368
-        return 0.5f * g * (1.0f + tanhf(k * (g + 0.044715f * g * g * g))) * u;
-    }
-    if (mode == EXACT) return silu_exact1(g) * u;
-    return g / (1.0f + expf(-g)) * u;                              // sp_session.c:354
 }
 
 // Sum GEMV_R = 8 per-lane int64 partials over the wave with 10 exchanges

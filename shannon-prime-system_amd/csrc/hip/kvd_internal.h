@@ -84,6 +84,32 @@ struct AttnArgs {
     const float *rope_cs;    // this step's rotation table for the layer's base: cos[HD/2], sin[HD/2]
     int NH, NKV, HD, win, max_chunks, chunk, mode;
     float eps, base, ascale;
+    int zstride;             // positions per q-head row of zscratch (>= pmax)
+    // batched prefill: nt tokens at positions pos0.. (token = blockIdx.y of
+    // qk_prep, blockIdx.z of attention); every per-token buffer is [nt][...]
+    int nt, pos0, rope_stride;
+};
+
+// Per-token GEMM input staging (batched prefill): the GEMV input transform of
+// token t's vector (pro pointers + t * n), then xq's three balanced base-256
+// digit planes in the GEMM's operand layout, planes[p][b][t][32], t < TP.
+struct StageArgs {
+    ProArgs pro;
+    int8_t *planes;
+    int *sh;           // [TP] grid exponent per token (SH_ZERO: all-zero input)
+    int T, TP, mode;   // tokens, padded token count (multiple of 32)
+};
+// OK_Q4B GEMM over T staged tokens: seg[i].out is [T][seg rows]; paired
+// gate/up write gate, up and act(gate)*up ([T][rows]).
+struct GemmArgs {
+    Seg  seg[3];
+    int  nseg, cols;
+    const int8_t *planes;
+    const int *sh;
+    int  T, TP;
+    int  act;
+    float *act_out;
+    int  mode;
 };
 
 // Hand-off between workgroups of one launch without cache-wide fences: all data
@@ -112,6 +138,12 @@ __device__ __forceinline__ void reset_counter(int *counter) {
 
 // launchers (kvd_kernels.hip)
 void launch_embed(const DevW &embd, const DState *st, const int *tokbuf, float *x, float scale, hipStream_t s);
+void launch_embed_batch(const DevW &embd, const int *tokbuf, int pos0, int T, float *x, float scale, hipStream_t s);
+void launch_rope_table_batch(int pos0, int T, int HD, int mode, float base_g, float base_l,
+                             const int64_t *fq_g, const int64_t *fq_l, float *out, hipStream_t s);
+void launch_stage(const StageArgs &a, hipStream_t s);
+void launch_gemm(const GemmArgs &a, int nrows_total, hipStream_t s);
+bool gemm_supported(const DevW &w);
 void launch_advance(DState *st, hipStream_t s);
 void launch_gemv(const GemvArgs &a, int nrows_total, hipStream_t s);
 void launch_qk_prep(const AttnArgs &a, hipStream_t s);

@@ -1,0 +1,233 @@
+// kvd_vec.h -- per-vector device building blocks shared by the GEMV and the
+// batched prefill kernels: block reductions, RMSNorm (float and exact island),
+// the GEMV input transform, f16 scale parts, FFN activations.
+#pragma once
+#include "kvd_internal.h"
+#include "kvd_exact.h"
+
+namespace kvd {
+
+// ---------------------------------------------------------------- reductions
+template <typename T> __device__ __forceinline__ T wave_sum(T v) {
+    #pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+    #pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+__device__ __forceinline__ i128 wave_sum128(i128 v) {
+    #pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        uint64_t lo = (uint64_t)v, hi = (uint64_t)((u128)v >> 64);
+        uint64_t lo2 = __shfl_xor(lo, o, 64), hi2 = __shfl_xor(hi, o, 64);
+        v += (i128)(((u128)hi2 << 64) | lo2);
+    }
+    return v;
+}
+// block-wide reductions for 256 threads through a small LDS scratch
+template <typename T> __device__ T block_sum(T v, T *red) {   // red: blockDim/64 slots
+    v = wave_sum(v);
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+    __syncthreads();
+    if (l == 0) red[w] = v;
+    __syncthreads();
+    T t = red[0];
+    for (int i = 1; i < (int)(blockDim.x >> 6); i++) t += red[i];
+    return t;
+}
+__device__ float block_max(float v, float *red) {
+    v = wave_max(v);
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+    __syncthreads();
+    if (l == 0) red[w] = v;
+    __syncthreads();
+    float t = red[0];
+    for (int i = 1; i < (int)(blockDim.x >> 6); i++) t = fmaxf(t, red[i]);
+    return t;
+}
+
+// ------------------------------------------------------- RMSNorm (both modes)
+// Float mode: core/forward_kernels/forward_kernels.c:17-22 (sum of squares in
+// double, 1/sqrtf((float)(ss/n)+eps), out = x*scale*w).  Exact mode: the
+// integer island core/exact_islands/exact_islands.c:60-79 (no eps).
+struct NormScale { float f; int64_t inv; int zero; };
+
+// One thread's share of a sum of squares: double in float mode, the exact
+// int64 sum of the Q16 values in exact mode.
+__device__ __forceinline__ int64_t llround_q16(float x) { return llround_pow2<16>(x); }
+struct SumSq {
+    double f = 0.0; int64_t i = 0;
+    __device__ __forceinline__ void add(float v, int mode) {
+        if (mode == FLOAT) f += (double)v * (double)v;
+        else { const int64_t q = llround_q16(v); i += q * q; }
+    }
+};
+__device__ NormScale norm_finish(const SumSq &p, int n, float eps, int mode, void *red) {
+    NormScale s; s.f = 0.0f; s.inv = 0; s.zero = 0;
+    if (mode == FLOAT) {
+        const double ss = block_sum<double>(p.f, (double *)red);
+        s.f = 1.0f / sqrtf((float)(ss / n) + eps);
+    } else {
+        const int64_t ss = block_sum<int64_t>(p.i, (int64_t *)red);
+        if (ss == 0) { s.zero = 1; return s; }
+        const uint64_t q = udiv128_64((u128)n << 72, (uint64_t)ss);
+        s.inv = (int64_t)isqrt_u64(q);
+    }
+    return s;
+}
+__device__ __forceinline__ float norm_apply(float x, float w, const NormScale &s, int mode) {
+    if (mode == FLOAT) return x * s.f * w;
+    if (s.zero) return 0.0f;
+    const int64_t xi = llround_q16(x), wi = llround_q16(w);
+    return (float)((double)mul3_lo64(xi, s.inv, wi) / 4503599627370496.0);   // 2^52
+}
+
+// ------------------------------------------------------- input transform
+// Latency matters more than work here (every GEMV workgroup runs it before its
+// matrix pass), so every pass over the vector issues PB loads per thread
+// before using any of them, and independent passes are fused: the residual
+// pass also sums the squares for the next norm, the last norm pass also takes
+// the maximum.
+constexpr int SH_ZERO = -1000000;
+constexpr int PB = 8;
+
+// The GEMV input transform of one vector by one workgroup: residual add (+
+// sandwich norm of the branch), RMSNorm, and the grid exponent
+// sh = 22 - frexp_exponent(max |x|) of the result (SH_ZERO for an all-zero
+// vector).  The result is left in xf (LDS, n floats), or read from p.x for
+// PRO_PLAIN.  x_out (the updated residual) is written when write_x is set.
+template <int PRO>
+__device__ int input_transform(const ProArgs &p, int mode, float *xf, void *red, bool write_x) {
+    const int n = p.n, T = blockDim.x, tid = threadIdx.x;
+    float m = 0.0f;
+    if constexpr (PRO == PRO_PLAIN) {
+        for (int base = 0; base < n; base += PB * T) {
+            float a[PB];
+            #pragma unroll
+            for (int k = 0; k < PB; k++) { const int i = base + k * T + tid; a[k] = i < n ? p.x[i] : 0.0f; }
+            #pragma unroll
+            for (int k = 0; k < PB; k++) m = fmaxf(m, fabsf(a[k]));
+        }
+    } else if (n <= PB * T) {
+        // whole vector in registers: one round of loads, then only reductions
+        float xv[PB], dv[PB], pw[PB], nw[PB];
+        #pragma unroll
+        for (int k = 0; k < PB; k++) {
+            const int i = k * T + tid;
+            const bool ok = i < n;
+            xv[k] = ok ? p.x[i] : 0.0f;
+            nw[k] = ok ? p.norm_w[i] : 0.0f;
+            dv[k] = (PRO == PRO_RESID && ok) ? p.delta[i] : 0.0f;
+            pw[k] = (PRO == PRO_RESID && ok && p.post_w) ? p.post_w[i] : 0.0f;
+        }
+        if constexpr (PRO == PRO_RESID) {
+            NormScale sd; sd.f = 0.0f; sd.inv = 0; sd.zero = 0;
+            if (p.post_w) {
+                SumSq q;
+                #pragma unroll
+                for (int k = 0; k < PB; k++) if (k * T + tid < n) q.add(dv[k], mode);
+                sd = norm_finish(q, n, p.eps, mode, red);
+            }
+            const bool wr = write_x && p.x_out;
+            #pragma unroll
+            for (int k = 0; k < PB; k++) {
+                const int i = k * T + tid;
+                xv[k] = xv[k] + (p.post_w ? norm_apply(dv[k], pw[k], sd, mode) : dv[k]);
+                if (wr && i < n) p.x_out[i] = xv[k];
+            }
+        }
+        SumSq q;
+        #pragma unroll
+        for (int k = 0; k < PB; k++) if (k * T + tid < n) q.add(xv[k], mode);
+        const NormScale s = norm_finish(q, n, p.eps, mode, red);
+        #pragma unroll
+        for (int k = 0; k < PB; k++) {
+            const int i = k * T + tid;
+            if (i < n) { const float y = norm_apply(xv[k], nw[k], s, mode); xf[i] = y; m = fmaxf(m, fabsf(y)); }
+        }
+    } else {
+        NormScale s;
+        if constexpr (PRO == PRO_NORM) {
+            SumSq q;
+            for (int base = 0; base < n; base += PB * T) {
+                float a[PB];
+                #pragma unroll
+                for (int k = 0; k < PB; k++) { const int i = base + k * T + tid; a[k] = i < n ? p.x[i] : 0.0f; }
+                #pragma unroll
+                for (int k = 0; k < PB; k++) q.add(a[k], mode);
+                #pragma unroll
+                for (int k = 0; k < PB; k++) { const int i = base + k * T + tid; if (i < n) xf[i] = a[k]; }
+            }
+            s = norm_finish(q, n, p.eps, mode, red);
+        } else {
+            NormScale sd; sd.f = 0.0f; sd.inv = 0; sd.zero = 0;
+            if (p.post_w) {
+                SumSq q;
+                for (int base = 0; base < n; base += PB * T) {
+                    float a[PB];
+                    #pragma unroll
+                    for (int k = 0; k < PB; k++) { const int i = base + k * T + tid; a[k] = i < n ? p.delta[i] : 0.0f; }
+                    #pragma unroll
+                    for (int k = 0; k < PB; k++) q.add(a[k], mode);
+                }
+                sd = norm_finish(q, n, p.eps, mode, red);
+            }
+            // residual add (+ sandwich norm of the branch), sum of squares of the result
+            SumSq q;
+            const bool wr = write_x && p.x_out;
+            for (int base = 0; base < n; base += PB * T) {
+                float xv[PB], dv[PB], pw[PB];
+                #pragma unroll
+                for (int k = 0; k < PB; k++) {
+                    const int i = base + k * T + tid;
+                    xv[k] = i < n ? p.x[i] : 0.0f;
+                    dv[k] = i < n ? p.delta[i] : 0.0f;
+                    pw[k] = (i < n && p.post_w) ? p.post_w[i] : 0.0f;
+                }
+                #pragma unroll
+                for (int k = 0; k < PB; k++) {
+                    const int i = base + k * T + tid;
+                    const float r = xv[k] + (p.post_w ? norm_apply(dv[k], pw[k], sd, mode) : dv[k]);
+                    if (i < n) { xf[i] = r; if (wr) p.x_out[i] = r; q.add(r, mode); }
+                }
+            }
+            s = norm_finish(q, n, p.eps, mode, red);
+        }
+        // xf <- norm(xf) * w; running max
+        for (int base = 0; base < n; base += PB * T) {
+            float w[PB];
+            #pragma unroll
+            for (int k = 0; k < PB; k++) { const int i = base + k * T + tid; w[k] = i < n ? p.norm_w[i] : 0.0f; }
+            #pragma unroll
+            for (int k = 0; k < PB; k++) {
+                const int i = base + k * T + tid;
+                if (i < n) { const float y = norm_apply(xf[i], w[k], s, mode); xf[i] = y; m = fmaxf(m, fabsf(y)); }
+            }
+        }
+    }
+    m = block_max(m, (float *)red);                      // also orders the xf writes above
+    if (m == 0.0f) return SH_ZERO;
+    int e; frexpf(m, &e);
+    return 22 - e;
+}
+
+__device__ __forceinline__ void f16_parts(uint32_t h, int32_t &M, int &e) {
+    const int E5 = (h >> 10) & 31, mant = h & 1023;
+    M = E5 ? 1024 + mant : mant;
+    if (h & 0x8000u) M = -M;
+    e = E5 ? E5 - 25 : -24;
+}
+__device__ __forceinline__ float act_apply(float g, float u, int act, int mode) {
+    if (act == ACT_GELU) {
+        if (mode == EXACT) return gelu_exact1(g) * u;
+        const float k = 0.7978845608028654f;                       // sp_session.c:365-368
+        return 0.5f * g * (1.0f + tanhf(k * (g + 0.044715f * g * g * g))) * u;
+    }
+    if (mode == EXACT) return silu_exact1(g) * u;
+    return g / (1.0f + expf(-g)) * u;                              // sp_session.c:354
+}
+
+}  // namespace kvd

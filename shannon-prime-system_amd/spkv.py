@@ -109,6 +109,7 @@ def kv():
         _sig(lib, "sp_hipkv_set_mode", c_int, [c_void_p, c_int])
         _sig(lib, "sp_hipkv_set_max_rewind", c_int, [c_void_p, c_int])
         _sig(lib, "sp_hipkv_set_graph", c_int, [c_void_p, c_int])
+        _sig(lib, "sp_hipkv_set_batch_prefill", c_int, [c_void_p, c_int])
         _sig(lib, "sp_hipkv_fork", c_int, [c_void_p, ctypes.POINTER(c_void_p)])
         _sig(lib, "sp_hipkv_attach", c_int, [c_void_p, c_int, c_int])
         _sig(lib, "sp_hipkv_greedy", c_int, [c_void_p, c_int32, c_int, c_void_p, ctypes.POINTER(c_double)])
@@ -225,7 +226,7 @@ class Session:
 class Backend:
     """A bare section-6b handle driven through the dispatch functions directly."""
 
-    def __init__(self, qm, pmax, exact=False, graph=True):
+    def __init__(self, qm, pmax, exact=False, graph=True, batch_prefill=True):
         h = c_void_p()
         check(kv().sp_hipkv_open(qm, pmax, ctypes.byref(h)), "sp_hipkv_open")
         self.h = h
@@ -233,6 +234,8 @@ class Backend:
             check(kv().sp_hipkv_set_mode(h, 1), "sp_hipkv_set_mode")
         if not graph:
             check(kv().sp_hipkv_set_graph(h, 0), "sp_hipkv_set_graph")
+        if not batch_prefill:
+            check(kv().sp_hipkv_set_batch_prefill(h, 0), "sp_hipkv_set_batch_prefill")
 
     @classmethod
     def wrap(cls, h):

@@ -107,6 +107,45 @@ def test_plain_launches_and_direct_table(tmpdir_models, exact):
     be.close(); close_all(s, o, m)
 
 
+@pytest.mark.parametrize("exact", [True, False])
+def test_batched_prefill_matches_stepwise(tmpdir_models, exact):
+    """Prefill through the batched path (int8-MFMA GEMMs, token-batched attention,
+    3 batches of up to 128 tokens, window and global layers, split GEMV columns)
+    leaves the K/V that one decode step per token leaves, and the same logits
+    for the next position (exact: bit for bit)."""
+    spm, spt = model_files(tmpdir_models, "gemma3-wide")
+    m = spkv.Model(spm, spt); s = spkv.Session(m, 512)
+    qm = spkv.l1().sp_session_qwen3_model(s.h)
+    V = 3000
+    pr = prompt(300, V, seed=7)
+    lg1, lg2 = np.zeros(V, np.float32), np.zeros(V, np.float32)
+    b1 = spkv.Backend(qm, 512, exact=exact)
+    b2 = spkv.Backend(qm, 512, exact=exact, batch_prefill=False)
+    b1.prefill(pr[:-1]); b1.decode(int(pr[-1]), lg1)
+    b2.prefill(pr[:-1]); b2.decode(int(pr[-1]), lg2)
+    if exact:
+        assert same_bits(lg1, lg2)
+    else:
+        assert rel(lg1, lg2) < 1e-4 and int(lg1.argmax()) == int(lg2.argmax())
+    kvd = 4 * 256
+    for layer in range(6):
+        k1, v1 = b1.read_kv(layer, 0, 300, kvd)
+        k2, v2 = b2.read_kv(layer, 0, 300, kvd)
+        if exact:
+            assert same_bits(k1, k2) and same_bits(v1, v2), f"layer {layer}"
+        else:
+            assert rel(k1, k2) < 1e-4 and rel(v1, v2) < 1e-4, f"layer {layer}"
+    b1.close(); b2.close(); close_all(s, m)
+
+
+def test_long_prefill_vs_oracle(tmpdir_models):
+    """A 300-token prompt (three prefill batches) then decode: exact mode == oracle."""
+    spm, spt = model_files(tmpdir_models, "gemma3-tiny")
+    m, s, o, be, res = run_pair(spm, spt, True, n_prompt=300, n_gen=8, pmax=512)
+    check(res, True)
+    close_all(s, o, m)
+
+
 def test_clone_fork_and_rewind(tmpdir_models):
     """sp_session_clone forks the device KV copy-on-write; both sessions then
     decode independently and bit-identically to independent oracle sessions;
