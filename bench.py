@@ -80,9 +80,15 @@ def main():
     ap.add_argument("--workdir", default=None)
     ap.add_argument("--ctx", type=int, default=None, help="override the workload's prefill length")
     ap.add_argument("--no-graph", action="store_true", help="plain kernel launches instead of one HIP graph per step")
+    ap.add_argument("--no-batch-prefill", action="store_true", help="prefill one decode step per token")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="run one device-to-device copy of this many MiB first (HBM counter calibration)")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("CSV", "COUNTER"), default=None,
+                    help="summarize a rocprofv3 --pmc counter_collection.csv per kernel and exit")
     args = ap.parse_args()
+    if args.pmc_summary:
+        pmc_summary(*args.pmc_summary)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
               "multi-GPU sharding is a design in DESIGN.md, not a measured path", file=sys.stderr)
@@ -109,6 +115,8 @@ def main():
         be = spkv.Backend.wrap(sess.backend_handle())
         if args.no_graph:
             spkv.check(spkv.kv().sp_hipkv_set_graph(be.h, 0), "sp_hipkv_set_graph")
+        if args.no_batch_prefill:
+            spkv.check(spkv.kv().sp_hipkv_set_batch_prefill(be.h, 0), "sp_hipkv_set_batch_prefill")
         info = be.info()
 
         if args.calib_copy_mib:
@@ -194,6 +202,24 @@ def main():
             shutil.rmtree(work, ignore_errors=True)
 
 
+def pmc_summary(path, counter):
+    """Per-kernel dispatch count and mean / max of one counter (KiB per dispatch for
+    FETCH_SIZE / WRITE_SIZE) from a rocprofv3 --pmc counter_collection.csv."""
+    import csv
+    from collections import defaultdict
+    agg = defaultdict(lambda: [0, 0.0, 0.0, set()])
+    for r in csv.DictReader(open(path)):
+        if r.get("Counter_Name") != counter:
+            continue
+        a = agg[r["Kernel_Name"]]
+        v = float(r["Counter_Value"])
+        a[0] += 1; a[1] += v; a[2] = max(a[2], v); a[3].add(r.get("Grid_Size", ""))
+    print(f"# {counter} per dispatch (KiB), from {os.path.basename(path)}")
+    print(f"{'kernel':100s} {'dispatches':>10s} {'mean':>14s} {'max':>14s}")
+    for k, (n, sm, mx, _) in sorted(agg.items(), key=lambda kv: -kv[1][1]):
+        print(f"{k[:100]:100s} {n:10d} {sm / n:14.1f} {mx:14.1f}")
+
+
 def calib_copy(nbytes):
     """One plain device-to-device copy of nbytes (the HIP runtime's copy kernel):
     its FETCH_SIZE / WRITE_SIZE counters calibrate the HBM traffic figures."""
@@ -220,9 +246,12 @@ def cpu_baseline(spm, be, info, shape, exact, n_steps, tok, sess):
     kvd = shape["n_kv_heads"] * shape["head_dim"]
     o = orc.Oracle(spm, pos + n_steps + 1, orc.EXACT if exact else orc.FLOAT)
     t0 = time.time()
+    win = shape.get("swa_window", 0) if shape.get("arch_id") == __import__("spkv").ARCH_GEMMA3 else 0
     for layer in range(shape["n_layers"]):
-        k, v = be.read_kv(layer, 0, pos, kvd)
-        o.set_kv(layer, 0, k, v)
+        # window layers attend the last `win` positions only (Gemma-3: global iff layer % 6 == 5)
+        p0 = max(0, pos - win) if (win and layer % 6 != 5) else 0
+        k, v = be.read_kv(layer, p0, pos - p0, kvd)
+        o.set_kv(layer, p0, k, v)
         del k, v
     o.set_pos(pos)
     log(f"cpu baseline: KV of {pos} positions loaded in {time.time()-t0:.1f}s")

@@ -66,6 +66,31 @@ __device__ __forceinline__ int64_t wsuml(int64_t v) {
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
     return v;
 }
+// Transposed butterfly over P per-lane int64 values (P a power of two, 2..64):
+// each exchange round halves the values a lane carries; afterwards every lane
+// holds the wave total of value treduce_index<P>(lane).
+template <int P> __device__ __forceinline__ int treduce_index(int lane) {
+    int idx = 0;
+    #pragma unroll
+    for (int r = 0, S = P; S > 1; r++, S >>= 1) idx += ((lane >> (5 - r)) & 1) * (S >> 1);
+    return idx;
+}
+template <int P, typename T> __device__ __forceinline__ T treduce(T v[P], int lane) {
+    int o = 32;
+    #pragma unroll
+    for (int S = P; S > 1; S >>= 1, o >>= 1) {
+        const bool hi = lane & o;
+        #pragma unroll
+        for (int i = 0; i < S / 2; i++) {
+            const T send = hi ? v[i] : v[i + S / 2];
+            const T keep = hi ? v[i + S / 2] : v[i];
+            v[i] = keep + __shfl_xor(send, o, 64);
+        }
+    }
+    T t = v[0];
+    for (; o > 0; o >>= 1) t += __shfl_xor(t, o, 64);
+    return t;
+}
 __device__ __forceinline__ float wmax(float v) {
     #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
@@ -79,8 +104,9 @@ __device__ __forceinline__ float *page_of(float *const *pages, int ring, int pos
 
 // Decode: the position comes from the step state.  Batched prefill: token t of
 // the batch sits at pos0 + t and every per-token buffer is offset to its row.
+template <bool BATCH>
 __device__ __forceinline__ void tok_select(AttnArgs &a, int t, int &pos) {
-    if (!a.nt) { pos = a.st->pos; return; }
+    if constexpr (!BATCH) { pos = a.st->pos; return; }
     pos = a.pos0 + t;
     const size_t QD = (size_t)a.NH * a.HD, KVD = (size_t)a.NKV * a.HD;
     a.q += t * QD; a.k += t * KVD; a.v += t * KVD; a.qr += t * QD; a.ao += t * QD;
@@ -95,10 +121,11 @@ __device__ __forceinline__ void tok_select(AttnArgs &a, int t, int &pos) {
 // ------------------------------------------------------------------ qk_prep
 // grid.x = NH (q heads) + NKV (k heads) + NKV (v heads); block = 64 threads
 // (one wave), each lane owning HD/64 pairs-halves.  float/exact by a.mode.
+template <bool BATCH>
 __global__ __launch_bounds__(64) void k_qk_prep(AttnArgs a_in) {
     AttnArgs a = a_in;
     int pos;
-    tok_select(a, blockIdx.y, pos);
+    tok_select<BATCH>(a, blockIdx.y, pos);
     const int HD = a.HD, half = HD / 2, lane = threadIdx.x;
     const int hb = blockIdx.x;
     const bool isq = hb < a.NH, isk = !isq && hb < a.NH + a.NKV;
@@ -136,7 +163,7 @@ __global__ __launch_bounds__(64) void k_qk_prep(AttnArgs a_in) {
         ss = wsuml(ss);
         if (ss == 0) { for (int j = 0; j < per; j++) v[j] = 0.0f; }
         else {
-            const int64_t inv = (int64_t)isqrt_u64(udiv128_64((u128)HD << 72, (uint64_t)ss));
+            const int64_t inv = rms_inv_q72(HD, ss);
             for (int j = 0; j < per; j++) {
                 int64_t xi = llround_pow2<16>(v[j]), wi = llround_pow2<16>(nw[lane + 64 * j]);
                 v[j] = (float)((double)mul3_lo64(xi, inv, wi) / 4503599627370496.0);
@@ -207,7 +234,8 @@ void launch_rope_table_batch(int pos0, int T, int HD, int mode, float base_g, fl
     hipLaunchKernelGGL(k_rope_table, dim3(T), dim3(256), 0, s, nullptr, pos0, HD, mode, base_g, base_l, fq_g, fq_l, out);
 }
 void launch_qk_prep(const AttnArgs &a, hipStream_t s) {
-    hipLaunchKernelGGL(k_qk_prep, dim3(a.NH + 2 * a.NKV, a.nt ? a.nt : 1), dim3(64), 0, s, a);
+    if (a.nt) hipLaunchKernelGGL(k_qk_prep<true>, dim3(a.NH + 2 * a.NKV, a.nt), dim3(64), 0, s, a);
+    else hipLaunchKernelGGL(k_qk_prep<false>, dim3(a.NH + 2 * a.NKV), dim3(64), 0, s, a);
 }
 void set_rope_tables(const int64_t atan_q60[64], int64_t kinv_q62) {
     hipMemcpyToSymbol(HIP_SYMBOL(g_atan_q60), atan_q60, 64 * sizeof(int64_t));
@@ -229,9 +257,13 @@ __device__ __forceinline__ void chunk_range(const AttnArgs &a, int pos, int c, i
 // 16 B-per-lane row loads of one head's HD elements at absolute position p
 template <int EPL, typename T>
 __device__ __forceinline__ void load_row(const AttnArgs &a, int h, int p, bool vpart, int lane, T out[EPL]) {
-    const float *page = page_of(a.pages, a.ring_pages, p);
+    // row and head are wave-uniform: the page pointer and the row base are
+    // scalar work, only the lane offset is per lane
+    const int pu = __builtin_amdgcn_readfirstlane(p), hu = __builtin_amdgcn_readfirstlane(h);
+    const float *page = page_of(a.pages, a.ring_pages, pu);
     const int HD = EPL * 64;
-    const T *src = (const T *)(page + (vpart ? (size_t)a.NKV * PAGE * HD : 0) + ((size_t)h * PAGE + p % PAGE) * HD) + lane * EPL;
+    const T *row = (const T *)(page + (vpart ? (size_t)a.NKV * PAGE * HD : 0) + ((size_t)hu * PAGE + (pu & (PAGE - 1))) * HD);
+    const T *src = row + lane * EPL;
     if constexpr (EPL == 4) {
         typedef T v4 __attribute__((ext_vector_type(4)));
         const v4 t = *(const v4 *)src; out[0] = t.x; out[1] = t.y; out[2] = t.z; out[3] = t.w;
@@ -248,13 +280,47 @@ constexpr int MAXCH = 256;       // positions per chunk (LDS score buffer)
 constexpr int MAXNCH = 4096;     // chunks per kv-head (combine weight buffer)
 constexpr int UNR = 4;           // positions in flight per wave
 
-template <int EPL, int G>
+// UNR rows j0.. of the chunk (zeros past n); the loops below load the next
+// UNR rows before working on the current ones, so a wave always has a row
+// group in flight
+template <int EPL, typename T>
+__device__ __forceinline__ void load_rows(const AttnArgs &a, int h, int cs, int j0, int n, bool vpart, int lane,
+                                          T out[UNR][EPL]) {
+    #pragma unroll
+    for (int u = 0; u < UNR; u++) {
+        if (j0 + u < n) load_row<EPL>(a, h, cs + j0 + u, vpart, lane, out[u]);
+        else {
+            #pragma unroll
+            for (int e = 0; e < EPL; e++) out[u][e] = (T)0;
+        }
+    }
+}
+
+// Row-quad layout for the score passes: a wave takes 16 consecutive positions
+// at a time, lane = 4 * row + quarter; in load i a quarter reads 16 B at
+// byte 64 i + 16 quarter of its row (each row's four lanes read 64
+// contiguous bytes), so every lane owns HD/4 dimensions of one row and the
+// dot product needs a 4-lane reduction only.  q sits in LDS and is read with
+// broadcast.  The 16 rows span at most two pages, looked up once per group.
+// p0: first position of the group, plast: last position the chunk holds
+template <int EPL, typename T>
+__device__ __forceinline__ const T *quad_row(const AttnArgs &a, int h, int p0, int plast, int p, bool vpart) {
+    const int pu0 = __builtin_amdgcn_readfirstlane(p0);
+    const int pu1 = __builtin_amdgcn_readfirstlane(p0 + 15 < plast ? p0 + 15 : plast);
+    const float *pg0 = page_of(a.pages, a.ring_pages, pu0);
+    const float *pg1 = page_of(a.pages, a.ring_pages, pu1);
+    const float *pg = (p >> 6) == (pu0 >> 6) ? pg0 : pg1;
+    const int HD = EPL * 64;
+    return (const T *)(pg + (vpart ? (size_t)a.NKV * PAGE * HD : 0) + ((size_t)h * PAGE + (p & (PAGE - 1))) * HD);
+}
+
+template <int EPL, int G, bool BATCH>
 __global__ __launch_bounds__(256) void k_attn_float(AttnArgs a_in) {
     AttnArgs a = a_in;
     int pos;
-    tok_select(a, blockIdx.z, pos);
+    tok_select<BATCH>(a, blockIdx.z, pos);
     const int HD = EPL * 64, c = blockIdx.x, h = blockIdx.y;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     int cs, ce, nch;
     chunk_range(a, pos, c, cs, ce, nch);
     if (c >= nch) return;
@@ -263,28 +329,43 @@ __global__ __launch_bounds__(256) void k_attn_float(AttnArgs a_in) {
     __shared__ float wk[MAXNCH];
     __shared__ float redf[4];
     __shared__ int is_last;
-    float q[G][EPL];
-    #pragma unroll
-    for (int g = 0; g < G; g++)
-        #pragma unroll
-        for (int e = 0; e < EPL; e++) q[g][e] = a.qr[(size_t)(h * G + g) * HD + lane * EPL + e];
+    __shared__ float4 qs[G][EPL * 16];
+    for (int i = threadIdx.x; i < G * HD / 4; i += 256) {
+        const int g = i / (HD / 4), d4 = i % (HD / 4);
+        qs[g][d4] = *(const float4 *)(a.qr + (size_t)(h * G + g) * HD + 4 * d4);
+    }
+    __syncthreads();
     const int n = ce - cs;
-    // scores: each wave takes UNR consecutive positions per iteration
-    for (int j0 = wave * UNR; j0 < n; j0 += 4 * UNR) {
-        float kv[UNR][EPL];
+    // scores in the row-quad layout (16 positions per wave and group)
+    const int r = lane >> 2, k4 = lane & 3;
+    for (int j0 = wave * 16; j0 < n; j0 += 64) {
+        const int j = j0 + r;
+        float acc[G];
         #pragma unroll
-        for (int u = 0; u < UNR; u++) if (j0 + u < n) load_row<EPL>(a, h, cs + j0 + u, false, lane, kv[u]);
-        #pragma unroll
-        for (int u = 0; u < UNR; u++) {
-            if (j0 + u >= n) break;
+        for (int g = 0; g < G; g++) acc[g] = 0.0f;
+        if (j < n) {
+            const float *row = quad_row<EPL, float>(a, h, cs + j0, ce - 1, cs + j, false) + 4 * k4;
+            float4 kv[4 * EPL];
             #pragma unroll
-            for (int g = 0; g < G; g++) {
-                float d = 0.0f;
+            for (int i = 0; i < 4 * EPL; i++) kv[i] = *(const float4 *)(row + 16 * i);
+            #pragma unroll
+            for (int i = 0; i < 4 * EPL; i++)
                 #pragma unroll
-                for (int e = 0; e < EPL; e++) d += q[g][e] * kv[u][e];
-                d = wsum(d);
-                if (lane == 0) sc[g][j0 + u] = d * a.ascale;
-            }
+                for (int g = 0; g < G; g++) {
+                    const float4 q = qs[g][4 * i + k4];
+                    acc[g] += q.x * kv[i].x + q.y * kv[i].y + q.z * kv[i].z + q.w * kv[i].w;
+                }
+        }
+        #pragma unroll
+        for (int g = 0; g < G; g++) {
+            acc[g] += __shfl_xor(acc[g], 1, 64);
+            acc[g] += __shfl_xor(acc[g], 2, 64);
+        }
+        if (j < n && k4 < G) {
+            float d = acc[0];
+            #pragma unroll
+            for (int g = 1; g < G; g++) if (k4 == g) d = acc[g];
+            sc[k4][j] = d * a.ascale;
         }
     }
     __syncthreads();
@@ -294,8 +375,18 @@ __global__ __launch_bounds__(256) void k_attn_float(AttnArgs a_in) {
         float mv = -INFINITY;
         for (int j = lane; j < n; j += 64) mv = fmaxf(mv, sc[g][j]);
         m[g] = wmax(mv);
+    }
+    __syncthreads();
+    // softmax numerators once per (head, position), in place
+    for (int i = threadIdx.x; i < G * n; i += 256) {
+        const int g = i / n, j = i % n;
+        sc[g][j] = expf(sc[g][j] - m[g]);
+    }
+    __syncthreads();
+    #pragma unroll
+    for (int g = 0; g < G; g++) {
         float lv = 0.0f;
-        for (int j = lane; j < n; j += 64) lv += expf(sc[g][j] - m[g]);
+        for (int j = lane; j < n; j += 64) lv += sc[g][j];
         l[g] = wsum(lv);
     }
     float o[G][EPL];
@@ -303,20 +394,24 @@ __global__ __launch_bounds__(256) void k_attn_float(AttnArgs a_in) {
     for (int g = 0; g < G; g++)
         #pragma unroll
         for (int e = 0; e < EPL; e++) o[g][e] = 0.0f;
+    float vv[UNR][EPL], vn[UNR][EPL];
+    load_rows<EPL>(a, h, cs, wave * UNR, n, true, lane, vv);
     for (int j0 = wave * UNR; j0 < n; j0 += 4 * UNR) {
-        float vv[UNR][EPL];
-        #pragma unroll
-        for (int u = 0; u < UNR; u++) if (j0 + u < n) load_row<EPL>(a, h, cs + j0 + u, true, lane, vv[u]);
+        load_rows<EPL>(a, h, cs, j0 + 4 * UNR, n, true, lane, vn);
         #pragma unroll
         for (int u = 0; u < UNR; u++) {
             if (j0 + u >= n) break;
             #pragma unroll
             for (int g = 0; g < G; g++) {
-                const float p = expf(sc[g][j0 + u] - m[g]);
+                const float p = sc[g][j0 + u];
                 #pragma unroll
                 for (int e = 0; e < EPL; e++) o[g][e] += p * vv[u][e];
             }
         }
+        #pragma unroll
+        for (int u = 0; u < UNR; u++)
+            #pragma unroll
+            for (int e = 0; e < EPL; e++) vv[u][e] = vn[u][e];
     }
     #pragma unroll
     for (int g = 0; g < G; g++)
@@ -373,47 +468,71 @@ __global__ __launch_bounds__(256) void k_attn_float(AttnArgs a_in) {
 }
 
 // ---- exact mode: pass 1, integer scores on the softmax grid + chunk max ----
-template <int EPL, int G>
+template <int EPL, int G, bool BATCH>
 __global__ __launch_bounds__(256) void k_attn_exact_scores(AttnArgs a_in) {
     AttnArgs a = a_in;
     int pos;
-    tok_select(a, blockIdx.z, pos);
+    tok_select<BATCH>(a, blockIdx.z, pos);
     const int HD = EPL * 64, c = blockIdx.x, h = blockIdx.y;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     int cs, ce, nch;
     chunk_range(a, pos, c, cs, ce, nch);
     if (c >= nch) return;
     __shared__ int zmax[4][G];
-    int32_t qi[G][EPL];
-    #pragma unroll
-    for (int g = 0; g < G; g++)
-        #pragma unroll
-        for (int e = 0; e < EPL; e++) qi[g][e] = (int32_t)rintf(a.qr[(size_t)(h * G + g) * HD + lane * EPL + e] * 65536.0f);
-    int mx[G];
-    #pragma unroll
-    for (int g = 0; g < G; g++) mx[g] = INT32_MIN;
+    __shared__ int4 qs[G][EPL * 16];                 // qi = rne(q * 2^16), 4 dims per entry
+    for (int i = threadIdx.x; i < G * HD / 4; i += 256) {
+        const int g = i / (HD / 4), d4 = i % (HD / 4);
+        const float *qp = a.qr + (size_t)(h * G + g) * HD + 4 * d4;
+        qs[g][d4] = make_int4((int)rintf(qp[0] * 65536.0f), (int)rintf(qp[1] * 65536.0f),
+                              (int)rintf(qp[2] * 65536.0f), (int)rintf(qp[3] * 65536.0f));
+    }
+    __syncthreads();
+    const int r = lane >> 2, k4 = lane & 3;
+    int mx = INT32_MIN;                              // lane with k4 == g tracks head g
     const int n = ce - cs;
-    for (int j0 = wave * UNR; j0 < n; j0 += 4 * UNR) {
-        int32_t kv[UNR][EPL];
+    for (int j0 = wave * 16; j0 < n; j0 += 64) {
+        const int j = j0 + r;
+        int64_t acc[G];
         #pragma unroll
-        for (int u = 0; u < UNR; u++) if (j0 + u < n) load_row<EPL>(a, h, cs + j0 + u, false, lane, kv[u]);
-        #pragma unroll
-        for (int u = 0; u < UNR; u++) {
-            if (j0 + u >= n) break;
+        for (int g = 0; g < G; g++) acc[g] = 0;
+        if (j < n) {
+            const int32_t *row = quad_row<EPL, int32_t>(a, h, cs + j0, ce - 1, cs + j, false) + 4 * k4;
+            int4 kv[4 * EPL];
             #pragma unroll
-            for (int g = 0; g < G; g++) {
-                int64_t ip = 0;
+            for (int i = 0; i < 4 * EPL; i++) kv[i] = *(const int4 *)(row + 16 * i);
+            #pragma unroll
+            for (int i = 0; i < 4 * EPL; i++)
                 #pragma unroll
-                for (int e = 0; e < EPL; e++) ip += (int64_t)qi[g][e] * kv[u][e];
-                ip = wsuml(ip);
-                const float scv = (float)((double)ip / 4294967296.0) * a.ascale;
-                const int32_t z = (int32_t)llround_pow2<14>(scv);
-                if (lane == 0) a.zscratch[(size_t)(h * G + g) * a.zstride + (size_t)(cs + j0 + u)] = z;
-                mx[g] = z > mx[g] ? z : mx[g];
-            }
+                for (int g = 0; g < G; g++) {
+                    const int4 q = qs[g][4 * i + k4];
+                    acc[g] += (int64_t)q.x * kv[i].x + (int64_t)q.y * kv[i].y + (int64_t)q.z * kv[i].z + (int64_t)q.w * kv[i].w;
+                }
+        }
+        #pragma unroll
+        for (int g = 0; g < G; g++) {
+            acc[g] += __shfl_xor(acc[g], 1, 64);
+            acc[g] += __shfl_xor(acc[g], 2, 64);
+        }
+        if (j < n && k4 < G) {
+            int64_t tot = acc[0];
+            #pragma unroll
+            for (int g = 1; g < G; g++) if (k4 == g) tot = acc[g];
+            const float scv = (float)((double)tot / 4294967296.0) * a.ascale;
+            const int32_t z = (int32_t)llround_pow2<14>(scv);
+            a.zscratch[(size_t)(h * G + k4) * a.zstride + (size_t)(cs + j)] = z;
+            mx = z > mx ? z : mx;
         }
     }
-    if (lane == 0) for (int g = 0; g < G; g++) zmax[wave][g] = mx[g];
+    // per-head maximum over this wave
+    int mxg[G];
+    #pragma unroll
+    for (int g = 0; g < G; g++) {
+        int t = k4 == g ? mx : INT32_MIN;
+        #pragma unroll
+        for (int o = 32; o > 0; o >>= 1) { const int u = __shfl_xor(t, o, 64); t = u > t ? u : t; }
+        mxg[g] = t;
+    }
+    if (lane == 0) for (int g = 0; g < G; g++) zmax[wave][g] = mxg[g];
     __syncthreads();
     if (threadIdx.x < G) {
         const int g = threadIdx.x;
@@ -424,13 +543,13 @@ __global__ __launch_bounds__(256) void k_attn_exact_scores(AttnArgs a_in) {
 }
 
 // ---- exact mode: pass 2, exp weights on the island grid, exact V-sum ----
-template <int EPL, int G>
+template <int EPL, int G, bool BATCH>
 __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a_in) {
     AttnArgs a = a_in;
     int pos;
-    tok_select(a, blockIdx.z, pos);
+    tok_select<BATCH>(a, blockIdx.z, pos);
     const int HD = EPL * 64, c = blockIdx.x, h = blockIdx.y;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     int cs, ce, nch;
     chunk_range(a, pos, c, cs, ce, nch);
     if (c >= nch) return;
@@ -472,10 +591,10 @@ __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a_in) {
     for (int g = 0; g < G; g++)
         #pragma unroll
         for (int e = 0; e < EPL; e++) o[g][e] = 0;
+    int32_t vv[UNR][EPL], vn[UNR][EPL];
+    load_rows<EPL>(a, h, cs, wave * UNR, n, true, lane, vv);
     for (int j0 = wave * UNR; j0 < n; j0 += 4 * UNR) {
-        int32_t vv[UNR][EPL];
-        #pragma unroll
-        for (int u = 0; u < UNR; u++) if (j0 + u < n) load_row<EPL>(a, h, cs + j0 + u, true, lane, vv[u]);
+        load_rows<EPL>(a, h, cs, j0 + 4 * UNR, n, true, lane, vn);
         #pragma unroll
         for (int u = 0; u < UNR; u++) {
             if (j0 + u >= n) break;
@@ -484,6 +603,10 @@ __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a_in) {
                 #pragma unroll
                 for (int e = 0; e < EPL; e++) o[g][e] += ew[g][j0 + u] * (int64_t)vv[u][e];
         }
+        #pragma unroll
+        for (int u = 0; u < UNR; u++)
+            #pragma unroll
+            for (int e = 0; e < EPL; e++) vv[u][e] = vn[u][e];
     }
     #pragma unroll
     for (int g = 0; g < G; g++)
@@ -527,13 +650,19 @@ __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a_in) {
     if (threadIdx.x == 0) reset_counter(&a.counter[h]);
 }
 
-template <int EPL, int G> static void attn_dispatch(const AttnArgs &a, int grid_chunks, hipStream_t s) {
-    dim3 grid(grid_chunks, a.NKV, a.nt ? a.nt : 1);
-    if (a.mode == FLOAT) hipLaunchKernelGGL((k_attn_float<EPL, G>), grid, dim3(256), 0, s, a);
+// decode (B = false: position from the step state) and batched prefill
+// (B = true: token grid dimension) are separate instances
+template <int EPL, int G, bool B> static void attn_dispatch_b(const AttnArgs &a, int grid_chunks, hipStream_t s) {
+    dim3 grid(grid_chunks, a.NKV, B ? a.nt : 1);
+    if (a.mode == FLOAT) hipLaunchKernelGGL((k_attn_float<EPL, G, B>), grid, dim3(256), 0, s, a);
     else {
-        hipLaunchKernelGGL((k_attn_exact_scores<EPL, G>), grid, dim3(256), 0, s, a);
-        hipLaunchKernelGGL((k_attn_exact_vsum<EPL, G>), grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL((k_attn_exact_scores<EPL, G, B>), grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL((k_attn_exact_vsum<EPL, G, B>), grid, dim3(256), 0, s, a);
     }
+}
+template <int EPL, int G> static void attn_dispatch(const AttnArgs &a, int grid_chunks, hipStream_t s) {
+    if (a.nt) attn_dispatch_b<EPL, G, true>(a, grid_chunks, s);
+    else attn_dispatch_b<EPL, G, false>(a, grid_chunks, s);
 }
 
 void launch_attention(const AttnArgs &a, int grid_chunks, hipStream_t s) {

@@ -467,16 +467,18 @@ struct StepShape { int logits, argmax, grid_global, grid_local, chunk_global, ch
 int attn_chunks(const sp_kvdecode_handle *h, int pos_hi, StepShape &sh) {
     const DevModel *m = h->m;
     // global layers: the largest chunk (<= 256 positions) that still gives about
-    // 2048 workgroups; fewer chunks make the merge of the partials cheaper
+    // 1024 workgroups (four per CU); fewer chunks mean fewer partials to merge
     int cg = 256;
-    while (cg > 16 && (long long)((pos_hi + 1) / cg + 1) * m->NKV < 2048) cg /= 2;
+    while (cg > 16 && (long long)((pos_hi + 1) / cg + 1) * m->NKV < 1024) cg /= 2;
     while ((pos_hi / cg + 1) > 4096) cg *= 2;
     sh.chunk_global = cg;
     sh.grid_global = pos_hi / cg + 1;
-    sh.chunk_local = 16;
+    // window layers: 64-position chunks; a window of W positions touches at most
+    // (W-1)/64 + 2 of them whatever its alignment
+    const int cl = 64;
+    sh.chunk_local = cl;
     const int span = m->SW > 0 ? std::min(m->SW, pos_hi + 1) : pos_hi + 1;
-    sh.grid_local = span / 16 + 2;
-    sh.grid_local = std::min(sh.grid_local, pos_hi / 16 + 1);
+    sh.grid_local = std::min((span - 1) / cl + 2, pos_hi / cl + 1);
     return 0;
 }
 

@@ -59,6 +59,23 @@ __device__ __forceinline__ uint64_t udiv128_64(u128 num, uint64_t den) {
 }
 // v mod m for v >= 0 (v < 2^100), 0 < m < 2^63: estimate the quotient in
 // double, correct exactly
+// isqrt(floor((n << 72) / ss)) for n > 0, ss > 0 -- the island's RMS inverse.
+// The quotient is estimated in double (exact to within 2 when below 2^52) and
+// corrected with exact 128-bit products; larger quotients take udiv128_64.
+__device__ __forceinline__ int64_t rms_inv_q72(int n, int64_t ss) {
+    const u128 num = (u128)(uint64_t)n << 72, den = (u128)(uint64_t)ss;
+    const double est = ldexp((double)n, 72) / (double)ss;
+    uint64_t q;
+    if (est < 4503599627370496.0) {                          // 2^52
+        q = (uint64_t)est;
+        u128 prod = (u128)q * den;
+        while (prod > num) { q--; prod -= den; }
+        while (num - prod >= den) { q++; prod += den; }
+    } else {
+        q = udiv128_64(num, (uint64_t)ss);
+    }
+    return (int64_t)isqrt_u64(q);
+}
 __device__ __forceinline__ int64_t umod128_64(i128 v, int64_t m) {
     const int64_t q = (int64_t)((double)v / (double)m);
     i128 r = v - (i128)q * m;

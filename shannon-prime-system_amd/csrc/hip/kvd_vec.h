@@ -73,8 +73,7 @@ __device__ NormScale norm_finish(const SumSq &p, int n, float eps, int mode, voi
     } else {
         const int64_t ss = block_sum<int64_t>(p.i, (int64_t *)red);
         if (ss == 0) { s.zero = 1; return s; }
-        const uint64_t q = udiv128_64((u128)n << 72, (uint64_t)ss);
-        s.inv = (int64_t)isqrt_u64(q);
+        s.inv = rms_inv_q72(n, ss);
     }
     return s;
 }
