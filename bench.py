@@ -32,8 +32,57 @@ sys.path.insert(0, os.path.join(ROOT, "shannon-prime-system_amd"))
 
 METRIC = "kvdecode tokens/s + KV-read HBM GB/s (% of peak), Gemma-12B shape 32k ctx"
 PEAK_GBS = 8000.0
-CLASSES = ["layer_gemv_q4b", "lm_head_gemv_q4b", "gqa_decode_attn_global", "gqa_decode_attn_window",
-           "qk_norm_rope_append", "embed_argmax"]
+CLASSES = ["qkv_gemv_q4b", "o_gemv_q4b", "gate_up_gemv_q4b", "down_gemv_q4b", "lm_head_gemv_q4b",
+           "gqa_decode_attn_global", "gqa_decode_attn_window", "qk_norm_rope_append", "embed_rope_argmax"]
+# the rocprofv3 kernel names of each class's launches (exact mode; float mode in brackets)
+KERNEL_NAMES = {
+    "qkv_gemv_q4b": ["kvd::k_gemv<2, false, false>", "kvd::k_gemv<1, false, false> (layer 0)"],
+    "o_gemv_q4b": ["kvd::k_gemv<0, false, false>"],
+    "gate_up_gemv_q4b": ["kvd::k_gemv<2, true, false>"],
+    "down_gemv_q4b": ["kvd::k_gemv<0, false, false>"],
+    "lm_head_gemv_q4b": ["kvd::k_gemv<2, false, false>"],
+    "gqa_decode_attn_global": ["kvd::k_attn_exact_scores<EPL, G, false> + kvd::k_attn_exact_vsum<EPL, G, false>",
+                               "[kvd::k_attn_float<EPL, G, false>]"],
+    "gqa_decode_attn_window": ["kvd::k_attn_exact_scores<EPL, G, false> + kvd::k_attn_exact_vsum<EPL, G, false>",
+                               "[kvd::k_attn_float<EPL, G, false>]"],
+    "qk_norm_rope_append": ["kvd::k_qk_prep<false>"],
+    "embed_rope_argmax": ["kvd::k_embed", "kvd::k_rope_table", "kvd::k_argmax"],
+}
+# committed rocprofv3 --pmc summaries (FETCH_SIZE / WRITE_SIZE per dispatch) of the
+# decode kernels at this model shape, with the 1 GiB calibration copy they hold
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "gemma3-12b_decode_pmc_fetch_write.txt")
+
+
+def pmc_traffic(kernel, path=PMC_SUMMARY):
+    """HBM bytes per launch of `kernel` from the committed PMC summary: FETCH_SIZE
+    and WRITE_SIZE means, each scaled by what the counter reads for the plain
+    1 GiB device copy in the same run.  None when the summary lacks it."""
+    try:
+        lines = open(path).read().splitlines()
+    except OSError:
+        return None
+    sec, val, cal = None, {}, {}
+    for ln in lines:
+        if ln.startswith("# FETCH_SIZE"):
+            sec = "FETCH_SIZE"
+        elif ln.startswith("# WRITE_SIZE"):
+            sec = "WRITE_SIZE"
+        elif sec and not ln.startswith("#") and ln.strip() and not ln.startswith("kernel"):
+            parts = ln.split()
+            name = " ".join(parts[:-3])
+            mean, mx = float(parts[-2]), float(parts[-1])
+            if "copyBuffer" in name:
+                cal[sec] = mx
+            if name.startswith("void " + kernel + "(") or name.startswith(kernel + "("):
+                val[sec] = mean
+    if len(val) < 2 or len(cal) < 2 or not cal["FETCH_SIZE"] or not cal["WRITE_SIZE"]:
+        return None
+    gib_kib = 1024.0 * 1024.0
+    f = val["FETCH_SIZE"] * gib_kib / cal["FETCH_SIZE"]
+    w = val["WRITE_SIZE"] * gib_kib / cal["WRITE_SIZE"]
+    return {"bytes": (f + w) * 1024.0, "fetch_scale": round(gib_kib / cal["FETCH_SIZE"], 4),
+            "write_scale": round(gib_kib / cal["WRITE_SIZE"], 4), "source": os.path.relpath(path, ROOT)}
+
 
 WORKLOADS = {
     "gemma3-12b-32k": dict(shape="gemma3-12b", ctx=32768),
@@ -159,7 +208,10 @@ def main():
                 cls.append(dict(kernel=name, launches=int(nl[i]), avg_us=1e3 * ms[i] / nl[i],
                                 total_ms=float(ms[i]), bytes=float(by[i]),
                                 gbs=float(by[i] / (ms[i] * 1e-3) / 1e9) if ms[i] > 0 else None))
-        dom = max(cls, key=lambda c: c["total_ms"])
+        dom = max(cls, key=lambda c: c["total_ms"])             # the class with the most device time per step
+        dom_names = KERNEL_NAMES.get(dom["kernel"], [])
+        dom_launch_bytes = dom["bytes"] / dom["launches"]
+        traffic = pmc_traffic(dom_names[0]) if len(dom_names) == 1 else None
         kv_gb = sum(c["bytes"] for c in cls if c["kernel"].startswith("gqa")) / 1e9
         kv_ms = sum(c["total_ms"] for c in cls if c["kernel"].startswith("gqa"))
         w_gb = sum(c["bytes"] for c in cls if "gemv" in c["kernel"]) / 1e9
@@ -180,8 +232,13 @@ def main():
             "data": "synthetic: seeded random-init OK_Q4B weights (SplitMix64 seed 0, N(0,0.02)), seeded uniform prompt (seed 1)",
             "config": {"workload": f"{args.workload}: {wl['shape']}-shape kvdecode, prefill {ctx} then {args.steps} greedy steps, batch 1",
                        "ctx": ctx, "mode": args.mode, "b_kv": 4, "pmax": pmax},
-            "roofline": {"bound": "hbm", "kernel": dom["kernel"], "achieved": round(dom["gbs"], 1),
-                         "peak": PEAK_GBS, "unit": "GB/s", "frac": round(dom["gbs"] / PEAK_GBS, 4), "traffic": None},
+            "roofline": {"bound": "hbm", "kernel": dom["kernel"], "rocprof_kernels": dom_names,
+                         "achieved": round(dom["gbs"], 1), "peak": PEAK_GBS, "unit": "GB/s",
+                         "frac": round(dom["gbs"] / PEAK_GBS, 4),
+                         "algorithmic_bytes_per_launch": round(dom_launch_bytes),
+                         "avg_launch_us": round(dom["avg_us"], 3),
+                         "traffic": round(traffic["bytes"]) if traffic else None,
+                         "traffic_source": traffic},
             "kv_read": {"gbs": round(kv_gb / (kv_ms * 1e-3), 1), "frac": round(kv_gb / (kv_ms * 1e-3) / PEAK_GBS, 4),
                         "bytes_per_step": kv_gb * 1e9 / args.kernel_steps},
             "weight_read": {"gbs": round(w_gb / (w_ms * 1e-3), 1), "frac": round(w_gb / (w_ms * 1e-3) / PEAK_GBS, 4),

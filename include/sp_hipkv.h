@@ -60,11 +60,14 @@ sp_status sp_hipkv_attach(sp_session *s, int pmax, int exact);
 int  sp_hipkv_greedy(sp_kvdecode_handle *h, int32_t first_token, int n, int32_t *out_tokens,
                      double *device_ms);
 /* Per-kernel-class device times over n greedy steps, each launch bracketed by HIP
- * events on the backend's stream.  Classes: 0 layer GEMV, 1 LM-head GEMV,
- * 2 attention (global layers), 3 attention (window layers), 4 q/k prep + append,
- * 5 embed + argmax.  ms[6], launches[6]; bytes[6] = algorithmic HBM bytes. */
+ * events on the backend's stream.  Classes: 0 QKV GEMV, 1 O GEMV, 2 gate/up GEMV
+ * (+ activation), 3 down GEMV, 4 LM-head GEMV, 5 attention (global layers),
+ * 6 attention (window layers), 7 q/k prep + append, 8 embed + RoPE table + argmax.
+ * ms, launches, bytes: SP_HIPKV_NCLASS entries; bytes = algorithmic HBM bytes. */
+#define SP_HIPKV_NCLASS 9
 int  sp_hipkv_kernel_times(sp_kvdecode_handle *h, int32_t first_token, int n,
-                           double ms[6], long long launches[6], double bytes[6]);
+                           double ms[SP_HIPKV_NCLASS], long long launches[SP_HIPKV_NCLASS],
+                           double bytes[SP_HIPKV_NCLASS]);
 /* Read K/V of one layer for positions [p0, p0+n) in the reference slab layout
  * ([n][n_kv_heads*head_dim] floats, or int32 grid values in exact mode). */
 int  sp_hipkv_read_kv(const sp_kvdecode_handle *h, int layer, int p0, int n, float *k, float *v);

@@ -22,6 +22,7 @@
 // finish a kv-head merges the chunk partials (arrival counter, self-resetting).
 #include "kvd_internal.h"
 #include "kvd_exact.h"
+#include "kvd_qkprep.h"
 #include <cstdio>
 #include <cstdlib>
 
@@ -119,85 +120,13 @@ __device__ __forceinline__ void tok_select(AttnArgs &a, int t, int &pos) {
 }
 
 // ------------------------------------------------------------------ qk_prep
-// grid.x = NH (q heads) + NKV (k heads) + NKV (v heads); block = 64 threads
-// (one wave), each lane owning HD/64 pairs-halves.  float/exact by a.mode.
+// grid.x = NH (q heads) + NKV (k heads) + NKV (v heads), one wave each
 template <bool BATCH>
 __global__ __launch_bounds__(64) void k_qk_prep(AttnArgs a_in) {
     AttnArgs a = a_in;
     int pos;
     tok_select<BATCH>(a, blockIdx.y, pos);
-    const int HD = a.HD, half = HD / 2, lane = threadIdx.x;
-    const int hb = blockIdx.x;
-    const bool isq = hb < a.NH, isk = !isq && hb < a.NH + a.NKV;
-    const int h = isq ? hb : (isk ? hb - a.NH : hb - a.NH - a.NKV);
-    float *page = page_of(a.pages, a.ring_pages, pos);
-    const int slot = pos % PAGE;
-    if (!isq && !isk) {                                        // V: raw copy
-        const float *src = a.v + (size_t)h * HD;
-        float *dst = page + (size_t)a.NKV * PAGE * HD + ((size_t)h * PAGE + slot) * HD;
-        for (int i = lane; i < HD; i += 64) {
-            if (a.mode == FLOAT) dst[i] = src[i];
-            else {
-                float r = rintf(src[i] * 65536.0f);
-                r = fminf(fmaxf(r, -8388607.0f), 8388607.0f);
-                ((int32_t *)dst)[i] = (int32_t)r;
-            }
-        }
-        return;
-    }
-    const float *src = isq ? a.q + (size_t)h * HD : a.k + (size_t)h * HD;
-    const float *nw = isq ? a.q_norm : a.k_norm;
-    float v[8];                                                // HD <= 512
-    const int per = HD / 64;
-    for (int j = 0; j < per; j++) v[j] = src[lane + 64 * j];
-    // per-head RMSNorm
-    if (a.mode == FLOAT) {
-        double ss = 0.0;
-        for (int j = 0; j < per; j++) ss += (double)v[j] * (double)v[j];
-        ss = wsumd(ss);
-        const float sc = 1.0f / sqrtf((float)(ss / HD) + a.eps);
-        for (int j = 0; j < per; j++) v[j] = v[j] * sc * nw[lane + 64 * j];
-    } else {
-        int64_t ss = 0;
-        for (int j = 0; j < per; j++) { int64_t xi = llround_pow2<16>(v[j]); ss += xi * xi; }
-        ss = wsuml(ss);
-        if (ss == 0) { for (int j = 0; j < per; j++) v[j] = 0.0f; }
-        else {
-            const int64_t inv = rms_inv_q72(HD, ss);
-            for (int j = 0; j < per; j++) {
-                int64_t xi = llround_pow2<16>(v[j]), wi = llround_pow2<16>(nw[lane + 64 * j]);
-                v[j] = (float)((double)mul3_lo64(xi, inv, wi) / 4503599627370496.0);
-            }
-        }
-    }
-    // NEOX RoPE: pairs (i, i+half), cos/sin from this step's rotation table
-    // (same values the per-pair formula gives; computed once per step).
-    __shared__ float rot[512];
-    for (int j = 0; j < per; j++) rot[lane + 64 * j] = v[j];
-    __syncthreads();
-    const float *cs = a.rope_cs;
-    for (int i = lane; i < half; i += 64) {
-        const float x0 = rot[i], x1 = rot[i + half];
-        const float c = cs[i], s = cs[half + i];
-        if (a.mode == FLOAT) {
-            rot[i] = x0 * c - x1 * s;
-            rot[i + half] = x0 * s + x1 * c;
-        } else {
-            const float ac = x0 * c, bs = x1 * s, as = x0 * s, bc = x1 * c;
-            rot[i] = ac - bs;
-            rot[i + half] = as + bc;
-        }
-    }
-    __syncthreads();
-    if (isq) {
-        for (int i = lane; i < HD; i += 64) a.qr[(size_t)h * HD + i] = rot[i];
-    } else {
-        float *dst = page + ((size_t)h * PAGE + slot) * HD;
-        for (int i = lane; i < HD; i += 64) {
-            if (a.mode == FLOAT) dst[i] = rot[i];
-            else ((int32_t *)dst)[i] = (int32_t)rintf(rot[i] * 65536.0f);
-        }
-    }
+    qk_prep_head<false>(head_prep_of(a), blockIdx.x, pos, threadIdx.x);
 }
 
 // Rotation table of the current position for both RoPE bases:

@@ -489,11 +489,11 @@ void enqueue_body(sp_kvdecode_handle *h, const StepShape &sh, TimeCb cb, void *c
     hipStream_t s = h->stream;
     const int QD = m->NH * m->HD, KVD = m->NKV * m->HD;
     auto T = [&](int cls, bool b) { if (cb) cb(ctx, cls, b); };
-    T(5, true);
+    T(8, true);
     launch_embed(m->embd, h->d_st, h->tokbuf, h->x1, m->gemma ? sqrtf((float)m->E) : 0.0f, s);
     launch_rope_table(h->d_st, m->HD, h->mode, m->base, m->gemma ? 10000.0f : m->base,
                       m->freq_global, m->gemma ? m->freq_local : m->freq_global, h->rope, s);
-    T(5, false);
+    T(8, false);
     for (int l = 0; l < m->NL; l++) {
         const DevLayer &d = m->L[l];
         const bool glob = is_global(m, l);
@@ -523,8 +523,8 @@ void enqueue_body(sp_kvdecode_handle *h, const StepShape &sh, TimeCb cb, void *c
         a.base = (m->gemma && !glob) ? 10000.0f : m->base;
         a.ascale = 1.0f / sqrtf((float)m->HD);
         a.chunk = glob ? sh.chunk_global : sh.chunk_local;
-        T(4, true); launch_qk_prep(a, s); T(4, false);
-        const int cls = (glob || a.win < 0) ? 2 : 3;
+        T(7, true); launch_qk_prep(a, s); T(7, false);
+        const int cls = (glob || a.win < 0) ? 5 : 6;
         T(cls, true); launch_attention(a, glob ? sh.grid_global : sh.grid_local, s); T(cls, false);
 
         GemvArgs o{};
@@ -532,7 +532,7 @@ void enqueue_body(sp_kvdecode_handle *h, const StepShape &sh, TimeCb cb, void *c
         o.mode = h->mode; o.cols = QD; o.act = ACT_NONE; o.nseg = 1;
         o.pro.kind = PRO_PLAIN; o.pro.x = h->ao; o.pro.n = QD;
         o.seg[0] = {d.o, h->ap};
-        T(0, true); launch_gemv(o, m->E, s); T(0, false);
+        T(1, true); launch_gemv(o, m->E, s); T(1, false);
 
         GemvArgs f{};
         f.accbuf = h->gacc; f.gcnt = h->gcnt; f.acc_rows = h->acc_rows;
@@ -540,14 +540,14 @@ void enqueue_body(sp_kvdecode_handle *h, const StepShape &sh, TimeCb cb, void *c
         f.pro.kind = PRO_RESID; f.pro.x = h->x1; f.pro.delta = h->ap; f.pro.post_w = d.post_attn;
         f.pro.norm_w = d.ffn_norm; f.pro.x_out = h->x0; f.pro.n = m->E; f.pro.eps = m->eps;
         f.seg[0] = {d.gate, h->gg}; f.seg[1] = {d.up, h->uu}; f.act_out = h->hh;
-        T(0, true); launch_gemv(f, m->FF, s); T(0, false);
+        T(2, true); launch_gemv(f, m->FF, s); T(2, false);
 
         GemvArgs dd{};
         dd.accbuf = h->gacc; dd.gcnt = h->gcnt; dd.acc_rows = h->acc_rows;
         dd.mode = h->mode; dd.cols = m->FF; dd.act = ACT_NONE; dd.nseg = 1;
         dd.pro.kind = PRO_PLAIN; dd.pro.x = h->hh; dd.pro.n = m->FF;
         dd.seg[0] = {d.down, h->dn};
-        T(0, true); launch_gemv(dd, m->E, s); T(0, false);
+        T(3, true); launch_gemv(dd, m->E, s); T(3, false);
     }
     if (sh.logits) {
         GemvArgs lm{};
@@ -557,11 +557,11 @@ void enqueue_body(sp_kvdecode_handle *h, const StepShape &sh, TimeCb cb, void *c
         lm.pro.post_w = m->gemma ? m->L[m->NL - 1].post_ffw : nullptr;
         lm.pro.norm_w = m->out_norm; lm.pro.x_out = nullptr; lm.pro.n = m->E; lm.pro.eps = m->eps;
         lm.seg[0] = {m->out, h->logits};
-        T(1, true); launch_gemv(lm, m->V, s); T(1, false);
+        T(4, true); launch_gemv(lm, m->V, s); T(4, false);
         if (sh.argmax) {
-            T(5, true);
+            T(8, true);
             launch_argmax(h->logits, m->V, h->am_v, h->am_i, h->am_cnt, h->d_st, h->gen_log, argmax_blocks(m->V), s);
-            T(5, false);
+            T(8, false);
         }
     } else {
         launch_advance(h->d_st, s);
@@ -971,8 +971,8 @@ int sp_hipkv_greedy(sp_kvdecode_handle *h, int32_t first_token, int n, int32_t *
     return 0;
 }
 
-int sp_hipkv_kernel_times(sp_kvdecode_handle *h, int32_t first_token, int n, double ms[6],
-                          long long launches[6], double bytes[6]) {
+int sp_hipkv_kernel_times(sp_kvdecode_handle *h, int32_t first_token, int n, double ms[SP_HIPKV_NCLASS],
+                          long long launches[SP_HIPKV_NCLASS], double bytes[SP_HIPKV_NCLASS]) {
     if (!h || n <= 0 || !ms || !launches || !bytes) return fail("sp_hipkv_kernel_times: bad argument%s");
     if (check_tok(h, first_token)) return 1;
     if (n > h->pmax - h->dpos) return fail("sp_hipkv_kernel_times: context full%s");
@@ -985,20 +985,31 @@ int sp_hipkv_kernel_times(sp_kvdecode_handle *h, int32_t first_token, int n, dou
         hipEvent_t e; hipEventCreate(&e); hipEventRecord(e, cc->s);
         if (begin) cc->cur = e; else cc->ev.push_back({cls, {cc->cur, e}});
     };
-    for (int i = 0; i < 6; i++) { ms[i] = 0; launches[i] = 0; bytes[i] = 0; }
+    for (int i = 0; i < SP_HIPKV_NCLASS; i++) { ms[i] = 0; launches[i] = 0; bytes[i] = 0; }
     const DevModel *m = h->m;
     const double kvb = (double)m->NKV * m->HD * 4 * 2;     // K+V bytes per position per layer
+    // algorithmic bytes of one GEMV: Q4B codes + f16 block scales, input and output vectors
+    auto gb = [](const DevW &w) {
+        return (double)w.rows * (w.cols / 2) + 2.0 * w.rows * w.nblk + 4.0 * w.cols + 4.0 * w.rows;
+    };
+    double per_step[SP_HIPKV_NCLASS] = {0};
+    for (const DevLayer &d : m->L) {
+        per_step[0] += gb(d.q) + gb(d.k) + gb(d.v) - 8.0 * d.k.cols;   // one shared input vector
+        per_step[1] += gb(d.o);
+        per_step[2] += gb(d.gate) + gb(d.up) + 4.0 * d.gate.rows - 4.0 * d.gate.cols;   // + act output
+        per_step[3] += gb(d.down);
+    }
+    per_step[4] = gb(m->out);
+    per_step[8] = (double)(m->embd.cols / 2 + m->embd.nblk * 2) + 4.0 * m->V;   // one embedding row + logits read by argmax
     for (int i = 0; i < n; i++) {
         const int pos = h->dpos + i;
         StepShape sh = shape_for(h, pos, 1, 1);
         enqueue_body(h, sh, cb, &c);
-        bytes[0] += (double)m->layer_bytes;
-        bytes[1] += (double)m->lm_bytes;
-        bytes[5] += (double)(m->embd.cols / 2 + m->embd.nblk * 2) + 4.0 * m->V;   // one embedding row + logits read by argmax
+        for (int k = 0; k < SP_HIPKV_NCLASS; k++) bytes[k] += per_step[k];
         for (int l = 0; l < m->NL; l++) {
             const bool glob = is_global(m, l);
             const int s0 = (!glob && m->SW > 0 && pos - m->SW + 1 > 0) ? pos - m->SW + 1 : 0;
-            bytes[(glob || m->SW <= 0) ? 2 : 3] += kvb * (pos - s0 + 1);
+            bytes[(glob || m->SW <= 0) ? 5 : 6] += kvb * (pos - s0 + 1);
         }
     }
     HIPCHK(hipStreamSynchronize(h->stream), "timed run");

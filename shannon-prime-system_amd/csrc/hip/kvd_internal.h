@@ -35,23 +35,6 @@ struct ProArgs {
     float eps;
 };
 
-struct Seg { DevW w; float *out; };
-enum Act { ACT_NONE = 0, ACT_GELU = 1, ACT_SILU = 2 };
-struct GemvArgs {
-    ProArgs pro;
-    Seg  seg[3];
-    int  nseg;
-    int  cols;
-    int  act;          // paired gate/up with activation: seg[0] = gate, seg[1] = up
-    float *act_out;    // h = act(gate) * up
-    int  mode;
-    int64_t *accbuf;   // split-K row totals [acc_rows] (zero between launches)
-    int  *gcnt;        // split arrival counters per row group [acc_rows] (zero between launches)
-    int  acc_rows;
-    int  nsplit, bps, groups;   // filled in by launch_gemv
-};
-struct GemvPlan { int groups, nsplit, bps, grid; };
-
 // Per-session device-side step state (graph-replay friendly: kernels read it).
 struct DState {
     int pos;           // position of the token being processed
@@ -89,6 +72,23 @@ struct AttnArgs {
     // qk_prep, blockIdx.z of attention); every per-token buffer is [nt][...]
     int nt, pos0, rope_stride;
 };
+
+struct Seg { DevW w; float *out; };
+enum Act { ACT_NONE = 0, ACT_GELU = 1, ACT_SILU = 2 };
+struct GemvArgs {
+    ProArgs pro;
+    Seg  seg[3];
+    int  nseg;
+    int  cols;
+    int  act;          // paired gate/up with activation: seg[0] = gate, seg[1] = up
+    float *act_out;    // h = act(gate) * up
+    int  mode;
+    int64_t *accbuf;   // split-K row totals [acc_rows] (zero between launches)
+    int  *gcnt;        // split arrival counters per row group [acc_rows] (zero between launches)
+    int  acc_rows;
+    int  nsplit, bps, groups;   // filled in by launch_gemv
+};
+struct GemvPlan { int groups, nsplit, bps, grid; };
 
 // Per-token GEMM input staging (batched prefill): the GEMV input transform of
 // token t's vector (pro pointers + t * n), then xq's three balanced base-256

@@ -1,0 +1,141 @@
+// kvd_qkprep.h -- one attention head's input preparation by one wave: per-head
+// RMSNorm, NEOX RoPE, and the K/V append into the paged store.
+//
+// Reference: core/session/sp_session.c:292-294 / :405-407 (sp_rmsnorm_head +
+// sp_rope_neox, forward_kernels.c:24-41) and the KV store at :321-323 (K after
+// norm and RoPE, V raw).
+#pragma once
+#include "kvd_internal.h"
+#include "kvd_exact.h"
+
+namespace kvd {
+
+// the fields of the attention arguments the head preparation reads
+struct HeadPrep {
+    const float *q, *k, *v, *q_norm, *k_norm, *rope_cs;
+    float *qr;
+    float *const *pages;
+    int ring_pages, NH, NKV, HD, mode;
+    float eps;
+};
+__device__ __forceinline__ HeadPrep head_prep_of(const AttnArgs &a) {
+    HeadPrep p;
+    p.q = a.q; p.k = a.k; p.v = a.v; p.q_norm = a.q_norm; p.k_norm = a.k_norm; p.rope_cs = a.rope_cs;
+    p.qr = a.qr; p.pages = a.pages; p.ring_pages = a.ring_pages; p.NH = a.NH; p.NKV = a.NKV; p.HD = a.HD;
+    p.mode = a.mode; p.eps = a.eps;
+    return p;
+}
+
+__device__ __forceinline__ float *qk_page_of(float *const *pages, int ring, int pos) {
+    const int lp = pos / PAGE;
+    return pages[ring ? lp % ring : lp];
+}
+
+// hb < NH: q head hb -> qr; hb < NH + NKV: k head -> page; else v head -> page.
+// src: the head's HD projections; lane l holds elements l + 64 j.  COHERENT
+// selects agent-scope loads, for projections written by other workgroups of
+// the same launch.
+template <bool COHERENT, int PER>
+__device__ __forceinline__ void qk_prep_head_t(const HeadPrep a, int hb, int pos, int lane) {
+    constexpr int HD = PER * 64, half = HD / 2, per = PER;
+    const bool isq = hb < a.NH, isk = !isq && hb < a.NH + a.NKV;
+    const int h = isq ? hb : (isk ? hb - a.NH : hb - a.NH - a.NKV);
+    float *page = qk_page_of(a.pages, a.ring_pages, pos);
+    const int slot = pos % PAGE;
+    const float *src = isq ? a.q + (size_t)h * HD : (isk ? a.k : a.v) + (size_t)h * HD;
+    float v[8];                                                 // HD <= 512
+    #pragma unroll
+    for (int j = 0; j < 8; j++)
+        if (j < per) v[j] = COHERENT ? ld_agent(&src[lane + 64 * j]) : src[lane + 64 * j];
+    if (!isq && !isk) {                                         // V: raw (exact: Q16 grid, clamped)
+        float *dst = page + (size_t)a.NKV * PAGE * HD + ((size_t)h * PAGE + slot) * HD;
+        #pragma unroll
+        for (int j = 0; j < 8; j++) {
+            if (j >= per) break;
+            if (a.mode == FLOAT) dst[lane + 64 * j] = v[j];
+            else {
+                float r = rintf(v[j] * 65536.0f);
+                r = fminf(fmaxf(r, -8388607.0f), 8388607.0f);
+                ((int32_t *)dst)[lane + 64 * j] = (int32_t)r;
+            }
+        }
+        return;
+    }
+    const float *nw = isq ? a.q_norm : a.k_norm;
+    // per-head RMSNorm
+    if (a.mode == FLOAT) {
+        double ss = 0.0;
+        #pragma unroll
+        for (int j = 0; j < 8; j++) if (j < per) ss += (double)v[j] * (double)v[j];
+        #pragma unroll
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        const float sc = 1.0f / sqrtf((float)(ss / HD) + a.eps);
+        #pragma unroll
+        for (int j = 0; j < 8; j++) if (j < per) v[j] = v[j] * sc * nw[lane + 64 * j];
+    } else {
+        int64_t ss = 0;
+        #pragma unroll
+        for (int j = 0; j < 8; j++) if (j < per) { const int64_t xi = llround_pow2<16>(v[j]); ss += xi * xi; }
+        #pragma unroll
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        if (ss == 0) {
+            #pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = 0.0f;
+        } else {
+            const int64_t inv = rms_inv_q72(HD, ss);
+            #pragma unroll
+            for (int j = 0; j < 8; j++) {
+                if (j >= per) break;
+                const int64_t xi = llround_pow2<16>(v[j]), wi = llround_pow2<16>(nw[lane + 64 * j]);
+                v[j] = (float)((double)mul3_lo64(xi, inv, wi) / 4503599627370496.0);
+            }
+        }
+    }
+    // NEOX RoPE on pairs (i, i + half), cos/sin from this position's table.
+    // HD >= 128: both halves of a pair sit in the same lane (j and j + per/2);
+    // HD == 64: the partner is lane ^ 32.
+    const float *cs = a.rope_cs;
+    float out[8];
+    if (per >= 2) {
+        #pragma unroll
+        for (int j = 0; j < 4; j++) {
+            if (j >= per / 2) break;
+            const int i = lane + 64 * j;
+            const float x0 = v[j], x1 = v[j + per / 2], c = cs[i], s = cs[half + i];
+            const float ac = x0 * c, bs = x1 * s, as = x0 * s, bc = x1 * c;
+            out[j] = ac - bs;
+            out[j + per / 2] = as + bc;
+        }
+    } else {
+        const float other = __shfl_xor(v[0], 32, 64);
+        const bool first = lane < 32;
+        const int i = first ? lane : lane - 32;
+        const float x0 = first ? v[0] : other, x1 = first ? other : v[0], c = cs[i], s = cs[half + i];
+        const float ac = x0 * c, bs = x1 * s, as = x0 * s, bc = x1 * c;
+        out[0] = first ? ac - bs : as + bc;
+    }
+    if (isq) {
+        #pragma unroll
+        for (int j = 0; j < 8; j++) if (j < per) a.qr[(size_t)h * HD + lane + 64 * j] = out[j];
+    } else {
+        float *dst = page + ((size_t)h * PAGE + slot) * HD;
+        #pragma unroll
+        for (int j = 0; j < 8; j++) {
+            if (j >= per) break;
+            if (a.mode == FLOAT) dst[lane + 64 * j] = out[j];
+            else ((int32_t *)dst)[lane + 64 * j] = (int32_t)rintf(out[j] * 65536.0f);
+        }
+    }
+}
+// head_dim 64 / 128 / 256 / 512: register arrays with compile-time indices
+template <bool COHERENT>
+__device__ __forceinline__ void qk_prep_head(const HeadPrep a, int hb, int pos, int lane) {
+    switch (a.HD) {
+    case 64:  qk_prep_head_t<COHERENT, 1>(a, hb, pos, lane); break;
+    case 128: qk_prep_head_t<COHERENT, 2>(a, hb, pos, lane); break;
+    case 256: qk_prep_head_t<COHERENT, 4>(a, hb, pos, lane); break;
+    default:  qk_prep_head_t<COHERENT, 8>(a, hb, pos, lane); break;
+    }
+}
+
+}  // namespace kvd

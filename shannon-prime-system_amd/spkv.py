@@ -223,6 +223,9 @@ class Session:
             self.h = None
 
 
+NCLASS = 9          # kernel classes of sp_hipkv_kernel_times (include/sp_hipkv.h)
+
+
 class Backend:
     """A bare section-6b handle driven through the dispatch functions directly."""
 
@@ -271,9 +274,9 @@ class Backend:
 
     def kernel_times(self, first_tok, n):
         import numpy as np
-        ms = np.zeros(6, np.float64)
-        nl = np.zeros(6, np.int64)
-        by = np.zeros(6, np.float64)
+        ms = np.zeros(NCLASS, np.float64)
+        nl = np.zeros(NCLASS, np.int64)
+        by = np.zeros(NCLASS, np.float64)
         check(kv().sp_hipkv_kernel_times(self.h, int(first_tok), n, ptr(ms), ptr(nl), ptr(by)),
               "sp_hipkv_kernel_times")
         return ms, nl, by
