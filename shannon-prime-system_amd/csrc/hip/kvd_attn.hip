@@ -115,7 +115,7 @@ __device__ __forceinline__ void tok_select(AttnArgs &a, int t, int &pos) {
     a.part_ml += t * (size_t)a.NH * a.max_chunks * 4;
     a.counter += t * a.NKV;
     a.zscratch += t * (size_t)a.NH * a.zstride;
-    a.vacc += t * QD; a.vacc_s += t * a.NH;
+    a.vacc += t * QD * VREP; a.vacc_s += t * a.NH * VREP;
     a.rope_cs += t * (size_t)a.rope_stride;
 }
 
@@ -212,11 +212,11 @@ constexpr int UNR = 4;           // positions in flight per wave
 // UNR rows j0.. of the chunk (zeros past n); the loops below load the next
 // UNR rows before working on the current ones, so a wave always has a row
 // group in flight
-template <int EPL, typename T>
+template <int EPL, typename T, int R = UNR>
 __device__ __forceinline__ void load_rows(const AttnArgs &a, int h, int cs, int j0, int n, bool vpart, int lane,
-                                          T out[UNR][EPL]) {
+                                          T out[R][EPL]) {
     #pragma unroll
-    for (int u = 0; u < UNR; u++) {
+    for (int u = 0; u < R; u++) {
         if (j0 + u < n) load_row<EPL>(a, h, cs + j0 + u, vpart, lane, out[u]);
         else {
             #pragma unroll
@@ -409,6 +409,18 @@ __global__ __launch_bounds__(256) void k_attn_exact_scores(AttnArgs a_in) {
     if (c >= nch) return;
     __shared__ int zmax[4][G];
     __shared__ int4 qs[G][EPL * 16];                 // qi = rne(q * 2^16), 4 dims per entry
+    const int r = lane >> 2, k4 = lane & 3;
+    const int n = ce - cs;
+    // the wave's first row group is requested before q is staged
+    int4 kv[4 * EPL];
+    {
+        const int j = wave * 16 + r;
+        if (j < n) {
+            const int32_t *row = quad_row<EPL, int32_t>(a, h, cs + wave * 16, ce - 1, cs + j, false) + 4 * k4;
+            #pragma unroll
+            for (int i = 0; i < 4 * EPL; i++) kv[i] = *(const int4 *)(row + 16 * i);
+        }
+    }
     for (int i = threadIdx.x; i < G * HD / 4; i += 256) {
         const int g = i / (HD / 4), d4 = i % (HD / 4);
         const float *qp = a.qr + (size_t)(h * G + g) * HD + 4 * d4;
@@ -416,19 +428,18 @@ __global__ __launch_bounds__(256) void k_attn_exact_scores(AttnArgs a_in) {
                               (int)rintf(qp[2] * 65536.0f), (int)rintf(qp[3] * 65536.0f));
     }
     __syncthreads();
-    const int r = lane >> 2, k4 = lane & 3;
     int mx = INT32_MIN;                              // lane with k4 == g tracks head g
-    const int n = ce - cs;
     for (int j0 = wave * 16; j0 < n; j0 += 64) {
         const int j = j0 + r;
         int64_t acc[G];
         #pragma unroll
         for (int g = 0; g < G; g++) acc[g] = 0;
         if (j < n) {
-            const int32_t *row = quad_row<EPL, int32_t>(a, h, cs + j0, ce - 1, cs + j, false) + 4 * k4;
-            int4 kv[4 * EPL];
-            #pragma unroll
-            for (int i = 0; i < 4 * EPL; i++) kv[i] = *(const int4 *)(row + 16 * i);
+            if (j0 != wave * 16) {
+                const int32_t *row = quad_row<EPL, int32_t>(a, h, cs + j0, ce - 1, cs + j, false) + 4 * k4;
+                #pragma unroll
+                for (int i = 0; i < 4 * EPL; i++) kv[i] = *(const int4 *)(row + 16 * i);
+            }
             #pragma unroll
             for (int i = 0; i < 4 * EPL; i++)
                 #pragma unroll
@@ -482,11 +493,25 @@ __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a_in) {
     int cs, ce, nch;
     chunk_range(a, pos, c, cs, ce, nch);
     if (c >= nch) return;
-    __shared__ int64_t ew[G][MAXCH];
+    __shared__ int32_t ew[G][MAXCH];                // island weights in Q22 (<= 2^22)
     __shared__ int64_t ored[4][G][EPL * 64];
     __shared__ int redi[4][G];
     __shared__ int64_t redl[4];
     __shared__ int is_last;
+    const int n = ce - cs;
+    // the first V rows and this chunk's scores are requested before the
+    // global-max reduction, so their latency overlaps it
+    constexpr int UV = 2 * UNR;                       // V rows per wave in flight
+    int32_t vv[UV][EPL], vn[UV][EPL];
+    load_rows<EPL, int32_t, UV>(a, h, cs, wave * UV, n, true, lane, vv);
+    constexpr int ZPT = G * MAXCH / 256;              // score slots per thread
+    int32_t zr[ZPT];
+    #pragma unroll
+    for (int k = 0; k < ZPT; k++) {
+        const int i = threadIdx.x + 256 * k;
+        const int g = i / MAXCH, j = i % MAXCH;
+        zr[k] = j < n ? a.zscratch[(size_t)(h * G + g) * a.zstride + (size_t)(cs + j)] : 0;
+    }
     const int32_t *pml = (const int32_t *)a.part_ml;
     // global max of the attended window over every chunk's maximum
     int M[G];
@@ -508,11 +533,11 @@ __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a_in) {
         for (int w = 1; w < 4; w++) t = redi[w][g] > t ? redi[w][g] : t;
         M[g] = t;
     }
-    const int n = ce - cs;
-    for (int i = threadIdx.x; i < G * n; i += 256) {
-        const int g = i / n, j = i % n;
-        const int64_t z = a.zscratch[(size_t)(h * G + g) * a.zstride + (size_t)(cs + j)];
-        ew[g][j] = exp_fixed(((z - (int64_t)M[g]) * ONE) >> 14) >> 8;
+    #pragma unroll
+    for (int k = 0; k < ZPT; k++) {
+        const int i = threadIdx.x + 256 * k;
+        const int g = i / MAXCH, j = i % MAXCH;
+        if (j < n) ew[g][j] = (int32_t)(exp_fixed((((int64_t)zr[k] - (int64_t)M[g]) * ONE) >> 14) >> 8);
     }
     __syncthreads();
     int64_t o[G][EPL];
@@ -520,20 +545,18 @@ __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a_in) {
     for (int g = 0; g < G; g++)
         #pragma unroll
         for (int e = 0; e < EPL; e++) o[g][e] = 0;
-    int32_t vv[UNR][EPL], vn[UNR][EPL];
-    load_rows<EPL>(a, h, cs, wave * UNR, n, true, lane, vv);
-    for (int j0 = wave * UNR; j0 < n; j0 += 4 * UNR) {
-        load_rows<EPL>(a, h, cs, j0 + 4 * UNR, n, true, lane, vn);
+    for (int j0 = wave * UV; j0 < n; j0 += 4 * UV) {
+        load_rows<EPL, int32_t, UV>(a, h, cs, j0 + 4 * UV, n, true, lane, vn);
         #pragma unroll
-        for (int u = 0; u < UNR; u++) {
+        for (int u = 0; u < UV; u++) {
             if (j0 + u >= n) break;
             #pragma unroll
             for (int g = 0; g < G; g++)
                 #pragma unroll
-                for (int e = 0; e < EPL; e++) o[g][e] += ew[g][j0 + u] * (int64_t)vv[u][e];
+                for (int e = 0; e < EPL; e++) o[g][e] += (int64_t)ew[g][j0 + u] * (int64_t)vv[u][e];   // 32x32 -> 64
         }
         #pragma unroll
-        for (int u = 0; u < UNR; u++)
+        for (int u = 0; u < UV; u++)
             #pragma unroll
             for (int e = 0; e < EPL; e++) vv[u][e] = vn[u][e];
     }
@@ -542,11 +565,16 @@ __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a_in) {
         #pragma unroll
         for (int e = 0; e < EPL; e++) ored[wave][g][lane * EPL + e] = o[g][e];
     __syncthreads();
-    // exact, order-free accumulation of this chunk into the kv-head's totals
+    // exact, order-free accumulation of this chunk into the kv-head's totals;
+    // VREP replicas (chunk c adds into replica c % VREP) spread the same-address
+    // atomics, the last workgroup sums them
+    const size_t QDh = (size_t)a.NH * HD;
+    int64_t *vrep = a.vacc + (size_t)(c % VREP) * QDh;
+    int64_t *srep = a.vacc_s + (size_t)(c % VREP) * a.NH;
     for (int i = threadIdx.x; i < G * HD; i += 256) {
         const int g = i / HD, d = i % HD;
         const int64_t t = ored[0][g][d] + ored[1][g][d] + ored[2][g][d] + ored[3][g][d];
-        atomicAdd((unsigned long long *)&a.vacc[(size_t)(h * G + g) * HD + d], (unsigned long long)t);
+        atomicAdd((unsigned long long *)&vrep[(size_t)(h * G + g) * HD + d], (unsigned long long)t);
     }
     #pragma unroll
     for (int g = 0; g < G; g++) {
@@ -556,7 +584,7 @@ __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a_in) {
         if (lane == 0) redl[wave] = S;
         __syncthreads();
         if (threadIdx.x == 0)
-            atomicAdd((unsigned long long *)&a.vacc_s[h * G + g], (unsigned long long)(redl[0] + redl[1] + redl[2] + redl[3]));
+            atomicAdd((unsigned long long *)&srep[h * G + g], (unsigned long long)(redl[0] + redl[1] + redl[2] + redl[3]));
         __syncthreads();
     }
     mem_complete();
@@ -565,17 +593,23 @@ __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a_in) {
     __syncthreads();
     if (!is_last) return;
     // the totals are read and cleared for the next launch in one atomic step
-    for (int i = threadIdx.x; i < G * HD; i += 256) {
-        const int g = i / HD;
-        const int64_t acc = (int64_t)__hip_atomic_exchange((unsigned long long *)&a.vacc[(size_t)h * G * HD + i], 0ull,
-                                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const int64_t S = (int64_t)__hip_atomic_fetch_add((unsigned long long *)&a.vacc_s[h * G + g], 0ull,
-                                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        a.ao[(size_t)h * G * HD + i] = rne_div_to_float((i128)acc, S, 16);
+    __shared__ int64_t Sg[G];
+    if (threadIdx.x < G) {
+        int64_t S = 0;
+        for (int r = 0; r < VREP; r++)
+            S += (int64_t)__hip_atomic_exchange((unsigned long long *)&a.vacc_s[(size_t)r * a.NH + h * G + threadIdx.x], 0ull,
+                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        Sg[threadIdx.x] = S;
     }
     __syncthreads();
-    if (threadIdx.x < G) __hip_atomic_exchange((unsigned long long *)&a.vacc_s[h * G + threadIdx.x], 0ull,
-                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int i = threadIdx.x; i < G * HD; i += 256) {
+        int64_t acc = 0;
+        #pragma unroll
+        for (int r = 0; r < VREP; r++)
+            acc += (int64_t)__hip_atomic_exchange((unsigned long long *)&a.vacc[(size_t)r * QDh + (size_t)h * G * HD + i], 0ull,
+                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        a.ao[(size_t)h * G * HD + i] = rne_div_to_float((i128)acc, Sg[i / HD], 16);
+    }
     if (threadIdx.x == 0) reset_counter(&a.counter[h]);
 }
 

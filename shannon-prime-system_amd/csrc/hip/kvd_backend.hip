@@ -447,7 +447,7 @@ int alloc_scratch(sp_kvdecode_handle *h) {
         {(void **)&h->zscratch, z_bytes}, {(void **)&h->counter, 64 * 4}, {(void **)&h->am_v, (size_t)amb * 4},
         {(void **)&h->am_i, (size_t)amb * 4}, {(void **)&h->am_cnt, 64}, {(void **)&h->gen_log, (size_t)h->pmax * 4 + 64},
         {(void **)&h->tokbuf, (size_t)h->pmax * 4 + 64}, {(void **)&h->rope, (size_t)m->HD * 2 * 4},
-        {(void **)&h->vacc, (size_t)QD * 8}, {(void **)&h->vacc_s, (size_t)m->NH * 8},
+        {(void **)&h->vacc, (size_t)QD * 8 * VREP}, {(void **)&h->vacc_s, (size_t)m->NH * 8 * VREP},
         {(void **)&h->d_st, sizeof(DState) * 4},
     };
     size_t tot = 0;
@@ -606,7 +606,7 @@ int alloc_batch(sp_kvdecode_handle *h) {
         {(void **)&b.zs, TB * m->NH * (size_t)h->max_chunks * 16 * 4},
         {(void **)&b.part_ml, TB * m->NH * (size_t)b.mcb * 16},
         {(void **)&b.part, h->mode == FLOAT ? TB * m->NH * (size_t)b.mcb * m->HD * 4 : 256},
-        {(void **)&b.vacc, TB * QD * 8}, {(void **)&b.vacc_s, TB * m->NH * 8},
+        {(void **)&b.vacc, TB * QD * 8 * VREP}, {(void **)&b.vacc_s, TB * m->NH * 8 * VREP},
     };
     size_t tot = 0;
     for (auto &it : items) tot = align_up(tot + it.n, 256);

@@ -42,15 +42,21 @@ __device__ __forceinline__ uint64_t isqrt_u64(uint64_t v) {
     return x;
 }
 // floor(num / den) for 0 <= num < 2^127, 0 < den < 2^63 with a quotient below
-// 2^64: double estimate refined twice, then exact +-1 correction
+// 2^64: double estimate refined twice, then exact +-1 correction.  128-bit
+// values go to double through their two 64-bit halves (one rounding each).
+__device__ __forceinline__ double u128_to_double(u128 v) {
+    return fma((double)(uint64_t)(v >> 64), 18446744073709551616.0, (double)(uint64_t)v);
+}
+__device__ __forceinline__ double i128_to_double(i128 v) {
+    return fma((double)(int64_t)(v >> 64), 18446744073709551616.0, (double)(uint64_t)v);
+}
 __device__ __forceinline__ uint64_t udiv128_64(u128 num, uint64_t den) {
     if ((uint64_t)(num >> 64) >= den) return (uint64_t)(num / (u128)den);   // quotient >= 2^64: wraps like the cast
     const double dd = (double)den;
-    uint64_t q = (uint64_t)fmin((double)num / dd, 1.8446744073709550e19);
+    uint64_t q = (uint64_t)fmin(u128_to_double(num) / dd, 1.8446744073709550e19);
     for (int it = 0; it < 2; it++) {
         const i128 r = (i128)num - (i128)((u128)q * den);
-        const double adj = (double)r / dd;
-        q = (uint64_t)((i128)q + (i128)adj);
+        q += (uint64_t)(int64_t)(i128_to_double(r) / dd);   // |step| <= q * 2^-51, wraps like the sum
     }
     i128 r = (i128)num - (i128)((u128)q * den);
     while (r < 0) { q--; r += den; }

@@ -316,7 +316,9 @@ GemvPlan gemv_plan(int nrows_total, int cols, int paired, int wide) {
     const int cap = 2 * num_cu();                       // workgroups
     const int max_split = (nblk + 63) / 64;
     int want = (cap * GEMV_WAVES + p.groups - 1) / p.groups;
-    if (wide || want < 1) want = 1;
+    // a split costs every task an atomic hand-off; it only pays when whole
+    // rows would leave more than half of the waves idle
+    if (wide || want <= 2) want = 1;
     p.nsplit = want < max_split ? want : max_split;
     p.bps = 64 * ((max_split + p.nsplit - 1) / p.nsplit);
     p.nsplit = (nblk + p.bps - 1) / p.bps;

@@ -10,6 +10,7 @@ constexpr int PAGE = 64;            // positions per KV page
 constexpr int GEMV_WAVES = 8;       // waves per GEMV workgroup (512 threads)
 constexpr int GEMV_R = 8;           // rows per wave pass
 constexpr int NDIG = 6;             // balanced base-16 digit planes of an activation (|xq| < 2^22)
+constexpr int VREP = 4;             // replicas of the exact V-sum accumulators
 
 enum Mode { FLOAT = 0, EXACT = 1 };
 
@@ -61,8 +62,8 @@ struct AttnArgs {
     float *part_ml;          // [NKV*G][max_chunks][2] (max, sum) or exact (max, S lo/hi)
     int   *counter;          // [NKV] arrival counters (self-resetting)
     int   *zscratch;         // exact mode: int32 score grid [NH][max_chunks*16] by absolute position
-    int64_t *vacc;           // exact mode: V-sum totals [NH][HD] (atomic, order-free)
-    int64_t *vacc_s;         // exact mode: softmax denominators [NH]
+    int64_t *vacc;           // exact mode: V-sum totals [VREP][NH][HD] (atomic, order-free)
+    int64_t *vacc_s;         // exact mode: softmax denominators [VREP][NH]
     const DState *st;
     const float *rope_cs;    // this step's rotation table for the layer's base: cos[HD/2], sin[HD/2]
     int NH, NKV, HD, win, max_chunks, chunk, mode;
