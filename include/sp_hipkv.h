@@ -53,6 +53,18 @@ int  sp_hipkv_fork(const sp_kvdecode_handle *parent, sp_kvdecode_handle **child)
  * sp_session_register_kvdecode_backend + ownership (closed with the session). */
 sp_status sp_hipkv_attach(sp_session *s, int pmax, int exact);
 
+/* Batched decode across sessions (many concurrent sessions of one model): hs[i]
+ * (opened on the same model, with the same mode, pmax and window ring) decodes
+ * tokens[i] at its own position and advances by one.  The projections run once
+ * for all rows as int8-MFMA GEMMs; each row's attention reads its own session's
+ * pages.  logits: n x vocab floats, row-major, host memory (may be NULL);
+ * next_tokens: n greedy tokens (lowest index on ties, may be NULL).  Exact mode
+ * gives the logits sp_hipkv_decode_step gives on each handle, bit for bit.  No
+ * counterpart in the reference's table (sp_l1.h:403-410 decodes one session per
+ * call); it serves the batched multi-session configuration. */
+int  sp_hipkv_decode_batch(sp_kvdecode_handle *const *hs, int n, const int32_t *tokens, float *logits,
+                           int32_t *next_tokens);
+
 /* ---- device-resident driver entry points (bench / tests) ---- */
 /* n greedy steps entirely on the device (argmax feeds the next token, no host
  * round trip), starting with `first_token` at dpos; writes the n generated

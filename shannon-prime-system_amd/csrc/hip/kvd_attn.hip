@@ -108,7 +108,8 @@ __device__ __forceinline__ float *page_of(float *const *pages, int ring, int pos
 template <bool BATCH>
 __device__ __forceinline__ void tok_select(AttnArgs &a, int t, int &pos) {
     if constexpr (!BATCH) { pos = a.st->pos; return; }
-    pos = a.pos0 + t;
+    pos = a.tpos ? a.tpos[t] : a.pos0 + t;
+    if (a.tpages) a.pages = a.tpages[t];
     const size_t QD = (size_t)a.NH * a.HD, KVD = (size_t)a.NKV * a.HD;
     a.q += t * QD; a.k += t * KVD; a.v += t * KVD; a.qr += t * QD; a.ao += t * QD;
     a.part += t * (size_t)a.NH * a.max_chunks * a.HD;
@@ -133,10 +134,11 @@ __global__ __launch_bounds__(64) void k_qk_prep(AttnArgs a_in) {
 // out[t][0..half) = cos, out[t][half..HD) = sin, t = 0 global base, 1 window base.
 // Float mode: freq = powf(base, -2i/d), theta = (float)p*freq, cosf/sinf
 // (forward_kernels.c:31-41); exact mode: p*F_i mod 2*pi (Q60) by CORDIC, RNE.
-__global__ __launch_bounds__(256) void k_rope_table(const DState *st, int pos0, int HD, int mode, float base_g, float base_l,
-                                                     const int64_t *fq_g, const int64_t *fq_l, float *out) {
-    // decode: one workgroup at the step's position; batched: workgroup t at pos0 + t
-    const int half = HD / 2, pos = st ? st->pos : pos0 + (int)blockIdx.x;
+__global__ __launch_bounds__(256) void k_rope_table(const DState *st, int pos0, const int *tpos, int HD, int mode, float base_g,
+                                                     float base_l, const int64_t *fq_g, const int64_t *fq_l, float *out) {
+    // decode: one workgroup at the step's position; batched: workgroup t at
+    // tpos[t] (several sessions) or pos0 + t (one session's prefill)
+    const int half = HD / 2, pos = st ? st->pos : (tpos ? tpos[blockIdx.x] : pos0 + (int)blockIdx.x);
     out += (size_t)blockIdx.x * 2 * HD;
     for (int idx = threadIdx.x; idx < 2 * half; idx += blockDim.x) {
         const int t = idx / half, i = idx % half;
@@ -156,11 +158,11 @@ __global__ __launch_bounds__(256) void k_rope_table(const DState *st, int pos0, 
 }
 void launch_rope_table(const DState *st, int HD, int mode, float base_g, float base_l,
                        const int64_t *fq_g, const int64_t *fq_l, float *out, hipStream_t s) {
-    hipLaunchKernelGGL(k_rope_table, dim3(1), dim3(256), 0, s, st, 0, HD, mode, base_g, base_l, fq_g, fq_l, out);
+    hipLaunchKernelGGL(k_rope_table, dim3(1), dim3(256), 0, s, st, 0, nullptr, HD, mode, base_g, base_l, fq_g, fq_l, out);
 }
 void launch_rope_table_batch(int pos0, int T, int HD, int mode, float base_g, float base_l,
-                             const int64_t *fq_g, const int64_t *fq_l, float *out, hipStream_t s) {
-    hipLaunchKernelGGL(k_rope_table, dim3(T), dim3(256), 0, s, nullptr, pos0, HD, mode, base_g, base_l, fq_g, fq_l, out);
+                             const int64_t *fq_g, const int64_t *fq_l, float *out, hipStream_t s, const int *tpos) {
+    hipLaunchKernelGGL(k_rope_table, dim3(T), dim3(256), 0, s, nullptr, pos0, tpos, HD, mode, base_g, base_l, fq_g, fq_l, out);
 }
 void launch_qk_prep(const AttnArgs &a, hipStream_t s) {
     if (a.nt) hipLaunchKernelGGL(k_qk_prep<true>, dim3(a.NH + 2 * a.NKV, a.nt), dim3(64), 0, s, a);
@@ -643,9 +645,12 @@ void launch_attention(const AttnArgs &a, int grid_chunks, hipStream_t s) {
 }
 
 // ------------------------------------------------------------------ embedding
-__global__ __launch_bounds__(256) void k_embed(DevW w, const DState *st, const int *tokbuf, int pos0, float *x, float scale) {
-    // decode: the step's token; batched: workgroup t embeds tokbuf[pos0 + t] into row t
-    const int tok = st ? (st->drive == DRIVE_STREAM ? tokbuf[st->pos] : st->tok) : tokbuf[pos0 + blockIdx.x], E = w.cols;
+__global__ __launch_bounds__(256) void k_embed(DevW w, const DState *st, const int *tokbuf, int pos0, const int *toks,
+                                                float *x, float scale) {
+    // decode: the step's token; batched: workgroup t embeds toks[t] (several
+    // sessions) or tokbuf[pos0 + t] (one session's prefill) into row t
+    const int tok = st ? (st->drive == DRIVE_STREAM ? tokbuf[st->pos] : st->tok)
+                       : (toks ? toks[blockIdx.x] : tokbuf[pos0 + blockIdx.x]), E = w.cols;
     x += (size_t)blockIdx.x * E;
     const uint8_t *rc = w.codes + (size_t)tok * ((E + 1) / 2);
     const uint16_t *bs = w.bs + (size_t)tok * w.nblk;
@@ -660,10 +665,11 @@ __global__ __launch_bounds__(256) void k_embed(DevW w, const DState *st, const i
     }
 }
 void launch_embed(const DevW &embd, const DState *st, const int *tokbuf, float *x, float scale, hipStream_t s) {
-    hipLaunchKernelGGL(k_embed, dim3(1), dim3(256), 0, s, embd, st, tokbuf, 0, x, scale);
+    hipLaunchKernelGGL(k_embed, dim3(1), dim3(256), 0, s, embd, st, tokbuf, 0, nullptr, x, scale);
 }
-void launch_embed_batch(const DevW &embd, const int *tokbuf, int pos0, int T, float *x, float scale, hipStream_t s) {
-    hipLaunchKernelGGL(k_embed, dim3(T), dim3(256), 0, s, embd, nullptr, tokbuf, pos0, x, scale);
+void launch_embed_batch(const DevW &embd, const int *tokbuf, int pos0, int T, float *x, float scale, hipStream_t s,
+                        const int *toks) {
+    hipLaunchKernelGGL(k_embed, dim3(T), dim3(256), 0, s, embd, nullptr, tokbuf, pos0, toks, x, scale);
 }
 __global__ void k_advance(DState *st) {
     if (threadIdx.x == 0 && st->drive == DRIVE_STREAM) st->pos = st->pos + 1;
@@ -699,6 +705,25 @@ __global__ __launch_bounds__(256) void k_argmax(const float *lg, int V, float *p
     if (st->drive == DRIVE_GREEDY) st->pos = st->pos + 1;
     reset_counter(counter);
 }
+// greedy token of each of T logit rows (lowest index among the maxima)
+__global__ __launch_bounds__(256) void k_argmax_rows(const float *lg, int V, int *out) {
+    __shared__ float sv[4]; __shared__ int si[4];
+    const float *row = lg + (size_t)blockIdx.x * V;
+    float v = -INFINITY; int idx = 0x7FFFFFFF;
+    for (int j = threadIdx.x; j < V; j += 256) amax_merge(v, idx, row[j], j);
+    #pragma unroll
+    for (int o = 32; o > 0; o >>= 1) amax_merge(v, idx, __shfl_xor(v, o, 64), __shfl_xor(idx, o, 64));
+    if ((threadIdx.x & 63) == 0) { sv[threadIdx.x >> 6] = v; si[threadIdx.x >> 6] = idx; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; w++) amax_merge(v, idx, sv[w], si[w]);
+        out[blockIdx.x] = idx == 0x7FFFFFFF ? 0 : idx;
+    }
+}
+void launch_argmax_rows(const float *logits, int V, int T, int *out, hipStream_t s) {
+    hipLaunchKernelGGL(k_argmax_rows, dim3(T), dim3(256), 0, s, logits, V, out);
+}
+
 int argmax_blocks(int V) { int b = (V + 2047) / 2048; return b < 1 ? 1 : (b > 256 ? 256 : b); }
 void launch_argmax(const float *logits, int V, float *pval, int *pidx, int *counter, DState *st,
                    int *gen_log, int nblocks, hipStream_t s) {

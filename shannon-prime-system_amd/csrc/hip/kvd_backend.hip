@@ -265,6 +265,11 @@ DevModel *model_get(const qwen3_model *qm) {
     m->freq_local = (int64_t *)(base + o_fl);
     const RopeConst &rc = rope_const();
     set_rope_tables(rc.atan_q60, rc.kinv_q62);
+    // the uploads above run on the null stream, which the handles' non-blocking
+    // streams do not wait for: finish them before any handle launches work
+    if (hipDeviceSynchronize() != hipSuccess) {
+        hipFree(m->buf); fail("sp_hipkv_open: weight upload failed%s", ""); return nullptr;
+    }
     m->refs = 1;
     DevModel *raw = m.release();
     g_models[qm] = raw;
@@ -346,6 +351,11 @@ struct sp_kvdecode_handle {
         float *x0, *x1, *q, *k, *v, *qr, *ao, *ap, *gg, *uu, *hh, *dn, *rope, *part, *part_ml;
         int8_t *planes; int *sh, *counter, *zs;
         int64_t *vacc, *vacc_s;
+        // batched decode over sessions (allocated on first use): logits rows,
+        // greedy tokens, per-token token / position / per-layer page tables
+        void *dbuf = nullptr;
+        float *logits; int *next, *toks, *tpos; float *const **tpages;
+        void *hstage = nullptr;              // pinned upload staging for toks/tpos/tpages
     } b;
     // graph cache: key (logits?, argmax?, grid_global, grid_local, chunk_global)
     struct GKey { int lg, am, gg, gl, cg; bool operator<(const GKey &o) const {
@@ -385,7 +395,8 @@ int build_tables(sp_kvdecode_handle *h) {
     HIPCHK(hipMalloc(&h->d_pt, tot * sizeof(float *)), "page table alloc");
     HIPCHK(hipHostMalloc(&h->h_pt, tot * sizeof(float *), hipHostMallocDefault), "page table mirror alloc");
     for (size_t i = 0; i < tot; i++) h->h_pt[i] = nullptr;
-    HIPCHK(hipMemcpy(h->d_pt, h->h_pt, tot * sizeof(float *), hipMemcpyHostToDevice), "page table init");
+    HIPCHK(hipMemcpyAsync(h->d_pt, h->h_pt, tot * sizeof(float *), hipMemcpyHostToDevice, h->stream), "page table init");
+    HIPCHK(hipStreamSynchronize(h->stream), "page table init sync");
     return 0;
 }
 
@@ -453,7 +464,9 @@ int alloc_scratch(sp_kvdecode_handle *h) {
     size_t tot = 0;
     for (auto &it : items) tot = align_up(tot + it.n, 256);
     HIPCHK(hipMalloc(&h->scratch, tot), "scratch alloc");
-    HIPCHK(hipMemset(h->scratch, 0, tot), "scratch clear");
+    // cleared on the handle's stream: a null-stream memset is not ordered
+    // before the handle's (non-blocking) kernels
+    HIPCHK(hipMemsetAsync(h->scratch, 0, tot, h->stream), "scratch clear");
     size_t off = 0;
     for (auto &it : items) { *it.p = (uint8_t *)h->scratch + off; off = align_up(off + it.n, 256); }
     HIPCHK(hipHostMalloc(&h->h_st, sizeof(DState) * 4, hipHostMallocDefault), "pinned state alloc");
@@ -611,21 +624,26 @@ int alloc_batch(sp_kvdecode_handle *h) {
     size_t tot = 0;
     for (auto &it : items) tot = align_up(tot + it.n, 256);
     HIPCHK(hipMalloc(&b.buf, tot), "prefill batch alloc");
-    HIPCHK(hipMemset(b.buf, 0, tot), "prefill batch clear");
+    HIPCHK(hipMemsetAsync(b.buf, 0, tot, h->stream), "prefill batch clear");     // ordered before the batch kernels
     size_t off = 0;
     for (auto &it : items) { *it.p = (uint8_t *)b.buf + off; off = align_up(off + it.n, 256); }
     return 0;
 }
 
-// n tokens at positions pos0.. (tokbuf already holds them), no logits
-int prefill_batch(sp_kvdecode_handle *h, int pos0, int T) {
+// T tokens through the model on h's stream and batch buffers.  One session's
+// prefill: positions pos0.., tokens in h->tokbuf, h's page tables.  Several
+// sessions' decode (multi): token t's id, position and page tables come from
+// b.toks / b.tpos / b.tpages; then the LM head writes b.logits and b.next.
+int run_batch(sp_kvdecode_handle *h, int T, int pos0, int pos_hi, bool multi) {
     const DevModel *m = h->m;
     auto &b = h->b;
     hipStream_t s = h->stream;
     const int QD = m->NH * m->HD, KVD = m->NKV * m->HD, TP = (T + 31) / 32 * 32;
-    launch_embed_batch(m->embd, h->tokbuf, pos0, T, b.x1, m->gemma ? sqrtf((float)m->E) : 0.0f, s);
+    launch_embed_batch(m->embd, h->tokbuf, pos0, T, b.x1, m->gemma ? sqrtf((float)m->E) : 0.0f, s,
+                       multi ? b.toks : nullptr);
     launch_rope_table_batch(pos0, T, m->HD, h->mode, m->base, m->gemma ? 10000.0f : m->base,
-                            m->freq_global, m->gemma ? m->freq_local : m->freq_global, b.rope, s);
+                            m->freq_global, m->gemma ? m->freq_local : m->freq_global, b.rope, s,
+                            multi ? b.tpos : nullptr);
     auto stage = [&](int kind, const float *x, const float *delta, const float *post_w, const float *norm_w,
                      float *x_out, int n) {
         StageArgs a{};
@@ -639,7 +657,6 @@ int prefill_batch(sp_kvdecode_handle *h, int pos0, int T) {
         g.cols = cols; g.planes = b.planes; g.sh = b.sh; g.T = T; g.TP = TP; g.mode = h->mode; g.act = ACT_NONE;
         return g;
     };
-    const int pos_hi = pos0 + T - 1;
     for (int l = 0; l < m->NL; l++) {
         const DevLayer &d = m->L[l];
         const bool glob = is_global(m, l);
@@ -662,6 +679,7 @@ int prefill_batch(sp_kvdecode_handle *h, int pos0, int T) {
         a.base = (m->gemma && !glob) ? 10000.0f : m->base;
         a.ascale = 1.0f / sqrtf((float)m->HD);
         a.nt = T; a.pos0 = pos0; a.rope_stride = 2 * m->HD;
+        if (multi) { a.tpos = b.tpos; a.tpages = b.tpages + (size_t)l * b.TB; }
         a.chunk = (glob || a.win < 0) ? 256 : 64;
         launch_qk_prep(a, s);
         // chunks of the batch's longest span: a window of W positions covers at
@@ -686,9 +704,19 @@ int prefill_batch(sp_kvdecode_handle *h, int pos0, int T) {
         dd.nseg = 1; dd.seg[0] = {d.down, b.dn};
         launch_gemm(dd, m->E, s);
     }
-    HIPCHK(hipGetLastError(), "prefill batch launch");
+    if (multi) {
+        // LM head over the T rows, then each row's greedy token
+        stage(PRO_RESID, b.x0, b.dn, m->gemma ? m->L[m->NL - 1].post_ffw : nullptr, m->out_norm, nullptr, m->E);
+        GemmArgs lm = gemm(m->E);
+        lm.nseg = 1; lm.seg[0] = {m->out, b.logits};
+        launch_gemm(lm, m->V, s);
+        launch_argmax_rows(b.logits, m->V, T, b.next, s);
+    }
+    HIPCHK(hipGetLastError(), "batch launch");
     return 0;
 }
+
+int prefill_batch(sp_kvdecode_handle *h, int pos0, int T) { return run_batch(h, T, pos0, pos0 + T - 1, false); }
 
 int run_body(sp_kvdecode_handle *h, const StepShape &sh) {
     if (!h->use_graph) {
@@ -782,6 +810,8 @@ void sp_hipkv_close(sp_kvdecode_handle *h) {
     if (h->h_pt) hipHostFree(h->h_pt);
     if (h->scratch) hipFree(h->scratch);
     if (h->b.buf) hipFree(h->b.buf);
+    if (h->b.dbuf) hipFree(h->b.dbuf);
+    if (h->b.hstage) hipHostFree(h->b.hstage);
     if (h->h_st) hipHostFree(h->h_st);
     if (h->h_logits) hipHostFree(h->h_logits);
     if (h->stream) hipStreamDestroy(h->stream);
@@ -812,7 +842,8 @@ int sp_hipkv_prefill(sp_kvdecode_handle *h, const int32_t *tokens, int n_tok) {
     for (int i = 0; i < n_tok; i++) if (check_tok(h, tokens[i])) return 1;
     if (ensure_pages(h, h->dpos, h->dpos + n_tok)) return 1;
     HIPCHK(hipStreamSynchronize(h->stream), "prefill staging");
-    HIPCHK(hipMemcpy(h->tokbuf + h->dpos, tokens, (size_t)n_tok * 4, hipMemcpyHostToDevice), "prefill tokens");
+    HIPCHK(hipMemcpyAsync(h->tokbuf + h->dpos, tokens, (size_t)n_tok * 4, hipMemcpyHostToDevice, h->stream),
+           "prefill tokens");
     if (h->use_batch && batch_supported(h)) {
         if (alloc_batch(h)) return 1;
         // window layers on a ring: writing position q reuses the page slot of
@@ -836,6 +867,85 @@ int sp_hipkv_prefill(sp_kvdecode_handle *h, const int32_t *tokens, int n_tok) {
     return 0;
 }
 
+// Several sessions of one model decode one token each, batched: the GEMMs run
+// once for all rows (int8 MFMA), attention reads each session's own pages.
+int sp_hipkv_decode_batch(sp_kvdecode_handle *const *hs, int n, const int32_t *tokens, float *logits,
+                          int32_t *next_tokens) {
+    if (!hs || !tokens || n <= 0) return fail("sp_hipkv_decode_batch: bad argument%s");
+    sp_kvdecode_handle *L = hs[0];
+    if (!L) return fail("sp_hipkv_decode_batch: null handle%s");
+    const DevModel *m = L->m;
+    for (int i = 0; i < n; i++) {
+        sp_kvdecode_handle *h = hs[i];
+        if (!h || h->m != m) return fail("sp_hipkv_decode_batch: handles must share one model%s");
+        if (h->mode != L->mode || h->pmax != L->pmax || h->slots != L->slots)
+            return fail("sp_hipkv_decode_batch: handles differ in mode, pmax or window ring%s");
+        if (check_tok(h, tokens[i])) return 1;
+        if (h->dpos >= h->pmax) return fail("sp_hipkv_decode_batch: context full (dpos == pmax %s%lld)", "", (long long)h->pmax);
+        for (int j = 0; j < i; j++)
+            if (hs[j] == h) return fail("sp_hipkv_decode_batch: a handle appears twice%s");
+    }
+    const bool batched = batch_supported(L) && gemm_supported(m->out);
+    if (!batched) {                                   // shapes the GEMM does not take: one step each
+        for (int i = 0; i < n; i++) {
+            if (step_one(hs[i], tokens[i], 1)) return 1;
+            if (logits) HIPCHK(hipMemcpyAsync(logits + (size_t)i * m->V, hs[i]->logits, (size_t)m->V * 4,
+                                              hipMemcpyDeviceToHost, hs[i]->stream), "logits download");
+            if (next_tokens) {
+                launch_argmax_rows(hs[i]->logits, m->V, 1, hs[i]->am_i, hs[i]->stream);
+                HIPCHK(hipMemcpyAsync(next_tokens + i, hs[i]->am_i, 4, hipMemcpyDeviceToHost, hs[i]->stream), "token download");
+            }
+            HIPCHK(hipStreamSynchronize(hs[i]->stream), "decode step");
+            hs[i]->dpos++;
+            hs[i]->hwm = std::max(hs[i]->hwm, hs[i]->dpos);
+        }
+        return 0;
+    }
+    for (int i = 0; i < n; i++) if (ensure_pages(hs[i], hs[i]->dpos, hs[i]->dpos + 1)) return 1;
+    if (alloc_batch(L)) return 1;
+    auto &b = L->b;
+    const int TB = b.TB;
+    if (!b.dbuf) {
+        const size_t lb = (size_t)TB * m->V * 4, nb = (size_t)TB * 4, pb = (size_t)m->NL * TB * sizeof(void *);
+        HIPCHK(hipMalloc(&b.dbuf, align_up(lb, 256) + 3 * align_up(nb, 256) + pb), "batch decode alloc");
+        uint8_t *p = (uint8_t *)b.dbuf;
+        b.logits = (float *)p; p += align_up(lb, 256);
+        b.next = (int *)p; p += align_up(nb, 256);
+        b.toks = (int *)p; p += align_up(nb, 256);
+        b.tpos = (int *)p; p += align_up(nb, 256);
+        b.tpages = (float *const **)p;
+        HIPCHK(hipHostMalloc(&b.hstage, 2 * nb + pb, hipHostMallocDefault), "batch decode staging");
+    }
+    for (int g0 = 0; g0 < n; g0 += TB) {
+        const int T = std::min(TB, n - g0);
+        int *htok = (int *)b.hstage, *hpos = htok + TB;
+        float *const **hpg = (float *const **)(hpos + TB);
+        int pos_hi = 0;
+        for (int t = 0; t < T; t++) {
+            sp_kvdecode_handle *h = hs[g0 + t];
+            htok[t] = tokens[g0 + t]; hpos[t] = h->dpos;
+            pos_hi = std::max(pos_hi, h->dpos);
+            for (int l = 0; l < m->NL; l++) hpg[(size_t)l * TB + t] = h->d_pt + h->pt_off[l];
+        }
+        HIPCHK(hipMemcpyAsync(b.toks, htok, (size_t)TB * 4, hipMemcpyHostToDevice, L->stream), "batch tokens");
+        HIPCHK(hipMemcpyAsync(b.tpos, hpos, (size_t)TB * 4, hipMemcpyHostToDevice, L->stream), "batch positions");
+        HIPCHK(hipMemcpyAsync((void *)b.tpages, hpg, (size_t)m->NL * TB * sizeof(void *), hipMemcpyHostToDevice, L->stream),
+               "batch page tables");
+        if (run_batch(L, T, 0, pos_hi, true)) return 1;
+        if (logits) HIPCHK(hipMemcpyAsync(logits + (size_t)g0 * m->V, b.logits, (size_t)T * m->V * 4,
+                                          hipMemcpyDeviceToHost, L->stream), "batch logits download");
+        if (next_tokens) HIPCHK(hipMemcpyAsync(next_tokens + g0, b.next, (size_t)T * 4, hipMemcpyDeviceToHost, L->stream),
+                                "batch tokens download");
+        HIPCHK(hipStreamSynchronize(L->stream), "batch decode");
+        for (int t = 0; t < T; t++) {
+            sp_kvdecode_handle *h = hs[g0 + t];
+            h->dpos++;
+            h->hwm = std::max(h->hwm, h->dpos);
+        }
+    }
+    return 0;
+}
+
 int sp_hipkv_decode_step(sp_kvdecode_handle *h, int32_t token, float *logits) {
     if (!h || !logits) return fail("sp_hipkv_decode_step: null argument%s");
     if (step_one(h, token, 1)) return 1;
@@ -856,7 +966,13 @@ int sp_hipkv_set_mode(sp_kvdecode_handle *h, int exact) {
     if (m == EXACT && h->pmax > (1 << 18)) return fail("sp_hipkv_set_mode: exact mode holds at most %s%lld positions", "", (long long)(1 << 18));
     h->mode = m;
     free_graphs(h);
-    if (h->b.buf) { hipStreamSynchronize(h->stream); hipFree(h->b.buf); h->b = sp_kvdecode_handle::Batch{}; }
+    if (h->b.buf || h->b.dbuf) {
+        hipStreamSynchronize(h->stream);
+        if (h->b.buf) hipFree(h->b.buf);
+        if (h->b.dbuf) hipFree(h->b.dbuf);
+        if (h->b.hstage) hipHostFree(h->b.hstage);
+        h->b = sp_kvdecode_handle::Batch{};
+    }
     return 0;
 }
 
@@ -910,7 +1026,8 @@ int sp_hipkv_fork(const sp_kvdecode_handle *p, sp_kvdecode_handle **out) {
         }
     }
     size_t tot = 0; for (int l = 0; l < h->m->NL; l++) tot += (size_t)h->slots[l];
-    if (hipMemcpy(h->d_pt, h->h_pt, tot * sizeof(float *), hipMemcpyHostToDevice) != hipSuccess) {
+    if (hipMemcpyAsync(h->d_pt, h->h_pt, tot * sizeof(float *), hipMemcpyHostToDevice, h->stream) != hipSuccess ||
+        hipStreamSynchronize(h->stream) != hipSuccess) {
         sp_hipkv_close(h.release()); return fail("sp_hipkv_fork: page table upload failed%s");
     }
     *out = h.release();

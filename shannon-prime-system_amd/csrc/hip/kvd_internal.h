@@ -72,6 +72,10 @@ struct AttnArgs {
     // batched prefill: nt tokens at positions pos0.. (token = blockIdx.y of
     // qk_prep, blockIdx.z of attention); every per-token buffer is [nt][...]
     int nt, pos0, rope_stride;
+    // batched decode over several sessions: token t's position and this
+    // layer's page table (NULL: pos0 + t and `pages`)
+    const int *tpos;
+    float *const *const *tpages;
 };
 
 struct Seg { DevW w; float *out; };
@@ -139,9 +143,12 @@ __device__ __forceinline__ void reset_counter(int *counter) {
 
 // launchers (kvd_kernels.hip)
 void launch_embed(const DevW &embd, const DState *st, const int *tokbuf, float *x, float scale, hipStream_t s);
-void launch_embed_batch(const DevW &embd, const int *tokbuf, int pos0, int T, float *x, float scale, hipStream_t s);
+void launch_embed_batch(const DevW &embd, const int *tokbuf, int pos0, int T, float *x, float scale, hipStream_t s,
+                        const int *toks = nullptr);
 void launch_rope_table_batch(int pos0, int T, int HD, int mode, float base_g, float base_l,
-                             const int64_t *fq_g, const int64_t *fq_l, float *out, hipStream_t s);
+                             const int64_t *fq_g, const int64_t *fq_l, float *out, hipStream_t s,
+                             const int *tpos = nullptr);
+void launch_argmax_rows(const float *logits, int V, int T, int *out, hipStream_t s);
 void launch_stage(const StageArgs &a, hipStream_t s);
 void launch_gemm(const GemmArgs &a, int nrows_total, hipStream_t s);
 bool gemm_supported(const DevW &w);

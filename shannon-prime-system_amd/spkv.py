@@ -113,6 +113,7 @@ def kv():
         _sig(lib, "sp_hipkv_fork", c_int, [c_void_p, ctypes.POINTER(c_void_p)])
         _sig(lib, "sp_hipkv_attach", c_int, [c_void_p, c_int, c_int])
         _sig(lib, "sp_hipkv_greedy", c_int, [c_void_p, c_int32, c_int, c_void_p, ctypes.POINTER(c_double)])
+        _sig(lib, "sp_hipkv_decode_batch", c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p])
         _sig(lib, "sp_hipkv_kernel_times", c_int, [c_void_p, c_int32, c_int, c_void_p, c_void_p, c_void_p])
         _sig(lib, "sp_hipkv_read_kv", c_int, [c_void_p, c_int, c_int, c_int, c_void_p, c_void_p])
         _sig(lib, "sp_hipkv_info", c_int, [c_void_p, c_void_p])
@@ -264,6 +265,20 @@ class Backend:
         c = c_void_p()
         check(kv().sp_hipkv_fork(self.h, ctypes.byref(c)), "sp_hipkv_fork")
         return Backend.wrap(c)
+
+    @staticmethod
+    def decode_batch(backends, tokens, vocab, want_logits=True):
+        """One batched decode step over several handles of one model: returns
+        (logits [n][vocab] or None, greedy next tokens [n])."""
+        import numpy as np
+        n = len(backends)
+        hs = (c_void_p * n)(*[b.h.value if isinstance(b.h, c_void_p) else b.h for b in backends])
+        toks = np.ascontiguousarray(tokens, dtype=np.int32)
+        lg = np.zeros((n, vocab), np.float32) if want_logits else None
+        nxt = np.zeros(n, np.int32)
+        check(kv().sp_hipkv_decode_batch(hs, n, ptr(toks), ptr(lg) if want_logits else None, ptr(nxt)),
+              "sp_hipkv_decode_batch")
+        return lg, nxt
 
     def greedy(self, first_tok, n):
         import numpy as np

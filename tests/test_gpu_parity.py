@@ -138,6 +138,94 @@ def test_batched_prefill_matches_stepwise(tmpdir_models, exact):
     b1.close(); b2.close(); close_all(s, m)
 
 
+def test_fresh_handles_prefill_identically(tmpdir_models):
+    """Handles opened, forked and closed in a row (each with freshly allocated
+    and cleared scratch and batch buffers, reusing memory that earlier handles
+    freed) leave bit-identical K/V after the same prefill: the buffer clears are
+    ordered before the handles' own kernels."""
+    spm, spt = model_files(tmpdir_models, "qwen3-hd128")
+    m = spkv.Model(spm, spt); s = spkv.Session(m, 512)
+    qm = spkv.l1().sp_session_qwen3_model(s.h)
+    pr = prompt(200, 2048, seed=21)
+    ref = None
+    for it in range(12):
+        b = spkv.Backend(qm, 512, exact=True)
+        if it % 2:                                   # a fork brings its own buffers
+            f = b.fork(); b.close(); b = f
+        b.prefill(pr)
+        kv = [b.read_kv(layer, 0, 200, 4 * 128) for layer in range(2)]
+        b.close()
+        if ref is None:
+            ref = kv
+            continue
+        for layer in range(2):
+            assert same_bits(kv[layer][0], ref[layer][0]) and same_bits(kv[layer][1], ref[layer][1]), \
+                f"handle {it} layer {layer}"
+    close_all(s, m)
+
+
+@pytest.mark.parametrize("name", ["qwen3-hd128", "gemma3-hd256"])
+@pytest.mark.parametrize("exact", [True, False])
+def test_decode_batch_matches_per_session(tmpdir_models, name, exact):
+    """Batched multi-session decode (the 64-session configuration's pattern at a
+    small scale): 6 sessions with ragged contexts; every step forks each session
+    copy-on-write, rewinds the fork 0-4 tokens and decodes all forks in one
+    sp_hipkv_decode_batch call.  The same sequence on independent handles with
+    sp_hipkv_decode_step gives the same logits (exact mode: bit for bit)."""
+    spm, spt = model_files(tmpdir_models, name)
+    m = spkv.Model(spm, spt); s = spkv.Session(m, 512)
+    qm = spkv.l1().sp_session_qwen3_model(s.h)
+    V = 2048
+    rng = np.random.default_rng(3)
+    lens = [10, 33, 64, 65, 100, 130]
+    A = [spkv.Backend(qm, 512, exact=exact) for _ in lens]
+    B = [spkv.Backend(qm, 512, exact=exact) for _ in lens]
+    toks = []
+    lg = np.zeros(V, np.float32)
+    for i, n in enumerate(lens):
+        pr = prompt(n, V, seed=10 + i)
+        A[i].prefill(pr[:-1]); B[i].prefill(pr[:-1])
+        toks.append(int(pr[-1]))
+    for step in range(5):
+        r = rng.integers(0, 5, size=len(lens))
+        A2, B2 = [], []
+        for i in range(len(lens)):
+            a, b = A[i].fork(), B[i].fork()
+            A[i].close(); B[i].close()
+            if step and r[i]:
+                assert a.rewind(int(r[i])) == 0 and b.rewind(int(r[i])) == 0
+            A2.append(a); B2.append(b)
+        A, B = A2, B2
+        lga, nxt = spkv.Backend.decode_batch(A, toks, V)
+        for i in range(len(lens)):
+            B[i].decode(toks[i], lg)
+            if exact:
+                assert same_bits(lga[i], lg), f"step {step} session {i}"
+            else:
+                assert rel(lga[i], lg) < FLOAT_TOL and int(lga[i].argmax()) == int(lg.argmax()), f"step {step} session {i}"
+            assert int(nxt[i]) == int(lga[i].argmax())
+            assert A[i].position() == B[i].position()
+        toks = [int(t) for t in nxt]
+    for x in A + B:
+        x.close()
+    close_all(s, m)
+
+
+def test_decode_batch_errors(tmpdir_models):
+    spm, spt = model_files(tmpdir_models, "qwen3-hd128")
+    m = spkv.Model(spm, spt); s = spkv.Session(m, 64)
+    qm = spkv.l1().sp_session_qwen3_model(s.h)
+    a, b = spkv.Backend(qm, 64, exact=True), spkv.Backend(qm, 64, exact=False)
+    with pytest.raises(RuntimeError, match="differ in mode"):
+        spkv.Backend.decode_batch([a, b], [1, 2], 2048)
+    with pytest.raises(RuntimeError, match="appears twice"):
+        spkv.Backend.decode_batch([a, a], [1, 2], 2048)
+    with pytest.raises(RuntimeError, match="out of vocabulary"):
+        spkv.Backend.decode_batch([a], [5000], 2048)
+    assert a.position() == 0
+    a.close(); b.close(); close_all(s, m)
+
+
 def test_long_prefill_vs_oracle(tmpdir_models):
     """A 300-token prompt (three prefill batches) then decode: exact mode == oracle."""
     spm, spt = model_files(tmpdir_models, "gemma3-tiny")
