@@ -88,7 +88,12 @@ WORKLOADS = {
     "gemma3-12b-32k": dict(shape="gemma3-12b", ctx=32768),
     "qwen3-0.6b-4k": dict(shape="qwen3-0.6b", ctx=4096),
     "gemma3-12b-128k": dict(shape="gemma3-12b", ctx=131072),
+    # 64 concurrent sessions, contexts uniform in [1024, 16384] (seed 2); every
+    # step clones each session (sp_session_clone), rewinds the clone 0-4 tokens
+    # (seed 3) and decodes all 64 in one batched call (spx_decode_batch)
+    "qwen3-8b-batch64": dict(shape="qwen3-8b", ctx=16384, sessions=64, ctx_lo=1024),
 }
+BATCH_METRIC = "batched multi-session kvdecode tokens/s (aggregate over sessions), Qwen3-8B shape, 64 sessions"
 
 
 def log(*a):
@@ -145,6 +150,8 @@ def main():
 
     import spkv
     wl = WORKLOADS[args.workload]
+    if wl.get("sessions"):
+        return run_sessions(args, wl)
     shape = dict(spkv.SHAPES[wl["shape"]])
     ctx, V, E = (args.ctx or wl["ctx"]), shape["vocab"], shape["hidden"]
     pmax = ctx + args.warmup + args.steps + args.kernel_steps + 64
@@ -253,6 +260,161 @@ def main():
         }
         print(json.dumps(rec), flush=True)
         sess.close()
+        model.close()
+    finally:
+        if not args.workdir:
+            shutil.rmtree(work, ignore_errors=True)
+
+
+def splitmix_u64(n, seed):
+    k = np.arange(1, n + 1, dtype=np.uint64)
+    with np.errstate(over="ignore"):
+        z = np.uint64(seed) + k * np.uint64(0x9E3779B97F4A7C15)
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+        return z ^ (z >> np.uint64(31))
+
+
+def run_sessions(args, wl):
+    """The batched multi-session workload: S sessions of one model with ragged
+    contexts, each step = sp_session_clone of every session (the parent is
+    closed, the clone carries on), sp_session_rewind of the clone by 0-4 tokens,
+    then one spx_decode_batch over all S sessions (greedy tokens feed the next
+    step).  value = S * steps / wall over the timed steps (clone + rewind +
+    batched decode), inputs resident in HBM."""
+    import spkv
+    shape = dict(spkv.SHAPES[wl["shape"]])
+    S, hi, lo = wl["sessions"], (args.ctx or wl["ctx"]), wl["ctx_lo"]
+    V = shape["vocab"]
+    exact = args.mode == "exact"
+    ctxs = (lo + splitmix_u64(S, 2) % np.uint64(hi - lo + 1)).astype(np.int64)
+    pmax = int(hi) + args.warmup + args.steps + 2 + 64
+    rew = (splitmix_u64(S * (args.warmup + args.steps + 2), 3) % np.uint64(5)).astype(np.int64)
+    rew = rew.reshape(args.warmup + args.steps + 2, S)
+    work = args.workdir or tempfile.mkdtemp(prefix="spkv_bench_", dir=os.environ.get("TMPDIR", "/tmp"))
+    prefix = os.path.join(work, wl["shape"])
+    t0 = time.time()
+    threads = min(16, os.cpu_count() or 1)
+    spm, spt = spkv.write_model(prefix, shape=wl["shape"], seed=0, max_context=pmax, threads=threads)
+    log(f"model written {os.path.getsize(spm)/1e9:.2f} GB in {time.time()-t0:.1f}s; contexts {ctxs.min()}..{ctxs.max()}, "
+        f"mean {ctxs.mean():.0f}, total {int(ctxs.sum())}")
+    try:
+        model = spkv.Model(spm, spt)
+        prompts = splitmix_tokens(int(ctxs.sum()), V, seed=1)
+        sess, toks = [], []
+        logits = np.zeros(V, np.float32)
+        t0 = time.time()
+        off = 0
+        for i in range(S):
+            s = spkv.Session(model, pmax)
+            s.attach(pmax, exact=exact)
+            pr = prompts[off:off + int(ctxs[i])]
+            off += int(ctxs[i])
+            for c0 in range(0, len(pr), 4096):
+                spkv.check(s.prefill(pr[c0:c0 + 4096], logits), "sp_prefill_chunk")
+            toks.append(int(np.argmax(logits)))
+            sess.append(s)
+            if i % 8 == 7 or i == S - 1:
+                log(f"prefilled {i + 1}/{S} sessions ({off} tokens, {time.time()-t0:.1f}s)")
+        prefill_s = time.time() - t0
+        step_i = [0]
+
+        def fork_and_rewind():
+            r = rew[step_i[0]]
+            step_i[0] += 1
+            for i in range(S):
+                c = sess[i].clone()
+                sess[i].close()
+                sess[i] = c
+                if r[i]:
+                    spkv.check(c.rewind(int(r[i])), "sp_session_rewind")
+
+        def step(want_logits=False):
+            nonlocal toks
+            fork_and_rewind()
+            rc, lg, nxt = spkv.Session.decode_batch(sess, toks, V, want_logits=want_logits)
+            spkv.check(rc, "spx_decode_batch")
+            toks = [int(t) for t in nxt]
+            return lg
+
+        for _ in range(args.warmup):
+            step()
+        t0 = time.perf_counter()
+        host_s = 0.0
+        for _ in range(args.steps):
+            h0 = time.perf_counter()
+            fork_and_rewind()
+            host_s += time.perf_counter() - h0
+            rc, _, nxt = spkv.Session.decode_batch(sess, toks, V, want_logits=False)
+            spkv.check(rc, "spx_decode_batch")
+            toks = [int(t) for t in nxt]
+        wall = time.perf_counter() - t0
+        value = S * args.steps / wall
+        log(f"{args.steps} steps x {S} sessions: wall {wall*1e3:.1f} ms ({1e3*wall/args.steps:.2f} ms/step, "
+            f"clone+rewind {1e3*host_s/args.steps:.2f} ms/step) -> {value:.1f} tok/s aggregate")
+
+        # PCIe-inclusive: one step with every session's logits row copied to the host
+        t1 = time.perf_counter()
+        step(want_logits=True)
+        pcie_s = time.perf_counter() - t1
+
+        # one step with each kernel class bracketed by HIP events
+        fork_and_rewind()
+        bes = [spkv.Backend.wrap(s.backend_handle()) for s in sess]
+        pos_before = [s.position() for s in sess]
+        nxt, ms, nl, by = spkv.Backend.decode_batch_times(bes, toks)
+        # the timed step went around the session layer: take it back on the
+        # backends so sessions and backends agree on every position again
+        for i, s in enumerate(sess):
+            assert bes[i].position() == pos_before[i] + 1
+            spkv.check(bes[i].rewind(1), "sp_hipkv_rewind")
+        cls = []
+        for i, name in enumerate(CLASSES):
+            if nl[i]:
+                cls.append(dict(kernel=name, launches=int(nl[i]), avg_us=1e3 * ms[i] / nl[i], total_ms=float(ms[i]),
+                                bytes=float(by[i]), gbs=float(by[i] / (ms[i] * 1e-3) / 1e9) if ms[i] > 0 else None))
+        for c in cls:
+            log(f"  {c['kernel']:26s} launches {c['launches']:6d} avg {c['avg_us']:9.2f} us  {c['gbs'] or 0:8.1f} GB/s")
+        dom = max(cls, key=lambda c: c["total_ms"])
+        kv = [c for c in cls if c["kernel"].startswith("gqa")]
+        kv_gb, kv_ms = sum(c["bytes"] for c in kv) / 1e9, sum(c["total_ms"] for c in kv)
+        step_bytes = sum(c["bytes"] for c in cls)
+        names = {"gqa_decode_attn_global": ["kvd::k_attn_exact_scores<2, 4, true> + kvd::k_attn_exact_vsum<2, 4, true>"
+                                            if exact else "kvd::k_attn_float<2, 4, true>"]}
+        rec = {
+            "metric": BATCH_METRIC, "value": round(value, 3), "unit": "tokens/s", "n_gpus": 1,
+            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(1e3 * wall / args.steps, 4),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "int8 MFMA digit-plane GEMMs (int4 weights), int32 KV (exact mode)" if exact
+                     else "int8 MFMA digit-plane GEMMs (int4 weights), f32 KV/attention",
+            "data": "synthetic: seeded random-init OK_Q4B weights (seed 0), contexts U[1024,16384] (seed 2), "
+                    "prompts (seed 1), rewinds U{0..4} (seed 3)",
+            "config": {"workload": f"{args.workload}: {wl['shape']}-shape, {S} sessions, ctx U[{lo},{hi}], "
+                                   f"per step clone + rewind 0-4 + one batched decode of all sessions",
+                       "sessions": S, "ctx_mean": float(ctxs.mean()), "mode": args.mode, "b_kv": 4, "pmax": pmax},
+            "roofline": {"bound": "hbm", "kernel": dom["kernel"], "rocprof_kernels": names.get(dom["kernel"], []),
+                         "achieved": round(dom["gbs"], 1), "peak": PEAK_GBS, "unit": "GB/s",
+                         "frac": round(dom["gbs"] / PEAK_GBS, 4),
+                         "algorithmic_bytes_per_launch": round(dom["bytes"] / dom["launches"]),
+                         "avg_launch_us": round(dom["avg_us"], 3), "traffic": None},
+            "kv_read": {"gbs": round(kv_gb / (kv_ms * 1e-3), 1), "frac": round(kv_gb / (kv_ms * 1e-3) / PEAK_GBS, 4),
+                        "bytes_per_step": kv_gb * 1e9},
+            "step_algorithmic_bytes": step_bytes,
+            "step_hbm_frac": round(step_bytes / (wall / args.steps) / 1e9 / PEAK_GBS, 4),
+            "clone_rewind_ms_per_step": round(1e3 * host_s / args.steps, 3),
+            "pcie_inclusive_tokens_per_s": round(S / pcie_s, 2),
+            "prefill_tokens_per_s": round(float(ctxs.sum()) / prefill_s, 1),
+            "kernels": cls,
+            "cpu_baseline": None,
+        }
+        if not args.no_cpu_baseline:
+            be0 = bes[0]
+            cpu = cpu_baseline(spm, be0, None, shape, exact, args.cpu_steps, toks[0], sess[0])
+            cpu["sample"] = "session 0 of the batch only: " + cpu["sample"]
+            rec["cpu_baseline"] = cpu
+        print(json.dumps(rec), flush=True)
+        for s in sess:
+            s.close()
         model.close()
     finally:
         if not args.workdir:

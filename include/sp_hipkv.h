@@ -80,6 +80,14 @@ int  sp_hipkv_greedy(sp_kvdecode_handle *h, int32_t first_token, int n, int32_t 
 int  sp_hipkv_kernel_times(sp_kvdecode_handle *h, int32_t first_token, int n,
                            double ms[SP_HIPKV_NCLASS], long long launches[SP_HIPKV_NCLASS],
                            double bytes[SP_HIPKV_NCLASS]);
+/* One sp_hipkv_decode_batch step (greedy tokens only, logits stay on the device)
+ * with each kernel class of the batched step bracketed by HIP events: the same
+ * classes as sp_hipkv_kernel_times, each GEMM class including its staging
+ * kernel; bytes = algorithmic HBM bytes (weights once per batch, every row's
+ * K/V span).  Fails for model shapes without the batched path. */
+int  sp_hipkv_decode_batch_times(sp_kvdecode_handle *const *hs, int n, const int32_t *tokens, int32_t *next_tokens,
+                                 double ms[SP_HIPKV_NCLASS], long long launches[SP_HIPKV_NCLASS],
+                                 double bytes[SP_HIPKV_NCLASS]);
 /* Read K/V of one layer for positions [p0, p0+n) in the reference slab layout
  * ([n][n_kv_heads*head_dim] floats, or int32 grid values in exact mode). */
 int  sp_hipkv_read_kv(const sp_kvdecode_handle *h, int layer, int p0, int n, float *k, float *v);

@@ -141,6 +141,26 @@ sp_status spx_session_own_kvdecode(sp_session *s, int owned);
 typedef int (*spx_fork_fn)(const sp_kvdecode_handle *parent, sp_kvdecode_handle **child);
 void spx_register_fork(const sp_kvdecode_dispatch_fn *dt, spx_fork_fn fn);
 
+/* A backend that decodes many handles in one batched step registers it against
+ * its dispatch table (sp_hipkv registers sp_hipkv_decode_batch).  No counterpart
+ * in sp_l1.h. */
+typedef int (*spx_batch_fn)(sp_kvdecode_handle *const *hs, int n, const int32_t *tokens, float *logits,
+                            int32_t *next_tokens);
+void spx_register_batch(const sp_kvdecode_dispatch_fn *dt, spx_batch_fn fn);
+
+/* sp_decode_step for n sessions at once: session i takes tokens[i] at its own
+ * position; logits (NULL allowed) receives n rows of vocab_size floats
+ * (logits_capacity >= n * vocab_size); next_tokens (NULL allowed) the greedy
+ * token of each row (lowest index on ties).  Same guards and status codes as
+ * sp_decode_step, checked for every session before any decodes; the sessions
+ * must be distinct and registered on one dispatch table.  With a registered
+ * batch hook the backend decodes them in one pass, otherwise one
+ * decode_step each.  Every session that advanced is committed (pos + 1, token
+ * in its history) even when a later one fails (SP_EBADSTATE).  No counterpart
+ * in sp_l1.h: the many-sessions-per-step entry of the batched configuration. */
+sp_status spx_decode_batch(sp_session *const *ss, size_t n, const int32_t *tokens, float *logits,
+                           size_t logits_capacity, int32_t *next_tokens);
+
 #if defined(__STDC_VERSION__) && __STDC_VERSION__ >= 201112L && !defined(__cplusplus)
 _Static_assert(sizeof(sp_arch_info) == 192, "sp_arch_info is 192 bytes");
 _Static_assert(sizeof(sp_session_config) == 32, "sp_session_config is 32 bytes");

@@ -705,23 +705,48 @@ __global__ __launch_bounds__(256) void k_argmax(const float *lg, int V, float *p
     if (st->drive == DRIVE_GREEDY) st->pos = st->pos + 1;
     reset_counter(counter);
 }
-// greedy token of each of T logit rows (lowest index among the maxima)
-__global__ __launch_bounds__(256) void k_argmax_rows(const float *lg, int V, int *out) {
-    __shared__ float sv[4]; __shared__ int si[4];
+// greedy token of each of T logit rows (lowest index among the maxima); one
+// 1024-thread workgroup per row, 16-byte loads with four in flight per thread
+constexpr int AMR_T = 1024;
+__global__ __launch_bounds__(AMR_T) void k_argmax_rows(const float *lg, int V, int *out) {
+    __shared__ float sv[AMR_T / 64]; __shared__ int si[AMR_T / 64];
     const float *row = lg + (size_t)blockIdx.x * V;
+    const int tid = threadIdx.x;
     float v = -INFINITY; int idx = 0x7FFFFFFF;
-    for (int j = threadIdx.x; j < V; j += 256) amax_merge(v, idx, row[j], j);
+    if ((V & 3) == 0) {                              // rows start 16-byte aligned
+        const float4 *r4 = (const float4 *)row;
+        const int V4 = V >> 2;
+        int j = tid;
+        for (; j + 3 * AMR_T < V4; j += 4 * AMR_T) {
+            float4 q[4];
+            #pragma unroll
+            for (int u = 0; u < 4; u++) q[u] = r4[j + u * AMR_T];
+            #pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int b = 4 * (j + u * AMR_T);
+                amax_merge(v, idx, q[u].x, b); amax_merge(v, idx, q[u].y, b + 1);
+                amax_merge(v, idx, q[u].z, b + 2); amax_merge(v, idx, q[u].w, b + 3);
+            }
+        }
+        for (; j < V4; j += AMR_T) {
+            const float4 q = r4[j];
+            amax_merge(v, idx, q.x, 4 * j); amax_merge(v, idx, q.y, 4 * j + 1);
+            amax_merge(v, idx, q.z, 4 * j + 2); amax_merge(v, idx, q.w, 4 * j + 3);
+        }
+    } else {
+        for (int j = tid; j < V; j += AMR_T) amax_merge(v, idx, row[j], j);
+    }
     #pragma unroll
     for (int o = 32; o > 0; o >>= 1) amax_merge(v, idx, __shfl_xor(v, o, 64), __shfl_xor(idx, o, 64));
-    if ((threadIdx.x & 63) == 0) { sv[threadIdx.x >> 6] = v; si[threadIdx.x >> 6] = idx; }
+    if ((tid & 63) == 0) { sv[tid >> 6] = v; si[tid >> 6] = idx; }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        for (int w = 1; w < 4; w++) amax_merge(v, idx, sv[w], si[w]);
+    if (tid == 0) {
+        for (int w = 1; w < AMR_T / 64; w++) amax_merge(v, idx, sv[w], si[w]);
         out[blockIdx.x] = idx == 0x7FFFFFFF ? 0 : idx;
     }
 }
 void launch_argmax_rows(const float *logits, int V, int T, int *out, hipStream_t s) {
-    hipLaunchKernelGGL(k_argmax_rows, dim3(T), dim3(256), 0, s, logits, V, out);
+    hipLaunchKernelGGL(k_argmax_rows, dim3(T), dim3(AMR_T), 0, s, logits, V, out);
 }
 
 int argmax_blocks(int V) { int b = (V + 2047) / 2048; return b < 1 ? 1 : (b > 256 ? 256 : b); }

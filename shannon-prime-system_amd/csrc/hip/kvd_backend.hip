@@ -125,8 +125,13 @@ struct DevModel {
     void *buf = nullptr;
     size_t bytes = 0, weight_bytes = 0, lm_bytes = 0, layer_bytes = 0, embd_bytes = 0;
     int64_t *freq_global = nullptr, *freq_local = nullptr;
+    // closed handles kept for reuse (stream, tables, scratch, batch buffers and
+    // captured graphs intact): a fork or open with the same pmax and window ring
+    // takes one instead of allocating; they hold no model reference
+    std::vector<sp_kvdecode_handle *> shells;
 };
 std::map<const qwen3_model *, DevModel *> g_models;
+void free_handle(sp_kvdecode_handle *h);
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
@@ -277,6 +282,8 @@ DevModel *model_get(const qwen3_model *qm) {
 }
 void model_put(DevModel *m) {
     if (!m || --m->refs > 0) return;
+    for (sp_kvdecode_handle *sh : m->shells) free_handle(sh);
+    m->shells.clear();
     g_models.erase(m->qm);
     hipFree(m->buf);
     delete m;
@@ -344,6 +351,7 @@ struct sp_kvdecode_handle {
     float *h_logits = nullptr;               // pinned staging
     int max_chunks = 0;
     void *scratch = nullptr;
+    int built = 0;                           // tables and scratch allocated (reusable as a shell)
     // batched prefill buffers ([TB][...] per token), allocated on first use
     struct Batch {
         void *buf = nullptr;
@@ -406,12 +414,13 @@ int ensure_pages(sp_kvdecode_handle *h, int p0, int p1) {
     const DevModel *m = h->m;
     if (p1 <= p0) return 0;
     std::lock_guard<std::mutex> lk(h->pool->mu);
+    size_t lo = SIZE_MAX, hi = 0;                // changed entries of the concatenated table
     for (int l = 0; l < m->NL; l++) {
         const int S = h->slots[l];
-        bool dirty = false;
         const int lp0 = p0 / PAGE, lp1 = (p1 - 1) / PAGE;
         for (int lp = lp0; lp <= lp1; lp++) {
             const int slot = (S == h->full_pages) ? lp : lp % S;
+            bool dirty = false;
             int &id = h->pt[l][slot];
             if (id < 0) {
                 id = h->pool->alloc();
@@ -427,13 +436,15 @@ int ensure_pages(sp_kvdecode_handle *h, int p0, int p1) {
                 dirty = true;
             }
             h->h_pt[h->pt_off[l] + slot] = h->pool->ptr[id];
+            if (dirty) { lo = std::min(lo, h->pt_off[l] + slot); hi = std::max(hi, h->pt_off[l] + slot + 1); }
         }
-        if (dirty) {
-            // whole-layer refresh keeps the pinned mirror authoritative
-            HIPCHK(hipMemcpyAsync(h->d_pt + h->pt_off[l], h->h_pt + h->pt_off[l], (size_t)S * sizeof(float *),
-                                  hipMemcpyHostToDevice, h->stream), "page table update");
-            HIPCHK(hipStreamSynchronize(h->stream), "page table update sync");
-        }
+    }
+    if (hi > lo) {
+        // one upload of the changed span (the pinned mirror is authoritative);
+        // the wait also covers the copy-on-write copies issued above
+        HIPCHK(hipMemcpyAsync(h->d_pt + lo, h->h_pt + lo, (hi - lo) * sizeof(float *), hipMemcpyHostToDevice, h->stream),
+               "page table update");
+        HIPCHK(hipStreamSynchronize(h->stream), "page table update sync");
     }
     return 0;
 }
@@ -471,7 +482,53 @@ int alloc_scratch(sp_kvdecode_handle *h) {
     for (auto &it : items) { *it.p = (uint8_t *)h->scratch + off; off = align_up(off + it.n, 256); }
     HIPCHK(hipHostMalloc(&h->h_st, sizeof(DState) * 4, hipHostMallocDefault), "pinned state alloc");
     HIPCHK(hipHostMalloc(&h->h_logits, (size_t)m->V * 4, hipHostMallocDefault), "pinned logits alloc");
+    h->built = 1;
     return 0;
+}
+
+// Drop the batch buffers and captured graphs when the arithmetic mode changes
+// (both are mode-specific); everything else of the handle is mode-independent.
+void set_handle_mode(sp_kvdecode_handle *h, int mode) {
+    if (h->mode == mode) return;
+    h->mode = mode;
+    free_graphs(h);
+    if (h->b.buf || h->b.dbuf) {
+        hipStreamSynchronize(h->stream);
+        if (h->b.buf) hipFree(h->b.buf);
+        if (h->b.dbuf) hipFree(h->b.dbuf);
+        if (h->b.hstage) hipHostFree(h->b.hstage);
+        h->b = sp_kvdecode_handle::Batch{};
+    }
+}
+
+// A kept shell of m with this pmax and window ring, or null (caller holds g_mu).
+// Its page tables are unmapped, its scratch in the between-launch state
+// (zero accumulators and counters), its graphs still valid.
+sp_kvdecode_handle *take_shell(DevModel *m, int pmax, int max_rewind) {
+    for (size_t i = m->shells.size(); i-- > 0;) {
+        sp_kvdecode_handle *h = m->shells[i];
+        if (h->pmax == pmax && h->max_rewind == max_rewind) {
+            m->shells.erase(m->shells.begin() + (ptrdiff_t)i);
+            return h;
+        }
+    }
+    return nullptr;
+}
+constexpr size_t MAX_SHELLS = 256;
+
+void free_handle(sp_kvdecode_handle *h) {
+    if (h->stream) hipStreamSynchronize(h->stream);
+    free_graphs(h);
+    if (h->d_pt) hipFree(h->d_pt);
+    if (h->h_pt) hipHostFree(h->h_pt);
+    if (h->scratch) hipFree(h->scratch);
+    if (h->b.buf) hipFree(h->b.buf);
+    if (h->b.dbuf) hipFree(h->b.dbuf);
+    if (h->b.hstage) hipHostFree(h->b.hstage);
+    if (h->h_st) hipHostFree(h->h_st);
+    if (h->h_logits) hipHostFree(h->h_logits);
+    if (h->stream) hipStreamDestroy(h->stream);
+    delete h;
 }
 
 // ------------------------------------------------------------ one step body
@@ -634,16 +691,19 @@ int alloc_batch(sp_kvdecode_handle *h) {
 // prefill: positions pos0.., tokens in h->tokbuf, h's page tables.  Several
 // sessions' decode (multi): token t's id, position and page tables come from
 // b.toks / b.tpos / b.tpages; then the LM head writes b.logits and b.next.
-int run_batch(sp_kvdecode_handle *h, int T, int pos0, int pos_hi, bool multi) {
+int run_batch(sp_kvdecode_handle *h, int T, int pos0, int pos_hi, bool multi, TimeCb cb = nullptr, void *ctx = nullptr) {
     const DevModel *m = h->m;
     auto &b = h->b;
     hipStream_t s = h->stream;
     const int QD = m->NH * m->HD, KVD = m->NKV * m->HD, TP = (T + 31) / 32 * 32;
+    auto TM = [&](int cls, bool begin) { if (cb) cb(ctx, cls, begin); };
+    TM(8, true);
     launch_embed_batch(m->embd, h->tokbuf, pos0, T, b.x1, m->gemma ? sqrtf((float)m->E) : 0.0f, s,
                        multi ? b.toks : nullptr);
     launch_rope_table_batch(pos0, T, m->HD, h->mode, m->base, m->gemma ? 10000.0f : m->base,
                             m->freq_global, m->gemma ? m->freq_local : m->freq_global, b.rope, s,
                             multi ? b.tpos : nullptr);
+    TM(8, false);
     auto stage = [&](int kind, const float *x, const float *delta, const float *post_w, const float *norm_w,
                      float *x_out, int n) {
         StageArgs a{};
@@ -660,11 +720,13 @@ int run_batch(sp_kvdecode_handle *h, int T, int pos0, int pos_hi, bool multi) {
     for (int l = 0; l < m->NL; l++) {
         const DevLayer &d = m->L[l];
         const bool glob = is_global(m, l);
+        TM(0, true);
         if (l == 0) stage(PRO_NORM, b.x1, nullptr, nullptr, d.attn_norm, nullptr, m->E);
         else stage(PRO_RESID, b.x0, b.dn, m->gemma ? m->L[l - 1].post_ffw : nullptr, d.attn_norm, b.x1, m->E);
         GemmArgs g = gemm(m->E);
         g.nseg = 3; g.seg[0] = {d.q, b.q}; g.seg[1] = {d.k, b.k}; g.seg[2] = {d.v, b.v};
         launch_gemm(g, QD + 2 * KVD, s);
+        TM(0, false);
 
         AttnArgs a{};
         a.q = b.q; a.k = b.k; a.v = b.v; a.q_norm = d.q_norm; a.k_norm = d.k_norm; a.qr = b.qr;
@@ -681,36 +743,44 @@ int run_batch(sp_kvdecode_handle *h, int T, int pos0, int pos_hi, bool multi) {
         a.nt = T; a.pos0 = pos0; a.rope_stride = 2 * m->HD;
         if (multi) { a.tpos = b.tpos; a.tpages = b.tpages + (size_t)l * b.TB; }
         a.chunk = (glob || a.win < 0) ? 256 : 64;
-        launch_qk_prep(a, s);
+        TM(7, true); launch_qk_prep(a, s); TM(7, false);
         // chunks of the batch's longest span: a window of W positions covers at
         // most (W-1)/chunk + 2 chunks whatever its alignment
         int nch = pos_hi / a.chunk + 1;
         if (a.win >= 0) nch = std::min(nch, (a.win - 1) / a.chunk + 2);
-        launch_attention(a, nch, s);
+        TM(a.win >= 0 ? 6 : 5, true); launch_attention(a, nch, s); TM(a.win >= 0 ? 6 : 5, false);
 
+        TM(1, true);
         stage(PRO_PLAIN, b.ao, nullptr, nullptr, nullptr, nullptr, QD);
         GemmArgs o = gemm(QD);
         o.nseg = 1; o.seg[0] = {d.o, b.ap};
         launch_gemm(o, m->E, s);
+        TM(1, false);
 
+        TM(2, true);
         stage(PRO_RESID, b.x1, b.ap, d.post_attn, d.ffn_norm, b.x0, m->E);
         GemmArgs f = gemm(m->E);
         f.nseg = 2; f.act = m->gemma ? ACT_GELU : ACT_SILU;
         f.seg[0] = {d.gate, b.gg}; f.seg[1] = {d.up, b.uu}; f.act_out = b.hh;
         launch_gemm(f, m->FF, s);
+        TM(2, false);
 
+        TM(3, true);
         stage(PRO_PLAIN, b.hh, nullptr, nullptr, nullptr, nullptr, m->FF);
         GemmArgs dd = gemm(m->FF);
         dd.nseg = 1; dd.seg[0] = {d.down, b.dn};
         launch_gemm(dd, m->E, s);
+        TM(3, false);
     }
     if (multi) {
         // LM head over the T rows, then each row's greedy token
+        TM(4, true);
         stage(PRO_RESID, b.x0, b.dn, m->gemma ? m->L[m->NL - 1].post_ffw : nullptr, m->out_norm, nullptr, m->E);
         GemmArgs lm = gemm(m->E);
         lm.nseg = 1; lm.seg[0] = {m->out, b.logits};
         launch_gemm(lm, m->V, s);
         launch_argmax_rows(b.logits, m->V, T, b.next, s);
+        TM(4, false);
     }
     HIPCHK(hipGetLastError(), "batch launch");
     return 0;
@@ -788,13 +858,31 @@ int sp_hipkv_open(const void *qm_opaque, int pmax, sp_kvdecode_handle **out) {
         return fail("sp_hipkv_open: no HIP device visible (this backend runs on MI355X / gfx950)%s");
     DevModel *m = model_get((const qwen3_model *)qm_opaque);
     if (!m) return 1;
+    auto new_pool = [m]() {
+        auto pool = std::make_shared<KvPool>();
+        pool->page_bytes = (size_t)2 * m->NKV * PAGE * m->HD * 4;
+        pool->pages_per_chunk = (int)std::max<size_t>(16, ((size_t)1 << 30) / pool->page_bytes);
+        return pool;
+    };
+    if (sp_kvdecode_handle *sh = take_shell(m, pmax, 0)) {
+        // a kept shell: reset to the open defaults, unmapped tables
+        set_handle_mode(sh, FLOAT);
+        sh->use_graph = 1; sh->use_batch = 1; sh->dpos = 0; sh->hwm = 0;
+        sh->pool = new_pool();
+        size_t tot = 0; for (int l = 0; l < m->NL; l++) tot += (size_t)sh->slots[l];
+        for (size_t i = 0; i < tot; i++) sh->h_pt[i] = nullptr;
+        if (hipMemcpyAsync(sh->d_pt, sh->h_pt, tot * sizeof(float *), hipMemcpyHostToDevice, sh->stream) != hipSuccess ||
+            hipStreamSynchronize(sh->stream) != hipSuccess) {
+            free_handle(sh); model_put(m); return fail("sp_hipkv_open: page table reset failed%s");
+        }
+        *out = sh;
+        return 0;
+    }
     std::unique_ptr<sp_kvdecode_handle> h(new sp_kvdecode_handle);
     h->m = m; h->pmax = pmax;
-    h->pool = std::make_shared<KvPool>();
-    h->pool->page_bytes = (size_t)2 * m->NKV * PAGE * m->HD * 4;
-    h->pool->pages_per_chunk = (int)std::max<size_t>(16, ((size_t)1 << 30) / h->pool->page_bytes);
+    h->pool = new_pool();
     if (hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking) != hipSuccess) { model_put(m); return fail("sp_hipkv_open: stream creation failed%s"); }
-    if (build_tables(h.get()) || alloc_scratch(h.get())) { sp_hipkv_close(h.release()); return 1; }
+    if (build_tables(h.get()) || alloc_scratch(h.get())) { free_handle(h.release()); model_put(m); return 1; }
     *out = h.release();
     return 0;
 }
@@ -802,22 +890,22 @@ int sp_hipkv_open(const void *qm_opaque, int pmax, sp_kvdecode_handle **out) {
 void sp_hipkv_close(sp_kvdecode_handle *h) {
     if (!h) return;
     std::lock_guard<std::mutex> lk(g_mu);
-    if (h->stream) hipStreamSynchronize(h->stream);
-    free_graphs(h);
+    const bool idle = !h->stream || hipStreamSynchronize(h->stream) == hipSuccess;
     if (h->pool) { std::lock_guard<std::mutex> pl(h->pool->mu); for (auto &v : h->pt) for (int id : v) h->pool->unref(id); }
     h->pool.reset();
-    if (h->d_pt) hipFree(h->d_pt);
-    if (h->h_pt) hipHostFree(h->h_pt);
-    if (h->scratch) hipFree(h->scratch);
-    if (h->b.buf) hipFree(h->b.buf);
-    if (h->b.dbuf) hipFree(h->b.dbuf);
-    if (h->b.hstage) hipHostFree(h->b.hstage);
-    if (h->h_st) hipHostFree(h->h_st);
-    if (h->h_logits) hipHostFree(h->h_logits);
-    if (h->stream) hipStreamDestroy(h->stream);
-    model_put(h->m);
-    delete h;
+    for (auto &v : h->pt) std::fill(v.begin(), v.end(), -1);
+    DevModel *m = h->m;
+    if (idle && h->built && m->refs > 1 && m->shells.size() < MAX_SHELLS) {
+        // other handles keep the model alive: keep this one as a shell
+        h->dpos = 0; h->hwm = 0;
+        m->shells.push_back(h);
+        m->refs--;
+        return;
+    }
+    free_handle(h);
+    model_put(m);
 }
+
 
 int sp_hipkv_position(const sp_kvdecode_handle *h) { return h ? h->dpos : -1; }
 
@@ -869,8 +957,9 @@ int sp_hipkv_prefill(sp_kvdecode_handle *h, const int32_t *tokens, int n_tok) {
 
 // Several sessions of one model decode one token each, batched: the GEMMs run
 // once for all rows (int8 MFMA), attention reads each session's own pages.
-int sp_hipkv_decode_batch(sp_kvdecode_handle *const *hs, int n, const int32_t *tokens, float *logits,
-                          int32_t *next_tokens) {
+// cb/ctx: optional per-kernel-class event hooks (run_batch's classes).
+static int decode_batch_impl(sp_kvdecode_handle *const *hs, int n, const int32_t *tokens, float *logits,
+                             int32_t *next_tokens, TimeCb cb, void *ctx) {
     if (!hs || !tokens || n <= 0) return fail("sp_hipkv_decode_batch: bad argument%s");
     sp_kvdecode_handle *L = hs[0];
     if (!L) return fail("sp_hipkv_decode_batch: null handle%s");
@@ -887,6 +976,7 @@ int sp_hipkv_decode_batch(sp_kvdecode_handle *const *hs, int n, const int32_t *t
     }
     const bool batched = batch_supported(L) && gemm_supported(m->out);
     if (!batched) {                                   // shapes the GEMM does not take: one step each
+        if (cb) return fail("sp_hipkv_decode_batch_times: this model shape has no batched path%s");
         for (int i = 0; i < n; i++) {
             if (step_one(hs[i], tokens[i], 1)) return 1;
             if (logits) HIPCHK(hipMemcpyAsync(logits + (size_t)i * m->V, hs[i]->logits, (size_t)m->V * 4,
@@ -931,7 +1021,7 @@ int sp_hipkv_decode_batch(sp_kvdecode_handle *const *hs, int n, const int32_t *t
         HIPCHK(hipMemcpyAsync(b.tpos, hpos, (size_t)TB * 4, hipMemcpyHostToDevice, L->stream), "batch positions");
         HIPCHK(hipMemcpyAsync((void *)b.tpages, hpg, (size_t)m->NL * TB * sizeof(void *), hipMemcpyHostToDevice, L->stream),
                "batch page tables");
-        if (run_batch(L, T, 0, pos_hi, true)) return 1;
+        if (run_batch(L, T, 0, pos_hi, true, cb, ctx)) return 1;
         if (logits) HIPCHK(hipMemcpyAsync(logits + (size_t)g0 * m->V, b.logits, (size_t)T * m->V * 4,
                                           hipMemcpyDeviceToHost, L->stream), "batch logits download");
         if (next_tokens) HIPCHK(hipMemcpyAsync(next_tokens + g0, b.next, (size_t)T * 4, hipMemcpyDeviceToHost, L->stream),
@@ -943,6 +1033,62 @@ int sp_hipkv_decode_batch(sp_kvdecode_handle *const *hs, int n, const int32_t *t
             h->hwm = std::max(h->hwm, h->dpos);
         }
     }
+    return 0;
+}
+
+int sp_hipkv_decode_batch(sp_kvdecode_handle *const *hs, int n, const int32_t *tokens, float *logits,
+                          int32_t *next_tokens) {
+    return decode_batch_impl(hs, n, tokens, logits, next_tokens, nullptr, nullptr);
+}
+
+int sp_hipkv_decode_batch_times(sp_kvdecode_handle *const *hs, int n, const int32_t *tokens, int32_t *next_tokens,
+                                double ms[SP_HIPKV_NCLASS], long long launches[SP_HIPKV_NCLASS],
+                                double bytes[SP_HIPKV_NCLASS]) {
+    if (!hs || n <= 0 || !hs[0] || !ms || !launches || !bytes) return fail("sp_hipkv_decode_batch_times: bad argument%s");
+    const DevModel *m = hs[0]->m;
+    for (int i = 0; i < SP_HIPKV_NCLASS; i++) { ms[i] = 0; launches[i] = 0; bytes[i] = 0; }
+    // algorithmic bytes: each weight matrix once for all rows (Q4B codes + f16
+    // scales), per row its GEMM input (f32) and output (f32); attention reads
+    // each row's K/V span; q/k prep reads the projections and writes q and K/V
+    const double rows_n = std::min(n, PREFILL_TB);
+    auto wb = [](const DevW &w) { return (double)w.rows * (w.cols / 2) + 2.0 * w.rows * w.nblk; };
+    auto io = [&](const DevW &w) { return rows_n * 4.0 * ((double)w.cols + w.rows); };
+    double per[SP_HIPKV_NCLASS] = {0};
+    const int QD = m->NH * m->HD, KVD = m->NKV * m->HD;
+    for (const DevLayer &d : m->L) {
+        per[0] += wb(d.q) + wb(d.k) + wb(d.v) + io(d.q) + 4.0 * rows_n * (d.k.rows + d.v.rows);
+        per[1] += wb(d.o) + io(d.o);
+        per[2] += wb(d.gate) + wb(d.up) + io(d.gate) + 8.0 * rows_n * d.up.rows;
+        per[3] += wb(d.down) + io(d.down);
+        per[7] += rows_n * 8.0 * (QD + 2.0 * KVD);
+    }
+    per[4] = wb(m->out) + io(m->out) + rows_n * 4.0 * m->V;
+    per[8] = rows_n * ((double)(m->embd.cols / 2 + m->embd.nblk * 2) + 4.0 * m->E);
+    const double kvb = (double)KVD * 4 * 2;
+    for (int i = 0; i < n; i++) {
+        const int pos = hs[i]->dpos;
+        for (int l = 0; l < m->NL; l++) {
+            const bool glob = is_global(m, l);
+            const int s0 = (!glob && m->SW > 0 && pos - m->SW + 1 > 0) ? pos - m->SW + 1 : 0;
+            bytes[(glob || m->SW <= 0) ? 5 : 6] += kvb * (pos - s0 + 1);
+        }
+    }
+    struct Ctx { hipStream_t s; std::vector<std::pair<int, std::pair<hipEvent_t, hipEvent_t>>> ev; hipEvent_t cur; };
+    Ctx c; c.s = hs[0]->stream;
+    auto cb = [](void *vp, int cls, bool begin) {
+        Ctx *cc = (Ctx *)vp;
+        hipEvent_t e; hipEventCreate(&e); hipEventRecord(e, cc->s);
+        if (begin) cc->cur = e; else cc->ev.push_back({cls, {cc->cur, e}});
+    };
+    const int rc = decode_batch_impl(hs, n, tokens, nullptr, next_tokens, cb, &c);
+    for (auto &e : c.ev) {
+        float t = 0; hipEventElapsedTime(&t, e.second.first, e.second.second);
+        ms[e.first] += t; launches[e.first]++;
+        hipEventDestroy(e.second.first); hipEventDestroy(e.second.second);
+    }
+    if (rc) return rc;
+    const double groups = (double)((n + PREFILL_TB - 1) / PREFILL_TB);
+    for (int k = 0; k < SP_HIPKV_NCLASS; k++) if (k != 5 && k != 6) bytes[k] = per[k] * groups;
     return 0;
 }
 
@@ -964,15 +1110,7 @@ int sp_hipkv_set_mode(sp_kvdecode_handle *h, int exact) {
     if (h->dpos != 0) return fail("sp_hipkv_set_mode: the mode is fixed once tokens are resident%s");
     // exact V-sum: weights <= 2^22, |vq| < 2^23, so int64 totals hold 2^18 positions
     if (m == EXACT && h->pmax > (1 << 18)) return fail("sp_hipkv_set_mode: exact mode holds at most %s%lld positions", "", (long long)(1 << 18));
-    h->mode = m;
-    free_graphs(h);
-    if (h->b.buf || h->b.dbuf) {
-        hipStreamSynchronize(h->stream);
-        if (h->b.buf) hipFree(h->b.buf);
-        if (h->b.dbuf) hipFree(h->b.dbuf);
-        if (h->b.hstage) hipHostFree(h->b.hstage);
-        h->b = sp_kvdecode_handle::Batch{};
-    }
+    set_handle_mode(h, m);
     return 0;
 }
 
@@ -1001,19 +1139,27 @@ int sp_hipkv_set_batch_prefill(sp_kvdecode_handle *h, int on) {
 int sp_hipkv_fork(const sp_kvdecode_handle *p, sp_kvdecode_handle **out) {
     if (!p || !out) return fail("sp_hipkv_fork: null argument%s");
     *out = nullptr;
-    std::unique_ptr<sp_kvdecode_handle> h(new sp_kvdecode_handle);
+    std::unique_ptr<sp_kvdecode_handle> h;
     {
         std::lock_guard<std::mutex> lk(g_mu);
-        h->m = p->m; h->m->refs++;
+        p->m->refs++;
+        h.reset(take_shell(p->m, p->pmax, p->max_rewind));
     }
-    h->pool = p->pool; h->mode = p->mode; h->pmax = p->pmax; h->dpos = p->dpos; h->hwm = p->hwm;
+    if (h) {
+        set_handle_mode(h.get(), p->mode);
+    } else {
+        h.reset(new sp_kvdecode_handle);
+        h->m = p->m; h->pmax = p->pmax; h->max_rewind = p->max_rewind; h->mode = p->mode;
+        if (hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking) != hipSuccess) {
+            std::lock_guard<std::mutex> lk(g_mu); model_put(p->m); return fail("sp_hipkv_fork: stream creation failed%s");
+        }
+        if (build_tables(h.get()) || alloc_scratch(h.get())) {
+            std::lock_guard<std::mutex> lk(g_mu); free_handle(h.release()); model_put(p->m); return 1;
+        }
+    }
+    h->pool = p->pool; h->dpos = p->dpos; h->hwm = p->hwm;
     h->use_batch = p->use_batch; h->use_graph = p->use_graph;
-    h->use_graph = p->use_graph; h->max_rewind = p->max_rewind;
-    if (hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking) != hipSuccess) {
-        std::lock_guard<std::mutex> lk(g_mu); model_put(h->m); return fail("sp_hipkv_fork: stream creation failed%s");
-    }
     hipStreamSynchronize(p->stream);
-    if (build_tables(h.get()) || alloc_scratch(h.get())) { sp_hipkv_close(h.release()); return 1; }
     // share every mapped page (copy-on-write on the next append into it)
     {
         std::lock_guard<std::mutex> pl(h->pool->mu);
@@ -1021,7 +1167,8 @@ int sp_hipkv_fork(const sp_kvdecode_handle *p, sp_kvdecode_handle **out) {
             for (int s = 0; s < h->slots[l]; s++) {
                 const int id = p->pt[l][s];
                 h->pt[l][s] = id;
-                if (id >= 0) { h->pool->refc[id]++; h->h_pt[h->pt_off[l] + s] = h->pool->ptr[id]; }
+                if (id >= 0) h->pool->refc[id]++;
+                h->h_pt[h->pt_off[l] + s] = id >= 0 ? h->pool->ptr[id] : nullptr;
             }
         }
     }

@@ -37,6 +37,18 @@ static spx_fork_fn fork_for(const sp_kvdecode_dispatch_fn *dt) {
     return NULL;
 }
 
+/* batch hook: a backend that decodes many handles in one pass registers it */
+static const sp_kvdecode_dispatch_fn *g_batch_dt[8];
+static spx_batch_fn g_batch_fn[8];
+void spx_register_batch(const sp_kvdecode_dispatch_fn *dt, spx_batch_fn fn) {
+    for (int i = 0; i < 8; i++)
+        if (!g_batch_dt[i] || g_batch_dt[i] == dt) { g_batch_dt[i] = dt; g_batch_fn[i] = fn; return; }
+}
+static spx_batch_fn batch_for(const sp_kvdecode_dispatch_fn *dt) {
+    for (int i = 0; i < 8; i++) if (dt && g_batch_dt[i] == dt) return g_batch_fn[i];
+    return NULL;
+}
+
 struct sp_session {
     const sp_model     *model;
     qwen3_model        *qm;         /* borrowed from the model handle */
@@ -159,6 +171,64 @@ sp_status sp_decode_step(sp_session *s, int32_t token, float *logits, size_t log
         return SP_EBADSTATE;
     }
     s->pos++;
+    return SP_OK;
+}
+
+sp_status spx_decode_batch(sp_session *const *ss, size_t n, const int32_t *tokens, float *logits,
+                           size_t logits_capacity, int32_t *next_tokens) {
+    if (!ss || !tokens || n == 0) { sp_set_error("spx_decode_batch: null arg"); return SP_EBADARG; }
+    if (n > 0x7FFFFFFF) { sp_set_error("spx_decode_batch: too many sessions"); return SP_EBADARG; }
+    const sp_kvdecode_dispatch_fn *dt = ss[0] ? ss[0]->kv_dt : NULL;
+    for (size_t i = 0; i < n; i++) {            /* every guard before any decode */
+        sp_session *s = ss[i];
+        if (!s) { sp_set_error("spx_decode_batch: null session"); return SP_EBADARG; }
+        if (logits && logits_capacity / n < s->n_vocab) {
+            sp_set_error("spx_decode_batch: logits_capacity < n * vocab_size"); return SP_EBADARG;
+        }
+        if (s->pos >= s->hist_cap) { sp_set_error("spx_decode_batch: context full"); return SP_ECONTEXT_FULL; }
+        if (cancelled(s)) return SP_ECANCEL;
+        if (!backend_ready(s, "spx_decode_batch")) return SP_EUNSUPPORTED;
+        if (s->kv_dt != dt || s->model != ss[0]->model) {
+            sp_set_error("spx_decode_batch: sessions use different models or backends"); return SP_EBADARG;
+        }
+        for (size_t j = 0; j < i; j++)
+            if (ss[j] == s) { sp_set_error("spx_decode_batch: a session appears twice"); return SP_EBADARG; }
+    }
+    const uint32_t V = ss[0]->n_vocab;
+    spx_batch_fn fn = batch_for(dt);
+    int rc = 0;
+    if (fn) {
+        sp_kvdecode_handle **hs = (sp_kvdecode_handle **)malloc(n * sizeof *hs);
+        if (!hs) { sp_set_error("spx_decode_batch: out of memory"); return SP_ENOMEM; }
+        for (size_t i = 0; i < n; i++) hs[i] = ss[i]->kv_h;
+        rc = fn(hs, (int)n, tokens, logits, next_tokens);
+        free(hs);
+    } else {                                    /* no batch hook: one step each */
+        float *row = logits ? NULL : (float *)malloc((size_t)V * sizeof(float));
+        if (!logits && !row) { sp_set_error("spx_decode_batch: out of memory"); return SP_ENOMEM; }
+        for (size_t i = 0; i < n && !rc; i++) {
+            float *lg = logits ? logits + i * V : row;
+            rc = dt->decode_step(ss[i]->kv_h, tokens[i], lg);
+            if (!rc && next_tokens) {
+                uint32_t best = 0;
+                for (uint32_t k = 1; k < V; k++) if (lg[k] > lg[best]) best = k;
+                next_tokens[i] = (int32_t)best;
+            }
+        }
+        free(row);
+    }
+    /* commit what the backend advanced (all of them on success) */
+    for (size_t i = 0; i < n; i++) {
+        sp_session *s = ss[i];
+        if (rc && (!dt->position || dt->position(s->kv_h) != (int)s->pos + 1)) continue;
+        s->hist[s->pos] = tokens[i];
+        s->pos++;
+    }
+    if (rc) {
+        const char *prev = sp_last_error();
+        if (!prev || !prev[0]) sp_set_error("spx_decode_batch: kvdecode backend batch step failed");
+        return SP_EBADSTATE;
+    }
     return SP_OK;
 }
 

@@ -87,6 +87,7 @@ def l1():
         _sig(lib, "sp_session_kvdecode_backend_handle", c_void_p, [c_void_p])
         _sig(lib, "sp_session_kvdecode_backend_dt", c_void_p, [c_void_p])
         _sig(lib, "spx_session_own_kvdecode", c_int, [c_void_p, c_int])
+        _sig(lib, "spx_decode_batch", c_int, [c_void_p, c_size_t, c_void_p, c_void_p, c_size_t, c_void_p])
         _l1 = lib
     return _l1
 
@@ -115,6 +116,7 @@ def kv():
         _sig(lib, "sp_hipkv_greedy", c_int, [c_void_p, c_int32, c_int, c_void_p, ctypes.POINTER(c_double)])
         _sig(lib, "sp_hipkv_decode_batch", c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p])
         _sig(lib, "sp_hipkv_kernel_times", c_int, [c_void_p, c_int32, c_int, c_void_p, c_void_p, c_void_p])
+        _sig(lib, "sp_hipkv_decode_batch_times", c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p])
         _sig(lib, "sp_hipkv_read_kv", c_int, [c_void_p, c_int, c_int, c_int, c_void_p, c_void_p])
         _sig(lib, "sp_hipkv_info", c_int, [c_void_p, c_void_p])
         _kv = lib
@@ -218,6 +220,20 @@ class Session:
     def backend_handle(self):
         return l1().sp_session_kvdecode_backend_handle(self.h)
 
+    @staticmethod
+    def decode_batch(sessions, tokens, vocab, want_logits=True):
+        """spx_decode_batch: one token per session in one call; returns
+        (status, logits [n][vocab] or None, greedy next tokens [n])."""
+        import numpy as np
+        n = len(sessions)
+        ss = (c_void_p * n)(*[s.h.value if isinstance(s.h, c_void_p) else s.h for s in sessions])
+        toks = np.ascontiguousarray(tokens, dtype=np.int32)
+        lg = np.zeros((n, vocab), np.float32) if want_logits else None
+        nxt = np.zeros(n, np.int32)
+        rc = l1().spx_decode_batch(ss, n, ptr(toks), ptr(lg) if want_logits else None,
+                                   lg.size if want_logits else 0, ptr(nxt))
+        return rc, lg, nxt
+
     def close(self):
         if self.h:
             l1().sp_session_destroy(self.h)
@@ -279,6 +295,22 @@ class Backend:
         check(kv().sp_hipkv_decode_batch(hs, n, ptr(toks), ptr(lg) if want_logits else None, ptr(nxt)),
               "sp_hipkv_decode_batch")
         return lg, nxt
+
+    @staticmethod
+    def decode_batch_times(backends, tokens):
+        """One timed batched step (sp_hipkv_decode_batch_times): returns
+        (next tokens, ms[NCLASS], launches[NCLASS], bytes[NCLASS])."""
+        import numpy as np
+        n = len(backends)
+        hs = (c_void_p * n)(*[b.h.value if isinstance(b.h, c_void_p) else b.h for b in backends])
+        toks = np.ascontiguousarray(tokens, dtype=np.int32)
+        nxt = np.zeros(n, np.int32)
+        ms = np.zeros(NCLASS, np.float64)
+        nl = np.zeros(NCLASS, np.int64)
+        by = np.zeros(NCLASS, np.float64)
+        check(kv().sp_hipkv_decode_batch_times(hs, n, ptr(toks), ptr(nxt), ptr(ms), ptr(nl), ptr(by)),
+              "sp_hipkv_decode_batch_times")
+        return nxt, ms, nl, by
 
     def greedy(self, first_tok, n):
         import numpy as np

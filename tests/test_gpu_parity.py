@@ -138,22 +138,31 @@ def test_batched_prefill_matches_stepwise(tmpdir_models, exact):
     b1.close(); b2.close(); close_all(s, m)
 
 
-def test_fresh_handles_prefill_identically(tmpdir_models):
-    """Handles opened, forked and closed in a row (each with freshly allocated
-    and cleared scratch and batch buffers, reusing memory that earlier handles
-    freed) leave bit-identical K/V after the same prefill: the buffer clears are
-    ordered before the handles' own kernels."""
+@pytest.mark.parametrize("anchor", [False, True])
+def test_fresh_handles_prefill_identically(tmpdir_models, anchor):
+    """Handles opened, forked and closed in a row leave bit-identical K/V and
+    logits after the same prefill.  Without an anchor every close frees the
+    device model, so each handle allocates and clears fresh buffers (reusing
+    memory earlier handles freed): the clears are ordered before the handles'
+    kernels.  With an anchor handle open, closed handles are kept as shells and
+    the next open / fork takes one (tables, scratch, graphs reused, also across
+    a float-mode user in between)."""
     spm, spt = model_files(tmpdir_models, "qwen3-hd128")
     m = spkv.Model(spm, spt); s = spkv.Session(m, 512)
     qm = spkv.l1().sp_session_qwen3_model(s.h)
     pr = prompt(200, 2048, seed=21)
+    keep = spkv.Backend(qm, 512, exact=True) if anchor else None
     ref = None
+    lg = np.zeros(2048, np.float32)
     for it in range(12):
+        if it % 4 == 3:                              # a float-mode user of the same shells
+            fb = spkv.Backend(qm, 512, exact=False); fb.prefill(pr[:50]); fb.decode(1, lg); fb.close()
         b = spkv.Backend(qm, 512, exact=True)
-        if it % 2:                                   # a fork brings its own buffers
+        if it % 2:                                   # a fork brings its own buffers (or a shell)
             f = b.fork(); b.close(); b = f
-        b.prefill(pr)
-        kv = [b.read_kv(layer, 0, 200, 4 * 128) for layer in range(2)]
+        b.prefill(pr[:-1])
+        b.decode(int(pr[-1]), lg)
+        kv = [b.read_kv(layer, 0, 200, 4 * 128) for layer in range(2)] + [lg.copy()]
         b.close()
         if ref is None:
             ref = kv
@@ -161,7 +170,56 @@ def test_fresh_handles_prefill_identically(tmpdir_models):
         for layer in range(2):
             assert same_bits(kv[layer][0], ref[layer][0]) and same_bits(kv[layer][1], ref[layer][1]), \
                 f"handle {it} layer {layer}"
+        assert same_bits(kv[2], ref[2]), f"handle {it} logits"
+    if keep:
+        keep.close()
     close_all(s, m)
+
+
+@pytest.mark.parametrize("exact", [True, False])
+def test_session_decode_batch_with_clone_and_rewind(tmpdir_models, exact):
+    """The batched configuration through the session layer: every step each
+    session is cloned (sp_session_clone, the parent closed), the clone rewound
+    0-4 tokens (sp_session_rewind) and all clones decoded by one
+    spx_decode_batch; the same sequence with sp_decode_step on a second set of
+    sessions gives the same logits (exact: bit for bit) and positions."""
+    spm, spt = model_files(tmpdir_models, "qwen3-g4")
+    m = spkv.Model(spm, spt)
+    V = 2048
+    lens = [20, 64, 65, 150, 7]
+    A, B = [], []
+    lg = np.zeros(V, np.float32)
+    toks = []
+    for i, n in enumerate(lens):
+        pr = prompt(n, V, seed=30 + i)
+        for group in (A, B):
+            s = spkv.Session(m, 512)
+            s.attach(512, exact=exact)
+            assert s.prefill(pr, lg) == 0
+            group.append(s)
+        toks.append(int(lg.argmax()))
+    rng = np.random.default_rng(5)
+    for step in range(6):
+        r = rng.integers(0, 5, size=len(lens))
+        for group in (A, B):
+            for i in range(len(lens)):
+                c = group[i].clone(); group[i].close(); group[i] = c
+                if r[i]:
+                    assert c.rewind(int(r[i])) == 0
+        rc, lga, nxt = spkv.Session.decode_batch(A, toks, V)
+        assert rc == 0, spkv.last_error()
+        for i in range(len(lens)):
+            assert B[i].decode(toks[i], lg) == 0
+            if exact:
+                assert same_bits(lga[i], lg), f"step {step} session {i}"
+            else:
+                assert rel(lga[i], lg) < FLOAT_TOL, f"step {step} session {i}"
+            assert int(nxt[i]) == int(lga[i].argmax())
+            assert A[i].position() == B[i].position()
+        toks = [int(t) for t in nxt]
+    for x in A + B:
+        x.close()
+    m.close()
 
 
 @pytest.mark.parametrize("name", ["qwen3-hd128", "gemma3-hd256"])

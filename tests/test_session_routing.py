@@ -194,3 +194,96 @@ def test_hipkv_open_without_gpu_fails_loudly(session):
     h = ctypes.c_void_p()
     rc = spkv.kv().sp_hipkv_open(qm, 16, ctypes.byref(h))
     assert rc != 0 and "no HIP device" in spkv.last_error()
+
+
+class SharedMock:
+    """One dispatch table serving several handles (per-handle positions), as a
+    backend serving many sessions does; no batch hook is registered for it."""
+
+    def __init__(self, vocab, fail_handle=None):
+        self.calls, self.dpos, self.vocab, self.fail_handle = [], {}, vocab, fail_handle
+        self._fns = [OPEN(lambda qm, p, out: 0), PREFILL(lambda h, t, n: 0), STEP(self.step),
+                     REWIND(lambda h, n: 0), POSN(lambda h: self.dpos.get(h, 0)), CLOSE(lambda h: None)]
+        self.table = spkv.DispatchTable(*[ctypes.cast(f, ctypes.c_void_p) for f in self._fns])
+
+    def step(self, h, tok, logits):
+        self.calls.append((h, tok))
+        if h == self.fail_handle:
+            return 1
+        for i in range(self.vocab):
+            logits[i] = float(i == (tok + 3) % self.vocab)
+        self.dpos[h] = self.dpos.get(h, 0) + 1
+        return 0
+
+
+@pytest.fixture
+def sessions(tmpdir_models):
+    spm, spt = model_files(tmpdir_models, "qwen3-tiny", max_context=32)
+    m = spkv.Model(spm, spt)
+    flag = ctypes.c_int(0)
+    ss = [spkv.Session(m, 0, cancel=flag) for _ in range(3)]
+    yield ss, flag, m
+    for s in ss:
+        s.close()
+    m.close()
+
+
+def test_decode_batch_without_hook_steps_each_session(sessions):
+    """spx_decode_batch on a table with no batch hook: one decode_step per
+    session in order, logits rows and greedy tokens returned, every session
+    advanced by one."""
+    ss, _, _ = sessions
+    mock = SharedMock(1000)
+    for i, s in enumerate(ss):
+        assert spkv.l1().sp_session_register_kvdecode_backend(s.h, ctypes.c_void_p(0x100 + i),
+                                                              ctypes.byref(mock.table)) == 0
+    rc, lg, nxt = spkv.Session.decode_batch(ss, [7, 8, 9], 1000)
+    assert rc == 0
+    assert mock.calls == [(0x100, 7), (0x101, 8), (0x102, 9)]
+    assert nxt.tolist() == [10, 11, 12] and [int(r.argmax()) for r in lg] == [10, 11, 12]
+    assert [s.position() for s in ss] == [1, 1, 1]
+    rc, lg, nxt = spkv.Session.decode_batch(ss, [1, 2, 3], 1000, want_logits=False)
+    assert rc == 0 and lg is None and nxt.tolist() == [4, 5, 6] and [s.position() for s in ss] == [2, 2, 2]
+
+
+def test_decode_batch_guards(sessions, tmpdir_models):
+    """Every guard is checked for every session before any decode: duplicates,
+    mixed tables, no backend, short logits buffer, cancel, context full."""
+    ss, flag, m = sessions
+    L = spkv.l1()
+    mock, other = SharedMock(1000), SharedMock(1000)
+    assert spkv.Session.decode_batch(ss, [1, 2, 3], 1000)[0] == spkv.SP_EUNSUPPORTED
+    for i, s in enumerate(ss):
+        L.sp_session_register_kvdecode_backend(s.h, ctypes.c_void_p(0x100 + i), ctypes.byref(mock.table))
+    assert spkv.Session.decode_batch([ss[0], ss[1], ss[0]], [1, 2, 3], 1000)[0] == spkv.SP_EBADARG
+    assert "twice" in spkv.last_error()
+    L.sp_session_register_kvdecode_backend(ss[2].h, ctypes.c_void_p(0x102), ctypes.byref(other.table))
+    assert spkv.Session.decode_batch(ss, [1, 2, 3], 1000)[0] == spkv.SP_EBADARG
+    L.sp_session_register_kvdecode_backend(ss[2].h, ctypes.c_void_p(0x102), ctypes.byref(mock.table))
+    lg = np.zeros((3, 999), np.float32)
+    n = (ctypes.c_void_p * 3)(*[s.h.value for s in ss])
+    t = np.array([1, 2, 3], np.int32)
+    assert L.spx_decode_batch(n, 3, spkv.ptr(t), spkv.ptr(lg), lg.size, None) == spkv.SP_EBADARG
+    assert L.spx_decode_batch(None, 3, spkv.ptr(t), None, 0, None) == spkv.SP_EBADARG
+    flag.value = 1
+    assert spkv.Session.decode_batch(ss, [1, 2, 3], 1000)[0] == spkv.SP_ECANCEL
+    flag.value = 0
+    assert mock.calls == [] and [s.position() for s in ss] == [0, 0, 0]
+    # context full on the last session: nothing decodes
+    for _ in range(32):
+        assert ss[2].decode(1, np.zeros(1000, np.float32)) == 0
+    mock.calls.clear()
+    assert spkv.Session.decode_batch(ss, [1, 2, 3], 1000)[0] == spkv.SP_ECONTEXT_FULL
+    assert mock.calls == [] and [s.position() for s in ss] == [0, 0, 32]
+
+
+def test_decode_batch_failure_commits_only_advanced_sessions(sessions):
+    """A backend failure at the second session: SP_EBADSTATE, the first session
+    (advanced by its backend) is committed, the others keep their position."""
+    ss, _, _ = sessions
+    mock = SharedMock(1000, fail_handle=0x101)
+    for i, s in enumerate(ss):
+        spkv.l1().sp_session_register_kvdecode_backend(s.h, ctypes.c_void_p(0x100 + i), ctypes.byref(mock.table))
+    rc, _, _ = spkv.Session.decode_batch(ss, [4, 5, 6], 1000)
+    assert rc == spkv.SP_EBADSTATE
+    assert [s.position() for s in ss] == [1, 0, 0]
