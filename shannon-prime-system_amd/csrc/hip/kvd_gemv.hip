@@ -179,7 +179,7 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
     const int b_lo = split * bps, b_hi = b_lo + bps < nblk ? b_lo + bps : nblk, nb = b_hi - b_lo;
     uint4 *dig = smem4;                                   // NDIG * nb
     float *xf = (float *)(dig + NDIG * nb);               // pro.n floats (norm prologues only)
-    __shared__ double red[GEMV_WAVES];
+    __shared__ double red[RED_SLOTS * RED_WAVES];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nwaves = blockDim.x >> 6;
     constexpr int HR = GEMV_R / 2;

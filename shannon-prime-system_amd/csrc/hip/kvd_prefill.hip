@@ -30,7 +30,7 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 template <int PRO>
 __global__ __launch_bounds__(512) void k_stage(StageArgs a) {
     extern __shared__ float xf[];                      // pro.n floats (norm prologues)
-    __shared__ double red[8];
+    __shared__ double red[RED_SLOTS * RED_WAVES];
     const int t = blockIdx.x, n = a.pro.n, nblk = n / 32, tid = threadIdx.x;
     int8_t *planes = a.planes;
     if (t >= a.T) {                                     // padding tokens: zero planes

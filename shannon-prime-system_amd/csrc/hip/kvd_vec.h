@@ -27,33 +27,66 @@ __device__ __forceinline__ i128 wave_sum128(i128 v) {
     }
     return v;
 }
-// block-wide reductions for 256 threads through a small LDS scratch
-template <typename T> __device__ T block_sum(T v, T *red) {   // red: blockDim/64 slots
-    v = wave_sum(v);
-    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
-    __syncthreads();
-    if (l == 0) red[w] = v;
+// Wave reductions to lane 63 through DPP (no LDS round trips): pair and quad
+// swaps, the half-row and row mirrors leave each 16-lane row's total in all of
+// its lanes, then row_bcast15 / row_bcast31 fold rows 0+1 and 2+3 and then
+// both halves into lane 63.  `ident` is what lanes outside a broadcast's row
+// mask add.
+template <int CTRL, int RMASK> __device__ __forceinline__ uint32_t dpp32(uint32_t v, uint32_t old) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)v, CTRL, RMASK, 0xF, false);
+}
+template <int CTRL, int RMASK> __device__ __forceinline__ uint64_t dpp64(uint64_t v, uint64_t old) {
+    return ((uint64_t)dpp32<CTRL, RMASK>((uint32_t)(v >> 32), (uint32_t)(old >> 32)) << 32) |
+           dpp32<CTRL, RMASK>((uint32_t)v, (uint32_t)old);
+}
+template <typename T, typename Op> __device__ __forceinline__ T wave_to63(T v, T ident, Op op) {
+    typedef typename std::conditional<sizeof(T) == 8, uint64_t, uint32_t>::type B;
+    auto mv = [&](auto ctrl_tag, T x) -> T {
+        constexpr int C = decltype(ctrl_tag)::value >> 4, M = decltype(ctrl_tag)::value & 15;
+        if constexpr (sizeof(T) == 8) return __builtin_bit_cast(T, dpp64<C, M>(__builtin_bit_cast(B, x), __builtin_bit_cast(B, ident)));
+        else return __builtin_bit_cast(T, dpp32<C, M>(__builtin_bit_cast(B, x), __builtin_bit_cast(B, ident)));
+    };
+    v = op(v, mv(std::integral_constant<int, (0xB1 << 4) | 0xF>{}, v));     // quad_perm 1,0,3,2
+    v = op(v, mv(std::integral_constant<int, (0x4E << 4) | 0xF>{}, v));     // quad_perm 2,3,0,1
+    v = op(v, mv(std::integral_constant<int, (0x141 << 4) | 0xF>{}, v));    // row_half_mirror
+    v = op(v, mv(std::integral_constant<int, (0x140 << 4) | 0xF>{}, v));    // row_mirror
+    v = op(v, mv(std::integral_constant<int, (0x142 << 4) | 0xA>{}, v));    // row_bcast15 -> rows 1, 3
+    v = op(v, mv(std::integral_constant<int, (0x143 << 4) | 0xC>{}, v));    // row_bcast31 -> rows 2, 3
+    return v;
+}
+
+// Block-wide reductions through one LDS slot array per reduction: lane 63 of
+// each wave posts its wave total, one barrier, every thread combines the
+// totals.  A reduction writes only its own `red` slots, so consecutive
+// reductions need no barrier in between; a slot array is used once per launch.
+constexpr int RED_WAVES = 16;                 // slots per reduction (waves per workgroup)
+constexpr int RED_SLOTS = 3;                  // reductions per input transform
+template <typename T> __device__ T block_sum(T v, T *red) {
+    v = wave_to63(v, (T)0, [](T a, T b) { return a + b; });
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 63) red[w] = v;
     __syncthreads();
     T t = red[0];
     for (int i = 1; i < (int)(blockDim.x >> 6); i++) t += red[i];
     return t;
 }
 __device__ float block_max(float v, float *red) {
-    v = wave_max(v);
-    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
-    __syncthreads();
-    if (l == 0) red[w] = v;
+    v = wave_to63(v, -INFINITY, [](float a, float b) { return fmaxf(a, b); });
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 63) red[w] = v;
     __syncthreads();
     float t = red[0];
     for (int i = 1; i < (int)(blockDim.x >> 6); i++) t = fmaxf(t, red[i]);
     return t;
 }
+// slot k of a RED_SLOTS x RED_WAVES x 8-byte reduction scratch
+__device__ __forceinline__ void *red_slot(void *red, int k) { return (uint8_t *)red + (size_t)k * RED_WAVES * 8; }
 
 // ------------------------------------------------------- RMSNorm (both modes)
 // Float mode: core/forward_kernels/forward_kernels.c:17-22 (sum of squares in
 // double, 1/sqrtf((float)(ss/n)+eps), out = x*scale*w).  Exact mode: the
 // integer island core/exact_islands/exact_islands.c:60-79 (no eps).
-struct NormScale { float f; int64_t inv; int zero; };
+struct NormScale { float f; int64_t inv; double invd; int zero; };
 
 // One thread's share of a sum of squares: double in float mode, the exact
 // int64 sum of the Q16 values in exact mode.
@@ -61,12 +94,16 @@ __device__ __forceinline__ int64_t llround_q16(float x) { return llround_pow2<16
 struct SumSq {
     double f = 0.0; int64_t i = 0;
     __device__ __forceinline__ void add(float v, int mode) {
-        if (mode == FLOAT) f += (double)v * (double)v;
+        if (mode == FLOAT) { f += (double)v * (double)v; return; }
+        // llround(v * 2^16): roundf of the exact float product is that integer;
+        // below 2^31 its square is one 32 x 32 -> 64 multiply
+        const float r = roundf(v * 65536.0f);
+        if (fabsf(r) < 2147483648.0f) { const int32_t q = (int32_t)r; i += (int64_t)q * q; }
         else { const int64_t q = llround_q16(v); i += q * q; }
     }
 };
 __device__ NormScale norm_finish(const SumSq &p, int n, float eps, int mode, void *red) {
-    NormScale s; s.f = 0.0f; s.inv = 0; s.zero = 0;
+    NormScale s; s.f = 0.0f; s.inv = 0; s.invd = 0.0; s.zero = 0;
     if (mode == FLOAT) {
         const double ss = block_sum<double>(p.f, (double *)red);
         s.f = 1.0f / sqrtf((float)(ss / n) + eps);
@@ -74,12 +111,25 @@ __device__ NormScale norm_finish(const SumSq &p, int n, float eps, int mode, voi
         const int64_t ss = block_sum<int64_t>(p.i, (int64_t *)red);
         if (ss == 0) { s.zero = 1; return s; }
         s.inv = rms_inv_q72(n, ss);
+        s.invd = (double)s.inv;                       // inv < 2^43: exact
     }
     return s;
 }
+// Exact mode: the island's (int64)(xi * inv * wi) / 2^52 rounded to float.
+// With xi = llround(x 2^16), wi = llround(w 2^16): xi * wi is exact in double
+// below 2^53, and the double product with inv is then the double nearest the
+// exact integer product -- the island's int64 -> double conversion -- as long
+// as that product does not wrap (|product| < 2^62 checked); otherwise the
+// 64-bit integer path.
 __device__ __forceinline__ float norm_apply(float x, float w, const NormScale &s, int mode) {
     if (mode == FLOAT) return x * s.f * w;
     if (s.zero) return 0.0f;
+    const double dx = (double)roundf(x * 65536.0f) * (double)roundf(w * 65536.0f);
+    if (fabs(dx) < 9007199254740992.0) {              // 2^53
+        const double pr = dx * s.invd;
+        if (fabs(pr) < 4611686018427387904.0)          // 2^62
+            return (float)(pr * 2.220446049250313e-16);  // 2^-52
+    }
     const int64_t xi = llround_q16(x), wi = llround_q16(w);
     return (float)((double)mul3_lo64(xi, s.inv, wi) / 4503599627370496.0);   // 2^52
 }
@@ -98,6 +148,7 @@ constexpr int PB = 8;
 // sh = 22 - frexp_exponent(max |x|) of the result (SH_ZERO for an all-zero
 // vector).  The result is left in xf (LDS, n floats), or read from p.x for
 // PRO_PLAIN.  x_out (the updated residual) is written when write_x is set.
+// red: RED_SLOTS x RED_WAVES x 8 bytes of LDS, used once per launch.
 template <int PRO>
 __device__ int input_transform(const ProArgs &p, int mode, float *xf, void *red, bool write_x) {
     const int n = p.n, T = blockDim.x, tid = threadIdx.x;
@@ -128,7 +179,7 @@ __device__ int input_transform(const ProArgs &p, int mode, float *xf, void *red,
                 SumSq q;
                 #pragma unroll
                 for (int k = 0; k < PB; k++) if (k * T + tid < n) q.add(dv[k], mode);
-                sd = norm_finish(q, n, p.eps, mode, red);
+                sd = norm_finish(q, n, p.eps, mode, red_slot(red, 0));
             }
             const bool wr = write_x && p.x_out;
             #pragma unroll
@@ -141,7 +192,7 @@ __device__ int input_transform(const ProArgs &p, int mode, float *xf, void *red,
         SumSq q;
         #pragma unroll
         for (int k = 0; k < PB; k++) if (k * T + tid < n) q.add(xv[k], mode);
-        const NormScale s = norm_finish(q, n, p.eps, mode, red);
+        const NormScale s = norm_finish(q, n, p.eps, mode, red_slot(red, 1));
         #pragma unroll
         for (int k = 0; k < PB; k++) {
             const int i = k * T + tid;
@@ -160,7 +211,7 @@ __device__ int input_transform(const ProArgs &p, int mode, float *xf, void *red,
                 #pragma unroll
                 for (int k = 0; k < PB; k++) { const int i = base + k * T + tid; if (i < n) xf[i] = a[k]; }
             }
-            s = norm_finish(q, n, p.eps, mode, red);
+            s = norm_finish(q, n, p.eps, mode, red_slot(red, 1));
         } else {
             NormScale sd; sd.f = 0.0f; sd.inv = 0; sd.zero = 0;
             if (p.post_w) {
@@ -172,7 +223,7 @@ __device__ int input_transform(const ProArgs &p, int mode, float *xf, void *red,
                     #pragma unroll
                     for (int k = 0; k < PB; k++) q.add(a[k], mode);
                 }
-                sd = norm_finish(q, n, p.eps, mode, red);
+                sd = norm_finish(q, n, p.eps, mode, red_slot(red, 0));
             }
             // residual add (+ sandwich norm of the branch), sum of squares of the result
             SumSq q;
@@ -193,7 +244,7 @@ __device__ int input_transform(const ProArgs &p, int mode, float *xf, void *red,
                     if (i < n) { xf[i] = r; if (wr) p.x_out[i] = r; q.add(r, mode); }
                 }
             }
-            s = norm_finish(q, n, p.eps, mode, red);
+            s = norm_finish(q, n, p.eps, mode, red_slot(red, 1));
         }
         // xf <- norm(xf) * w; running max
         for (int base = 0; base < n; base += PB * T) {
@@ -207,7 +258,7 @@ __device__ int input_transform(const ProArgs &p, int mode, float *xf, void *red,
             }
         }
     }
-    m = block_max(m, (float *)red);                      // also orders the xf writes above
+    m = block_max(m, (float *)red_slot(red, 2));         // its barrier also orders the xf writes above
     if (m == 0.0f) return SH_ZERO;
     int e; frexpf(m, &e);
     return 22 - e;
