@@ -87,7 +87,9 @@ def pmc_traffic(kernel, path=PMC_SUMMARY):
 WORKLOADS = {
     "gemma3-12b-32k": dict(shape="gemma3-12b", ctx=32768),
     "qwen3-0.6b-4k": dict(shape="qwen3-0.6b", ctx=4096),
-    "gemma3-12b-128k": dict(shape="gemma3-12b", ctx=131072),
+    # 131072-token prefill, then greedy decode with a rewind of 1-64 tokens
+    # (seed 4) after every 16 steps; window layers keep a ring of W + 64
+    "gemma3-12b-128k": dict(shape="gemma3-12b", ctx=131072, rewind_every=16, rewind_max=64),
     # 64 concurrent sessions, contexts uniform in [1024, 16384] (seed 2); every
     # step clones each session (sp_session_clone), rewinds the clone 0-4 tokens
     # (seed 3) and decodes all 64 in one batched call (spx_decode_batch)
@@ -173,6 +175,13 @@ def main():
             spkv.check(spkv.kv().sp_hipkv_set_graph(be.h, 0), "sp_hipkv_set_graph")
         if args.no_batch_prefill:
             spkv.check(spkv.kv().sp_hipkv_set_batch_prefill(be.h, 0), "sp_hipkv_set_batch_prefill")
+        every = wl.get("rewind_every", 0)
+        if every:
+            # the window ring must hold every position a rewind can return to:
+            # rewinds are measured from the highest position ever written, and
+            # 1..rewind_max back every `every` steps can drift that far per run
+            max_rewind = (args.steps // every + 1) * wl["rewind_max"]
+            spkv.check(spkv.kv().sp_hipkv_set_max_rewind(be.h, max_rewind), "sp_hipkv_set_max_rewind")
         info = be.info()
 
         if args.calib_copy_mib:
@@ -200,12 +209,29 @@ def main():
         # device-resident greedy loop: warmup, then the timed steps
         toks, _ = be.greedy(tok, args.warmup)
         tok = int(toks[-1]) if args.warmup else tok
-        t0 = time.perf_counter()
-        toks, dev_ms = be.greedy(tok, args.steps)
-        wall = time.perf_counter() - t0
-        tok = int(toks[-1])
+        rewinds = []
+        if every:
+            # greedy runs of `every` steps, each followed by an O(1) rewind of
+            # 1..rewind_max tokens (the next run decodes from the rewound position)
+            rw = 1 + (splitmix_u64(args.steps // every + 1, 4) % np.uint64(wl["rewind_max"])).astype(np.int64)
+            dev_ms = 0.0
+            t0 = time.perf_counter()
+            for i in range(0, args.steps, every):
+                toks, ms_i = be.greedy(tok, min(every, args.steps - i))
+                dev_ms += ms_i
+                r = int(rw[i // every])
+                spkv.check(be.rewind(r), "sp_hipkv_rewind")
+                rewinds.append(r)
+                tok = int(toks[-1])
+            wall = time.perf_counter() - t0
+        else:
+            t0 = time.perf_counter()
+            toks, dev_ms = be.greedy(tok, args.steps)
+            wall = time.perf_counter() - t0
+            tok = int(toks[-1])
         value = args.steps / wall
-        log(f"decode {args.steps} steps: wall {wall*1e3:.1f} ms, device {dev_ms:.1f} ms -> {value:.1f} tok/s")
+        log(f"decode {args.steps} steps: wall {wall*1e3:.1f} ms, device {dev_ms:.1f} ms -> {value:.1f} tok/s"
+            + (f" ({len(rewinds)} rewinds, {sum(rewinds)} tokens)" if rewinds else ""))
 
         # per-kernel-class device times (each launch bracketed by HIP events)
         ms, nl, by = be.kernel_times(tok, args.kernel_steps)
@@ -232,13 +258,17 @@ def main():
             cpu = cpu_baseline(spm, be, info, shape, exact, args.cpu_steps, tok, sess)
 
         rec = {
-            "metric": METRIC, "value": round(value, 3), "unit": "tokens/s", "n_gpus": 1,
+            "metric": METRIC if args.workload == "gemma3-12b-32k" and ctx == 32768 else
+                      f"kvdecode tokens/s + KV-read HBM GB/s (% of peak), {args.workload} at ctx {ctx}",
+            "value": round(value, 3), "unit": "tokens/s", "n_gpus": 1,
             "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(1e3 * wall / args.steps, 4),
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
             "dtype": "int4xint4->int64 GEMV, int32 KV (exact mode)" if exact else "int4xint4->int64 GEMV, f32 KV/attention",
             "data": "synthetic: seeded random-init OK_Q4B weights (SplitMix64 seed 0, N(0,0.02)), seeded uniform prompt (seed 1)",
-            "config": {"workload": f"{args.workload}: {wl['shape']}-shape kvdecode, prefill {ctx} then {args.steps} greedy steps, batch 1",
-                       "ctx": ctx, "mode": args.mode, "b_kv": 4, "pmax": pmax},
+            "config": {"workload": f"{args.workload}: {wl['shape']}-shape kvdecode, prefill {ctx} then {args.steps} greedy steps, batch 1"
+                                   + (f", rewind 1-{wl['rewind_max']} tokens every {every} steps" if every else ""),
+                       "ctx": ctx, "mode": args.mode, "b_kv": 4, "pmax": pmax,
+                       **({"rewinds": rewinds, "max_rewind": max_rewind} if every else {})},
             "roofline": {"bound": "hbm", "kernel": dom["kernel"], "rocprof_kernels": dom_names,
                          "achieved": round(dom["gbs"], 1), "peak": PEAK_GBS, "unit": "GB/s",
                          "frac": round(dom["gbs"] / PEAK_GBS, 4),

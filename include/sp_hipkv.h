@@ -42,9 +42,12 @@ void sp_hipkv_close(sp_kvdecode_handle *h);
  * (integer islands + CORDIC RoPE + integer attention/GEMV, bit-reproducible).
  * Changing the mode invalidates the resident cache (dpos must be 0). */
 int  sp_hipkv_set_mode(sp_kvdecode_handle *h, int exact);
-/* Sliding-window layers keep a ring of window + max_rewind positions instead of a
- * full table (the SWA W-ring knob, sp_l1.h:466-479).  Rewinds beyond max_rewind
- * then fail.  Only before the first token (dpos == 0).  0 = full table (default). */
+/* Sliding-window layers keep a ring of window + max_rewind positions (rounded up
+ * to whole pages, plus one page) instead of a full table (the SWA W-ring knob,
+ * sp_l1.h:466-479).  A rewind then fails when the new position would lie more
+ * than the ring's slack (ring positions - window) behind the highest position
+ * ever written, since the ring has overwritten part of that position's window.
+ * Only before the first token (dpos == 0).  0 = full table (default). */
 int  sp_hipkv_set_max_rewind(sp_kvdecode_handle *h, int max_rewind);
 /* Copy-on-write fork of the resident cache (no counterpart in sp_l1.h: the
  * table has no fork row; sp_session_clone uses it through spx_register_fork). */
