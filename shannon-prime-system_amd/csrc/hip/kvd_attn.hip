@@ -23,6 +23,7 @@
 #include "kvd_internal.h"
 #include "kvd_exact.h"
 #include "kvd_qkprep.h"
+#include "kvd_vec.h"
 #include <cstdio>
 #include <cstdlib>
 
@@ -364,6 +365,7 @@ __global__ __launch_bounds__(256) void k_attn_float(AttnArgs a_in) {
     if (threadIdx.x == 0) is_last = (arrive(&a.counter[h]) == nch - 1);
     __syncthreads();
     if (!is_last) return;
+    StatAcc sacc;
     for (int g = 0; g < G; g++) {
         const size_t base = (size_t)(h * G + g) * a.max_chunks;
         const float *pml = a.part_ml + base * 2;
@@ -391,10 +393,13 @@ __global__ __launch_bounds__(256) void k_attn_float(AttnArgs a_in) {
                 acc3 += ld_agent(&po[(size_t)(k + 3) * HD + d]) * wk[k + 3];
             }
             for (; k < nch; k++) acc0 += ld_agent(&po[(size_t)k * HD + d]) * wk[k];
-            a.ao[(size_t)(h * G + g) * HD + d] = ((acc0 + acc1) + (acc2 + acc3)) / L;
+            const float o = ((acc0 + acc1) + (acc2 + acc3)) / L;
+            a.ao[(size_t)(h * G + g) * HD + d] = o;
+            sacc.add(o);
         }
         __syncthreads();
     }
+    if (a.stat_out) stat_flush_block(a.stat_out, sacc);       // max |ao| for the O GEMV
     if (threadIdx.x == 0) reset_counter(&a.counter[h]);
 }
 
@@ -604,14 +609,18 @@ __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a_in) {
         Sg[threadIdx.x] = S;
     }
     __syncthreads();
+    StatAcc sacc;
     for (int i = threadIdx.x; i < G * HD; i += 256) {
         int64_t acc = 0;
         #pragma unroll
         for (int r = 0; r < VREP; r++)
             acc += (int64_t)__hip_atomic_exchange((unsigned long long *)&a.vacc[(size_t)r * QDh + (size_t)h * G * HD + i], 0ull,
                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        a.ao[(size_t)h * G * HD + i] = rne_div_to_float((i128)acc, Sg[i / HD], 16);
+        const float o = rne_div_to_float((i128)acc, Sg[i / HD], 16);
+        a.ao[(size_t)h * G * HD + i] = o;
+        sacc.add(o);
     }
+    if (a.stat_out) stat_flush_block(a.stat_out, sacc);      // max |ao| for the O GEMV
     if (threadIdx.x == 0) reset_counter(&a.counter[h]);
 }
 
@@ -646,7 +655,11 @@ void launch_attention(const AttnArgs &a, int grid_chunks, hipStream_t s) {
 
 // ------------------------------------------------------------------ embedding
 __global__ __launch_bounds__(256) void k_embed(DevW w, const DState *st, const int *tokbuf, int pos0, const int *toks,
-                                                float *x, float scale) {
+                                                float *x, float scale, VecStat *stats, int nstats) {
+    // a decode step starts here: clear the step's vector statistics (plain
+    // stores; the step's later kernels accumulate into them)
+    static_assert(sizeof(VecStat) == 16, "one 16-byte store per statistic replica");
+    for (int i = threadIdx.x; i < nstats; i += blockDim.x) ((uint4 *)stats)[i] = make_uint4(0, 0, 0, 0);
     // decode: the step's token; batched: workgroup t embeds toks[t] (several
     // sessions) or tokbuf[pos0 + t] (one session's prefill) into row t
     const int tok = st ? (st->drive == DRIVE_STREAM ? tokbuf[st->pos] : st->tok)
@@ -664,12 +677,13 @@ __global__ __launch_bounds__(256) void k_embed(DevW w, const DState *st, const i
         x[i] = v;
     }
 }
-void launch_embed(const DevW &embd, const DState *st, const int *tokbuf, float *x, float scale, hipStream_t s) {
-    hipLaunchKernelGGL(k_embed, dim3(1), dim3(256), 0, s, embd, st, tokbuf, 0, nullptr, x, scale);
+void launch_embed(const DevW &embd, const DState *st, const int *tokbuf, float *x, float scale, hipStream_t s,
+                  VecStat *stats, int nstats) {
+    hipLaunchKernelGGL(k_embed, dim3(1), dim3(256), 0, s, embd, st, tokbuf, 0, nullptr, x, scale, stats, nstats);
 }
 void launch_embed_batch(const DevW &embd, const int *tokbuf, int pos0, int T, float *x, float scale, hipStream_t s,
                         const int *toks) {
-    hipLaunchKernelGGL(k_embed, dim3(T), dim3(256), 0, s, embd, nullptr, tokbuf, pos0, toks, x, scale);
+    hipLaunchKernelGGL(k_embed, dim3(T), dim3(256), 0, s, embd, nullptr, tokbuf, pos0, toks, x, scale, nullptr, 0);
 }
 __global__ void k_advance(DState *st) {
     if (threadIdx.x == 0 && st->drive == DRIVE_STREAM) st->pos = st->pos + 1;

@@ -346,6 +346,7 @@ struct sp_kvdecode_handle {
     float *rope = nullptr;                   // [2][HD] rotation table of the current step
     int64_t *vacc = nullptr, *vacc_s = nullptr;
     int64_t *gacc = nullptr;                 // GEMV split-K row totals (zero between launches)
+    VecStat *stats = nullptr;                // [NL][STAT_PER_LAYER][STAT_REP] vector statistics of the step
     int *gcnt = nullptr;                     // GEMV split arrival counters
     int acc_rows = 0;
     float *h_logits = nullptr;               // pinned staging
@@ -471,6 +472,7 @@ int alloc_scratch(sp_kvdecode_handle *h) {
         {(void **)&h->tokbuf, (size_t)h->pmax * 4 + 64}, {(void **)&h->rope, (size_t)m->HD * 2 * 4},
         {(void **)&h->vacc, (size_t)QD * 8 * VREP}, {(void **)&h->vacc_s, (size_t)m->NH * 8 * VREP},
         {(void **)&h->d_st, sizeof(DState) * 4},
+        {(void **)&h->stats, (size_t)m->NL * STAT_PER_LAYER * STAT_REP * sizeof(VecStat)},
     };
     size_t tot = 0;
     for (auto &it : items) tot = align_up(tot + it.n, 256);
@@ -560,7 +562,12 @@ void enqueue_body(sp_kvdecode_handle *h, const StepShape &sh, TimeCb cb, void *c
     const int QD = m->NH * m->HD, KVD = m->NKV * m->HD;
     auto T = [&](int cls, bool b) { if (cb) cb(ctx, cls, b); };
     T(8, true);
-    launch_embed(m->embd, h->d_st, h->tokbuf, h->x1, m->gemma ? sqrtf((float)m->E) : 0.0f, s);
+    // per layer: statistics of ao, ap, hh, dn, accumulated by the kernel that
+    // writes the vector and read by the GEMV that consumes it
+    VecStat *stat = h->stats;
+    auto st = [&](int l, int k) { return stat + ((size_t)l * STAT_PER_LAYER + k) * STAT_REP; };
+    launch_embed(m->embd, h->d_st, h->tokbuf, h->x1, m->gemma ? sqrtf((float)m->E) : 0.0f, s,
+                 stat, m->NL * STAT_PER_LAYER * STAT_REP);
     launch_rope_table(h->d_st, m->HD, h->mode, m->base, m->gemma ? 10000.0f : m->base,
                       m->freq_global, m->gemma ? m->freq_local : m->freq_global, h->rope, s);
     T(8, false);
@@ -574,6 +581,7 @@ void enqueue_body(sp_kvdecode_handle *h, const StepShape &sh, TimeCb cb, void *c
         else {
             g.pro.kind = PRO_RESID; g.pro.x = h->x0; g.pro.delta = h->dn; g.pro.x_out = h->x1;
             g.pro.post_w = m->gemma ? m->L[l - 1].post_ffw : nullptr;
+            g.pro.stat = st(l - 1, STAT_DN);
         }
         g.pro.norm_w = d.attn_norm; g.pro.n = m->E; g.pro.eps = m->eps;
         g.seg[0] = {d.q, h->q}; g.seg[1] = {d.k, h->k}; g.seg[2] = {d.v, h->v};
@@ -593,6 +601,7 @@ void enqueue_body(sp_kvdecode_handle *h, const StepShape &sh, TimeCb cb, void *c
         a.base = (m->gemma && !glob) ? 10000.0f : m->base;
         a.ascale = 1.0f / sqrtf((float)m->HD);
         a.chunk = glob ? sh.chunk_global : sh.chunk_local;
+        a.stat_out = st(l, STAT_AO);
         T(7, true); launch_qk_prep(a, s); T(7, false);
         const int cls = (glob || a.win < 0) ? 5 : 6;
         T(cls, true); launch_attention(a, glob ? sh.grid_global : sh.grid_local, s); T(cls, false);
@@ -600,8 +609,8 @@ void enqueue_body(sp_kvdecode_handle *h, const StepShape &sh, TimeCb cb, void *c
         GemvArgs o{};
         o.accbuf = h->gacc; o.gcnt = h->gcnt; o.acc_rows = h->acc_rows;
         o.mode = h->mode; o.cols = QD; o.act = ACT_NONE; o.nseg = 1;
-        o.pro.kind = PRO_PLAIN; o.pro.x = h->ao; o.pro.n = QD;
-        o.seg[0] = {d.o, h->ap};
+        o.pro.kind = PRO_PLAIN; o.pro.x = h->ao; o.pro.n = QD; o.pro.stat = st(l, STAT_AO);
+        o.seg[0] = {d.o, h->ap}; o.stat_out = st(l, STAT_AP);
         T(1, true); launch_gemv(o, m->E, s); T(1, false);
 
         GemvArgs f{};
@@ -610,13 +619,14 @@ void enqueue_body(sp_kvdecode_handle *h, const StepShape &sh, TimeCb cb, void *c
         f.pro.kind = PRO_RESID; f.pro.x = h->x1; f.pro.delta = h->ap; f.pro.post_w = d.post_attn;
         f.pro.norm_w = d.ffn_norm; f.pro.x_out = h->x0; f.pro.n = m->E; f.pro.eps = m->eps;
         f.seg[0] = {d.gate, h->gg}; f.seg[1] = {d.up, h->uu}; f.act_out = h->hh;
+        f.pro.stat = st(l, STAT_AP); f.stat_out = st(l, STAT_HH);
         T(2, true); launch_gemv(f, m->FF, s); T(2, false);
 
         GemvArgs dd{};
         dd.accbuf = h->gacc; dd.gcnt = h->gcnt; dd.acc_rows = h->acc_rows;
         dd.mode = h->mode; dd.cols = m->FF; dd.act = ACT_NONE; dd.nseg = 1;
-        dd.pro.kind = PRO_PLAIN; dd.pro.x = h->hh; dd.pro.n = m->FF;
-        dd.seg[0] = {d.down, h->dn};
+        dd.pro.kind = PRO_PLAIN; dd.pro.x = h->hh; dd.pro.n = m->FF; dd.pro.stat = st(l, STAT_HH);
+        dd.seg[0] = {d.down, h->dn}; dd.stat_out = st(l, STAT_DN);
         T(3, true); launch_gemv(dd, m->E, s); T(3, false);
     }
     if (sh.logits) {
@@ -626,6 +636,7 @@ void enqueue_body(sp_kvdecode_handle *h, const StepShape &sh, TimeCb cb, void *c
         lm.pro.kind = PRO_RESID; lm.pro.x = h->x0; lm.pro.delta = h->dn;
         lm.pro.post_w = m->gemma ? m->L[m->NL - 1].post_ffw : nullptr;
         lm.pro.norm_w = m->out_norm; lm.pro.x_out = nullptr; lm.pro.n = m->E; lm.pro.eps = m->eps;
+        lm.pro.stat = st(m->NL - 1, STAT_DN);
         lm.seg[0] = {m->out, h->logits};
         T(4, true); launch_gemv(lm, m->V, s); T(4, false);
         if (sh.argmax) {

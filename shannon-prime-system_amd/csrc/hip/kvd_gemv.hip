@@ -172,7 +172,7 @@ __device__ __forceinline__ void load_iter(const GemvArgs &a, const Task &t, bool
 // for the next launch.  The first weights are requested before the prologue,
 // and each task requests the next task's weights before its own epilogue.
 template <int PRO, bool PAIRED, bool WIDE>
-__global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
+__global__ __launch_bounds__(512, 4) void k_gemv(GemvArgs a) {   // 4 waves per SIMD: two workgroups per CU
     extern __shared__ uint4 smem4[];
     const int nblk = (a.cols + 31) / 32, nsplit = a.nsplit, bps = a.bps;
     const int split = blockIdx.x % nsplit;
@@ -194,6 +194,7 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
 
     const int sh = gemv_prologue<PRO>(a.pro, a.mode, xf, dig, b_lo, b_hi, red);
     const int nit = (nb + 63) / 64;
+    StatAcc sacc;                                          // this thread's outputs, for stat_out
 
     for (; grp < a.groups; grp += gstride) {
         int eb[GEMV_R];
@@ -240,17 +241,25 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
                 const i128 tt = wave_sum128(acc[r]);
                 y[r] = sh == SH_ZERO ? 0.0f : rne_i128_scaled(tt, -24 - sh);
             }
-            if (lane == 0) {
-                if (PAIRED) {
-                    for (int r = 0; r < t.nvalid; r++) {
-                        const int j = t.row0 + r;
-                        a.seg[0].out[j] = y[r]; a.seg[1].out[j] = y[r + HR];
-                        a.act_out[j] = act_apply(y[r], y[r + HR], a.act, a.mode);
-                    }
-                } else {
-                    for (int r = 0; r < t.nvalid; r++) a.seg[t.seg].out[t.row0 + r] = y[r];
+            // lane r < nvalid writes row r (its value is the statistic's input)
+            float yv = 0.0f;
+            const bool mine = lane < t.nvalid;
+            #pragma unroll
+            for (int r = 0; r < GEMV_R; r++) if (lane == r) yv = y[r];
+            if (PAIRED) {
+                float yu = 0.0f;
+                #pragma unroll
+                for (int r = 0; r < HR; r++) if (lane == r) yu = y[r + HR];
+                if (mine) {
+                    const int j = t.row0 + lane;
+                    a.seg[0].out[j] = yv; a.seg[1].out[j] = yu;
+                    yv = act_apply(yv, yu, a.act, a.mode);
+                    a.act_out[j] = yv;
                 }
+            } else if (mine) {
+                a.seg[t.seg].out[t.row0 + lane] = yv;
             }
+            if (mine) sacc.add(yv);
         } else {
             int64_t tot = transpose_reduce8(acc, lane);
             const int myrow = ((lane >> 5) & 1) * 4 + ((lane >> 4) & 1) * 2 + ((lane >> 3) & 1);
@@ -277,21 +286,28 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
                 const float y = sh == SH_ZERO ? 0.0f : rne_i64_scaled(tot, ebm - sh);
                 // lane (myrow*8) owns row myrow's total; paired rows fetch their up partner
                 const float partner = __shfl_xor(y, 32, 64);          // row myrow^4
+                bool wrote = false;
+                float sv = 0.0f;                                      // the statistic's input
                 if (holder) {
                     if (PAIRED) {
                         if (myrow < HR) {
                             const int j = t.row0 + myrow;
                             a.seg[0].out[j] = y; a.seg[1].out[j] = partner;
-                            a.act_out[j] = act_apply(y, partner, a.act, a.mode);
+                            sv = act_apply(y, partner, a.act, a.mode);
+                            a.act_out[j] = sv;
+                            wrote = true;
                         }
                     } else {
                         a.seg[t.seg].out[t.row0 + myrow] = y;
+                        sv = y; wrote = true;
                     }
                 }
+                if (wrote) sacc.add(sv);
             }
         }
         t = tn;
     }
+    if (a.stat_out) stat_flush_block(a.stat_out, sacc);
 }
 
 static int g_num_cu = 0;

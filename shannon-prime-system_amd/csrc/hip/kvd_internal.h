@@ -24,6 +24,19 @@ struct DevW {
     int rows, cols, nblk, wide;   // wide: a row's exponent spread needs the int128 path
 };
 
+// Whole-vector statistics that the kernel producing a vector accumulates while
+// it writes it, for the next GEMV's input transform: the exact sum of
+// llround(v * 2^16)^2 (int64, order-free) and max |v| (float bits; atomic max
+// of non-negative floats orders like the float).  Zeroed at the start of every
+// decode step.  A statistic is STAT_REP consecutive VecStat replicas.
+struct VecStat {
+    unsigned long long ss;      // int64 two's complement
+    unsigned int maxbits;
+    unsigned int pad;
+};
+enum StatSlot { STAT_AO = 0, STAT_AP = 1, STAT_HH = 2, STAT_DN = 3, STAT_PER_LAYER = 4 };
+constexpr int STAT_REP = 32;        // replicas per statistic (spread the producers' atomics)
+
 // Input transform run by every GEMV workgroup before the matrix pass.
 enum ProKind { PRO_PLAIN = 0, PRO_NORM = 1, PRO_RESID = 2 };
 struct ProArgs {
@@ -32,6 +45,9 @@ struct ProArgs {
     const float *post_w;   // PRO_RESID: sandwich norm weight on delta (NULL = add raw)
     const float *norm_w;   // PRO_NORM / PRO_RESID: pre-norm weight
     float       *x_out;    // PRO_RESID: updated residual (written by workgroup 0)
+    // statistics of the input the producer accumulated (NULL: computed here):
+    // PRO_PLAIN takes max |x|, PRO_RESID in exact mode the sum of squares of delta
+    const VecStat *stat;
     int   kind, n;
     float eps;
 };
@@ -76,6 +92,7 @@ struct AttnArgs {
     // layer's page table (NULL: pos0 + t and `pages`)
     const int *tpos;
     float *const *const *tpages;
+    VecStat *stat_out;       // decode: statistics of ao for the O GEMV (NULL: none)
 };
 
 struct Seg { DevW w; float *out; };
@@ -92,6 +109,7 @@ struct GemvArgs {
     int  *gcnt;        // split arrival counters per row group [acc_rows] (zero between launches)
     int  acc_rows;
     int  nsplit, bps, groups;   // filled in by launch_gemv
+    VecStat *stat_out;          // statistics of the output (paired: of act_out), NULL: none
 };
 struct GemvPlan { int groups, nsplit, bps, grid; };
 
@@ -142,7 +160,8 @@ __device__ __forceinline__ void reset_counter(int *counter) {
 }
 
 // launchers (kvd_kernels.hip)
-void launch_embed(const DevW &embd, const DState *st, const int *tokbuf, float *x, float scale, hipStream_t s);
+void launch_embed(const DevW &embd, const DState *st, const int *tokbuf, float *x, float scale, hipStream_t s,
+                  VecStat *stats = nullptr, int nstats = 0);
 void launch_embed_batch(const DevW &embd, const int *tokbuf, int pos0, int T, float *x, float scale, hipStream_t s,
                         const int *toks = nullptr);
 void launch_rope_table_batch(int pos0, int T, int HD, int mode, float base_g, float base_l,

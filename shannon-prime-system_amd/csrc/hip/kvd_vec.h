@@ -87,6 +87,7 @@ __device__ __forceinline__ void *red_slot(void *red, int k) { return (uint8_t *)
 // double, 1/sqrtf((float)(ss/n)+eps), out = x*scale*w).  Exact mode: the
 // integer island core/exact_islands/exact_islands.c:60-79 (no eps).
 struct NormScale { float f; int64_t inv; double invd; int zero; };
+constexpr int SH_ZERO_V = -1000000;       // grid exponent of an all-zero vector
 
 // One thread's share of a sum of squares: double in float mode, the exact
 // int64 sum of the Q16 values in exact mode.
@@ -102,6 +103,71 @@ struct SumSq {
         else { const int64_t q = llround_q16(v); i += q * q; }
     }
 };
+// A producer statistic (VecStat) is kept in STAT_REP replicas so that the
+// atomics of many workgroups spread over addresses: a thread accumulates the
+// values it writes (StatAcc: llround(v 2^16)^2 -- the consumer's exact sum of
+// squares -- and max |v|, NaN adding nothing as in the consumer's fmaxf scan),
+// the workgroup combines its threads, and one atomic of each kind goes to
+// replica blockIdx.x % STAT_REP.  The consumer sums / maxes the replicas.
+struct StatAcc {
+    int64_t q2 = 0;
+    float mx = 0.0f;
+    __device__ __forceinline__ void add(float v) {
+        const float r = roundf(v * 65536.0f);
+        if (fabsf(r) < 2147483648.0f) { const int32_t q = (int32_t)r; q2 += (int64_t)q * q; }
+        else { const int64_t q = llround_q16(v); q2 += q * q; }
+        mx = fmaxf(mx, fabsf(v));
+    }
+};
+// Every thread of the workgroup calls this (it has a barrier).
+__device__ __forceinline__ void stat_flush_block(VecStat *slot, StatAcc acc) {
+    __shared__ int64_t sq[RED_WAVES];
+    __shared__ float sm[RED_WAVES];
+    const int64_t q2 = wave_to63(acc.q2, (int64_t)0, [](int64_t a, int64_t b) { return a + b; });
+    const float mx = wave_to63(acc.mx, 0.0f, [](float a, float b) { return fmaxf(a, b); });
+    if ((threadIdx.x & 63) == 63) { sq[threadIdx.x >> 6] = q2; sm[threadIdx.x >> 6] = mx; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int64_t t = sq[0];
+        float m = sm[0];
+        for (int w = 1; w < (int)(blockDim.x >> 6); w++) { t += sq[w]; m = fmaxf(m, sm[w]); }
+        VecStat *r = slot + blockIdx.x % STAT_REP;
+        if (t) atomicAdd(&r->ss, (unsigned long long)t);
+        atomicMax(&r->maxbits, __float_as_uint(m));
+    }
+}
+// The totals over a statistic's replicas, uniform across the wave.
+__device__ __forceinline__ void stat_read(const VecStat *slot, int64_t &ss, float &mx) {
+    const int lane = threadIdx.x & 63;
+    int64_t q = 0;
+    float m = 0.0f;
+    if (lane < STAT_REP) {
+        q = (int64_t)ld_agent(&slot[lane].ss);
+        m = __uint_as_float(ld_agent(&slot[lane].maxbits));
+    }
+    q = wave_to63(q, (int64_t)0, [](int64_t a, int64_t b) { return a + b; });
+    m = wave_to63(m, 0.0f, [](float a, float b) { return fmaxf(a, b); });
+    const uint64_t qu = (uint64_t)q;
+    ss = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(qu >> 32), 63) << 32) |
+                   (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)qu, 63));
+    mx = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 63));
+}
+// The exact-mode RMS scale of a vector whose sum of squares a producer accumulated
+__device__ __forceinline__ NormScale stat_scale(const VecStat *st, int n) {
+    NormScale s; s.f = 0.0f; s.inv = 0; s.invd = 0.0; s.zero = 0;
+    int64_t ss; float mx;
+    stat_read(st, ss, mx);
+    if (ss == 0) { s.zero = 1; return s; }
+    s.inv = rms_inv_q72(n, ss);
+    s.invd = (double)s.inv;
+    return s;
+}
+__device__ __forceinline__ int sh_of_max(float m) {
+    if (m == 0.0f) return SH_ZERO_V;
+    int e; frexpf(m, &e);
+    return 22 - e;
+}
+
 __device__ NormScale norm_finish(const SumSq &p, int n, float eps, int mode, void *red) {
     NormScale s; s.f = 0.0f; s.inv = 0; s.invd = 0.0; s.zero = 0;
     if (mode == FLOAT) {
@@ -140,7 +206,7 @@ __device__ __forceinline__ float norm_apply(float x, float w, const NormScale &s
 // before using any of them, and independent passes are fused: the residual
 // pass also sums the squares for the next norm, the last norm pass also takes
 // the maximum.
-constexpr int SH_ZERO = -1000000;
+constexpr int SH_ZERO = SH_ZERO_V;
 constexpr int PB = 8;
 
 // The GEMV input transform of one vector by one workgroup: residual add (+
@@ -154,6 +220,9 @@ __device__ int input_transform(const ProArgs &p, int mode, float *xf, void *red,
     const int n = p.n, T = blockDim.x, tid = threadIdx.x;
     float m = 0.0f;
     if constexpr (PRO == PRO_PLAIN) {
+        // the producer's maximum: no pass over the vector here (callers read
+        // only the columns they need)
+        if (p.stat) { int64_t ss; float mx; stat_read(p.stat, ss, mx); return sh_of_max(mx); }
         for (int base = 0; base < n; base += PB * T) {
             float a[PB];
             #pragma unroll
@@ -174,8 +243,10 @@ __device__ int input_transform(const ProArgs &p, int mode, float *xf, void *red,
             pw[k] = (PRO == PRO_RESID && ok && p.post_w) ? p.post_w[i] : 0.0f;
         }
         if constexpr (PRO == PRO_RESID) {
-            NormScale sd; sd.f = 0.0f; sd.inv = 0; sd.zero = 0;
-            if (p.post_w) {
+            NormScale sd; sd.f = 0.0f; sd.inv = 0; sd.invd = 0.0; sd.zero = 0;
+            if (p.post_w && p.stat && mode == EXACT) {
+                sd = stat_scale(p.stat, n);              // the producer's exact sum of squares
+            } else if (p.post_w) {
                 SumSq q;
                 #pragma unroll
                 for (int k = 0; k < PB; k++) if (k * T + tid < n) q.add(dv[k], mode);
@@ -213,8 +284,10 @@ __device__ int input_transform(const ProArgs &p, int mode, float *xf, void *red,
             }
             s = norm_finish(q, n, p.eps, mode, red_slot(red, 1));
         } else {
-            NormScale sd; sd.f = 0.0f; sd.inv = 0; sd.zero = 0;
-            if (p.post_w) {
+            NormScale sd; sd.f = 0.0f; sd.inv = 0; sd.invd = 0.0; sd.zero = 0;
+            if (p.post_w && p.stat && mode == EXACT) {
+                sd = stat_scale(p.stat, n);
+            } else if (p.post_w) {
                 SumSq q;
                 for (int base = 0; base < n; base += PB * T) {
                     float a[PB];
@@ -259,9 +332,7 @@ __device__ int input_transform(const ProArgs &p, int mode, float *xf, void *red,
         }
     }
     m = block_max(m, (float *)red_slot(red, 2));         // its barrier also orders the xf writes above
-    if (m == 0.0f) return SH_ZERO;
-    int e; frexpf(m, &e);
-    return 22 - e;
+    return sh_of_max(m);
 }
 
 __device__ __forceinline__ void f16_parts(uint32_t h, int32_t &M, int &e) {
