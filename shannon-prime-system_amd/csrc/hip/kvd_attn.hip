@@ -53,21 +53,10 @@ __device__ void cordic_q62(int64_t th, int64_t &co, int64_t &si) {
     }
 }
 
-__device__ __forceinline__ float wsum(float v) {
-    #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
-__device__ __forceinline__ double wsumd(double v) {
-    #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
-__device__ __forceinline__ int64_t wsuml(int64_t v) {
-    #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
+// wave all-reductions (DPP, kvd_vec.h)
+__device__ __forceinline__ float wsum(float v) { return wave_allsum(v); }
+__device__ __forceinline__ double wsumd(double v) { return wave_allsum(v); }
+__device__ __forceinline__ int64_t wsuml(int64_t v) { return wave_allsum(v); }
 // Transposed butterfly over P per-lane int64 values (P a power of two, 2..64):
 // each exchange round halves the values a lane carries; afterwards every lane
 // holds the wave total of value treduce_index<P>(lane).
@@ -93,11 +82,7 @@ template <int P, typename T> __device__ __forceinline__ T treduce(T v[P], int la
     for (; o > 0; o >>= 1) t += __shfl_xor(t, o, 64);
     return t;
 }
-__device__ __forceinline__ float wmax(float v) {
-    #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
-}
+__device__ __forceinline__ float wmax(float v) { return wave_allmax(v); }
 
 __device__ __forceinline__ float *page_of(float *const *pages, int ring, int pos) {
     const int lp = pos / PAGE;
@@ -290,8 +275,7 @@ __global__ __launch_bounds__(256) void k_attn_float(AttnArgs a_in) {
         }
         #pragma unroll
         for (int g = 0; g < G; g++) {
-            acc[g] += __shfl_xor(acc[g], 1, 64);
-            acc[g] += __shfl_xor(acc[g], 2, 64);
+            acc[g] = quad_sum(acc[g]);
         }
         if (j < n && k4 < G) {
             float d = acc[0];
@@ -457,8 +441,7 @@ __global__ __launch_bounds__(256) void k_attn_exact_scores(AttnArgs a_in) {
         }
         #pragma unroll
         for (int g = 0; g < G; g++) {
-            acc[g] += __shfl_xor(acc[g], 1, 64);
-            acc[g] += __shfl_xor(acc[g], 2, 64);
+            acc[g] = quad_sum(acc[g]);
         }
         if (j < n && k4 < G) {
             int64_t tot = acc[0];
@@ -475,8 +458,7 @@ __global__ __launch_bounds__(256) void k_attn_exact_scores(AttnArgs a_in) {
     #pragma unroll
     for (int g = 0; g < G; g++) {
         int t = k4 == g ? mx : INT32_MIN;
-        #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) { const int u = __shfl_xor(t, o, 64); t = u > t ? u : t; }
+        t = wave_allmax_i(t);
         mxg[g] = t;
     }
     if (lane == 0) for (int g = 0; g < G; g++) zmax[wave][g] = mxg[g];
@@ -529,8 +511,7 @@ __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a_in) {
             const int v = pml[((size_t)(h * G + g) * a.max_chunks + k) * 4];
             t = v > t ? v : t;
         }
-        #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) { const int u = __shfl_xor(t, o, 64); t = u > t ? u : t; }
+        t = wave_allmax_i(t);
         if (lane == 0) redi[wave][g] = t;
     }
     __syncthreads();

@@ -7,6 +7,7 @@
 #pragma once
 #include "kvd_internal.h"
 #include "kvd_exact.h"
+#include "kvd_vec.h"
 
 namespace kvd {
 
@@ -67,8 +68,7 @@ __device__ __forceinline__ void qk_prep_head_t(const HeadPrep a, int hb, int pos
         double ss = 0.0;
         #pragma unroll
         for (int j = 0; j < 8; j++) if (j < per) ss += (double)v[j] * (double)v[j];
-        #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        ss = wave_allsum(ss);
         const float sc = 1.0f / sqrtf((float)(ss / HD) + a.eps);
         #pragma unroll
         for (int j = 0; j < 8; j++) if (j < per) v[j] = v[j] * sc * nw[lane + 64 * j];
@@ -76,8 +76,7 @@ __device__ __forceinline__ void qk_prep_head_t(const HeadPrep a, int hb, int pos
         int64_t ss = 0;
         #pragma unroll
         for (int j = 0; j < 8; j++) if (j < per) { const int64_t xi = llround_pow2<16>(v[j]); ss += xi * xi; }
-        #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        ss = wave_allsum(ss);
         if (ss == 0) {
             #pragma unroll
             for (int j = 0; j < 8; j++) v[j] = 0.0f;

@@ -55,6 +55,38 @@ template <typename T, typename Op> __device__ __forceinline__ T wave_to63(T v, T
     return v;
 }
 
+// All-lane results: the lane-63 total read back as a wave-uniform value.
+template <typename T> __device__ __forceinline__ T bcast63(T v) {
+    if constexpr (sizeof(T) == 8) {
+        const uint64_t u = __builtin_bit_cast(uint64_t, v);
+        const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, 63);
+        const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), 63);
+        return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
+    } else {
+        return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+    }
+}
+template <typename T> __device__ __forceinline__ T wave_allsum(T v) {
+    return bcast63(wave_to63(v, (T)0, [](T a, T b) { return a + b; }));
+}
+__device__ __forceinline__ float wave_allmax(float v) {
+    return bcast63(wave_to63(v, -INFINITY, [](float a, float b) { return fmaxf(a, b); }));
+}
+__device__ __forceinline__ int wave_allmax_i(int v) {
+    return bcast63(wave_to63(v, (int)INT32_MIN, [](int a, int b) { return a > b ? a : b; }));
+}
+// Sum over the 4 lanes of each quad (all four get it): two DPP quad swaps.
+template <typename T> __device__ __forceinline__ T quad_sum(T v) {
+    typedef typename std::conditional<sizeof(T) == 8, uint64_t, uint32_t>::type B;
+    auto sw = [](T x, auto ctrl_tag) -> T {
+        constexpr int C = decltype(ctrl_tag)::value;
+        if constexpr (sizeof(T) == 8) return __builtin_bit_cast(T, dpp64<C, 0xF>(__builtin_bit_cast(B, x), 0));
+        else return __builtin_bit_cast(T, dpp32<C, 0xF>(__builtin_bit_cast(B, x), 0));
+    };
+    v = v + sw(v, std::integral_constant<int, 0xB1>{});      // quad_perm 1,0,3,2
+    return v + sw(v, std::integral_constant<int, 0x4E>{});   // quad_perm 2,3,0,1
+}
+
 // Block-wide reductions through one LDS slot array per reduction: lane 63 of
 // each wave posts its wave total, one barrier, every thread combines the
 // totals.  A reduction writes only its own `red` slots, so consecutive
