@@ -30,8 +30,9 @@
 namespace kvd {
 
 // exact-mode RoPE tables (host-computed integer constants, see kvd_backend.hip)
-__device__ int64_t g_atan_q60[64];
-__device__ int64_t g_kinv_q62;
+// (constant memory: the CORDIC loop index is uniform, so these are scalar loads)
+__constant__ int64_t g_atan_q60[64];
+__constant__ int64_t g_kinv_q62;
 
 constexpr int64_t TWO_PI_Q60 = 7244019458077122842LL;     // round(2*pi * 2^60)
 constexpr int64_t HALF_PI_Q60 = 1811004864519280711LL;    // round(pi/2 * 2^60)
@@ -648,14 +649,32 @@ __global__ __launch_bounds__(256) void k_embed(DevW w, const DState *st, const i
     x += (size_t)blockIdx.x * E;
     const uint8_t *rc = w.codes + (size_t)tok * ((E + 1) / 2);
     const uint16_t *bs = w.bs + (size_t)tok * w.nblk;
-    for (int i = threadIdx.x; i < E; i += blockDim.x) {
-        const int nib = (rc[i >> 1] >> ((i & 1) * 4)) & 15;
-        const int q = nib >= 8 ? nib - 16 : nib;
-        const uint32_t hb = bs[i >> 5];
-        const float sv = (float)__builtin_bit_cast(_Float16, (unsigned short)hb);
-        float v = (float)q * sv;
-        if (scale != 0.0f) v *= scale;
-        x[i] = v;
+    if ((E & 7) == 0) {
+        // 8 columns per thread and step: one 4-byte code load, one scale; the
+        // steps' loads are independent, so they are all in flight together
+        for (int g = threadIdx.x; g < E / 8; g += blockDim.x) {
+            const uint32_t c8 = *(const uint32_t *)(rc + 4 * g);
+            const float sv = (float)__builtin_bit_cast(_Float16, (unsigned short)bs[g >> 2]);
+            float v[8];
+            #pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int nib = (c8 >> (4 * j)) & 15;           // low nibble = even column
+                v[j] = (float)(nib >= 8 ? nib - 16 : nib) * sv;
+                if (scale != 0.0f) v[j] *= scale;
+            }
+            *(float4 *)(x + 8 * g) = make_float4(v[0], v[1], v[2], v[3]);
+            *(float4 *)(x + 8 * g + 4) = make_float4(v[4], v[5], v[6], v[7]);
+        }
+    } else {
+        for (int i = threadIdx.x; i < E; i += blockDim.x) {
+            const int nib = (rc[i >> 1] >> ((i & 1) * 4)) & 15;
+            const int q = nib >= 8 ? nib - 16 : nib;
+            const uint32_t hb = bs[i >> 5];
+            const float sv = (float)__builtin_bit_cast(_Float16, (unsigned short)hb);
+            float v = (float)q * sv;
+            if (scale != 0.0f) v *= scale;
+            x[i] = v;
+        }
     }
 }
 void launch_embed(const DevW &embd, const DState *st, const int *tokbuf, float *x, float scale, hipStream_t s,
@@ -691,9 +710,17 @@ __global__ __launch_bounds__(256) void k_argmax(const float *lg, int V, float *p
         is_last = arrive(counter) == (int)gridDim.x - 1;
     }
     __syncthreads();
-    if (!is_last || threadIdx.x != 0) return;
+    if (!is_last) return;
+    // the last workgroup merges the per-workgroup maxima, one per thread
     float bv = -INFINITY; int bi = 0x7FFFFFFF;
-    for (int b = 0; b < (int)gridDim.x; b++) amax_merge(bv, bi, ld_agent(&pv[b]), ld_agent(&pi[b]));
+    for (int b = threadIdx.x; b < (int)gridDim.x; b += 256) amax_merge(bv, bi, ld_agent(&pv[b]), ld_agent(&pi[b]));
+    #pragma unroll
+    for (int o = 32; o > 0; o >>= 1) amax_merge(bv, bi, __shfl_xor(bv, o, 64), __shfl_xor(bi, o, 64));
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) { sv[threadIdx.x >> 6] = bv; si[threadIdx.x >> 6] = bi; }
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+    for (int w = 1; w < 4; w++) amax_merge(bv, bi, sv[w], si[w]);
     if (bi == 0x7FFFFFFF) bi = 0;
     st->tok = bi;
     if (gen_log) gen_log[st->pos] = bi;
