@@ -158,7 +158,8 @@ int load_weight(const qwen3_model *qm, const gguf_tensor *t, int rows, int cols,
     if (cols % 32 != 0) return fail("sp_hipkv_open: %s: cols must be a multiple of 32", t->name);
     // per-row smallest block exponent; rows whose exponent spread could overflow
     // the int64 accumulator (see kvd_gemv.hip) switch the tensor to int128
-    ebase_store.emplace_back(rows);
+    // (8 zero bytes of padding: the GEMV reads a task's 8 rows in one load)
+    ebase_store.emplace_back(rows + 8);
     std::vector<int8_t> &eb = ebase_store.back();
     int lg = 0; while ((1 << lg) < (int)nb) lg++;
     const int max_spread = 21 - lg;
@@ -179,7 +180,7 @@ int load_weight(const qwen3_model *qm, const gguf_tensor *t, int rows, int cols,
     }
     offs[0] = up.add(p.codes, rb * rows);
     offs[1] = up.add(p.bscale, nb * 2 * rows);
-    offs[2] = up.add(eb.data(), (size_t)rows);
+    offs[2] = up.add(eb.data(), (size_t)rows + 8);
     w.rows = rows; w.cols = cols; w.nblk = (int)nb; w.wide = wide;
     return 0;
 }

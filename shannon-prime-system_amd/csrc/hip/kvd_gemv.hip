@@ -49,24 +49,44 @@ __device__ __forceinline__ void digits8(const float v[8], int sh, uint32_t dw[ND
     for (int k = 0; k < NDIG; k++) dw[k] ^= 0x88888888u;
 }
 
+// The prologue's global loads (pro_load, plus for PRO_PLAIN this thread's
+// first 8 input columns of the split), issued before the weight prefetch.
+struct GemvLoads { ProLoads pro; float4 c0, c1; };
 template <int PRO>
-__device__ int gemv_prologue(const ProArgs &p, int mode, float *xf, uint4 *dig, int b_lo, int b_hi, void *red) {
+__device__ __forceinline__ void gemv_pro_load(const ProArgs &p, int mode, GemvLoads &L, int b_lo, int b_hi) {
+    pro_load<PRO>(p, mode, L.pro);
+    if constexpr (PRO == PRO_PLAIN) {
+        const int g = b_lo * 4 + (int)threadIdx.x, gc = g < b_hi * 4 ? g : b_lo * 4;   // in range: read, used only if g is
+        L.c0 = *(const float4 *)(p.x + gc * 8);
+        L.c1 = *(const float4 *)(p.x + gc * 8 + 4);
+    }
+}
+
+template <int PRO>
+__device__ int gemv_prologue(const ProArgs &p, int mode, const GemvLoads &L, float *xf, uint4 *dig, int b_lo, int b_hi, void *red) {
     const int T = blockDim.x, tid = threadIdx.x;
-    const int sh = input_transform<PRO>(p, mode, xf, red, blockIdx.x == 0);
+    const int sh = input_transform<PRO>(p, mode, L.pro, xf, red, blockIdx.x == 0);
     if (sh == SH_ZERO) return SH_ZERO;
     // digits: one thread per 8 consecutive columns (one nibble-dword per plane);
     // the column count is a multiple of 32, so a group never runs past n
     const float *src = PRO == PRO_PLAIN ? p.x : xf;
     const int g_lo = b_lo * 4, g_hi = b_hi * 4, nb = b_hi - b_lo;
-    for (int g = g_lo + tid; g < g_hi; g += T) {
-        const float4 v0 = *(const float4 *)(src + g * 8), v1 = *(const float4 *)(src + g * 8 + 4);
+    auto put = [&](int g, const float4 &v0, const float4 &v1) {
         const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
         uint32_t dw[NDIG];
         digits8(v, sh, dw);
         const int b = (g >> 2) - b_lo, q = g & 3;
         #pragma unroll
         for (int k = 0; k < NDIG; k++) ((uint32_t *)&dig[k * nb + b])[q] = dw[k];
+    };
+    int g = g_lo + tid;
+    if constexpr (PRO == PRO_PLAIN) {
+        // the preloaded first group, outside the loop: a loop body shared with
+        // loaded groups would make its waits cover the weight prefetch
+        if (g < g_hi) put(g, L.c0, L.c1);
+        g += T;
     }
+    for (; g < g_hi; g += T) put(g, *(const float4 *)(src + g * 8), *(const float4 *)(src + g * 8 + 4));
     __syncthreads();
     return sh;
 }
@@ -127,10 +147,10 @@ __device__ __forceinline__ Task task_of(const GemvArgs &a, int grp) {
     } else {
         // a group never straddles segments (segment row counts are multiples
         // of GEMV_R, checked by the host), so its rows are consecutive
-        int g = grp * GEMV_R, s = 0, off = 0;
-        while (s < a.nseg - 1 && g >= a.seg[s].w.rows) { g -= a.seg[s].w.rows; off += a.seg[s].w.rows; s++; }
+        int g = grp * GEMV_R, s = 0, off = 0, rows = a.seg[0].w.rows;
+        while (s < a.nseg - 1 && g >= rows) { g -= rows; off += rows; s++; rows = a.seg[s].w.rows; }
         t.seg = s; t.row0 = g; t.grow0 = off + g;
-        t.nvalid = a.seg[s].w.rows - g < GEMV_R ? a.seg[s].w.rows - g : GEMV_R;
+        t.nvalid = rows - g < GEMV_R ? rows - g : GEMV_R;
     }
     t.seg = __builtin_amdgcn_readfirstlane(t.seg);
     t.row0 = __builtin_amdgcn_readfirstlane(t.row0);
@@ -139,38 +159,58 @@ __device__ __forceinline__ Task task_of(const GemvArgs &a, int grp) {
     return t;
 }
 
-// 16 B of codes and the f16 scale of block b for each of the task's rows
-// (zeros for rows past the end and for b >= b_hi)
+// 16 B of codes and the f16 scale of block b for each of the task's rows.
+// Every load is issued, at a valid address (rows past the end re-read the
+// task's first row, b >= b_hi re-reads block b_lo): a conditional load would
+// leave the compiler unsure how many loads are in flight, and its waits for
+// earlier loads would then wait for these too.  Users ignore those values
+// (b >= b_hi is skipped, rows past the end are never written).
 template <bool PAIRED>
-__device__ __forceinline__ void load_iter(const GemvArgs &a, const Task &t, bool ok, int b, int b_hi,
+__device__ __forceinline__ void load_iter(const GemvArgs &a, const Task &t, int b, int b_lo, int b_hi,
                                           uint4 c[GEMV_R], uint32_t h[GEMV_R]) {
     const int per = PAIRED ? GEMV_R / 2 : GEMV_R;
     const DevW &wa = a.seg[t.seg].w;
     const DevW &wb = a.seg[PAIRED ? 1 : t.seg].w;
     const int nblk = wa.nblk;
     const size_t rb = (size_t)(wa.cols + 1) / 2;
+    const int bc = b < b_hi ? b : b_lo;
     #pragma unroll
     for (int r = 0; r < GEMV_R; r++) {
         const int rr = r % per;
+        const int row = t.row0 + (rr < t.nvalid ? rr : 0);
         const bool second = PAIRED && r >= per;
-        if (ok && rr < t.nvalid && b < b_hi) {
-            typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-            const DevW &w = second ? wb : wa;
-            const uint8_t *cp = w.codes + (size_t)(t.row0 + rr) * rb + (size_t)b * 16;
-            const u32x4 v = __builtin_nontemporal_load((const u32x4 *)cp);
-            c[r] = make_uint4(v.x, v.y, v.z, v.w);
-            h[r] = w.bs[(size_t)(t.row0 + rr) * nblk + b];
-        } else { c[r] = make_uint4(0, 0, 0, 0); h[r] = 0; }
+        typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+        const DevW &w = second ? wb : wa;
+        const uint8_t *cp = w.codes + (size_t)row * rb + (size_t)bc * 16;
+        const u32x4 v = __builtin_nontemporal_load((const u32x4 *)cp);
+        c[r] = make_uint4(v.x, v.y, v.z, v.w);
+        h[r] = w.bs[(size_t)row * nblk + bc];
     }
 }
+
+// The task's row exponent bases, row r's in byte r (paired: gate rows, then
+// up rows): one load per half.  The host pads every ebase array by 8 bytes,
+// so the read may run past the last row; those rows are never written.
+template <bool PAIRED, bool WIDE>
+__device__ __forceinline__ uint64_t load_eb(const GemvArgs &a, const Task &t) {
+    if constexpr (WIDE) return 0;
+    if constexpr (PAIRED) {
+        const uint32_t lo = *(const uint32_t *)(a.seg[0].w.ebase + t.row0);
+        const uint32_t hi = *(const uint32_t *)(a.seg[1].w.ebase + t.row0);
+        return (uint64_t)hi << 32 | lo;
+    }
+    return *(const uint64_t *)(a.seg[t.seg].w.ebase + t.row0);
+}
+__device__ __forceinline__ int eb_of(uint64_t ebw, int r) { return (int)(int8_t)(ebw >> (8 * r)); }
 
 // The matrix pass.  Workgroup w works on column split s = w % nsplit (blocks
 // [s*bps, min(nblk, (s+1)*bps)) ); its waves take row groups in a grid stride.
 // With nsplit > 1 every task adds its exact int64 row partials atomically into
 // accbuf (order-free, so still bit-exact); the wave that completes a group's
 // last split converts the totals, writes the outputs and clears accbuf/gcnt
-// for the next launch.  The first weights are requested before the prologue,
-// and each task requests the next task's weights before its own epilogue.
+// for the next launch.  The first weights are requested before the prologue
+// (after the prologue's own loads), and each task requests the next task's
+// weights before its own epilogue.
 template <int PRO, bool PAIRED, bool WIDE>
 __global__ __launch_bounds__(512, 4) void k_gemv(GemvArgs a) {   // 4 waves per SIMD: two workgroups per CU
     extern __shared__ uint4 smem4[];
@@ -180,37 +220,38 @@ __global__ __launch_bounds__(512, 4) void k_gemv(GemvArgs a) {   // 4 waves per 
     uint4 *dig = smem4;                                   // NDIG * nb
     float *xf = (float *)(dig + NDIG * nb);               // pro.n floats (norm prologues only)
     __shared__ double red[RED_SLOTS * RED_WAVES];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nwaves = blockDim.x >> 6;
     constexpr int HR = GEMV_R / 2;
     constexpr int per = PAIRED ? HR : GEMV_R;
     const int gstride = (gridDim.x / nsplit) * nwaves;
     int grp = (blockIdx.x / nsplit) * nwaves + wave;
 
+    // the prologue's loads first, then the weights: its waits then need only
+    // its own data, and the weight prefetch streams in under its work
+    GemvLoads L;
+    gemv_pro_load<PRO>(a.pro, a.mode, L, b_lo, b_hi);
+    __builtin_amdgcn_sched_barrier(0);
     Task t = task_of<PAIRED>(a, grp < a.groups ? grp : 0);
     uint4 c[GEMV_R];
     uint32_t h[GEMV_R];
-    load_iter<PAIRED>(a, t, grp < a.groups, b_lo + lane, b_hi, c, h);
+    uint64_t ebn = load_eb<PAIRED, WIDE>(a, t);            // first: the task's start waits for it alone
+    load_iter<PAIRED>(a, t, b_lo + lane, b_lo, b_hi, c, h);
+    __builtin_amdgcn_sched_barrier(0);
 
-    const int sh = gemv_prologue<PRO>(a.pro, a.mode, xf, dig, b_lo, b_hi, red);
+    const int sh = gemv_prologue<PRO>(a.pro, a.mode, L, xf, dig, b_lo, b_hi, red);
     const int nit = (nb + 63) / 64;
     StatAcc sacc;                                          // this thread's outputs, for stat_out
 
     for (; grp < a.groups; grp += gstride) {
-        int eb[GEMV_R];
-        #pragma unroll
-        for (int r = 0; r < GEMV_R; r++) {
-            const int rr = r % per;
-            const DevW &w = (PAIRED && r >= HR) ? a.seg[1].w : a.seg[t.seg].w;
-            eb[r] = WIDE ? -24 : (rr < t.nvalid ? (int)w.ebase[t.row0 + rr] : 0);
-        }
+        const uint64_t ebw = ebn;                          // this task's (ebn is reloaded for the next)
         typedef typename std::conditional<WIDE, i128, int64_t>::type acc_t;
         acc_t acc[GEMV_R];
         #pragma unroll
         for (int r = 0; r < GEMV_R; r++) acc[r] = 0;
         for (int it = 0; it < nit; it++) {
             const int b = b_lo + it * 64 + lane;
-            if (it > 0) load_iter<PAIRED>(a, t, true, b, b_hi, c, h);
+            if (it > 0) load_iter<PAIRED>(a, t, b, b_lo, b_hi, c, h);
             if (b < b_hi && sh != SH_ZERO) {
                 uint4 D[NDIG];
                 #pragma unroll
@@ -222,7 +263,7 @@ __global__ __launch_bounds__(512, 4) void k_gemv(GemvArgs a) {   // 4 waves per 
                     const int64_t p = (int64_t)d * (int64_t)M;
                     if constexpr (WIDE) acc[r] += (i128)((u128)(i128)p << (e + 24));
                     else {
-                        const int s = e - eb[r];
+                        const int s = e - eb_of(ebw, r);       // unpacked at use: fewer live registers
                         acc[r] += (int64_t)((uint64_t)p << (s > 0 ? s : 0));
                     }
                 }
@@ -231,7 +272,8 @@ __global__ __launch_bounds__(512, 4) void k_gemv(GemvArgs a) {   // 4 waves per 
         // request the next task's first weights before this task's epilogue
         const int ngrp = grp + gstride;
         const Task tn = task_of<PAIRED>(a, ngrp < a.groups ? ngrp : 0);
-        load_iter<PAIRED>(a, tn, ngrp < a.groups, b_lo + lane, b_hi, c, h);
+        ebn = load_eb<PAIRED, WIDE>(a, tn);
+        load_iter<PAIRED>(a, tn, b_lo + lane, b_lo, b_hi, c, h);
 
         if constexpr (WIDE) {
             // int128 rows: whole rows per task (nsplit == 1, enforced by the host)
@@ -280,9 +322,7 @@ __global__ __launch_bounds__(512, 4) void k_gemv(GemvArgs a) {   // 4 waves per 
                 }
             }
             if (finish) {
-                int ebm = eb[0];
-                #pragma unroll
-                for (int r = 1; r < GEMV_R; r++) if (myrow == r) ebm = eb[r];
+                const int ebm = eb_of(ebw, myrow);
                 const float y = sh == SH_ZERO ? 0.0f : rne_i64_scaled(tot, ebm - sh);
                 // lane (myrow*8) owns row myrow's total; paired rows fetch their up partner
                 const float partner = __shfl_xor(y, 32, 64);          // row myrow^4

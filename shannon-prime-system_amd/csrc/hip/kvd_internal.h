@@ -16,7 +16,8 @@ enum Mode { FLOAT = 0, EXACT = 1 };
 
 // One OK_Q4B weight tensor on the device, reference row layout:
 // codes [rows][cols/2] nibbles (low = even column), scales [rows][cols/32] f16,
-// plus ebase[rows] = smallest block exponent of the row (for the int64 fast path).
+// plus ebase[rows + 8] = smallest block exponent of the row (for the int64 fast path;
+// 8 bytes of padding: the GEMV reads 8 rows at a time).
 struct DevW {
     const uint8_t  *codes;
     const uint16_t *bs;

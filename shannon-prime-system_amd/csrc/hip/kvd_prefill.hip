@@ -10,8 +10,9 @@
 //   d = sum_p 256^p * plane_p (|d| < 2^30), and d * M_jb << (e_jb - ebase_j)
 //   accumulates in int64 exactly as in the GEMV.
 // A workgroup (4 waves) owns 64 rows x 16 or 32 tokens; a wave owns 16 rows
-// and one or two 16-token MFMA tiles that share its A operand (the unpacked
-// weight codes).
+// and one or two 16-token MFMA tiles that share its unpacked weight codes.
+// The activation planes, which all four waves read, go through LDS once per
+// workgroup; each wave streams its own codes and scales.
 #include "kvd_internal.h"
 #include "kvd_exact.h"
 #include "kvd_vec.h"
@@ -81,24 +82,14 @@ __device__ __forceinline__ long unpack_codes(uint32_t w) {
     return (long)(((uint64_t)shi << 32) | slo);
 }
 
-// One group of U blocks of a wave's operands, loaded a group ahead of use:
-// weight codes (one dword per lane and block), the activation planes of its TT
-// token tiles, and the f16 block scales of the lane's output row.
-template <bool PAIRED, int TT, int U> struct GemmBuf {
-    uint32_t A[U], A2[PAIRED ? U : 1];
-    long B[U][TT][3];
-    uint32_t S[U / 2], S2[PAIRED ? U / 2 : 1];
-};
-
-
 // d = sum_k code_k * xq_k over one 32-column block for a 16-token x 16-row
 // tile: one independent MFMA per digit plane, combined as
 // (p2 * 256 + p1) * 256 + p0 (|d| < 2^31, exact in int32)
-__device__ __forceinline__ v4i block_dot(const long (&b)[3], long w) {
+__device__ __forceinline__ v4i block_dot(long b0, long b1, long b2, long w) {
     const v4i z = {0, 0, 0, 0};
-    const v4i p0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(b[0], w, z, 0, 0, 0);
-    const v4i p1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(b[1], w, z, 0, 0, 0);
-    const v4i p2 = __builtin_amdgcn_mfma_i32_16x16x32_i8(b[2], w, z, 0, 0, 0);
+    const v4i p0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(b0, w, z, 0, 0, 0);
+    const v4i p1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(b1, w, z, 0, 0, 0);
+    const v4i p2 = __builtin_amdgcn_mfma_i32_16x16x32_i8(b2, w, z, 0, 0, 0);
     return (((p2 << 8) + p1) << 8) + p0;
 }
 
@@ -109,135 +100,177 @@ constexpr int BUF_WORD3 = 0x00020000;                  // 32-bit data format, ra
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, BUF_WORD3);
 }
-__device__ __forceinline__ uint32_t buf_ld32(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
-    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+__device__ __forceinline__ uint4 buf_ld128(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+    const u4 v = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+    return make_uint4(v.x, v.y, v.z, v.w);
 }
-__device__ __forceinline__ long buf_ld64(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
-    return __builtin_bit_cast(long, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+// 4 x 4 transpose across the four 16-lane rows of a wave: afterwards lane row
+// r, register k holds what lane row k held in register r (same lane in the row)
+__device__ __forceinline__ void transpose4(uint4 &v) {
+    const auto a = __builtin_amdgcn_permlane32_swap(v.x, v.z, false, false);
+    const auto b = __builtin_amdgcn_permlane32_swap(v.y, v.w, false, false);
+    const auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
+    const auto d = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
+    v = make_uint4(c[0], c[1], d[0], d[1]);
 }
 
-// A wave owns 16 weight rows x TT 16-token tiles.  The activations are the
-// MFMA's A operand and the weight codes its B operand, so a lane's outputs are
-// one weight row (16-lane index) x 4 tokens, and each block's scale is decoded
-// once per lane: the exact integer Ms = M * 2^(e - ebase) = f16 * 2^-ebase
-// (below 2^31 for every row the GEMM takes); each block adds d * Ms to the
-// int64 total.  Loads use a wave-uniform base and a 32-bit lane offset.
+constexpr int GEMM_KC = 8;                // 32-column blocks per pipeline chunk
+constexpr int GEMM_AG = GEMM_KC / 4;      // 16-byte code loads per lane and chunk
+
+// A wave's own operands of one chunk: the codes of its 16 rows (a lane loads
+// 16 bytes = 4 blocks of its row; transpose4 turns that into one dword per
+// block), the 8 f16 scales of the lane's row.
+template <bool PAIRED> struct WaveChunk {
+    uint4 A[GEMM_AG], A2[PAIRED ? GEMM_AG : 1];
+    uint4 S, S2;
+};
+
+// A workgroup (4 waves) owns 64 weight rows x TT 16-token tiles; a wave owns
+// 16 rows.  The activations are the MFMA's A operand and the weight codes its
+// B operand, so a lane's outputs are one weight row (16-lane index) x 4
+// tokens, and each block's scale is decoded once per lane: the exact integer
+// Ms = M * 2^(e - ebase) = f16 * 2^-ebase (below 2^31 for every row the GEMM
+// takes); each block adds d * Ms to the int64 total.
+//
+// The K dimension runs in chunks of GEMM_KC blocks.  A chunk's activation
+// planes (3 planes x TT tiles x 512 bytes per block), which all four waves
+// read, are loaded once per workgroup with 16-byte loads, parked in registers
+// for one chunk and written to one of two LDS buffers; the MFMAs read them
+// back with ds_read_b64.  Each wave loads its own codes 16 bytes per lane and
+// its scales 16 bytes per lane (8 blocks) one chunk ahead.  All buffer
+// offsets are 32-bit (checked by the launcher).
 template <bool PAIRED, int TT>
 __global__ __launch_bounds__(256) void k_gemm_q4b(GemmArgs a) {
-    constexpr int U = 4;
-    typedef GemmBuf<PAIRED, TT, U> Buf;
-    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    constexpr int KC = GEMM_KC, AG = GEMM_AG;
+    constexpr int SEG = 3 * TT;                        // 512-byte tiles per block (planes x token tiles)
+    constexpr int PPT = KC * SEG * 32 / 256;           // 16-byte staging pieces per thread and chunk
+    __shared__ uint4 Bs[2][KC * SEG * 32];             // [buf][(kb * 3 + p) * TT + j][32 pieces]
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int c16 = lane & 15, g = lane >> 4;
     // row tile -> segment (segment row counts are multiples of 64)
     int tile_row = blockIdx.x * 64, s = 0;
     if (!PAIRED) while (s < a.nseg - 1 && tile_row >= a.seg[s].w.rows) { tile_row -= a.seg[s].w.rows; s++; }
     const DevW &wa = a.seg[s].w;
     const DevW &wb = a.seg[PAIRED ? 1 : s].w;
-    const int nblk = wa.nblk, TP = a.TP;
-    const int rb = wa.cols / 2;
-    const int rbase = tile_row + wave * 16;              // this wave's 16 rows
-    const int t0 = blockIdx.y * 16 * TT;
-    const int row = rbase + c16;                         // this lane's output row
-    // this wave's 16 rows of codes and scales, the workgroup's token columns of
-    // the planes (all offsets below 2^31: checked by the launcher)
+    const int nblk = wa.nblk, TP = a.TP, rb = wa.cols / 2;
+    const int nck = nblk / KC;
+    const int rbase = tile_row + wave * 16, t0 = blockIdx.y * 16 * TT, row = rbase + c16;
     const __amdgpu_buffer_rsrc_t rca = buf_rsrc(wa.codes + (size_t)rbase * rb, 16u * rb);
     const __amdgpu_buffer_rsrc_t rcb = buf_rsrc(wb.codes + (size_t)rbase * rb, 16u * rb);
-    const int lo_c = c16 * rb + 4 * g;
-    const int pstride = nblk * TP * 32;                  // bytes per plane
+    const int lo_c = c16 * rb + 16 * g;                // lane's 16 bytes of a 4-block group of its row
+    const int pstride = nblk * TP * 32;                // bytes per plane
     const __amdgpu_buffer_rsrc_t rpl = buf_rsrc(a.planes + (size_t)t0 * 32, 3u * pstride - 32u * t0);
-    const int lo_p = c16 * 32 + 8 * g;
     const __amdgpu_buffer_rsrc_t rsa = buf_rsrc(wa.bs + (size_t)rbase * nblk, 32u * nblk);
     const __amdgpu_buffer_rsrc_t rsb = buf_rsrc(wb.bs + (size_t)rbase * nblk, 32u * nblk);
     const int lo_s = c16 * nblk * 2;
     const int eb_a = wa.ebase[row], eb_b = PAIRED ? wb.ebase[row] : 0;
     const float sc_a = ldexpf(1.0f, -eb_a), sc_b = ldexpf(1.0f, -eb_b);
+    // staging piece q = tid + 256 r: tile q / 32, 16 bytes at (q % 32) * 16
+    int goff[PPT];
+    #pragma unroll
+    for (int r = 0; r < PPT; r++) {
+        const int q = tid + 256 * r, sg = q / 32, kb = sg / SEG, p = (sg % SEG) / TT, j = sg % TT;
+        goff[r] = p * pstride + (kb * TP + 16 * j) * 32 + (q % 32) * 16;
+    }
+    auto stage_load = [&](uint4 (&st)[PPT], int ck) {
+        const int so = __builtin_amdgcn_readfirstlane(ck * KC * TP * 32);
+        #pragma unroll
+        for (int r = 0; r < PPT; r++) st[r] = buf_ld128(rpl, goff[r], so);
+    };
+    auto stage_store = [&](const uint4 (&st)[PPT], int buf) {
+        #pragma unroll
+        for (int r = 0; r < PPT; r++) Bs[buf][tid + 256 * r] = st[r];
+    };
+    auto wave_load = [&](WaveChunk<PAIRED> &w, int ck) {
+        const int b0 = __builtin_amdgcn_readfirstlane(ck * KC);
+        #pragma unroll
+        for (int q = 0; q < AG; q++) {
+            w.A[q] = buf_ld128(rca, lo_c, (b0 + 4 * q) * 16);
+            if constexpr (PAIRED) w.A2[q] = buf_ld128(rcb, lo_c, (b0 + 4 * q) * 16);
+        }
+        w.S = buf_ld128(rsa, lo_s, b0 * 2);
+        if constexpr (PAIRED) w.S2 = buf_ld128(rsb, lo_s, b0 * 2);
+    };
     int64_t acc_a[TT][4], acc_b[TT][4];
     #pragma unroll
     for (int j = 0; j < TT; j++)
         #pragma unroll
         for (int i = 0; i < 4; i++) { acc_a[j][i] = 0; acc_b[j][i] = 0; }
-
-    auto load = [&](Buf &X, int b0_) {
-        // the block index is wave-uniform: keep every scalar offset in SGPRs
-        // (a VGPR offset would need a per-lane loop and a full wait).  Groups
-        // past the end re-read the last group (never used): every iteration
-        // issues the same loads, so the waits count exactly the groups ahead
-        const int b0 = __builtin_amdgcn_readfirstlane(b0_ < nblk - U ? b0_ : nblk - U);
+    auto pick = [](const uint4 &v, int k) { return k == 0 ? v.x : k == 1 ? v.y : k == 2 ? v.z : v.w; };
+    auto compute = [&](const WaveChunk<PAIRED> &w, int buf) {
+        uint4 At[AG], A2t[PAIRED ? AG : 1];
         #pragma unroll
-        for (int u = 0; u < U; u++) {
-            X.A[u] = buf_ld32(rca, lo_c, (b0 + u) * 16);
-            if constexpr (PAIRED) X.A2[u] = buf_ld32(rcb, lo_c, (b0 + u) * 16);
+        for (int q = 0; q < AG; q++) {
+            At[q] = w.A[q]; transpose4(At[q]);
+            if constexpr (PAIRED) { A2t[q] = w.A2[q]; transpose4(A2t[q]); }
+        }
+        const uint32_t sa[4] = {w.S.x, w.S.y, w.S.z, w.S.w};
+        const uint32_t sb[4] = {w.S2.x, w.S2.y, w.S2.z, w.S2.w};
+        #pragma unroll
+        for (int kb = 0; kb < KC; kb++) {
+            const long wA = unpack_codes(pick(At[kb / 4], kb & 3));
+            const unsigned short h = (unsigned short)(sa[kb >> 1] >> (16 * (kb & 1)));
+            const int32_t ms_a = (int32_t)((float)__builtin_bit_cast(_Float16, h) * sc_a);
+            long B[TT][3];
             #pragma unroll
             for (int j = 0; j < TT; j++)
                 #pragma unroll
                 for (int p = 0; p < 3; p++)
-                    X.B[u][j][p] = buf_ld64(rpl, lo_p, p * pstride + ((b0 + u) * TP + 16 * j) * 32);
-        }
-        static_assert(U == 4, "scales: one 8-byte load per lane and group");
-        const long sa2 = buf_ld64(rsa, lo_s, b0 * 2);
-        X.S[0] = (uint32_t)sa2; X.S[1] = (uint32_t)((unsigned long)sa2 >> 32);
-        if constexpr (PAIRED) {
-            const long sb2 = buf_ld64(rsb, lo_s, b0 * 2);
-            X.S2[0] = (uint32_t)sb2; X.S2[1] = (uint32_t)((unsigned long)sb2 >> 32);
-        }
-    };
-    auto compute = [&](const Buf &X) {
-        #pragma unroll
-        for (int u = 0; u < U; u++) {
-            const long wA = unpack_codes(X.A[u]);
-            const unsigned short h = (unsigned short)(X.S[u >> 1] >> (16 * (u & 1)));
-            const int32_t ms_a = (int32_t)((float)__builtin_bit_cast(_Float16, h) * sc_a);
+                    B[j][p] = ((const long *)&Bs[buf][((kb * 3 + p) * TT + j) * 32])[c16 * 4 + g];
             #pragma unroll
             for (int j = 0; j < TT; j++) {
-                const v4i d = block_dot(X.B[u][j], wA);
+                const v4i d = block_dot(B[j][0], B[j][1], B[j][2], wA);
                 #pragma unroll
                 for (int i = 0; i < 4; i++) acc_a[j][i] += (int64_t)d[i] * ms_a;
             }
             if constexpr (PAIRED) {
-                const long wB = unpack_codes(X.A2[u]);
-                const unsigned short h2 = (unsigned short)(X.S2[u >> 1] >> (16 * (u & 1)));
+                const long wB = unpack_codes(pick(A2t[kb / 4], kb & 3));
+                const unsigned short h2 = (unsigned short)(sb[kb >> 1] >> (16 * (kb & 1)));
                 const int32_t ms_b = (int32_t)((float)__builtin_bit_cast(_Float16, h2) * sc_b);
                 #pragma unroll
                 for (int j = 0; j < TT; j++) {
-                    const v4i d = block_dot(X.B[u][j], wB);
+                    const v4i d = block_dot(B[j][0], B[j][1], B[j][2], wB);
                     #pragma unroll
                     for (int i = 0; i < 4; i++) acc_b[j][i] += (int64_t)d[i] * ms_b;
                 }
             }
+            // keep each block's products in order: reassociating the int64 sums
+            // across blocks would hold every block's MFMA results live at once
+            #pragma unroll
+            for (int j = 0; j < TT; j++)
+                #pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    asm volatile("" : "+v"(acc_a[j][i]));
+                    if constexpr (PAIRED) asm volatile("" : "+v"(acc_b[j][i]));
+                }
         }
     };
-    // a ring of register buffers: with one tile per wave, three groups' loads
-    // are in flight while the fourth runs through the matrix cores (the loads'
-    // latency under load is several times one group's work); two tiles per
-    // wave double the work per group and leave room for two buffers
-    if constexpr (TT == 1) {
-        Buf X0, X1, X2, X3;
-        load(X0, 0);
-        load(X1, U);
-        load(X2, 2 * U);
-        for (int b0 = 0; b0 < nblk; b0 += 4 * U) {
-            load(X3, b0 + 3 * U);
-            compute(X0);
-            if (b0 + U >= nblk) break;
-            load(X0, b0 + 4 * U);
-            compute(X1);
-            if (b0 + 2 * U >= nblk) break;
-            load(X1, b0 + 5 * U);
-            compute(X2);
-            if (b0 + 3 * U >= nblk) break;
-            load(X2, b0 + 6 * U);
-            compute(X3);
-        }
-    } else {
-        Buf X, Y;
-        load(X, 0);
-        for (int b0 = 0; b0 < nblk; b0 += 2 * U) {
-            load(Y, b0 + U);
-            compute(X);
-            if (b0 + U >= nblk) break;
-            load(X, b0 + 2 * U);
-            compute(Y);
-        }
+    // pipeline: chunk ck computes from LDS buffer ck % 2 while the next
+    // chunk's activation pieces wait in registers for the other buffer; a
+    // wave's codes and scales are requested right after their registers' use.
+    // Every buffer write is separated from the previous reads of that buffer
+    // by the barrier that published the other buffer.
+    uint4 st0[PPT], st1[PPT];
+    WaveChunk<PAIRED> w0, w1;
+    stage_load(st0, 0);
+    wave_load(w0, 0);
+    if (nck > 1) { stage_load(st1, 1); wave_load(w1, 1); }
+    stage_store(st0, 0);
+    __syncthreads();
+    for (int ck = 0; ck < nck; ck += 2) {
+        if (ck + 2 < nck) stage_load(st0, ck + 2);
+        compute(w0, 0);
+        if (ck + 2 < nck) wave_load(w0, ck + 2);
+        if (ck + 1 >= nck) break;
+        stage_store(st1, 1);
+        __syncthreads();
+        if (ck + 3 < nck) stage_load(st1, ck + 3);
+        compute(w1, 1);
+        if (ck + 3 < nck) wave_load(w1, ck + 3);
+        if (ck + 2 >= nck) break;
+        stage_store(st0, 0);
+        __syncthreads();
     }
     // outputs: lane holds row `row` for tokens t0 + 16j + 4g + i
     #pragma unroll
@@ -271,7 +304,7 @@ void launch_stage(const StageArgs &a, hipStream_t s) {
 }
 
 bool gemm_supported(const DevW &w) {
-    return !w.wide && w.rows % 64 == 0 && w.cols % 256 == 0;
+    return !w.wide && w.rows % 64 == 0 && w.cols % (32 * GEMM_KC) == 0;
 }
 
 void launch_gemm(const GemmArgs &a, int nrows_total, hipStream_t s) {
@@ -286,6 +319,7 @@ void launch_gemm(const GemmArgs &a, int nrows_total, hipStream_t s) {
     if ((size_t)3 * (a.cols / 32) * a.TP * 32 >= ((size_t)1 << 31)) { fprintf(stderr, "kvd: GEMM planes too large\n"); abort(); }
     // 32-token tiles per wave (codes unpacked and scales decoded once for two
     // tiles) when that still gives >= 512 workgroups, else 16-token tiles
+    // (LDS: 24 KiB per workgroup with 16-token tiles, 48 KiB with 32)
     if ((nrows_total / 64) * (a.TP / 32) < 512) {
         const dim3 grid(nrows_total / 64, a.TP / 16);
         if (paired) hipLaunchKernelGGL((k_gemm_q4b<true, 1>), grid, dim3(256), 0, s, a);

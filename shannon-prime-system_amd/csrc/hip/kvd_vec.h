@@ -168,15 +168,20 @@ __device__ __forceinline__ void stat_flush_block(VecStat *slot, StatAcc acc) {
         atomicMax(&r->maxbits, __float_as_uint(m));
     }
 }
-// The totals over a statistic's replicas, uniform across the wave.
-__device__ __forceinline__ void stat_read(const VecStat *slot, int64_t &ss, float &mx) {
-    const int lane = threadIdx.x & 63;
-    int64_t q = 0;
-    float m = 0.0f;
-    if (lane < STAT_REP) {
-        q = (int64_t)ld_agent(&slot[lane].ss);
-        m = __uint_as_float(ld_agent(&slot[lane].maxbits));
-    }
+// A statistic is read in two steps so that its loads can be issued early:
+// stat_load gives lane l < STAT_REP replica l's values, stat_reduce the
+// totals over the replicas, uniform across the wave.
+// (stat_load reads replica lane % STAT_REP on every lane, unconditionally, so
+// that nothing waits for the values before stat_reduce masks the copies, and
+// only the fields asked for: an unused load would still occupy its register.)
+template <bool SS = true, bool MAX = true>
+__device__ __forceinline__ void stat_load(const VecStat *slot, int64_t &q, float &m) {
+    const int r = threadIdx.x & (STAT_REP - 1);
+    q = SS ? (int64_t)ld_agent(&slot[r].ss) : 0;
+    m = MAX ? __uint_as_float(ld_agent(&slot[r].maxbits)) : 0.0f;
+}
+__device__ __forceinline__ void stat_reduce(int64_t q, float m, int64_t &ss, float &mx) {
+    if ((threadIdx.x & 63) >= STAT_REP) { q = 0; m = 0.0f; }
     q = wave_to63(q, (int64_t)0, [](int64_t a, int64_t b) { return a + b; });
     m = wave_to63(m, 0.0f, [](float a, float b) { return fmaxf(a, b); });
     const uint64_t qu = (uint64_t)q;
@@ -185,10 +190,8 @@ __device__ __forceinline__ void stat_read(const VecStat *slot, int64_t &ss, floa
     mx = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 63));
 }
 // The exact-mode RMS scale of a vector whose sum of squares a producer accumulated
-__device__ __forceinline__ NormScale stat_scale(const VecStat *st, int n) {
+__device__ __forceinline__ NormScale stat_scale(int64_t ss, int n) {
     NormScale s; s.f = 0.0f; s.inv = 0; s.invd = 0.0; s.zero = 0;
-    int64_t ss; float mx;
-    stat_read(st, ss, mx);
     if (ss == 0) { s.zero = 1; return s; }
     s.inv = rms_inv_q72(n, ss);
     s.invd = (double)s.inv;
@@ -234,12 +237,52 @@ __device__ __forceinline__ float norm_apply(float x, float w, const NormScale &s
 
 // ------------------------------------------------------- input transform
 // Latency matters more than work here (every GEMV workgroup runs it before its
-// matrix pass), so every pass over the vector issues PB loads per thread
-// before using any of them, and independent passes are fused: the residual
-// pass also sums the squares for the next norm, the last norm pass also takes
-// the maximum.
+// matrix pass), so every pass over the vector issues its loads before using
+// any of them, and independent passes are fused: the residual pass also sums
+// the squares for the next norm, the last norm pass also takes the maximum.
 constexpr int SH_ZERO = SH_ZERO_V;
 constexpr int PB = 8;
+constexpr int PB4 = 2;          // float4 loads per thread and array on the register path (n <= 4 * PB4 * T)
+
+// The global-memory inputs of the input transform, loaded by pro_load before
+// anything else the kernel requests: vector-memory loads complete in order, so
+// waiting for a value requested after a weight prefetch waits for the
+// prefetch too.  Register path only (n <= 4 * PB4 * T); the loop path for
+// longer vectors loads as it goes.
+struct ProLoads {
+    float4 xv[PB4], dv[PB4], pw[PB4], nw[PB4];
+    int64_t sq;                 // this lane's replica of the producer's statistic
+    float sm;
+};
+template <int PRO>
+__device__ __forceinline__ bool pro_uses_stat(const ProArgs &p, int mode) {
+    return p.stat && (PRO == PRO_PLAIN || (PRO == PRO_RESID && p.post_w && mode == EXACT));
+}
+template <int PRO>
+__device__ __forceinline__ void pro_load(const ProArgs &p, int mode, ProLoads &L) {
+    const int n = p.n, T = blockDim.x, tid = threadIdx.x;
+    // PRO_PLAIN takes the maximum, PRO_RESID the sum of squares
+    if (pro_uses_stat<PRO>(p, mode)) stat_load<PRO != PRO_PLAIN, PRO == PRO_PLAIN>(p.stat, L.sq, L.sm);
+    if (PRO == PRO_PLAIN || n > 4 * PB4 * T) return;
+    // every load reads a valid address (a lane past the end re-reads element
+    // 0, a missing post_w reads x); input_transform masks the values when it
+    // uses them -- masking here would wait for the loads at once, and a select
+    // between loads would become a load through a selected pointer
+    const float *pwp = p.post_w ? p.post_w : p.x;
+    #pragma unroll
+    for (int k = 0; k < PB4; k++) {
+        const int i = 4 * (k * T + tid);
+        const int ic = i < n ? i : 0;                    // n is a multiple of 4
+        L.xv[k] = *(const float4 *)(p.x + ic);
+        L.nw[k] = *(const float4 *)(p.norm_w + ic);
+        if constexpr (PRO == PRO_RESID) {
+            L.dv[k] = *(const float4 *)(p.delta + ic);
+            L.pw[k] = *(const float4 *)(pwp + ic);
+        }
+    }
+}
+__device__ __forceinline__ float f4c(const float4 &v, int c) { return c == 0 ? v.x : c == 1 ? v.y : c == 2 ? v.z : v.w; }
+__device__ __forceinline__ void f4s(float4 &v, int c, float x) { if (c == 0) v.x = x; else if (c == 1) v.y = x; else if (c == 2) v.z = x; else v.w = x; }
 
 // The GEMV input transform of one vector by one workgroup: residual add (+
 // sandwich norm of the branch), RMSNorm, and the grid exponent
@@ -247,59 +290,82 @@ constexpr int PB = 8;
 // vector).  The result is left in xf (LDS, n floats), or read from p.x for
 // PRO_PLAIN.  x_out (the updated residual) is written when write_x is set.
 // red: RED_SLOTS x RED_WAVES x 8 bytes of LDS, used once per launch.
+// L: what pro_load<PRO> loaded for the same p and mode.
 template <int PRO>
-__device__ int input_transform(const ProArgs &p, int mode, float *xf, void *red, bool write_x) {
+__device__ int input_transform(const ProArgs &p, int mode, const ProLoads &L, float *xf, void *red, bool write_x) {
     const int n = p.n, T = blockDim.x, tid = threadIdx.x;
     float m = 0.0f;
     if constexpr (PRO == PRO_PLAIN) {
         // the producer's maximum: no pass over the vector here (callers read
         // only the columns they need)
-        if (p.stat) { int64_t ss; float mx; stat_read(p.stat, ss, mx); return sh_of_max(mx); }
+        if (p.stat) { int64_t ss; float mx; stat_reduce(L.sq, L.sm, ss, mx); return sh_of_max(mx); }
         for (int base = 0; base < n; base += PB * T) {
             float a[PB];
             #pragma unroll
-            for (int k = 0; k < PB; k++) { const int i = base + k * T + tid; a[k] = i < n ? p.x[i] : 0.0f; }
+            for (int k = 0; k < PB; k++) { const int i = base + k * T + tid; a[k] = p.x[i < n ? i : 0]; }
             #pragma unroll
-            for (int k = 0; k < PB; k++) m = fmaxf(m, fabsf(a[k]));
+            for (int k = 0; k < PB; k++) m = fmaxf(m, fabsf(a[k]));     // a re-read x[0] changes no maximum
         }
-    } else if (n <= PB * T) {
-        // whole vector in registers: one round of loads, then only reductions
-        float xv[PB], dv[PB], pw[PB], nw[PB];
+    } else if (n <= 4 * PB4 * T) {
+        // whole vector in registers (loaded by pro_load): only reductions here;
+        // lanes past the end hold copies of element 0 and are zeroed
+        const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        float4 xv[PB4], dv[PB4], pw[PB4], nw[PB4];
         #pragma unroll
-        for (int k = 0; k < PB; k++) {
-            const int i = k * T + tid;
-            const bool ok = i < n;
-            xv[k] = ok ? p.x[i] : 0.0f;
-            nw[k] = ok ? p.norm_w[i] : 0.0f;
-            dv[k] = (PRO == PRO_RESID && ok) ? p.delta[i] : 0.0f;
-            pw[k] = (PRO == PRO_RESID && ok && p.post_w) ? p.post_w[i] : 0.0f;
+        for (int k = 0; k < PB4; k++) {
+            const bool ok = 4 * (k * T + tid) < n;
+            xv[k] = ok ? L.xv[k] : z;
+            nw[k] = ok ? L.nw[k] : z;
+            dv[k] = (PRO == PRO_RESID && ok) ? L.dv[k] : z;
+            pw[k] = (PRO == PRO_RESID && ok && p.post_w) ? L.pw[k] : z;
         }
         if constexpr (PRO == PRO_RESID) {
             NormScale sd; sd.f = 0.0f; sd.inv = 0; sd.invd = 0.0; sd.zero = 0;
-            if (p.post_w && p.stat && mode == EXACT) {
-                sd = stat_scale(p.stat, n);              // the producer's exact sum of squares
+            if (pro_uses_stat<PRO>(p, mode)) {
+                int64_t ss; float mx;
+                stat_reduce(L.sq, L.sm, ss, mx);             // the producer's exact sum of squares
+                sd = stat_scale(ss, n);
             } else if (p.post_w) {
                 SumSq q;
                 #pragma unroll
-                for (int k = 0; k < PB; k++) if (k * T + tid < n) q.add(dv[k], mode);
+                for (int k = 0; k < PB4; k++)
+                    if (4 * (k * T + tid) < n)
+                        #pragma unroll
+                        for (int c = 0; c < 4; c++) q.add(f4c(dv[k], c), mode);
                 sd = norm_finish(q, n, p.eps, mode, red_slot(red, 0));
             }
             const bool wr = write_x && p.x_out;
             #pragma unroll
-            for (int k = 0; k < PB; k++) {
-                const int i = k * T + tid;
-                xv[k] = xv[k] + (p.post_w ? norm_apply(dv[k], pw[k], sd, mode) : dv[k]);
-                if (wr && i < n) p.x_out[i] = xv[k];
+            for (int k = 0; k < PB4; k++) {
+                const int i = 4 * (k * T + tid);
+                #pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const float d = f4c(dv[k], c);
+                    f4s(xv[k], c, f4c(xv[k], c) + (p.post_w ? norm_apply(d, f4c(pw[k], c), sd, mode) : d));
+                }
+                if (wr && i < n) *(float4 *)(p.x_out + i) = xv[k];
             }
         }
         SumSq q;
         #pragma unroll
-        for (int k = 0; k < PB; k++) if (k * T + tid < n) q.add(xv[k], mode);
+        for (int k = 0; k < PB4; k++)
+            if (4 * (k * T + tid) < n)
+                #pragma unroll
+                for (int c = 0; c < 4; c++) q.add(f4c(xv[k], c), mode);
         const NormScale s = norm_finish(q, n, p.eps, mode, red_slot(red, 1));
         #pragma unroll
-        for (int k = 0; k < PB; k++) {
-            const int i = k * T + tid;
-            if (i < n) { const float y = norm_apply(xv[k], nw[k], s, mode); xf[i] = y; m = fmaxf(m, fabsf(y)); }
+        for (int k = 0; k < PB4; k++) {
+            const int i = 4 * (k * T + tid);
+            if (i < n) {
+                float4 y;
+                #pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const float v = norm_apply(f4c(xv[k], c), f4c(nw[k], c), s, mode);
+                    f4s(y, c, v);
+                    m = fmaxf(m, fabsf(v));
+                }
+                *(float4 *)(xf + i) = y;
+            }
         }
     } else {
         NormScale s;
@@ -317,8 +383,10 @@ __device__ int input_transform(const ProArgs &p, int mode, float *xf, void *red,
             s = norm_finish(q, n, p.eps, mode, red_slot(red, 1));
         } else {
             NormScale sd; sd.f = 0.0f; sd.inv = 0; sd.invd = 0.0; sd.zero = 0;
-            if (p.post_w && p.stat && mode == EXACT) {
-                sd = stat_scale(p.stat, n);
+            if (pro_uses_stat<PRO>(p, mode)) {
+                int64_t ss; float mx;
+                stat_reduce(L.sq, L.sm, ss, mx);
+                sd = stat_scale(ss, n);
             } else if (p.post_w) {
                 SumSq q;
                 for (int base = 0; base < n; base += PB * T) {
@@ -365,6 +433,14 @@ __device__ int input_transform(const ProArgs &p, int mode, float *xf, void *red,
     }
     m = block_max(m, (float *)red_slot(red, 2));         // its barrier also orders the xf writes above
     return sh_of_max(m);
+}
+
+// Loads and transforms in one call (kernels with nothing to prefetch).
+template <int PRO>
+__device__ int input_transform(const ProArgs &p, int mode, float *xf, void *red, bool write_x) {
+    ProLoads L;
+    pro_load<PRO>(p, mode, L);
+    return input_transform<PRO>(p, mode, L, xf, red, write_x);
 }
 
 __device__ __forceinline__ void f16_parts(uint32_t h, int32_t &M, int &e) {
