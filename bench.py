@@ -41,11 +41,12 @@ KERNEL_NAMES = {
     "gate_up_gemv_q4b": ["kvd::k_gemv<2, true, false>"],
     "down_gemv_q4b": ["kvd::k_gemv<0, false, false>"],
     "lm_head_gemv_q4b": ["kvd::k_gemv<2, false, false>"],
-    "gqa_decode_attn_global": ["kvd::k_attn_exact_scores<EPL, G, false> + kvd::k_attn_exact_vsum<EPL, G, false>",
-                               "[kvd::k_attn_float<EPL, G, false>]"],
-    "gqa_decode_attn_window": ["kvd::k_attn_exact_scores<EPL, G, false> + kvd::k_attn_exact_vsum<EPL, G, false>",
-                               "[kvd::k_attn_float<EPL, G, false>]"],
-    "qk_norm_rope_append": ["kvd::k_qk_prep<false>"],
+    "gqa_decode_attn_global": ["kvd::k_attn_exact_scores<EPL, G, false, true> + kvd::k_attn_exact_vsum<EPL, G, false>",
+                               "[kvd::k_qk_prep<false> + kvd::k_attn_float<EPL, G, false>]"],
+    "gqa_decode_attn_window": ["kvd::k_attn_exact_scores<EPL, G, false, true> + kvd::k_attn_exact_vsum<EPL, G, false>",
+                               "[kvd::k_qk_prep<false> + kvd::k_attn_float<EPL, G, false>]"],
+    # float mode only: exact-mode decode prepares the heads inside the score pass
+    "qk_norm_rope_append": ["[kvd::k_qk_prep<false>]"],
     "embed_rope_argmax": ["kvd::k_embed", "kvd::k_rope_table", "kvd::k_argmax"],
 }
 # committed rocprofv3 --pmc summaries (FETCH_SIZE / WRITE_SIZE per dispatch) of the

@@ -389,8 +389,15 @@ __global__ __launch_bounds__(256) void k_attn_float(AttnArgs a_in) {
 }
 
 // ---- exact mode: pass 1, integer scores on the softmax grid + chunk max ----
-template <int EPL, int G, bool BATCH>
+// PREP (decode): the kernel also does the step's head preparation -- every
+// workgroup normalizes and rotates its G q heads itself (wave g, head h*G+g)
+// straight into LDS, and the workgroup of the last chunk, which holds pos,
+// appends the new K (after norm and RoPE) and V rows to the paged store and
+// scores position pos from the new K row it keeps in LDS (its own loads of
+// that row may predate the append).  Same arithmetic as k_qk_prep.
+template <int EPL, int G, bool BATCH, bool PREP>
 __global__ __launch_bounds__(256) void k_attn_exact_scores(AttnArgs a_in) {
+    static_assert(!(BATCH && PREP), "head preparation is fused for decode only");
     AttnArgs a = a_in;
     int pos;
     tok_select<BATCH>(a, blockIdx.z, pos);
@@ -401,8 +408,10 @@ __global__ __launch_bounds__(256) void k_attn_exact_scores(AttnArgs a_in) {
     if (c >= nch) return;
     __shared__ int zmax[4][G];
     __shared__ int4 qs[G][EPL * 16];                 // qi = rne(q * 2^16), 4 dims per entry
+    __shared__ int4 kn[PREP ? EPL * 16 : 1];         // PREP, last chunk: the new K row (ki)
     const int r = lane >> 2, k4 = lane & 3;
     const int n = ce - cs;
+    const bool holds_pos = PREP && c == nch - 1;     // chunk ranges end at pos
     // the wave's first row group is requested before q is staged
     int4 kv[4 * EPL];
     {
@@ -413,11 +422,41 @@ __global__ __launch_bounds__(256) void k_attn_exact_scores(AttnArgs a_in) {
             for (int i = 0; i < 4 * EPL; i++) kv[i] = *(const int4 *)(row + 16 * i);
         }
     }
-    for (int i = threadIdx.x; i < G * HD / 4; i += 256) {
-        const int g = i / (HD / 4), d4 = i % (HD / 4);
-        const float *qp = a.qr + (size_t)(h * G + g) * HD + 4 * d4;
-        qs[g][d4] = make_int4((int)rintf(qp[0] * 65536.0f), (int)rintf(qp[1] * 65536.0f),
-                              (int)rintf(qp[2] * 65536.0f), (int)rintf(qp[3] * 65536.0f));
+    if constexpr (PREP) {
+        const HeadPrep hp = head_prep_of(a);
+        float out[8];
+        static_assert(G <= 4, "one wave per q head of the group");
+        if (wave < G) {
+            head_norm_rope<false, EPL>(hp, a.q + (size_t)(h * G + wave) * HD, a.q_norm, lane, out);
+            #pragma unroll
+            for (int j = 0; j < EPL; j++) ((int *)qs[wave])[lane + 64 * j] = (int)rintf(out[j] * 65536.0f);
+        }
+        if (holds_pos) {
+            // K by wave G % 4 and V by wave (G + 1) % 4 (spare waves when G == 2)
+            float *page = qk_page_of(a.pages, a.ring_pages, pos);
+            const size_t rowoff = ((size_t)h * PAGE + pos % PAGE) * HD;
+            if (wave == G % 4) {
+                head_norm_rope<false, EPL>(hp, a.k + (size_t)h * HD, a.k_norm, lane, out);
+                #pragma unroll
+                for (int j = 0; j < EPL; j++) {
+                    const int32_t ki = kv_code_k(out[j]);
+                    ((int32_t *)(page + rowoff))[lane + 64 * j] = ki;
+                    ((int *)kn)[lane + 64 * j] = ki;
+                }
+            }
+            if (wave == (G + 1) % 4) {
+                int32_t *dst = (int32_t *)(page + (size_t)a.NKV * PAGE * HD + rowoff);
+                #pragma unroll
+                for (int j = 0; j < EPL; j++) dst[lane + 64 * j] = kv_code_v(a.v[(size_t)h * HD + lane + 64 * j]);
+            }
+        }
+    } else {
+        for (int i = threadIdx.x; i < G * HD / 4; i += 256) {
+            const int g = i / (HD / 4), d4 = i % (HD / 4);
+            const float *qp = a.qr + (size_t)(h * G + g) * HD + 4 * d4;
+            qs[g][d4] = make_int4((int)rintf(qp[0] * 65536.0f), (int)rintf(qp[1] * 65536.0f),
+                                  (int)rintf(qp[2] * 65536.0f), (int)rintf(qp[3] * 65536.0f));
+        }
     }
     __syncthreads();
     int mx = INT32_MIN;                              // lane with k4 == g tracks head g
@@ -431,6 +470,10 @@ __global__ __launch_bounds__(256) void k_attn_exact_scores(AttnArgs a_in) {
                 const int32_t *row = quad_row<EPL, int32_t>(a, h, cs + j0, ce - 1, cs + j, false) + 4 * k4;
                 #pragma unroll
                 for (int i = 0; i < 4 * EPL; i++) kv[i] = *(const int4 *)(row + 16 * i);
+            }
+            if (holds_pos && cs + j == pos) {
+                #pragma unroll
+                for (int i = 0; i < 4 * EPL; i++) kv[i] = kn[4 * i + k4];
             }
             #pragma unroll
             for (int i = 0; i < 4 * EPL; i++)
@@ -486,7 +529,7 @@ __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a_in) {
     __shared__ int32_t ew[G][MAXCH];                // island weights in Q22 (<= 2^22)
     __shared__ int64_t ored[4][G][EPL * 64];
     __shared__ int redi[4][G];
-    __shared__ int64_t redl[4];
+    __shared__ int64_t redl[4][G];
     __shared__ int is_last;
     const int n = ce - cs;
     // the first V rows and this chunk's scores are requested before the
@@ -565,16 +608,18 @@ __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a_in) {
         const int64_t t = ored[0][g][d] + ored[1][g][d] + ored[2][g][d] + ored[3][g][d];
         atomicAdd((unsigned long long *)&vrep[(size_t)(h * G + g) * HD + d], (unsigned long long)t);
     }
+    // the chunk's softmax denominators, all heads of the group in one round
     #pragma unroll
     for (int g = 0; g < G; g++) {
         int64_t S = 0;
         for (int j = threadIdx.x; j < n; j += 256) S += ew[g][j];
         S = wsuml(S);
-        if (lane == 0) redl[wave] = S;
-        __syncthreads();
-        if (threadIdx.x == 0)
-            atomicAdd((unsigned long long *)&srep[h * G + g], (unsigned long long)(redl[0] + redl[1] + redl[2] + redl[3]));
-        __syncthreads();
+        if (lane == 0) redl[wave][g] = S;
+    }
+    __syncthreads();
+    if (threadIdx.x < G) {
+        const int g = threadIdx.x;
+        atomicAdd((unsigned long long *)&srep[h * G + g], (unsigned long long)(redl[0][g] + redl[1][g] + redl[2][g] + redl[3][g]));
     }
     mem_complete();
     __syncthreads();
@@ -592,13 +637,24 @@ __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a_in) {
     }
     __syncthreads();
     StatAcc sacc;
-    for (int i = threadIdx.x; i < G * HD; i += 256) {
-        int64_t acc = 0;
-        #pragma unroll
-        for (int r = 0; r < VREP; r++)
-            acc += (int64_t)__hip_atomic_exchange((unsigned long long *)&a.vacc[(size_t)r * QDh + (size_t)h * G * HD + i], 0ull,
-                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const float o = rne_div_to_float((i128)acc, Sg[i / HD], 16);
+    // every exchange is issued before any total is used: one round trip
+    constexpr int PT = (G * EPL * 64 + 255) / 256;   // elements per thread
+    int64_t tot[PT];
+    #pragma unroll
+    for (int k = 0; k < PT; k++) {
+        const int i = threadIdx.x + 256 * k;
+        tot[k] = 0;
+        if (i < G * HD)
+            #pragma unroll
+            for (int r = 0; r < VREP; r++)
+                tot[k] += (int64_t)__hip_atomic_exchange((unsigned long long *)&a.vacc[(size_t)r * QDh + (size_t)h * G * HD + i], 0ull,
+                                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    #pragma unroll
+    for (int k = 0; k < PT; k++) {
+        const int i = threadIdx.x + 256 * k;
+        if (i >= G * HD) break;
+        const float o = rne_div_to_float((i128)tot[k], Sg[i / HD], 16);
         a.ao[(size_t)h * G * HD + i] = o;
         sacc.add(o);
     }
@@ -608,31 +664,42 @@ __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a_in) {
 
 // decode (B = false: position from the step state) and batched prefill
 // (B = true: token grid dimension) are separate instances
-template <int EPL, int G, bool B> static void attn_dispatch_b(const AttnArgs &a, int grid_chunks, hipStream_t s) {
+template <int EPL, int G, bool B> static void attn_dispatch_b(const AttnArgs &a, int grid_chunks, bool prep, hipStream_t s) {
     dim3 grid(grid_chunks, a.NKV, B ? a.nt : 1);
     if (a.mode == FLOAT) hipLaunchKernelGGL((k_attn_float<EPL, G, B>), grid, dim3(256), 0, s, a);
     else {
-        hipLaunchKernelGGL((k_attn_exact_scores<EPL, G, B>), grid, dim3(256), 0, s, a);
+        if (!B && prep) hipLaunchKernelGGL((k_attn_exact_scores<EPL, G, B, !B>), grid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((k_attn_exact_scores<EPL, G, B, false>), grid, dim3(256), 0, s, a);
         hipLaunchKernelGGL((k_attn_exact_vsum<EPL, G, B>), grid, dim3(256), 0, s, a);
     }
 }
-template <int EPL, int G> static void attn_dispatch(const AttnArgs &a, int grid_chunks, hipStream_t s) {
-    if (a.nt) attn_dispatch_b<EPL, G, true>(a, grid_chunks, s);
-    else attn_dispatch_b<EPL, G, false>(a, grid_chunks, s);
+template <int EPL, int G> static void attn_dispatch(const AttnArgs &a, int grid_chunks, bool prep, hipStream_t s) {
+    if (a.nt) attn_dispatch_b<EPL, G, true>(a, grid_chunks, false, s);
+    else attn_dispatch_b<EPL, G, false>(a, grid_chunks, prep, s);
 }
 
-void launch_attention(const AttnArgs &a, int grid_chunks, hipStream_t s) {
+static void attention_go(const AttnArgs &a, int grid_chunks, bool prep, hipStream_t s) {
     const int G = a.NH / a.NKV;
     if (a.chunk > MAXCH || a.chunk % 16 || grid_chunks > MAXNCH) {
         fprintf(stderr, "kvd: attention chunk %d / grid %d outside the kernel's limits\n", a.chunk, grid_chunks);
         abort();
     }
-    if (a.HD == 256 && G == 2) attn_dispatch<4, 2>(a, grid_chunks, s);
-    else if (a.HD == 128 && G == 2) attn_dispatch<2, 2>(a, grid_chunks, s);
-    else if (a.HD == 128 && G == 4) attn_dispatch<2, 4>(a, grid_chunks, s);
-    else if (a.HD == 64 && G == 2) attn_dispatch<1, 2>(a, grid_chunks, s);
-    else if (a.HD == 256 && G == 4) attn_dispatch<4, 4>(a, grid_chunks, s);
-    else if (a.HD == 64 && G == 4) attn_dispatch<1, 4>(a, grid_chunks, s);
+    if (a.HD == 256 && G == 2) attn_dispatch<4, 2>(a, grid_chunks, prep, s);
+    else if (a.HD == 128 && G == 2) attn_dispatch<2, 2>(a, grid_chunks, prep, s);
+    else if (a.HD == 128 && G == 4) attn_dispatch<2, 4>(a, grid_chunks, prep, s);
+    else if (a.HD == 64 && G == 2) attn_dispatch<1, 2>(a, grid_chunks, prep, s);
+    else if (a.HD == 256 && G == 4) attn_dispatch<4, 4>(a, grid_chunks, prep, s);
+    else if (a.HD == 64 && G == 4) attn_dispatch<1, 4>(a, grid_chunks, prep, s);
+}
+void launch_attention(const AttnArgs &a, int grid_chunks, hipStream_t s) { attention_go(a, grid_chunks, false, s); }
+
+// The step's head preparation and attention: exact-mode decode runs the
+// preparation inside the score pass; float mode and batched tokens launch
+// k_qk_prep first.
+bool attention_fuses_prep(const AttnArgs &a) { return a.mode == EXACT && !a.nt; }
+void launch_prep_attention(const AttnArgs &a, int grid_chunks, hipStream_t s) {
+    if (!attention_fuses_prep(a)) launch_qk_prep(a, s);
+    attention_go(a, grid_chunks, attention_fuses_prep(a), s);
 }
 
 // ------------------------------------------------------------------ embedding

@@ -603,9 +603,13 @@ void enqueue_body(sp_kvdecode_handle *h, const StepShape &sh, TimeCb cb, void *c
         a.ascale = 1.0f / sqrtf((float)m->HD);
         a.chunk = glob ? sh.chunk_global : sh.chunk_local;
         a.stat_out = st(l, STAT_AO);
-        T(7, true); launch_qk_prep(a, s); T(7, false);
-        const int cls = (glob || a.win < 0) ? 5 : 6;
-        T(cls, true); launch_attention(a, glob ? sh.grid_global : sh.grid_local, s); T(cls, false);
+        const int cls = (glob || a.win < 0) ? 5 : 6, grid = glob ? sh.grid_global : sh.grid_local;
+        if (attention_fuses_prep(a)) {
+            T(cls, true); launch_prep_attention(a, grid, s); T(cls, false);
+        } else {
+            T(7, true); launch_qk_prep(a, s); T(7, false);
+            T(cls, true); launch_attention(a, grid, s); T(cls, false);
+        }
 
         GemvArgs o{};
         o.accbuf = h->gacc; o.gcnt = h->gcnt; o.acc_rows = h->acc_rows;

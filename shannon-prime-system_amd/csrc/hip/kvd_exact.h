@@ -66,21 +66,20 @@ __device__ __forceinline__ uint64_t udiv128_64(u128 num, uint64_t den) {
 // v mod m for v >= 0 (v < 2^100), 0 < m < 2^63: estimate the quotient in
 // double, correct exactly
 // isqrt(floor((n << 72) / ss)) for n > 0, ss > 0 -- the island's RMS inverse.
-// The quotient is estimated in double (exact to within 2 when below 2^52) and
-// corrected with exact 128-bit products; larger quotients take udiv128_64.
+// While the quotient is below 2^64 this is the largest x with
+// x^2 * ss <= n << 72 (floor(sqrt(floor(v))) = floor(sqrt(v))): a double
+// estimate of sqrt((n << 72) / ss), off by at most one, corrected with exact
+// 128-bit products.  Larger quotients wrap in the island's 64-bit cast, so
+// they take the division and the integer square root of the wrapped value.
 __device__ __forceinline__ int64_t rms_inv_q72(int n, int64_t ss) {
     const u128 num = (u128)(uint64_t)n << 72, den = (u128)(uint64_t)ss;
-    const double est = ldexp((double)n, 72) / (double)ss;
-    uint64_t q;
-    if (est < 4503599627370496.0) {                          // 2^52
-        q = (uint64_t)est;
-        u128 prod = (u128)q * den;
-        while (prod > num) { q--; prod -= den; }
-        while (num - prod >= den) { q++; prod += den; }
-    } else {
-        q = udiv128_64(num, (uint64_t)ss);
-    }
-    return (int64_t)isqrt_u64(q);
+    if ((uint64_t)(num >> 64) >= (uint64_t)ss)
+        return (int64_t)isqrt_u64(udiv128_64(num, (uint64_t)ss));
+    uint64_t x = (uint64_t)sqrt(ldexp((double)n, 72) / (double)ss);
+    if (x > 0xFFFFFFFFull) x = 0xFFFFFFFFull;
+    while ((u128)(x * x) * den > num) x--;
+    while (x < 0xFFFFFFFFull && (u128)((x + 1) * (x + 1)) * den <= num) x++;
+    return (int64_t)x;
 }
 __device__ __forceinline__ int64_t umod128_64(i128 v, int64_t m) {
     const int64_t q = (int64_t)((double)v / (double)m);
@@ -178,7 +177,18 @@ __device__ __forceinline__ float rne_div_to_float(i128 num, int64_t den, int k) 
     n <<= sh;
     u128 q, r;
     if ((uint64_t)(n >> 64) < (uint64_t)den) {            // quotient fits 64 bits: fast path
-        q = udiv128_64(n, (uint64_t)den); r = n - q * d;
+        // a quotient below 2^52 (the usual case: n is scaled to ~2^29 d) is the
+        // double estimate (within 2) corrected exactly; larger ones refine
+        const double qe = u128_to_double(n) / (double)den;
+        if (qe < 4503599627370496.0) {
+            uint64_t q64 = (uint64_t)qe;
+            i128 rr = (i128)n - (i128)((u128)q64 * d);
+            while (rr < 0) { q64--; rr += (i128)d; }
+            while (rr >= (i128)d) { q64++; rr -= (i128)d; }
+            q = q64; r = (u128)rr;
+        } else {
+            q = udiv128_64(n, (uint64_t)den); r = n - q * d;
+        }
     } else { q = n / d; r = n % d; }
     q = (q << 1) | (r ? 1u : 0u);
     float f = rne_u128_scaled(q, -(k + sh + 1));

@@ -32,37 +32,17 @@ __device__ __forceinline__ float *qk_page_of(float *const *pages, int ring, int 
     return pages[ring ? lp % ring : lp];
 }
 
-// hb < NH: q head hb -> qr; hb < NH + NKV: k head -> page; else v head -> page.
-// src: the head's HD projections; lane l holds elements l + 64 j.  COHERENT
-// selects agent-scope loads, for projections written by other workgroups of
-// the same launch.
+// One q or k head's per-head RMSNorm and NEOX RoPE: src holds the head's HD
+// projections, nw its norm weight; lane l gets elements l + 64 j in out[j].
+// COHERENT selects agent-scope loads, for projections written by other
+// workgroups of the same launch.
 template <bool COHERENT, int PER>
-__device__ __forceinline__ void qk_prep_head_t(const HeadPrep a, int hb, int pos, int lane) {
+__device__ __forceinline__ void head_norm_rope(const HeadPrep &a, const float *src, const float *nw, int lane, float out[8]) {
     constexpr int HD = PER * 64, half = HD / 2, per = PER;
-    const bool isq = hb < a.NH, isk = !isq && hb < a.NH + a.NKV;
-    const int h = isq ? hb : (isk ? hb - a.NH : hb - a.NH - a.NKV);
-    float *page = qk_page_of(a.pages, a.ring_pages, pos);
-    const int slot = pos % PAGE;
-    const float *src = isq ? a.q + (size_t)h * HD : (isk ? a.k : a.v) + (size_t)h * HD;
     float v[8];                                                 // HD <= 512
     #pragma unroll
     for (int j = 0; j < 8; j++)
         if (j < per) v[j] = COHERENT ? ld_agent(&src[lane + 64 * j]) : src[lane + 64 * j];
-    if (!isq && !isk) {                                         // V: raw (exact: Q16 grid, clamped)
-        float *dst = page + (size_t)a.NKV * PAGE * HD + ((size_t)h * PAGE + slot) * HD;
-        #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            if (j >= per) break;
-            if (a.mode == FLOAT) dst[lane + 64 * j] = v[j];
-            else {
-                float r = rintf(v[j] * 65536.0f);
-                r = fminf(fmaxf(r, -8388607.0f), 8388607.0f);
-                ((int32_t *)dst)[lane + 64 * j] = (int32_t)r;
-            }
-        }
-        return;
-    }
-    const float *nw = isq ? a.q_norm : a.k_norm;
     // per-head RMSNorm
     if (a.mode == FLOAT) {
         double ss = 0.0;
@@ -94,7 +74,6 @@ __device__ __forceinline__ void qk_prep_head_t(const HeadPrep a, int hb, int pos
     // HD >= 128: both halves of a pair sit in the same lane (j and j + per/2);
     // HD == 64: the partner is lane ^ 32.
     const float *cs = a.rope_cs;
-    float out[8];
     if (per >= 2) {
         #pragma unroll
         for (int j = 0; j < 4; j++) {
@@ -113,6 +92,40 @@ __device__ __forceinline__ void qk_prep_head_t(const HeadPrep a, int hb, int pos
         const float ac = x0 * c, bs = x1 * s, as = x0 * s, bc = x1 * c;
         out[0] = first ? ac - bs : as + bc;
     }
+}
+
+// The stored form of a K or V element: the float itself, or in exact mode
+// K ki = rne(k * 2^16) and V vq = clamp(rne(v * 2^16), +-(2^23 - 1)).
+__device__ __forceinline__ int32_t kv_code_k(float k) { return (int32_t)rintf(k * 65536.0f); }
+__device__ __forceinline__ int32_t kv_code_v(float v) {
+    float r = rintf(v * 65536.0f);
+    r = fminf(fmaxf(r, -8388607.0f), 8388607.0f);
+    return (int32_t)r;
+}
+
+// hb < NH: q head hb -> qr; hb < NH + NKV: k head -> page; else v head -> page.
+// src: the head's HD projections; lane l holds elements l + 64 j.
+template <bool COHERENT, int PER>
+__device__ __forceinline__ void qk_prep_head_t(const HeadPrep a, int hb, int pos, int lane) {
+    constexpr int HD = PER * 64, per = PER;
+    const bool isq = hb < a.NH, isk = !isq && hb < a.NH + a.NKV;
+    const int h = isq ? hb : (isk ? hb - a.NH : hb - a.NH - a.NKV);
+    float *page = qk_page_of(a.pages, a.ring_pages, pos);
+    const int slot = pos % PAGE;
+    const float *src = isq ? a.q + (size_t)h * HD : (isk ? a.k : a.v) + (size_t)h * HD;
+    if (!isq && !isk) {                                         // V: raw (exact: Q16 grid, clamped)
+        float *dst = page + (size_t)a.NKV * PAGE * HD + ((size_t)h * PAGE + slot) * HD;
+        #pragma unroll
+        for (int j = 0; j < 8; j++) {
+            if (j >= per) break;
+            const float v = COHERENT ? ld_agent(&src[lane + 64 * j]) : src[lane + 64 * j];
+            if (a.mode == FLOAT) dst[lane + 64 * j] = v;
+            else ((int32_t *)dst)[lane + 64 * j] = kv_code_v(v);
+        }
+        return;
+    }
+    float out[8];
+    head_norm_rope<COHERENT, PER>(a, src, isq ? a.q_norm : a.k_norm, lane, out);
     if (isq) {
         #pragma unroll
         for (int j = 0; j < 8; j++) if (j < per) a.qr[(size_t)h * HD + lane + 64 * j] = out[j];
@@ -122,7 +135,7 @@ __device__ __forceinline__ void qk_prep_head_t(const HeadPrep a, int hb, int pos
         for (int j = 0; j < 8; j++) {
             if (j >= per) break;
             if (a.mode == FLOAT) dst[lane + 64 * j] = out[j];
-            else ((int32_t *)dst)[lane + 64 * j] = (int32_t)rintf(out[j] * 65536.0f);
+            else ((int32_t *)dst)[lane + 64 * j] = kv_code_k(out[j]);
         }
     }
 }
