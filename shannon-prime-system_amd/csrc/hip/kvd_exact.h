@@ -93,12 +93,22 @@ __device__ __forceinline__ int64_t umod128_64(i128 v, int64_t m) {
 __device__ __forceinline__ int64_t mul3_lo64(int64_t a, int64_t b, int64_t c) {
     return (int64_t)((uint64_t)a * (uint64_t)b * (uint64_t)c);
 }
+// floor(num / den) for 0 <= num < 2^62, 0 < den < 2^62 and a quotient below
+// 2^31 (the islands' divisions): the double estimate is within one of it and
+// is corrected exactly, in place of a generic 64/128-bit division routine.
+__device__ __forceinline__ int64_t udiv_small(int64_t num, int64_t den) {
+    int64_t q = (int64_t)((double)num / (double)den);
+    int64_t r = num - q * den;
+    while (r < 0) { q--; r += den; }
+    while (r >= den) { q++; r -= den; }
+    return q;
+}
 __device__ __forceinline__ int64_t tanh_fixed(int64_t t) {
     int s = (t >= 0) ? 1 : -1;
     int64_t a = (t >= 0) ? t : -t;
     int64_t e2 = exp_fixed(-(2 * a));
-    int64_t num = (2 * e2) << FB;
-    return (int64_t)s * (ONE - num / (ONE + e2));
+    int64_t num = (2 * e2) << FB;                  // <= 2^61, quotient <= 2^31
+    return (int64_t)s * (ONE - udiv_small(num, ONE + e2));
 }
 // round half away from zero of a double to int64 (llround)
 __device__ __forceinline__ int64_t llround_d(double d) { return (int64_t)round(d); }
@@ -125,8 +135,8 @@ __device__ __forceinline__ float silu_exact1(float x) {
     int64_t xq = llround_pow2<16>(x);
     int64_t X = (xq * ONE) >> 16;
     int64_t e = exp_fixed(X >= 0 ? -X : X);
-    int64_t sg = X >= 0 ? (int64_t)(((i128)ONE << FB) / (ONE + e))
-                        : (int64_t)(((i128)e << FB) / (ONE + e));
+    int64_t sg = X >= 0 ? udiv_small(ONE << FB, ONE + e)          // 2^60 / [2^30, 2^31]
+                        : udiv_small(e << FB, ONE + e);
     int64_t g = (int64_t)(((i128)X * sg) >> FB);
     return (float)((double)g / (double)ONE);
 }

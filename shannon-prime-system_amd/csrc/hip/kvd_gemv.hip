@@ -65,7 +65,7 @@ __device__ __forceinline__ void gemv_pro_load(const ProArgs &p, int mode, GemvLo
 template <int PRO>
 __device__ int gemv_prologue(const ProArgs &p, int mode, const GemvLoads &L, float *xf, uint4 *dig, int b_lo, int b_hi, void *red) {
     const int T = blockDim.x, tid = threadIdx.x;
-    const int sh = input_transform<PRO>(p, mode, L.pro, xf, red, blockIdx.x == 0);
+    const int sh = input_transform<PRO>(p, mode, L.pro, xf, red, blockIdx.x == 0, b_lo * 32, b_hi * 32);
     if (sh == SH_ZERO) return SH_ZERO;
     // digits: one thread per 8 consecutive columns (one nibble-dword per plane);
     // the column count is a multiple of 32, so a group never runs past n
@@ -369,12 +369,20 @@ GemvPlan gemv_plan(int nrows_total, int cols, int paired, int wide) {
     GemvPlan p;
     const int nblk = (cols + 31) / 32;
     p.groups = paired ? (nrows_total + GEMV_R / 2 - 1) / (GEMV_R / 2) : (nrows_total + GEMV_R - 1) / GEMV_R;
-    const int cap = 2 * num_cu();                       // workgroups
+    int cap = 2 * num_cu();                             // workgroups
     const int max_split = (nblk + 63) / 64;
     int want = (cap * GEMV_WAVES + p.groups - 1) / p.groups;
     // a split costs every task an atomic hand-off; it only pays when whole
     // rows would leave more than half of the waves idle
     if (wide || want <= 2) want = 1;
+    if ((long long)p.groups * (want < max_split ? want : max_split) <= (long long)cap * GEMV_WAVES) {
+        // one round of tasks: one workgroup per CU.  A second workgroup on a
+        // CU runs its input transform behind the first one's (older waves
+        // issue first), which costs more than the waves it adds; the split
+        // then fills the CUs' waves once.
+        cap = num_cu();
+        want = wide ? 1 : (cap * GEMV_WAVES + p.groups - 1) / p.groups;
+    }
     p.nsplit = want < max_split ? want : max_split;
     p.bps = 64 * ((max_split + p.nsplit - 1) / p.nsplit);
     p.nsplit = (nblk + p.bps - 1) / p.bps;

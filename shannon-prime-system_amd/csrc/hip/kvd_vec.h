@@ -92,7 +92,7 @@ template <typename T> __device__ __forceinline__ T quad_sum(T v) {
 // totals.  A reduction writes only its own `red` slots, so consecutive
 // reductions need no barrier in between; a slot array is used once per launch.
 constexpr int RED_WAVES = 16;                 // slots per reduction (waves per workgroup)
-constexpr int RED_SLOTS = 3;                  // reductions per input transform
+constexpr int RED_SLOTS = 4;                  // reductions per input transform
 template <typename T> __device__ T block_sum(T v, T *red) {
     v = wave_to63(v, (T)0, [](T a, T b) { return a + b; });
     const int w = threadIdx.x >> 6;
@@ -291,8 +291,11 @@ __device__ __forceinline__ void f4s(float4 &v, int c, float x) { if (c == 0) v.x
 // PRO_PLAIN.  x_out (the updated residual) is written when write_x is set.
 // red: RED_SLOTS x RED_WAVES x 8 bytes of LDS, used once per launch.
 // L: what pro_load<PRO> loaded for the same p and mode.
+// [c_lo, c_hi): the columns of xf the caller reads (the exact residual path
+// forms only those; every other path writes the whole vector).
 template <int PRO>
-__device__ int input_transform(const ProArgs &p, int mode, const ProLoads &L, float *xf, void *red, bool write_x) {
+__device__ int input_transform(const ProArgs &p, int mode, const ProLoads &L, float *xf, void *red, bool write_x,
+                               int c_lo = 0, int c_hi = 0x7FFFFFFF) {
     const int n = p.n, T = blockDim.x, tid = threadIdx.x;
     float m = 0.0f;
     if constexpr (PRO == PRO_PLAIN) {
@@ -335,6 +338,116 @@ __device__ int input_transform(const ProArgs &p, int mode, const ProLoads &L, fl
                 sd = norm_finish(q, n, p.eps, mode, red_slot(red, 0));
             }
             const bool wr = write_x && p.x_out;
+            if (mode == EXACT) {
+                // The residual add and the statistics of the exact norm of the
+                // result in one pass: the sum of squares of the Q16 values and
+                // the largest exact product |llround(r 2^16) * llround(w 2^16)|.
+                // Branch-free for inputs on the norms' double paths (products
+                // below 2^53, scaled below 2^62, Q16 values below 2^31); a
+                // thread with any other element redoes its elements with the
+                // general per-element arithmetic (same results).
+                int64_t ss = 0;
+                double pm = 0.0;
+                const bool pn = p.post_w != nullptr;
+                bool bad = false;
+                #pragma unroll
+                for (int k = 0; k < PB4; k++)
+                    #pragma unroll
+                    for (int c = 0; c < 4; c++) {
+                        const float d = f4c(dv[k], c);
+                        float nd = d;
+                        if (pn) {
+                            const double dx = (double)roundf(d * 65536.0f) * (double)roundf(f4c(pw[k], c) * 65536.0f);
+                            const double pr = dx * sd.invd;
+                            bad |= !(fabs(dx) < 9007199254740992.0) | !(fabs(pr) < 4611686018427387904.0);
+                            nd = sd.zero ? 0.0f : (float)(pr * 2.220446049250313e-16);
+                        }
+                        const float r = f4c(xv[k], c) + nd;
+                        f4s(xv[k], c, r);
+                        const float r16 = roundf(r * 65536.0f), w16 = roundf(f4c(nw[k], c) * 65536.0f);
+                        bad |= !(fabsf(r16) < 2147483648.0f);
+                        const int32_t q = (int32_t)r16;
+                        ss += (int64_t)q * q;
+                        const double dx2 = fabs((double)r16 * (double)w16);
+                        bad |= !(dx2 < 9007199254740992.0);
+                        pm = fmax(pm, dx2);
+                    }
+                if (bad) {
+                    // (a rolled loop over reloaded inputs, the results passed
+                    // through xf: the fast pass keeps no registers for this)
+                    ss = 0; pm = 0.0;
+                    #pragma unroll 1
+                    for (int j = 0; j < 4 * PB4; j++) {
+                        const int i = 4 * ((j >> 2) * T + tid) + (j & 3);
+                        if (i >= n) continue;
+                        const float d = p.delta[i];
+                        const float r = p.x[i] + (pn ? norm_apply(d, p.post_w[i], sd, mode) : d);
+                        xf[i] = r;
+                        const float r16 = roundf(r * 65536.0f);
+                        if (fabsf(r16) < 2147483648.0f) { const int32_t q = (int32_t)r16; ss += (int64_t)q * q; }
+                        else { const int64_t q = llround_q16(r); ss += q * q; }
+                        const double dx2 = fabs((double)r16 * (double)roundf(p.norm_w[i] * 65536.0f));
+                        pm = dx2 < 9007199254740992.0 ? fmax(pm, dx2) : INFINITY;     // NaN too
+                    }
+                    #pragma unroll
+                    for (int k = 0; k < PB4; k++)
+                        if (4 * (k * T + tid) < n) xv[k] = *(const float4 *)(xf + 4 * (k * T + tid));
+                }
+                #pragma unroll
+                for (int k = 0; k < PB4; k++) {
+                    const int i = 4 * (k * T + tid);
+                    if (wr && i < n) *(float4 *)(p.x_out + i) = xv[k];
+                }
+                // max |y| is the largest product's when every product takes
+                // norm_apply's double path (each |y| is then a monotone function
+                // of its product); otherwise every y is formed and compared.
+                // Only the columns [c_lo, c_hi) of the result are formed.
+                int64_t *rs = (int64_t *)red_slot(red, 1);
+                double *rm = (double *)red_slot(red, 2);
+                ss = wave_to63(ss, (int64_t)0, [](int64_t a, int64_t b) { return a + b; });
+                pm = wave_to63(pm, 0.0, [](double a, double b) { return fmax(a, b); });
+                if ((tid & 63) == 63) { rs[tid >> 6] = ss; rm[tid >> 6] = pm; }
+                __syncthreads();
+                ss = rs[0]; pm = rm[0];
+                for (int w = 1; w < (T >> 6); w++) { ss += rs[w]; pm = fmax(pm, rm[w]); }
+                NormScale s; s.f = 0.0f; s.inv = 0; s.invd = 0.0; s.zero = ss == 0;
+                if (!s.zero) { s.inv = rms_inv_q72(n, ss); s.invd = (double)s.inv; }
+                const double pmx = pm * s.invd;
+                if (s.zero || (pm < 9007199254740992.0 && pmx < 4611686018427387904.0)) {
+                    m = s.zero ? 0.0f : (float)(pmx * 2.220446049250313e-16);
+                    #pragma unroll
+                    for (int k = 0; k < PB4; k++) {
+                        const int i = 4 * (k * T + tid);
+                        if (i < n && i + 3 >= c_lo && i < c_hi) {
+                            float4 y;
+                            #pragma unroll
+                            for (int c = 0; c < 4; c++)
+                                f4s(y, c, s.zero ? 0.0f : (float)(((double)roundf(f4c(xv[k], c) * 65536.0f) *
+                                                                   (double)roundf(f4c(nw[k], c) * 65536.0f) * s.invd) *
+                                                                  2.220446049250313e-16));
+                            *(float4 *)(xf + i) = y;
+                        }
+                    }
+                    __syncthreads();                                   // orders the xf writes
+                    return sh_of_max(m);
+                }
+                #pragma unroll
+                for (int k = 0; k < PB4; k++) {
+                    const int i = 4 * (k * T + tid);
+                    if (i < n) {
+                        float4 y;
+                        #pragma unroll
+                        for (int c = 0; c < 4; c++) {
+                            const float v = norm_apply(f4c(xv[k], c), f4c(nw[k], c), s, mode);
+                            f4s(y, c, v);
+                            m = fmaxf(m, fabsf(v));
+                        }
+                        *(float4 *)(xf + i) = y;
+                    }
+                }
+                m = block_max(m, (float *)red_slot(red, 3));
+                return sh_of_max(m);
+            }
             #pragma unroll
             for (int k = 0; k < PB4; k++) {
                 const int i = 4 * (k * T + tid);
