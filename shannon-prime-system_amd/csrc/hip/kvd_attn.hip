@@ -85,6 +85,14 @@ template <int P, typename T> __device__ __forceinline__ T treduce(T v[P], int la
 }
 __device__ __forceinline__ float wmax(float v) { return wave_allmax(v); }
 
+// K/V rows are streamed once per step: nontemporal 16-byte loads (measured
+// ~15% more read bandwidth than cached loads for this streaming pattern).
+template <typename T> __device__ __forceinline__ T ld_stream(const T *p) {
+    typedef typename std::conditional<sizeof(T) == 16, int __attribute__((ext_vector_type(4))),
+                                      int __attribute__((ext_vector_type(2)))>::type V;
+    static_assert(sizeof(T) == sizeof(V), "8- or 16-byte rows");
+    return __builtin_bit_cast(T, __builtin_nontemporal_load((const V *)p));
+}
 __device__ __forceinline__ float *page_of(float *const *pages, int ring, int pos) {
     const int lp = pos / PAGE;
     return pages[ring ? lp % ring : lp];
@@ -184,17 +192,17 @@ __device__ __forceinline__ void load_row(const AttnArgs &a, int h, int p, bool v
     const T *src = row + lane * EPL;
     if constexpr (EPL == 4) {
         typedef T v4 __attribute__((ext_vector_type(4)));
-        const v4 t = *(const v4 *)src; out[0] = t.x; out[1] = t.y; out[2] = t.z; out[3] = t.w;
+        const v4 t = ld_stream((const v4 *)src); out[0] = t.x; out[1] = t.y; out[2] = t.z; out[3] = t.w;
     } else if constexpr (EPL == 2) {
         typedef T v2 __attribute__((ext_vector_type(2)));
-        const v2 t = *(const v2 *)src; out[0] = t.x; out[1] = t.y;
+        const v2 t = ld_stream((const v2 *)src); out[0] = t.x; out[1] = t.y;
     } else {
         #pragma unroll
         for (int e = 0; e < EPL; e++) out[e] = src[e];
     }
 }
 
-constexpr int MAXCH = 256;       // positions per chunk (LDS score buffer)
+constexpr int MAXCH = ATTN_MAXCH;   // positions per chunk (LDS score buffer)
 constexpr int MAXNCH = 4096;     // chunks per kv-head (combine weight buffer)
 constexpr int UNR = 4;           // positions in flight per wave
 
@@ -265,7 +273,7 @@ __global__ __launch_bounds__(256) void k_attn_float(AttnArgs a_in) {
             const float *row = quad_row<EPL, float>(a, h, cs + j0, ce - 1, cs + j, false) + 4 * k4;
             float4 kv[4 * EPL];
             #pragma unroll
-            for (int i = 0; i < 4 * EPL; i++) kv[i] = *(const float4 *)(row + 16 * i);
+            for (int i = 0; i < 4 * EPL; i++) kv[i] = ld_stream((const float4 *)(row + 16 * i));
             #pragma unroll
             for (int i = 0; i < 4 * EPL; i++)
                 #pragma unroll
@@ -388,6 +396,55 @@ __global__ __launch_bounds__(256) void k_attn_float(AttnArgs a_in) {
     if (threadIdx.x == 0) reset_counter(&a.counter[h]);
 }
 
+// The step's head preparation inside the exact score pass (decode): wave g < G
+// normalizes and rotates q head h*G + g into qs; in the workgroup holding pos,
+// wave G % 4 prepares the new K row (paged store + kn) and wave (G + 1) % 4
+// appends the new V row.  prep_load requests the inputs, prep_finish computes
+// and stores.
+template <int EPL> struct PrepIn { HeadIn q, k; float v[EPL]; };
+template <int EPL, int G>
+__device__ __forceinline__ void prep_load(const AttnArgs &a, int h, int pos, int wave, int lane, bool holds_pos, PrepIn<EPL> &in) {
+    static_assert(G <= 4, "one wave per q head of the group");
+    constexpr int HD = EPL * 64;
+    const HeadPrep hp = head_prep_of(a);
+    if (wave < G) head_load<false, EPL>(hp, a.q + (size_t)(h * G + wave) * HD, a.q_norm, lane, in.q);
+    if (holds_pos && wave == G % 4) head_load<false, EPL>(hp, a.k + (size_t)h * HD, a.k_norm, lane, in.k);
+    if (holds_pos && wave == (G + 1) % 4) {
+        #pragma unroll
+        for (int j = 0; j < EPL; j++) in.v[j] = a.v[(size_t)h * HD + lane + 64 * j];
+    }
+}
+template <int EPL, int G>
+__device__ __forceinline__ void prep_finish(const AttnArgs &a, int h, int pos, int wave, int lane, bool holds_pos,
+                                            const PrepIn<EPL> &in, int4 (*qs)[EPL * 16], int4 *kn) {
+    constexpr int HD = EPL * 64;
+    const HeadPrep hp = head_prep_of(a);
+    float out[8];
+    if (wave < G) {
+        head_norm_rope_in<EPL>(hp, in.q, lane, out);
+        #pragma unroll
+        for (int j = 0; j < EPL; j++) ((int *)qs[wave])[lane + 64 * j] = (int)rintf(out[j] * 65536.0f);
+    }
+    if (holds_pos) {
+        float *page = qk_page_of(a.pages, a.ring_pages, pos);
+        const size_t rowoff = ((size_t)h * PAGE + pos % PAGE) * HD;
+        if (wave == G % 4) {
+            head_norm_rope_in<EPL>(hp, in.k, lane, out);
+            #pragma unroll
+            for (int j = 0; j < EPL; j++) {
+                const int32_t ki = kv_code_k(out[j]);
+                ((int32_t *)(page + rowoff))[lane + 64 * j] = ki;
+                ((int *)kn)[lane + 64 * j] = ki;
+            }
+        }
+        if (wave == (G + 1) % 4) {
+            int32_t *dst = (int32_t *)(page + (size_t)a.NKV * PAGE * HD + rowoff);
+            #pragma unroll
+            for (int j = 0; j < EPL; j++) dst[lane + 64 * j] = kv_code_v(in.v[j]);
+        }
+    }
+}
+
 // ---- exact mode: pass 1, integer scores on the softmax grid + chunk max ----
 // PREP (decode): the kernel also does the step's head preparation -- every
 // workgroup normalizes and rotates its G q heads itself (wave g, head h*G+g)
@@ -412,44 +469,23 @@ __global__ __launch_bounds__(256) void k_attn_exact_scores(AttnArgs a_in) {
     const int r = lane >> 2, k4 = lane & 3;
     const int n = ce - cs;
     const bool holds_pos = PREP && c == nch - 1;     // chunk ranges end at pos
-    // the wave's first row group is requested before q is staged
+    // The head preparation's inputs are requested first, then the wave's first
+    // row group: the preparation then runs while the rows stream in.
+    PrepIn<EPL> pin;
+    if constexpr (PREP) prep_load<EPL, G>(a, h, pos, wave, lane, holds_pos, pin);
+    __builtin_amdgcn_sched_barrier(0);
     int4 kv[4 * EPL];
     {
         const int j = wave * 16 + r;
         if (j < n) {
             const int32_t *row = quad_row<EPL, int32_t>(a, h, cs + wave * 16, ce - 1, cs + j, false) + 4 * k4;
             #pragma unroll
-            for (int i = 0; i < 4 * EPL; i++) kv[i] = *(const int4 *)(row + 16 * i);
+            for (int i = 0; i < 4 * EPL; i++) kv[i] = ld_stream((const int4 *)(row + 16 * i));
         }
     }
+    __builtin_amdgcn_sched_barrier(0);
     if constexpr (PREP) {
-        const HeadPrep hp = head_prep_of(a);
-        float out[8];
-        static_assert(G <= 4, "one wave per q head of the group");
-        if (wave < G) {
-            head_norm_rope<false, EPL>(hp, a.q + (size_t)(h * G + wave) * HD, a.q_norm, lane, out);
-            #pragma unroll
-            for (int j = 0; j < EPL; j++) ((int *)qs[wave])[lane + 64 * j] = (int)rintf(out[j] * 65536.0f);
-        }
-        if (holds_pos) {
-            // K by wave G % 4 and V by wave (G + 1) % 4 (spare waves when G == 2)
-            float *page = qk_page_of(a.pages, a.ring_pages, pos);
-            const size_t rowoff = ((size_t)h * PAGE + pos % PAGE) * HD;
-            if (wave == G % 4) {
-                head_norm_rope<false, EPL>(hp, a.k + (size_t)h * HD, a.k_norm, lane, out);
-                #pragma unroll
-                for (int j = 0; j < EPL; j++) {
-                    const int32_t ki = kv_code_k(out[j]);
-                    ((int32_t *)(page + rowoff))[lane + 64 * j] = ki;
-                    ((int *)kn)[lane + 64 * j] = ki;
-                }
-            }
-            if (wave == (G + 1) % 4) {
-                int32_t *dst = (int32_t *)(page + (size_t)a.NKV * PAGE * HD + rowoff);
-                #pragma unroll
-                for (int j = 0; j < EPL; j++) dst[lane + 64 * j] = kv_code_v(a.v[(size_t)h * HD + lane + 64 * j]);
-            }
-        }
+        prep_finish<EPL, G>(a, h, pos, wave, lane, holds_pos, pin, qs, kn);
     } else {
         for (int i = threadIdx.x; i < G * HD / 4; i += 256) {
             const int g = i / (HD / 4), d4 = i % (HD / 4);
@@ -469,7 +505,7 @@ __global__ __launch_bounds__(256) void k_attn_exact_scores(AttnArgs a_in) {
             if (j0 != wave * 16) {
                 const int32_t *row = quad_row<EPL, int32_t>(a, h, cs + j0, ce - 1, cs + j, false) + 4 * k4;
                 #pragma unroll
-                for (int i = 0; i < 4 * EPL; i++) kv[i] = *(const int4 *)(row + 16 * i);
+                for (int i = 0; i < 4 * EPL; i++) kv[i] = ld_stream((const int4 *)(row + 16 * i));
             }
             if (holds_pos && cs + j == pos) {
                 #pragma unroll
@@ -516,7 +552,7 @@ __global__ __launch_bounds__(256) void k_attn_exact_scores(AttnArgs a_in) {
 }
 
 // ---- exact mode: pass 2, exp weights on the island grid, exact V-sum ----
-template <int EPL, int G, bool BATCH>
+template <int EPL, int G, bool BATCH, int UV>
 __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a_in) {
     AttnArgs a = a_in;
     int pos;
@@ -532,11 +568,9 @@ __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a_in) {
     __shared__ int64_t redl[4][G];
     __shared__ int is_last;
     const int n = ce - cs;
-    // the first V rows and this chunk's scores are requested before the
-    // global-max reduction, so their latency overlaps it
-    constexpr int UV = 2 * UNR;                       // V rows per wave in flight
-    int32_t vv[UV][EPL], vn[UV][EPL];
-    load_rows<EPL, int32_t, UV>(a, h, cs, wave * UV, n, true, lane, vv);
+    // This chunk's scores and the chunk maxima are requested first, then the
+    // first UV V rows of each wave: the global-max reduction and the weights
+    // then overlap the rows' latency.
     constexpr int ZPT = G * MAXCH / 256;              // score slots per thread
     int32_t zr[ZPT];
     #pragma unroll
@@ -546,12 +580,20 @@ __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a_in) {
         zr[k] = j < n ? a.zscratch[(size_t)(h * G + g) * a.zstride + (size_t)(cs + j)] : 0;
     }
     const int32_t *pml = (const int32_t *)a.part_ml;
+    int pm0[G];
+    #pragma unroll
+    for (int g = 0; g < G; g++)
+        pm0[g] = (int)threadIdx.x < nch ? pml[((size_t)(h * G + g) * a.max_chunks + threadIdx.x) * 4] : INT32_MIN;
+    __builtin_amdgcn_sched_barrier(0);
+    int32_t vv[UV][EPL];
+    load_rows<EPL, int32_t, UV>(a, h, cs, wave * UV, n, true, lane, vv);
+    __builtin_amdgcn_sched_barrier(0);
     // global max of the attended window over every chunk's maximum
     int M[G];
     #pragma unroll
     for (int g = 0; g < G; g++) {
-        int t = INT32_MIN;
-        for (int k = threadIdx.x; k < nch; k += 256) {
+        int t = pm0[g];
+        for (int k = threadIdx.x + 256; k < nch; k += 256) {
             const int v = pml[((size_t)(h * G + g) * a.max_chunks + k) * 4];
             t = v > t ? v : t;
         }
@@ -572,20 +614,27 @@ __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a_in) {
         if (j < n) ew[g][j] = (int32_t)(exp_fixed((((int64_t)zr[k] - (int64_t)M[g]) * ONE) >> 14) >> 8);
     }
     __syncthreads();
-    int64_t o[G][EPL];
+    // The V-sum of this wave's rows in FP64, exactly: weights are Q22 (<= 2^22)
+    // and |vq| < 2^23, so every product and every partial sum of a wave's rows
+    // (at most MAXCH / 4 = 128 of them) is an integer below 2^53 -- one exact
+    // FMA per term instead of an emulated 64-bit multiply-add.
+    double o[G][EPL];
     #pragma unroll
     for (int g = 0; g < G; g++)
         #pragma unroll
-        for (int e = 0; e < EPL; e++) o[g][e] = 0;
+        for (int e = 0; e < EPL; e++) o[g][e] = 0.0;
+    int32_t vn[UV][EPL];
     for (int j0 = wave * UV; j0 < n; j0 += 4 * UV) {
         load_rows<EPL, int32_t, UV>(a, h, cs, j0 + 4 * UV, n, true, lane, vn);
         #pragma unroll
         for (int u = 0; u < UV; u++) {
             if (j0 + u >= n) break;
             #pragma unroll
-            for (int g = 0; g < G; g++)
+            for (int g = 0; g < G; g++) {
+                const double w = (double)ew[g][j0 + u];
                 #pragma unroll
-                for (int e = 0; e < EPL; e++) o[g][e] += (int64_t)ew[g][j0 + u] * (int64_t)vv[u][e];   // 32x32 -> 64
+                for (int e = 0; e < EPL; e++) o[g][e] = fma(w, (double)vv[u][e], o[g][e]);
+            }
         }
         #pragma unroll
         for (int u = 0; u < UV; u++)
@@ -595,7 +644,7 @@ __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a_in) {
     #pragma unroll
     for (int g = 0; g < G; g++)
         #pragma unroll
-        for (int e = 0; e < EPL; e++) ored[wave][g][lane * EPL + e] = o[g][e];
+        for (int e = 0; e < EPL; e++) ored[wave][g][lane * EPL + e] = (int64_t)o[g][e];
     __syncthreads();
     // exact, order-free accumulation of this chunk into the kv-head's totals;
     // VREP replicas (chunk c adds into replica c % VREP) spread the same-address
@@ -670,7 +719,7 @@ template <int EPL, int G, bool B> static void attn_dispatch_b(const AttnArgs &a,
     else {
         if (!B && prep) hipLaunchKernelGGL((k_attn_exact_scores<EPL, G, B, !B>), grid, dim3(256), 0, s, a);
         else hipLaunchKernelGGL((k_attn_exact_scores<EPL, G, B, false>), grid, dim3(256), 0, s, a);
-        hipLaunchKernelGGL((k_attn_exact_vsum<EPL, G, B>), grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL((k_attn_exact_vsum<EPL, G, B, 2 * UNR>), grid, dim3(256), 0, s, a);
     }
 }
 template <int EPL, int G> static void attn_dispatch(const AttnArgs &a, int grid_chunks, bool prep, hipStream_t s) {
@@ -692,6 +741,31 @@ static void attention_go(const AttnArgs &a, int grid_chunks, bool prep, hipStrea
     else if (a.HD == 64 && G == 4) attn_dispatch<1, 4>(a, grid_chunks, prep, s);
 }
 void launch_attention(const AttnArgs &a, int grid_chunks, hipStream_t s) { attention_go(a, grid_chunks, false, s); }
+
+// Workgroups of the exact decode attention (score pass and V-sum) the device
+// holds at once, the smaller of the two (0: no such instance).  The host sizes
+// global-layer chunks so that a launch is one round of them where it can.
+template <int EPL, int G> static int attn_cap_t() {
+    int a = 0, b = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&a, k_attn_exact_scores<EPL, G, false, true>, 256, 0) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, k_attn_exact_vsum<EPL, G, false, 2 * UNR>, 256, 0) != hipSuccess)
+        return 0;
+    return a < b ? a : b;
+}
+int attn_capacity(int HD, int G) {
+    int nb = 0, dev = 0, ncu = 0;
+    if (HD == 256 && G == 2) nb = attn_cap_t<4, 2>();
+    else if (HD == 128 && G == 2) nb = attn_cap_t<2, 2>();
+    else if (HD == 128 && G == 4) nb = attn_cap_t<2, 4>();
+    else if (HD == 64 && G == 2) nb = attn_cap_t<1, 2>();
+    else if (HD == 256 && G == 4) nb = attn_cap_t<4, 4>();
+    else if (HD == 64 && G == 4) nb = attn_cap_t<1, 4>();
+    if (nb <= 0 || hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return 0;
+    return nb * ncu;
+}
+
 
 // The step's head preparation and attention: exact-mode decode runs the
 // preparation inside the score pass; float mode and batched tokens launch

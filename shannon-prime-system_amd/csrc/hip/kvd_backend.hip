@@ -352,6 +352,7 @@ struct sp_kvdecode_handle {
     int acc_rows = 0;
     float *h_logits = nullptr;               // pinned staging
     int max_chunks = 0;
+    int attn_cap = 0;                        // exact decode attention workgroups resident at once
     void *scratch = nullptr;
     int built = 0;                           // tables and scratch allocated (reusable as a shell)
     // batched prefill buffers ([TB][...] per token), allocated on first use
@@ -455,6 +456,7 @@ int alloc_scratch(sp_kvdecode_handle *h) {
     const DevModel *m = h->m;
     const int QD = m->NH * m->HD, KVD = m->NKV * m->HD;
     h->max_chunks = (h->pmax + 15) / 16 + 2;
+    h->attn_cap = attn_capacity(m->HD, m->NH / m->NKV);
     struct Item { void **p; size_t n; };
     const size_t part_bytes = (size_t)m->NH * h->max_chunks * m->HD * 8;
     const size_t ml_bytes = (size_t)m->NH * h->max_chunks * 16;
@@ -539,10 +541,17 @@ struct StepShape { int logits, argmax, grid_global, grid_local, chunk_global, ch
 
 int attn_chunks(const sp_kvdecode_handle *h, int pos_hi, StepShape &sh) {
     const DevModel *m = h->m;
-    // global layers: the largest chunk (<= 256 positions) that still gives about
-    // 1024 workgroups (four per CU); fewer chunks mean fewer partials to merge
-    int cg = 256;
-    while (cg > 16 && (long long)((pos_hi + 1) / cg + 1) * m->NKV < 1024) cg /= 2;
+    // global layers: the smallest chunk (a multiple of 16, at most ATTN_MAXCH)
+    // whose workgroups fit the device in R rounds, R as small as possible: a
+    // launch a few workgroups over one round would run a second, nearly empty
+    // round at the length of the first
+    const int per_head = std::max(1, (h->attn_cap > 0 ? h->attn_cap : 1024) / m->NKV);
+    int cg = 16;
+    for (int R = 1;; R++) {
+        cg = 16;
+        while (cg < ATTN_MAXCH && pos_hi / cg + 1 > R * per_head) cg += 16;
+        if (pos_hi / cg + 1 <= R * per_head) break;
+    }
     while ((pos_hi / cg + 1) > 4096) cg *= 2;
     sh.chunk_global = cg;
     sh.grid_global = pos_hi / cg + 1;

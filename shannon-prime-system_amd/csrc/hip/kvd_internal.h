@@ -178,6 +178,8 @@ void launch_qk_prep(const AttnArgs &a, hipStream_t s);
 void launch_rope_table(const DState *st, int HD, int mode, float base_g, float base_l,
                        const int64_t *fq_g, const int64_t *fq_l, float *out, hipStream_t s);
 void launch_attention(const AttnArgs &a, int grid_chunks, hipStream_t s);
+int  attn_capacity(int HD, int G);
+constexpr int ATTN_MAXCH = 512;         // largest chunk of the two-kernel attention
 void launch_prep_attention(const AttnArgs &a, int grid_chunks, hipStream_t s);   // qk_prep + attention, fused where possible
 bool attention_fuses_prep(const AttnArgs &a);
 void set_rope_tables(const int64_t atan_q60[64], int64_t kinv_q62);

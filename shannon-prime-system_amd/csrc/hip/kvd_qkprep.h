@@ -32,17 +32,39 @@ __device__ __forceinline__ float *qk_page_of(float *const *pages, int ring, int 
     return pages[ring ? lp % ring : lp];
 }
 
-// One q or k head's per-head RMSNorm and NEOX RoPE: src holds the head's HD
-// projections, nw its norm weight; lane l gets elements l + 64 j in out[j].
-// COHERENT selects agent-scope loads, for projections written by other
-// workgroups of the same launch.
+// The global inputs of one head's preparation, loaded by head_load so that a
+// caller can request them before a bulk (K/V) request: vector loads complete
+// in order, so inputs requested after the bulk would wait for all of it.
+struct HeadIn { float v[8], w[8], c[4], s[4]; };
 template <bool COHERENT, int PER>
-__device__ __forceinline__ void head_norm_rope(const HeadPrep &a, const float *src, const float *nw, int lane, float out[8]) {
+__device__ __forceinline__ void head_load(const HeadPrep &a, const float *src, const float *nw, int lane, HeadIn &in) {
     constexpr int HD = PER * 64, half = HD / 2, per = PER;
-    float v[8];                                                 // HD <= 512
     #pragma unroll
     for (int j = 0; j < 8; j++)
-        if (j < per) v[j] = COHERENT ? ld_agent(&src[lane + 64 * j]) : src[lane + 64 * j];
+        if (j < per) {
+            in.v[j] = COHERENT ? ld_agent(&src[lane + 64 * j]) : src[lane + 64 * j];
+            in.w[j] = nw[lane + 64 * j];
+        }
+    if (per >= 2) {
+        #pragma unroll
+        for (int j = 0; j < 4; j++) {
+            if (j >= per / 2) break;
+            in.c[j] = a.rope_cs[lane + 64 * j]; in.s[j] = a.rope_cs[half + lane + 64 * j];
+        }
+    } else {
+        const int i = lane < 32 ? lane : lane - 32;
+        in.c[0] = a.rope_cs[i]; in.s[0] = a.rope_cs[half + i];
+    }
+}
+
+// One q or k head's per-head RMSNorm and NEOX RoPE from what head_load read:
+// lane l gets elements l + 64 j in out[j].
+template <int PER>
+__device__ __forceinline__ void head_norm_rope_in(const HeadPrep &a, const HeadIn &in, int lane, float out[8]) {
+    constexpr int HD = PER * 64, per = PER;
+    float v[8];                                                 // HD <= 512
+    #pragma unroll
+    for (int j = 0; j < 8; j++) if (j < per) v[j] = in.v[j];
     // per-head RMSNorm
     if (a.mode == FLOAT) {
         double ss = 0.0;
@@ -51,7 +73,7 @@ __device__ __forceinline__ void head_norm_rope(const HeadPrep &a, const float *s
         ss = wave_allsum(ss);
         const float sc = 1.0f / sqrtf((float)(ss / HD) + a.eps);
         #pragma unroll
-        for (int j = 0; j < 8; j++) if (j < per) v[j] = v[j] * sc * nw[lane + 64 * j];
+        for (int j = 0; j < 8; j++) if (j < per) v[j] = v[j] * sc * in.w[j];
     } else {
         int64_t ss = 0;
         #pragma unroll
@@ -65,7 +87,7 @@ __device__ __forceinline__ void head_norm_rope(const HeadPrep &a, const float *s
             #pragma unroll
             for (int j = 0; j < 8; j++) {
                 if (j >= per) break;
-                const int64_t xi = llround_pow2<16>(v[j]), wi = llround_pow2<16>(nw[lane + 64 * j]);
+                const int64_t xi = llround_pow2<16>(v[j]), wi = llround_pow2<16>(in.w[j]);
                 v[j] = (float)((double)mul3_lo64(xi, inv, wi) / 4503599627370496.0);
             }
         }
@@ -73,13 +95,11 @@ __device__ __forceinline__ void head_norm_rope(const HeadPrep &a, const float *s
     // NEOX RoPE on pairs (i, i + half), cos/sin from this position's table.
     // HD >= 128: both halves of a pair sit in the same lane (j and j + per/2);
     // HD == 64: the partner is lane ^ 32.
-    const float *cs = a.rope_cs;
     if (per >= 2) {
         #pragma unroll
         for (int j = 0; j < 4; j++) {
             if (j >= per / 2) break;
-            const int i = lane + 64 * j;
-            const float x0 = v[j], x1 = v[j + per / 2], c = cs[i], s = cs[half + i];
+            const float x0 = v[j], x1 = v[j + per / 2], c = in.c[j], s = in.s[j];
             const float ac = x0 * c, bs = x1 * s, as = x0 * s, bc = x1 * c;
             out[j] = ac - bs;
             out[j + per / 2] = as + bc;
@@ -87,11 +107,21 @@ __device__ __forceinline__ void head_norm_rope(const HeadPrep &a, const float *s
     } else {
         const float other = __shfl_xor(v[0], 32, 64);
         const bool first = lane < 32;
-        const int i = first ? lane : lane - 32;
-        const float x0 = first ? v[0] : other, x1 = first ? other : v[0], c = cs[i], s = cs[half + i];
+        const float x0 = first ? v[0] : other, x1 = first ? other : v[0], c = in.c[0], s = in.s[0];
         const float ac = x0 * c, bs = x1 * s, as = x0 * s, bc = x1 * c;
         out[0] = first ? ac - bs : as + bc;
     }
+}
+
+// One q or k head's per-head RMSNorm and NEOX RoPE: src holds the head's HD
+// projections, nw its norm weight; lane l gets elements l + 64 j in out[j].
+// COHERENT selects agent-scope loads, for projections written by other
+// workgroups of the same launch.
+template <bool COHERENT, int PER>
+__device__ __forceinline__ void head_norm_rope(const HeadPrep &a, const float *src, const float *nw, int lane, float out[8]) {
+    HeadIn in;
+    head_load<COHERENT, PER>(a, src, nw, lane, in);
+    head_norm_rope_in<PER>(a, in, lane, out);
 }
 
 // The stored form of a K or V element: the float itself, or in exact mode
