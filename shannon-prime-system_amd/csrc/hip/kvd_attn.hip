@@ -675,18 +675,16 @@ __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a_in) {
     if (threadIdx.x == 0) is_last = (arrive(&a.counter[h]) == nch - 1);
     __syncthreads();
     if (!is_last) return;
-    // the totals are read and cleared for the next launch in one atomic step
+    // the totals are read and cleared for the next launch in one atomic step;
+    // every exchange (denominators and V-sums) is issued before any total is
+    // used: one round trip
     __shared__ int64_t Sg[G];
-    if (threadIdx.x < G) {
-        int64_t S = 0;
+    int64_t S = 0;
+    if (threadIdx.x < G)
+        #pragma unroll
         for (int r = 0; r < VREP; r++)
             S += (int64_t)__hip_atomic_exchange((unsigned long long *)&a.vacc_s[(size_t)r * a.NH + h * G + threadIdx.x], 0ull,
                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        Sg[threadIdx.x] = S;
-    }
-    __syncthreads();
-    StatAcc sacc;
-    // every exchange is issued before any total is used: one round trip
     constexpr int PT = (G * EPL * 64 + 255) / 256;   // elements per thread
     int64_t tot[PT];
     #pragma unroll
@@ -699,6 +697,9 @@ __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a_in) {
                 tot[k] += (int64_t)__hip_atomic_exchange((unsigned long long *)&a.vacc[(size_t)r * QDh + (size_t)h * G * HD + i], 0ull,
                                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    if (threadIdx.x < G) Sg[threadIdx.x] = S;
+    __syncthreads();
+    StatAcc sacc;
     #pragma unroll
     for (int k = 0; k < PT; k++) {
         const int i = threadIdx.x + 256 * k;

@@ -180,6 +180,17 @@ __device__ __forceinline__ int bitlen128(u128 v) {
 }
 __device__ __forceinline__ float rne_div_to_float(i128 num, int64_t den, int k) {
     if (!num) return 0.0f;
+    // Fast path: with both operands below 2^53 the double quotient is the
+    // correctly rounded exact one, and scaling by 2^-k is exact; it rounds to
+    // the float the exact quotient rounds to unless it lies exactly on a float
+    // rounding midpoint (low 29 mantissa bits 1000...0) -- then, and for
+    // results outside the normal float range, the exact path below decides.
+    if (num > -((i128)1 << 53) && num < ((i128)1 << 53) && den < ((int64_t)1 << 53) && k >= 0 && k < 64) {
+        const double q = ldexp((double)(int64_t)num / (double)den, -k);
+        const uint64_t b = (uint64_t)__double_as_longlong(q);
+        const int ex = (int)((b >> 52) & 0x7FF) - 1023;
+        if (ex >= -126 && ex < 128 && (b & 0x1FFFFFFFull) != 0x10000000ull) return (float)q;
+    }
     bool neg = num < 0;
     u128 n = neg ? (u128)(-num) : (u128)num, d = (u128)(uint64_t)den;
     int sh = 28 + bitlen128(d) - bitlen128(n);
