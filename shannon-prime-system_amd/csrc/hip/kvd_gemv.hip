@@ -394,9 +394,9 @@ GemvPlan gemv_plan(int nrows_total, int cols, int paired, int wide) {
 }
 
 template <int PRO, bool PAIRED>
-static void launch_pro(const GemvArgs &a, bool wide, int grid, size_t lds, hipStream_t s) {
-    if (wide) hipLaunchKernelGGL((k_gemv<PRO, PAIRED, true>), dim3(grid), dim3(GEMV_WAVES * 64), lds, s, a);
-    else      hipLaunchKernelGGL((k_gemv<PRO, PAIRED, false>), dim3(grid), dim3(GEMV_WAVES * 64), lds, s, a);
+static void launch_pro(const GemvArgs &a, bool wide, int grid, int waves, size_t lds, hipStream_t s) {
+    if (wide) hipLaunchKernelGGL((k_gemv<PRO, PAIRED, true>), dim3(grid), dim3(waves * 64), lds, s, a);
+    else      hipLaunchKernelGGL((k_gemv<PRO, PAIRED, false>), dim3(grid), dim3(waves * 64), lds, s, a);
 }
 
 void launch_gemv(const GemvArgs &a_in, int nrows_total, hipStream_t s) {
@@ -407,7 +407,12 @@ void launch_gemv(const GemvArgs &a_in, int nrows_total, hipStream_t s) {
     bool wide = false;
     for (int i = 0; i < a.nseg; i++) wide |= a.seg[i].w.wide != 0;
     const bool paired = a.act != ACT_NONE;
-    const GemvPlan p = gemv_plan(nrows_total, a.cols, paired, wide);
+    GemvPlan p = gemv_plan(nrows_total, a.cols, paired, wide);
+    // A plan that leaves over half of the CUs without a workgroup runs the
+    // same waves in half-size workgroups on twice as many CUs (plain inputs
+    // only: the norm prologues keep the whole vector in registers of 8 waves)
+    int waves = GEMV_WAVES;
+    if (a.pro.kind == PRO_PLAIN && p.grid * 2 <= num_cu()) { p.grid *= 2; waves = GEMV_WAVES / 2; }
     if (p.nsplit > 1 && (!a.accbuf || !a.gcnt || nrows_total * (paired ? 2 : 1) > a.acc_rows || p.groups > a.acc_rows)) {
         fprintf(stderr, "kvd: GEMV split accumulators missing or too small\n"); abort();
     }
@@ -416,12 +421,12 @@ void launch_gemv(const GemvArgs &a_in, int nrows_total, hipStream_t s) {
     const size_t lds = (size_t)NDIG * nb * sizeof(uint4) +
                        (a.pro.kind == PRO_PLAIN ? 0 : (size_t)a.pro.n * sizeof(float));
     switch (a.pro.kind * 2 + (paired ? 1 : 0)) {
-    case PRO_PLAIN * 2:     launch_pro<PRO_PLAIN, false>(a, wide, p.grid, lds, s); break;
-    case PRO_PLAIN * 2 + 1: launch_pro<PRO_PLAIN, true>(a, wide, p.grid, lds, s); break;
-    case PRO_NORM * 2:      launch_pro<PRO_NORM, false>(a, wide, p.grid, lds, s); break;
-    case PRO_NORM * 2 + 1:  launch_pro<PRO_NORM, true>(a, wide, p.grid, lds, s); break;
-    case PRO_RESID * 2:     launch_pro<PRO_RESID, false>(a, wide, p.grid, lds, s); break;
-    default:                launch_pro<PRO_RESID, true>(a, wide, p.grid, lds, s); break;
+    case PRO_PLAIN * 2:     launch_pro<PRO_PLAIN, false>(a, wide, p.grid, waves, lds, s); break;
+    case PRO_PLAIN * 2 + 1: launch_pro<PRO_PLAIN, true>(a, wide, p.grid, waves, lds, s); break;
+    case PRO_NORM * 2:      launch_pro<PRO_NORM, false>(a, wide, p.grid, waves, lds, s); break;
+    case PRO_NORM * 2 + 1:  launch_pro<PRO_NORM, true>(a, wide, p.grid, waves, lds, s); break;
+    case PRO_RESID * 2:     launch_pro<PRO_RESID, false>(a, wide, p.grid, waves, lds, s); break;
+    default:                launch_pro<PRO_RESID, true>(a, wide, p.grid, waves, lds, s); break;
     }
 }
 
