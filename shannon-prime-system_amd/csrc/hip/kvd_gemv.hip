@@ -93,18 +93,28 @@ __device__ int gemv_prologue(const ProArgs &p, int mode, const GemvLoads &L, flo
 
 // ------------------------------------------------------- main kernel
 __device__ __forceinline__ int32_t dot_digits(const uint4 c, const uint4 *D) {
-    // sum over the 32 codes of code * xq, xq = sum_k 16^k digit_k
+    // sum over the 32 codes of code * xq, xq = sum_k 16^k digit_k, Horner form
+    // folded into the dot accumulator: a = 16 a + dots of plane k (|a| < 2^30
+    // at the end; 32-bit wrap-around in between cancels exactly)
     int32_t a = 0;
     #pragma unroll
     for (int k = NDIG - 1; k >= 0; k--) {
-        int32_t t = 0;
-        t = __builtin_amdgcn_sdot8((int)c.x, (int)D[k].x, t, false);
-        t = __builtin_amdgcn_sdot8((int)c.y, (int)D[k].y, t, false);
-        t = __builtin_amdgcn_sdot8((int)c.z, (int)D[k].z, t, false);
-        t = __builtin_amdgcn_sdot8((int)c.w, (int)D[k].w, t, false);
-        a = a * 16 + t;
+        a = (int32_t)((uint32_t)a << 4);
+        a = __builtin_amdgcn_sdot8((int)c.x, (int)D[k].x, a, false);
+        a = __builtin_amdgcn_sdot8((int)c.y, (int)D[k].y, a, false);
+        a = __builtin_amdgcn_sdot8((int)c.z, (int)D[k].z, a, false);
+        a = __builtin_amdgcn_sdot8((int)c.w, (int)D[k].w, a, false);
     }
     return a;
+}
+
+// The exact block multiplier Ms = M * 2^(e - ebase) of an f16 scale M * 2^e
+// relative to its row's smallest block exponent: an integer below 2^31 for
+// every row that is not WIDE (the host sets WIDE when a row's exponent spread
+// could exceed 21 - ceil(log2 nblk); one block has no spread).  The f16 -> f32
+// conversion, the scaling by 2^-ebase and the conversion to int32 are exact.
+__device__ __forceinline__ int32_t block_mult(uint32_t h, int ebase) {
+    return (int32_t)ldexpf((float)__builtin_bit_cast(_Float16, (unsigned short)h), -ebase);
 }
 
 // Sum GEMV_R = 8 per-lane int64 partials over the wave with 10 exchanges
@@ -259,12 +269,13 @@ __global__ __launch_bounds__(512, 4) void k_gemv(GemvArgs a) {   // 4 waves per 
                 #pragma unroll
                 for (int r = 0; r < GEMV_R; r++) {
                     const int32_t d = dot_digits(c[r], D);
-                    int32_t M; int e; f16_parts(h[r], M, e);
-                    const int64_t p = (int64_t)d * (int64_t)M;
-                    if constexpr (WIDE) acc[r] += (i128)((u128)(i128)p << (e + 24));
-                    else {
-                        const int s = e - eb_of(ebw, r);       // unpacked at use: fewer live registers
-                        acc[r] += (int64_t)((uint64_t)p << (s > 0 ? s : 0));
+                    if constexpr (WIDE) {
+                        int32_t M; int e; f16_parts(h[r], M, e);
+                        const int64_t p = (int64_t)d * (int64_t)M;
+                        acc[r] += (i128)((u128)(i128)p << (e + 24));
+                    } else {
+                        // (d * M) << (e - ebase) == d * Ms: one 32 x 32 + 64 multiply-add
+                        acc[r] += (int64_t)d * (int64_t)block_mult(h[r], eb_of(ebw, r));
                     }
                 }
             }
