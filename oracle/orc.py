@@ -8,6 +8,7 @@ import os
 HERE = os.path.dirname(os.path.abspath(__file__))
 c_void_p, c_int, c_float, c_double = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_double
 FLOAT, EXACT = 0, 1
+KV_SPINOR, KV_SPINOR_REF = 1, 2          # sp_session_config.flags bits (sp_l1.h:156-157)
 _orc = None
 _ref = None
 
@@ -44,6 +45,13 @@ def lib():
             ("orc_rope_exact", None, [c_void_p, c_int, c_int, c_float]),
             ("orc_q4b_gemv_exact", c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p]),
             ("orc_rope_freq_q60", ctypes.c_int64, [c_float, c_int, c_int]),
+            ("orc_sess_new_kv", c_void_p, [c_void_p, c_int, c_int, ctypes.c_uint32]),
+            ("orc_crc8", ctypes.c_uint8, [c_void_p, c_int]),
+            ("orc_spinor_blocks_for", c_int, [c_int]),
+            ("orc_spinor_encode", None, [c_void_p, c_int, c_void_p]),
+            ("orc_spinor_decode", c_int, [c_void_p, c_void_p, c_int]),
+            ("orc_spinor_encode_vec", None, [c_void_p, c_int, c_void_p]),
+            ("orc_spinor_decode_vec", c_int, [c_void_p, c_int, c_void_p]),
         ]:
             f = getattr(L, name); f.restype = res; f.argtypes = args
         _orc = L
@@ -61,6 +69,14 @@ def ref_lib():
         L.refh_decode.restype = c_int
         L.refh_decode.argtypes = [ctypes.c_char_p, ctypes.c_char_p, c_void_p, c_int, c_int, c_void_p,
                                   c_void_p, c_void_p, c_void_p]
+        L.refh_decode_flags.restype = c_int
+        L.refh_decode_flags.argtypes = L.refh_decode.argtypes + [ctypes.c_uint32]
+        for name in ("sp_spinor_encode_vec", "sp_spinor_decode_vec"):
+            f = getattr(L, name)
+            f.restype = None if name.endswith("encode_vec") else c_int
+            f.argtypes = [c_void_p, c_int, c_void_p]
+        L.sp_crc8.restype = ctypes.c_uint8
+        L.sp_crc8.argtypes = [c_void_p, c_int]
         L.refh_qwen3_fixture_sha.restype = c_int
         L.refh_qwen3_fixture_sha.argtypes = [c_void_p, c_void_p]
         for name in ("sp_rmsnorm_exact", "sp_gelu_exact"):
@@ -74,7 +90,7 @@ def ref_lib():
 class Oracle:
     """One oracle session over a .sp-model file."""
 
-    def __init__(self, spm, max_ctx, mode=FLOAT):
+    def __init__(self, spm, max_ctx, mode=FLOAT, kv_flags=0):
         import numpy as np
         L = lib()
         self.m = L.orc_model_load(spm.encode())
@@ -83,7 +99,7 @@ class Oracle:
         d = np.zeros(9, np.uint32)
         L.orc_model_dims(self.m, ptr(d))
         self.arch, self.V, self.E, self.NL, self.NH, self.NKV, self.HD, self.FF, self.SW = [int(x) for x in d]
-        self.s = L.orc_sess_new(self.m, max_ctx, mode)
+        self.s = L.orc_sess_new_kv(self.m, max_ctx, mode, kv_flags)
         if not self.s:
             raise RuntimeError("oracle session allocation failed")
 

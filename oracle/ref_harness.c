@@ -18,15 +18,25 @@ static int argmax_lowest(const float *v, int n) {
 /* prefill `prompt`, then n_gen decode steps; step k feeds forced[k] when forced
  * is non-NULL, else the greedy argmax of the previous logits.  Writes the
  * prefill logits (V), every decode step's logits (n_gen x V) and the fed tokens. */
+int refh_decode_flags(const char *spm, const char *spt, const int32_t *prompt, int n_prompt,
+                      int n_gen, const int32_t *forced, float *prefill_logits, float *logits,
+                      int32_t *fed, uint32_t flags);
 int refh_decode(const char *spm, const char *spt, const int32_t *prompt, int n_prompt,
                 int n_gen, const int32_t *forced, float *prefill_logits, float *logits,
                 int32_t *fed) {
+    return refh_decode_flags(spm, spt, prompt, n_prompt, n_gen, forced, prefill_logits, logits, fed, 0u);
+}
+/* the same with sp_session_config.flags (SP_KV_SPINOR / SP_KV_SPINOR_REF) */
+int refh_decode_flags(const char *spm, const char *spt, const int32_t *prompt, int n_prompt,
+                      int n_gen, const int32_t *forced, float *prefill_logits, float *logits,
+                      int32_t *fed, uint32_t flags) {
     sp_model *m = NULL;
     if (sp_model_load(spm, spt, &m) != SP_OK) return -1;
     sp_arch_info ai; sp_model_arch(m, &ai);
     const int V = (int)ai.vocab_size;
     sp_session_config cfg; memset(&cfg, 0, sizeof cfg);
     cfg.deterministic = 1; cfg.max_context = (size_t)(n_prompt + n_gen + 1);
+    cfg.flags = flags;
     sp_session *s = NULL;
     int rc = -2;
     if (sp_session_create(m, &cfg, NULL, &s) != SP_OK) goto out;

@@ -536,19 +536,96 @@ void orc_rope_exact(float *v, int d, int p, float base) {
     }
 }
 
+
+/* ======================= Spinor-63 KV block codec =======================
+ * Restates core/vht2/vht2.c:31-104 (CRC-8, VHT2 canonical projection and int8
+ * quantization), core/vht2/mobius_reorder.c:16-55 (the affine permutation,
+ * A = 17 mod 55) and core/vht2/spinor_block.c:59-149 (63-byte assembly and the
+ * balanced multi-block split).  Byte image: [0..3] scale float32 LE, [4] exponent
+ * (0), [5] basis (0 = canonical), [6] reserved (0), [7..61] body with
+ * body[17 i mod 55] = coeff[i], [62] CRC-8 of bytes 0..61. */
+#define SPN_BODY 55
+#define SPN_MOBIUS_A 17
+
+uint8_t orc_crc8(const uint8_t *d, int n) {
+    /* CRC-8/SMBus: polynomial x^8 + x^2 + x + 1 (0x07), MSB first, init 0 */
+    unsigned r = 0;
+    for (int i = 0; i < n; i++) {
+        r ^= d[i];
+        for (int b = 0; b < 8; b++) r = (r & 0x80u) ? ((r << 1) ^ 0x07u) & 0xFFu : (r << 1) & 0xFFu;
+    }
+    return (uint8_t)r;
+}
+int orc_spinor_blocks_for(int k) { return k <= SPN_BODY ? 1 : (k + SPN_BODY - 1) / SPN_BODY; }
+
+/* round half away from zero as the reference writes it (x + 0.5 rounded in float first) */
+static int32_t spn_round(float x) { return (int32_t)(x >= 0.0f ? floorf(x + 0.5f) : ceilf(x - 0.5f)); }
+
+void orc_spinor_encode(const float *vec, int k, uint8_t blk[63]) {
+    const int lim = k < 0 ? 0 : (k < SPN_BODY ? k : SPN_BODY);
+    float mx = 0.0f;
+    for (int i = 0; i < lim; i++) if (fabsf(vec[i]) > mx) mx = fabsf(vec[i]);
+    const float scale = mx > 0.0f ? mx : 1.0f;
+    memset(blk, 0, 63);
+    uint32_t sb; memcpy(&sb, &scale, 4);
+    for (int j = 0; j < 4; j++) blk[j] = (uint8_t)(sb >> (8 * j));
+    for (int i = 0; i < lim; i++) {
+        int32_t c = spn_round((vec[i] / scale) * 127.0f);
+        c = c > 127 ? 127 : (c < -127 ? -127 : c);
+        blk[7 + (SPN_MOBIUS_A * i) % SPN_BODY] = (uint8_t)(int8_t)c;
+    }
+    blk[62] = orc_crc8(blk, 62);
+}
+int orc_spinor_decode(const uint8_t blk[63], float *vec, int k) {
+    if (orc_crc8(blk, 62) != blk[62]) return 1;
+    const uint32_t sb = (uint32_t)blk[0] | (uint32_t)blk[1] << 8 | (uint32_t)blk[2] << 16 | (uint32_t)blk[3] << 24;
+    float scale; memcpy(&scale, &sb, 4);
+    const float mul = scale * ldexpf(1.0f, (int)(int8_t)blk[4]) / 127.0f;
+    const int lim = k < 0 ? 0 : (k < SPN_BODY ? k : SPN_BODY);
+    for (int i = 0; i < lim; i++) vec[i] = (float)(int8_t)blk[7 + (SPN_MOBIUS_A * i) % SPN_BODY] * mul;
+    for (int i = SPN_BODY; i < k; i++) vec[i] = 0.0f;
+    return 0;
+}
+/* k coordinates in nblk contiguous chunks of k/nblk, the first k % nblk one longer */
+void orc_spinor_encode_vec(const float *vec, int k, uint8_t *blocks) {
+    const int nb = orc_spinor_blocks_for(k), base = k / nb, extra = k % nb;
+    for (int b = 0, off = 0; b < nb; b++) {
+        const int len = base + (b < extra);
+        orc_spinor_encode(vec + off, len, blocks + 63 * b);
+        off += len;
+    }
+}
+int orc_spinor_decode_vec(const uint8_t *blocks, int k, float *vec) {
+    const int nb = orc_spinor_blocks_for(k), base = k / nb, extra = k % nb;
+    int rc = 0;
+    for (int b = 0, off = 0; b < nb; b++) {
+        const int len = base + (b < extra);
+        rc |= orc_spinor_decode(blocks + 63 * b, vec + off, len);
+        off += len;
+    }
+    return rc;
+}
+static void spinor_roundtrip(float *v, int k) {
+    uint8_t blk[63 * 16];                 /* k <= 880 */
+    orc_spinor_encode_vec(v, k, blk);
+    (void)orc_spinor_decode_vec(blk, k, v);
+}
+
 /* ======================= session + steps ======================= */
 struct orc_sess {
     orc_model *m;
     int mode, P, pos, kv_filled;
+    uint32_t kv_flags;                /* ORC_KV_SPINOR / ORC_KV_SPINOR_REF: K/V pass the Spinor codec */
     float *kc, *vc;                   /* [NL][P][KVD]; int32 payload in exact mode */
     float *x, *nx, *q, *kn, *vn, *ao, *ap, *gg, *up, *dn, *sc;
     double *pd;
 };
 
-orc_sess *orc_sess_new(orc_model *m, int max_ctx, int mode) {
+orc_sess *orc_sess_new(orc_model *m, int max_ctx, int mode) { return orc_sess_new_kv(m, max_ctx, mode, 0u); }
+orc_sess *orc_sess_new_kv(orc_model *m, int max_ctx, int mode, uint32_t kv_flags) {
     if (!m || max_ctx <= 0) return NULL;
     orc_sess *s = (orc_sess *)calloc(1, sizeof *s);
-    s->m = m; s->mode = mode; s->P = max_ctx;
+    s->m = m; s->mode = mode; s->P = max_ctx; s->kv_flags = kv_flags;
     const size_t KVD = (size_t)m->NKV * m->HD, QD = (size_t)m->NH * m->HD;
     const size_t kv = (size_t)m->NL * (size_t)max_ctx * KVD;
     s->kc = (float *)malloc(kv * sizeof(float)); s->vc = (float *)malloc(kv * sizeof(float));
@@ -579,7 +656,7 @@ int orc_rewind(orc_sess *s, int n) {
     return 0;
 }
 orc_sess *orc_clone(const orc_sess *s) {
-    orc_sess *c = orc_sess_new(s->m, s->P, s->mode);
+    orc_sess *c = orc_sess_new_kv(s->m, s->P, s->mode, s->kv_flags);
     if (!c) return NULL;
     const size_t kv = (size_t)s->m->NL * (size_t)s->P * s->m->NKV * s->m->HD;
     memcpy(c->kc, s->kc, kv * sizeof(float)); memcpy(c->vc, s->vc, kv * sizeof(float));
@@ -670,6 +747,10 @@ static int step_any(orc_sess *s, int32_t tok, int pos, float *logits) {
             if (ex) { orc_rmsnorm_exact(kh, ly->k_norm, HD, kh); orc_rope_exact(kh, HD, pos, rbase); }
             else { rmsnorm_head(kh, ly->k_norm, HD, eps); orc_rope_neox(kh, HD, pos, rbase); }
         }
+        if (s->kv_flags & (ORC_KV_SPINOR | ORC_KV_SPINOR_REF))
+            /* sp_session.c:298-320: the block cache (mode 1) and the in-place
+             * round trip (mode 2) hand the attention the same decoded values */
+            for (int h = 0; h < 2 * NKV; h++) spinor_roundtrip((h < NKV ? kn : vn) + (size_t)(h % NKV) * HD, HD);
         float *kcl = s->kc + (size_t)L * P * KVD, *vcl = s->vc + (size_t)L * P * KVD;
         if (ex) {
             int32_t *kd = (int32_t *)(kcl + (size_t)pos * KVD), *vd = (int32_t *)(vcl + (size_t)pos * KVD);

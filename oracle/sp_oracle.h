@@ -31,6 +31,10 @@ void       orc_model_free(orc_model *m);
 void       orc_model_dims(const orc_model *m, uint32_t out[9]);
 
 orc_sess *orc_sess_new(orc_model *m, int max_ctx, int mode);
+/* kv_flags as sp_session_config.flags (include/sp/sp_l1.h:156-157): either bit
+ * passes every stored K/V head through the Spinor-63 codec */
+enum { ORC_KV_SPINOR = 1u << 0, ORC_KV_SPINOR_REF = 1u << 1 };
+orc_sess *orc_sess_new_kv(orc_model *m, int max_ctx, int mode, uint32_t kv_flags);
 void      orc_sess_free(orc_sess *s);
 /* one token at the session position (kv_step semantics); logits may be NULL */
 int       orc_step(orc_sess *s, int32_t tok, float *logits);
@@ -50,6 +54,13 @@ void  orc_attn_head(const float *qh, const float *KC, const float *VC, int pos, 
                     int kvh, int HD, float ascale, int win, float *sc, float *out);
 int   orc_q4b_gemv(const uint8_t *codes, const uint16_t *bscale, int rows, int cols,
                    const float *x, float *y);
+/* ---- Spinor-63 KV block codec (core/vht2/, include/sp/spinor_block.h) ---- */
+uint8_t orc_crc8(const uint8_t *d, int n);
+int   orc_spinor_blocks_for(int k);
+void  orc_spinor_encode(const float *vec, int k, uint8_t blk[63]);
+int   orc_spinor_decode(const uint8_t blk[63], float *vec, int k);
+void  orc_spinor_encode_vec(const float *vec, int k, uint8_t *blocks);
+int   orc_spinor_decode_vec(const uint8_t *blocks, int k, float *vec);
 /* ---- exact islands (reference arithmetic) ---- */
 void  orc_rmsnorm_exact(const float *x, const float *w, int n, float *out);
 void  orc_softmax_exact(const float *z, int m, double *p);

@@ -249,3 +249,104 @@ def test_exact_silu_fidelity():
     orc.lib().orc_silu_exact(P(g), g.size, P(out))
     ref = g.astype(np.float64) / (1 + np.exp(-g.astype(np.float64)))
     assert np.abs(out - ref).max() < 2e-5 * 12
+
+
+# ---------------------------------------------------------------- Spinor-63 KV codec
+def test_spinor_crc8_check_value():
+    """CRC-8/SMBus (poly 0x07, init 0, no reflection): the catalogued check value
+    of the ASCII string "123456789" is 0xF4; a single flipped bit anywhere in a
+    62-byte payload changes it (core/vht2/spinor_test.c:89-111)."""
+    L = orc.lib()
+    s = np.frombuffer(b"123456789", np.uint8).copy()
+    assert L.orc_crc8(P(s), 9) == 0xF4
+    rng = np.random.default_rng(3)
+    pay = rng.integers(0, 256, 62, dtype=np.uint8)
+    good = L.orc_crc8(P(pay), 62)
+    for bit in range(62 * 8):
+        c = pay.copy(); c[bit // 8] ^= np.uint8(1 << (bit % 8))
+        assert L.orc_crc8(P(c), 62) != good
+
+
+def test_spinor_block_layout_and_split():
+    """The byte image of include/sp/spinor_block.h:29-72: little-endian float
+    scale (the largest magnitude: 0.15625 -> 00 00 20 3E), exponent/basis/reserved
+    bytes 0, coefficient i at body byte 17 i mod 55, the CRC over bytes 0..61;
+    the balanced split of spinor_test.c:201-238 (128 -> 43/43/42)."""
+    L = orc.lib()
+    v = np.zeros(40, np.float32); v[5] = -0.15625; v[9] = 0.078125
+    blk = np.zeros(63, np.uint8)
+    L.orc_spinor_encode(P(v), 40, P(blk))
+    assert list(blk[:7]) == [0x00, 0x00, 0x20, 0x3E, 0, 0, 0]
+    assert blk[7 + (17 * 5) % 55].view(np.int8) == -127
+    assert blk[7 + (17 * 9) % 55].view(np.int8) == 64          # 0.5 * 127 = 63.5 rounds away from zero
+    assert np.count_nonzero(blk[7:62]) == 2
+    assert blk[62] == L.orc_crc8(P(blk), 62)
+    # every body byte is hit exactly once: 17 is a unit mod 55
+    assert sorted((17 * i) % 55 for i in range(55)) == list(range(55))
+    assert [L.orc_spinor_blocks_for(k) for k in (1, 55, 56, 110, 111, 128, 256)] == [1, 1, 2, 2, 3, 3, 5]
+    x = np.arange(128, dtype=np.float32) + 1.0
+    blks = np.zeros(3 * 63, np.uint8)
+    L.orc_spinor_encode_vec(P(x), 128, P(blks))
+    for b, (lo, n) in enumerate([(0, 43), (43, 43), (86, 42)]):
+        one = np.zeros(63, np.uint8)
+        L.orc_spinor_encode(P(np.ascontiguousarray(x[lo:lo + n])), n, P(one))
+        assert np.array_equal(one, blks[63 * b:63 * b + 63])
+    # decode: within half a quantization step of each block's scale, corruption rejected
+    y = np.zeros(128, np.float32)
+    assert L.orc_spinor_decode_vec(P(blks), 128, P(y)) == 0
+    for lo, n in [(0, 43), (43, 43), (86, 42)]:
+        sc = float(np.max(np.abs(x[lo:lo + n])))
+        assert np.max(np.abs(y[lo:lo + n] - x[lo:lo + n])) <= sc / 254 * (1 + 1e-6)
+    bad = blks.copy(); bad[70] ^= 1
+    assert L.orc_spinor_decode_vec(P(bad), 128, P(y)) != 0
+
+
+@pytest.mark.parametrize("k", [1, 7, 43, 55, 56, 64, 128, 200, 256, 512])
+def test_spinor_codec_bitexact_vs_reference(k):
+    """Byte images and decoded floats identical to the compiled reference's
+    sp_spinor_encode_vec / sp_spinor_decode_vec (core/vht2/spinor_block.c:128-149)
+    on vectors with zeros, ties at half a step, tiny and large magnitudes."""
+    R = _ref(); L = orc.lib()
+    rng = np.random.default_rng(k)
+    for trial in range(40):
+        x = (rng.standard_normal(k) * (10.0 ** rng.integers(-6, 4))).astype(np.float32)
+        if trial % 5 == 1: x[rng.integers(0, k, max(1, k // 3))] = 0.0
+        if trial % 5 == 2: x[:] = 0.0
+        if trial % 5 == 3:                                  # exact half-step ties
+            x = (rng.integers(-254, 255, k).astype(np.float32) / 2.0) * np.float32(0.125)
+        nb = L.orc_spinor_blocks_for(k)
+        a = np.zeros(63 * nb, np.uint8); b = np.zeros(63 * nb, np.uint8)
+        L.orc_spinor_encode_vec(P(x), k, P(a)); R.sp_spinor_encode_vec(P(x), k, P(b))
+        assert np.array_equal(a, b), (k, trial)
+        ya = np.zeros(k, np.float32); yb = np.zeros(k, np.float32)
+        assert L.orc_spinor_decode_vec(P(a), k, P(ya)) == R.sp_spinor_decode_vec(P(b), k, P(yb)) == 0
+        assert np.array_equal(ya.view(np.uint32), yb.view(np.uint32))
+
+
+@pytest.mark.parametrize("name", ["qwen3-tiny", "gemma3-tiny"])
+@pytest.mark.parametrize("flags", [orc.KV_SPINOR, orc.KV_SPINOR_REF])
+def test_float_decode_spinor_kv_bitexact_vs_reference(tmpdir_models, name, flags):
+    """Sessions created with SP_KV_SPINOR (the block cache) and SP_KV_SPINOR_REF
+    (the in-place round trip), core/session/sp_session.c:298-323 and :410-432:
+    every decode step's logits bit-identical to the compiled reference's, and
+    different from the f32 cache's (the codec is in the path).  The reference's
+    prefill logits come from a full forward that keeps no K/V (sp_session.c:
+    154-212, the cache is backfilled by the next decode step), so they carry no
+    codec; the oracle prefills step by step and its prompt logits are not compared."""
+    R = _ref()
+    spm, spt = model_files(tmpdir_models, name)
+    o = orc.Oracle(spm, 64, orc.FLOAT, kv_flags=flags)
+    V = o.V
+    n_prompt, n_gen = 20, 8
+    pr = prompt(n_prompt, V)
+    pre = np.zeros(V, np.float32); lg = np.zeros((n_gen, V), np.float32); fed = np.zeros(n_gen, np.int32)
+    assert R.refh_decode_flags(spm.encode(), spt.encode(), P(pr), n_prompt, n_gen, None, P(pre), P(lg), P(fed), flags) == 0
+    pre0 = np.zeros(V, np.float32); lg0 = np.zeros((n_gen, V), np.float32); fed0 = np.zeros(n_gen, np.int32)
+    assert R.refh_decode(spm.encode(), spt.encode(), P(pr), n_prompt, n_gen, P(fed), P(pre0), P(lg0), P(fed0)) == 0
+    assert np.array_equal(pre0, pre) and not np.array_equal(lg0[0], lg[0])
+    for t in pr:
+        o.step(int(t), False)
+    for k in range(n_gen):
+        ol = o.step(int(fed[k]))
+        assert np.array_equal(ol.view(np.uint32), lg[k].view(np.uint32)), f"decode step {k}"
+    o.close()
