@@ -52,8 +52,18 @@ int  sp_hipkv_set_max_rewind(sp_kvdecode_handle *h, int max_rewind);
 /* Copy-on-write fork of the resident cache (no counterpart in sp_l1.h: the
  * table has no fork row; sp_session_clone uses it through spx_register_fork). */
 int  sp_hipkv_fork(const sp_kvdecode_handle *parent, sp_kvdecode_handle **child);
+/* K/V codec of the resident cache (sp_session_config.flags, sp_l1.h:156-157,
+ * the reference's session KV codec at core/session/sp_session.c:298-323):
+ * 0 = plain (f32, or the int32 grid in exact mode), 1 = Spinor-63: every stored
+ * K/V head passes the VHT2 int8 block codec, and attention reads the decoded
+ * values, which SP_KV_SPINOR and SP_KV_SPINOR_REF share.  Float mode keeps the
+ * int8 codes and chunk multipliers in HBM (HD + 4 ceil(HD/55) bytes per row,
+ * padded to 16, for 4 HD); exact mode keeps the decoded values' int32 grid.
+ * Head dims 64, 128, 256.  Only before the first token (dpos == 0). */
+int  sp_hipkv_set_kv_codec(sp_kvdecode_handle *h, int codec);
 /* Register the backend on a session: open(sp_session_qwen3_model(s), pmax) +
- * sp_session_register_kvdecode_backend + ownership (closed with the session). */
+ * sp_session_register_kvdecode_backend + ownership (closed with the session).
+ * A session created with SP_KV_SPINOR or SP_KV_SPINOR_REF gets codec 1. */
 sp_status sp_hipkv_attach(sp_session *s, int pmax, int exact);
 
 /* Batched decode across sessions (many concurrent sessions of one model): hs[i]

@@ -134,6 +134,9 @@ const sp_kvdecode_dispatch_fn *sp_session_kvdecode_backend_dt(const sp_session *
  * sp_session_destroy and on re-registration.  Used for handles the session
  * creates itself (the fork made by sp_session_clone) and by sp_hipkv_attach. */
 sp_status spx_session_own_kvdecode(sp_session *s, int owned);
+/* The session's sp_session_config.flags (SP_KV_SPINOR, SP_KV_SPINOR_REF), for a
+ * backend that stores the session's K/V itself.  0 for NULL. */
+uint32_t spx_session_flags(const sp_session *s);
 
 /* A backend that can fork its resident cache copy-on-write registers the fork
  * against its dispatch table; sp_session_clone then forks instead of dropping

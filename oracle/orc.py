@@ -46,6 +46,7 @@ def lib():
             ("orc_q4b_gemv_exact", c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p]),
             ("orc_rope_freq_q60", ctypes.c_int64, [c_float, c_int, c_int]),
             ("orc_sess_new_kv", c_void_p, [c_void_p, c_int, c_int, ctypes.c_uint32]),
+            ("orc_set_kv_forced", None, [c_void_p, c_int]),
             ("orc_crc8", ctypes.c_uint8, [c_void_p, c_int]),
             ("orc_spinor_blocks_for", c_int, [c_int]),
             ("orc_spinor_encode", None, [c_void_p, c_int, c_void_p]),
@@ -135,6 +136,9 @@ class Oracle:
         import numpy as np
         k = np.ascontiguousarray(k, np.float32); v = np.ascontiguousarray(v, np.float32)
         return lib().orc_kv_set(self.s, layer, p0, k.shape[0], ptr(k), ptr(v))
+
+    def set_kv_forced(self, on):
+        lib().orc_set_kv_forced(self.s, 1 if on else 0)
 
     def set_pos(self, p):
         return lib().orc_set_pos(self.s, p)

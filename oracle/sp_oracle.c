@@ -616,6 +616,7 @@ struct orc_sess {
     orc_model *m;
     int mode, P, pos, kv_filled;
     uint32_t kv_flags;                /* ORC_KV_SPINOR / ORC_KV_SPINOR_REF: K/V pass the Spinor codec */
+    int kv_forced;                    /* steps keep the K/V rows resident at pos (set by orc_kv_set) */
     float *kc, *vc;                   /* [NL][P][KVD]; int32 payload in exact mode */
     float *x, *nx, *q, *kn, *vn, *ao, *ap, *gg, *up, *dn, *sc;
     double *pd;
@@ -645,6 +646,7 @@ void orc_sess_free(orc_sess *s) {
     free(s->ao); free(s->ap); free(s->gg); free(s->up); free(s->dn); free(s->sc); free(s->pd); free(s);
 }
 int orc_pos(const orc_sess *s) { return s->pos; }
+void orc_set_kv_forced(orc_sess *s, int on) { s->kv_forced = on ? 1 : 0; }
 int orc_set_pos(orc_sess *s, int pos) {
     if (pos < 0 || pos > s->P) return 1;
     s->pos = pos; s->kv_filled = pos; return 0;
@@ -720,7 +722,7 @@ static int step_any(orc_sess *s, int32_t tok, int pos, float *logits) {
     orc_model *m = s->m;
     const int gemma = (m->arch == 3u), ex = (s->mode == ORC_EXACT);
     const int E = (int)m->E, FF = (int)m->FF, HD = (int)m->HD, NH = (int)m->NH, NKV = (int)m->NKV;
-    const int QD = NH * HD, KVD = NKV * HD, group = NH / NKV, P = s->P;
+    const int KVD = NKV * HD, group = NH / NKV, P = s->P;
     const float eps = m->eps, ascale = 1.0f / sqrtf((float)HD);
     float *x = s->x, *nx = s->nx, *q = s->q, *kn = s->kn, *vn = s->vn, *ao = s->ao, *ap = s->ap,
           *gg = s->gg, *up = s->up, *dn = s->dn, *sc = s->sc;
@@ -747,20 +749,24 @@ static int step_any(orc_sess *s, int32_t tok, int pos, float *logits) {
             if (ex) { orc_rmsnorm_exact(kh, ly->k_norm, HD, kh); orc_rope_exact(kh, HD, pos, rbase); }
             else { rmsnorm_head(kh, ly->k_norm, HD, eps); orc_rope_neox(kh, HD, pos, rbase); }
         }
-        if (s->kv_flags & (ORC_KV_SPINOR | ORC_KV_SPINOR_REF))
+        if (s->kv_forced) { /* the caller's rows at pos stand */ }
+        else if (s->kv_flags & (ORC_KV_SPINOR | ORC_KV_SPINOR_REF))
             /* sp_session.c:298-320: the block cache (mode 1) and the in-place
              * round trip (mode 2) hand the attention the same decoded values */
             for (int h = 0; h < 2 * NKV; h++) spinor_roundtrip((h < NKV ? kn : vn) + (size_t)(h % NKV) * HD, HD);
         float *kcl = s->kc + (size_t)L * P * KVD, *vcl = s->vc + (size_t)L * P * KVD;
         if (ex) {
             int32_t *kd = (int32_t *)(kcl + (size_t)pos * KVD), *vd = (int32_t *)(vcl + (size_t)pos * KVD);
-            for (int i = 0; i < KVD; i++) { kd[i] = (int32_t)rintf(kn[i] * 65536.0f); vd[i] = vq_of(vn[i]); }
+            if (!s->kv_forced)
+                for (int i = 0; i < KVD; i++) { kd[i] = (int32_t)rintf(kn[i] * 65536.0f); vd[i] = vq_of(vn[i]); }
             for (int h = 0; h < NH; h++)
                 attn_head_exact(q + (size_t)h * HD, (const int32_t *)kcl, (const int32_t *)vcl, pos, KVD,
                                 h / group, HD, ascale, win, sc, ao + (size_t)h * HD);
         } else {
-            memcpy(kcl + (size_t)pos * KVD, kn, (size_t)KVD * sizeof(float));
-            memcpy(vcl + (size_t)pos * KVD, vn, (size_t)KVD * sizeof(float));
+            if (!s->kv_forced) {
+                memcpy(kcl + (size_t)pos * KVD, kn, (size_t)KVD * sizeof(float));
+                memcpy(vcl + (size_t)pos * KVD, vn, (size_t)KVD * sizeof(float));
+            }
             for (int h = 0; h < NH; h++)
                 orc_attn_head(q + (size_t)h * HD, kcl, vcl, pos, KVD, h / group, HD, ascale, win, sc,
                               ao + (size_t)h * HD);

@@ -45,6 +45,10 @@ orc_sess *orc_clone(const orc_sess *s);
 int       orc_kv_get(const orc_sess *s, int layer, int p0, int n, float *k, float *v);
 int       orc_kv_set(orc_sess *s, int layer, int p0, int n, const float *k, const float *v);
 int       orc_set_pos(orc_sess *s, int pos);
+/* on: steps leave the K/V rows at their position as orc_kv_set wrote them (the
+ * attention then reads caller-given rows: a float-mode check of a lossy K/V
+ * codec against the codes another implementation chose) */
+void      orc_set_kv_forced(orc_sess *s, int on);
 
 /* ---- unit kernels (float mode: reference order) ---- */
 float orc_f16_to_f32(uint16_t h);

@@ -202,6 +202,34 @@ __device__ __forceinline__ void load_row(const AttnArgs &a, int h, int p, bool v
     }
 }
 
+// Spinor-63 code rows (float mode with KVC_SPINOR): row p of kv-head h holds
+// HD int8 codes and the chunk multipliers (kvd_spinor.h).  v' = code * mul of
+// the coordinate's chunk; a lane's consecutive coordinates cross at most one
+// chunk boundary (chunks hold at least 28 coordinates).
+template <int EPL>
+__device__ __forceinline__ const uint8_t *spn_row(const AttnArgs &a, const float *page, int h, int p, bool vpart) {
+    constexpr int RB = spn_row_bytes(EPL * 64);
+    return (const uint8_t *)page + ((vpart ? (size_t)a.NKV * PAGE : 0) + (size_t)h * PAGE + (p & (PAGE - 1))) * RB;
+}
+template <int EPL>
+__device__ __forceinline__ void load_row_spn(const AttnArgs &a, int h, int p, bool vpart, int lane, float out[EPL]) {
+    constexpr int HD = EPL * 64;
+    const int pu = __builtin_amdgcn_readfirstlane(p), hu = __builtin_amdgcn_readfirstlane(h);
+    const uint8_t *row = spn_row<EPL>(a, page_of(a.pages, a.ring_pages, pu), hu, pu, vpart);
+    const int e0 = lane * EPL, b0 = spn_block_of(HD, e0), b1 = spn_block_of(HD, e0 + EPL - 1);
+    const float *mul = (const float *)(row + HD);
+    const float m0 = mul[b0], m1 = mul[b1];
+    const int bnd = spn_block_start(HD, b0 + 1);
+    uint32_t w[(EPL + 3) / 4];
+    if constexpr (EPL == 1) w[0] = __builtin_nontemporal_load(row + e0);
+    else if constexpr (EPL == 2) w[0] = __builtin_nontemporal_load((const uint16_t *)(row + e0));
+    else if constexpr (EPL == 4) w[0] = __builtin_nontemporal_load((const uint32_t *)(row + e0));
+    else { const uint2 t = ld_stream((const uint2 *)(row + e0)); w[0] = t.x; w[1] = t.y; }
+    #pragma unroll
+    for (int e = 0; e < EPL; e++)
+        out[e] = (float)(int32_t)(int8_t)(w[e >> 2] >> (8 * (e & 3))) * (e0 + e < bnd ? m0 : m1);
+}
+
 constexpr int MAXCH = ATTN_MAXCH;   // positions per chunk (LDS score buffer)
 constexpr int MAXNCH = 4096;     // chunks per kv-head (combine weight buffer)
 constexpr int UNR = 4;           // positions in flight per wave
@@ -209,12 +237,15 @@ constexpr int UNR = 4;           // positions in flight per wave
 // UNR rows j0.. of the chunk (zeros past n); the loops below load the next
 // UNR rows before working on the current ones, so a wave always has a row
 // group in flight
-template <int EPL, typename T, int R = UNR>
+template <int EPL, typename T, int R = UNR, bool SPN = false>
 __device__ __forceinline__ void load_rows(const AttnArgs &a, int h, int cs, int j0, int n, bool vpart, int lane,
                                           T out[R][EPL]) {
     #pragma unroll
     for (int u = 0; u < R; u++) {
-        if (j0 + u < n) load_row<EPL>(a, h, cs + j0 + u, vpart, lane, out[u]);
+        if (j0 + u < n) {
+            if constexpr (SPN) load_row_spn<EPL>(a, h, cs + j0 + u, vpart, lane, out[u]);
+            else load_row<EPL>(a, h, cs + j0 + u, vpart, lane, out[u]);
+        }
         else {
             #pragma unroll
             for (int e = 0; e < EPL; e++) out[u][e] = (T)0;
@@ -229,18 +260,21 @@ __device__ __forceinline__ void load_rows(const AttnArgs &a, int h, int cs, int 
 // dot product needs a 4-lane reduction only.  q sits in LDS and is read with
 // broadcast.  The 16 rows span at most two pages, looked up once per group.
 // p0: first position of the group, plast: last position the chunk holds
-template <int EPL, typename T>
-__device__ __forceinline__ const T *quad_row(const AttnArgs &a, int h, int p0, int plast, int p, bool vpart) {
+__device__ __forceinline__ const float *quad_page(const AttnArgs &a, int p0, int plast, int p) {
     const int pu0 = __builtin_amdgcn_readfirstlane(p0);
     const int pu1 = __builtin_amdgcn_readfirstlane(p0 + 15 < plast ? p0 + 15 : plast);
     const float *pg0 = page_of(a.pages, a.ring_pages, pu0);
     const float *pg1 = page_of(a.pages, a.ring_pages, pu1);
-    const float *pg = (p >> 6) == (pu0 >> 6) ? pg0 : pg1;
+    return p / PAGE == pu0 / PAGE ? pg0 : pg1;
+}
+template <int EPL, typename T>
+__device__ __forceinline__ const T *quad_row(const AttnArgs &a, int h, int p0, int plast, int p, bool vpart) {
+    const float *pg = quad_page(a, p0, plast, p);
     const int HD = EPL * 64;
     return (const T *)(pg + (vpart ? (size_t)a.NKV * PAGE * HD : 0) + ((size_t)h * PAGE + (p & (PAGE - 1))) * HD);
 }
 
-template <int EPL, int G, bool BATCH>
+template <int EPL, int G, bool BATCH, bool SPN>
 __global__ __launch_bounds__(256) void k_attn_float(AttnArgs a_in) {
     AttnArgs a = a_in;
     int pos;
@@ -269,7 +303,40 @@ __global__ __launch_bounds__(256) void k_attn_float(AttnArgs a_in) {
         float acc[G];
         #pragma unroll
         for (int g = 0; g < G; g++) acc[g] = 0.0f;
-        if (j < n) {
+        if (SPN && j < n) {
+            // code rows: quarter k4 takes the 16 coordinates 64 i + 16 k4 .. + 15
+            constexpr int NB = spn_blocks(HD), NM4 = (4 * NB + 15) / 16;
+            const uint8_t *row = spn_row<EPL>(a, quad_page(a, cs + j0, ce - 1, cs + j), h, cs + j, false);
+            uint4 cw[EPL];
+            #pragma unroll
+            for (int i = 0; i < EPL; i++) cw[i] = ld_stream((const uint4 *)(row + 64 * i + 16 * k4));
+            float mu[4 * NM4];
+            #pragma unroll
+            for (int t = 0; t < NM4; t++) {
+                const float4 m4 = *(const float4 *)(row + HD + 16 * t);
+                mu[4 * t] = m4.x; mu[4 * t + 1] = m4.y; mu[4 * t + 2] = m4.z; mu[4 * t + 3] = m4.w;
+            }
+            #pragma unroll
+            for (int i = 0; i < EPL; i++) {
+                const int d0 = 64 * i + 16 * k4, b = spn_block_of(HD, d0), bnd = spn_block_start(HD, b + 1);
+                float m0 = mu[0], m1 = mu[0];
+                #pragma unroll
+                for (int bb = 1; bb < NB; bb++) { if (b == bb) m0 = mu[bb]; if (b + 1 == bb) m1 = mu[bb]; }
+                const uint32_t cwv[4] = {cw[i].x, cw[i].y, cw[i].z, cw[i].w};
+                #pragma unroll
+                for (int t4 = 0; t4 < 4; t4++) {
+                    float kv[4];
+                    #pragma unroll
+                    for (int t = 0; t < 4; t++)
+                        kv[t] = (float)(int32_t)(int8_t)(cwv[t4] >> (8 * t)) * (d0 + 4 * t4 + t < bnd ? m0 : m1);
+                    #pragma unroll
+                    for (int g = 0; g < G; g++) {
+                        const float4 q = qs[g][16 * i + 4 * k4 + t4];
+                        acc[g] += q.x * kv[0] + q.y * kv[1] + q.z * kv[2] + q.w * kv[3];
+                    }
+                }
+            }
+        } else if (j < n) {
             const float *row = quad_row<EPL, float>(a, h, cs + j0, ce - 1, cs + j, false) + 4 * k4;
             float4 kv[4 * EPL];
             #pragma unroll
@@ -320,9 +387,9 @@ __global__ __launch_bounds__(256) void k_attn_float(AttnArgs a_in) {
         #pragma unroll
         for (int e = 0; e < EPL; e++) o[g][e] = 0.0f;
     float vv[UNR][EPL], vn[UNR][EPL];
-    load_rows<EPL>(a, h, cs, wave * UNR, n, true, lane, vv);
+    load_rows<EPL, float, UNR, SPN>(a, h, cs, wave * UNR, n, true, lane, vv);
     for (int j0 = wave * UNR; j0 < n; j0 += 4 * UNR) {
-        load_rows<EPL>(a, h, cs, j0 + 4 * UNR, n, true, lane, vn);
+        load_rows<EPL, float, UNR, SPN>(a, h, cs, j0 + 4 * UNR, n, true, lane, vn);
         #pragma unroll
         for (int u = 0; u < UNR; u++) {
             if (j0 + u >= n) break;
@@ -716,7 +783,8 @@ __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a_in) {
 // (B = true: token grid dimension) are separate instances
 template <int EPL, int G, bool B> static void attn_dispatch_b(const AttnArgs &a, int grid_chunks, bool prep, hipStream_t s) {
     dim3 grid(grid_chunks, a.NKV, B ? a.nt : 1);
-    if (a.mode == FLOAT) hipLaunchKernelGGL((k_attn_float<EPL, G, B>), grid, dim3(256), 0, s, a);
+    if (a.mode == FLOAT && a.kvc == KVC_SPINOR) hipLaunchKernelGGL((k_attn_float<EPL, G, B, true>), grid, dim3(256), 0, s, a);
+    else if (a.mode == FLOAT) hipLaunchKernelGGL((k_attn_float<EPL, G, B, false>), grid, dim3(256), 0, s, a);
     else {
         if (!B && prep) hipLaunchKernelGGL((k_attn_exact_scores<EPL, G, B, !B>), grid, dim3(256), 0, s, a);
         else hipLaunchKernelGGL((k_attn_exact_scores<EPL, G, B, false>), grid, dim3(256), 0, s, a);
@@ -769,9 +837,9 @@ int attn_capacity(int HD, int G) {
 
 
 // The step's head preparation and attention: exact-mode decode runs the
-// preparation inside the score pass; float mode and batched tokens launch
-// k_qk_prep first.
-bool attention_fuses_prep(const AttnArgs &a) { return a.mode == EXACT && !a.nt; }
+// preparation inside the score pass; float mode, batched tokens and the
+// Spinor codec launch k_qk_prep first.
+bool attention_fuses_prep(const AttnArgs &a) { return a.mode == EXACT && !a.nt && a.kvc == KVC_PLAIN; }
 void launch_prep_attention(const AttnArgs &a, int grid_chunks, hipStream_t s) {
     if (!attention_fuses_prep(a)) launch_qk_prep(a, s);
     attention_go(a, grid_chunks, attention_fuses_prep(a), s);

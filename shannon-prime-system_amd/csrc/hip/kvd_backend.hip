@@ -11,6 +11,7 @@
 #include "sp_model_abi.h"
 #include "sp_hipkv.h"
 #include "kvd_internal.h"
+#include "kvd_spinor.h"
 #include <hip/hip_runtime.h>
 #include <algorithm>
 #include <cmath>
@@ -328,6 +329,7 @@ struct sp_kvdecode_handle {
     DevModel *m = nullptr;
     std::shared_ptr<KvPool> pool;
     int mode = FLOAT, pmax = 0, dpos = 0, use_graph = 1, hwm = 0;
+    int kvc = KVC_PLAIN;                     // KV codec (KVC_SPINOR: SP_KV_SPINOR sessions)
     int use_batch = 1;                       // batched (MFMA) prefill where the shapes allow it
     int max_rewind = 0;                      // 0: full tables for window layers
     int full_pages = 0, ring_pages = 0;
@@ -386,6 +388,22 @@ void free_graphs(sp_kvdecode_handle *h) {
 int layer_slots(const sp_kvdecode_handle *h, int l) {
     if (!is_global(h->m, l) && h->max_rewind > 0 && h->m->SW > 0) return h->ring_pages;
     return h->full_pages;
+}
+
+// Bytes of one stored K or V row: f32 / int32 values, or in float mode with
+// the Spinor codec the row of int8 codes and chunk multipliers.
+size_t kv_row_bytes(const DevModel *m, int mode, int kvc) {
+    return mode == FLOAT && kvc == KVC_SPINOR ? (size_t)spn_row_bytes(m->HD) : (size_t)m->HD * 4;
+}
+// the bytes of such a row the attention needs (no alignment padding)
+double kv_row_payload(const DevModel *m, int mode, int kvc) {
+    return mode == FLOAT && kvc == KVC_SPINOR ? (double)(m->HD + 4 * spn_blocks(m->HD)) : 4.0 * m->HD;
+}
+std::shared_ptr<KvPool> make_pool(const DevModel *m, int mode, int kvc) {
+    auto pool = std::make_shared<KvPool>();
+    pool->page_bytes = (size_t)2 * m->NKV * PAGE * kv_row_bytes(m, mode, kvc);
+    pool->pages_per_chunk = (int)std::max<size_t>(16, ((size_t)1 << 30) / pool->page_bytes);
+    return pool;
 }
 
 int build_tables(sp_kvdecode_handle *h) {
@@ -506,6 +524,18 @@ void set_handle_mode(sp_kvdecode_handle *h, int mode) {
     }
 }
 
+// A fresh pool when the stored row format changes (mode or codec, only before
+// the first token): unmaps every page and rebuilds the empty tables.
+int repage(sp_kvdecode_handle *h, const char *who) {
+    const size_t want = (size_t)2 * h->m->NKV * PAGE * kv_row_bytes(h->m, h->mode, h->kvc);
+    if (h->pool->page_bytes == want) return 0;
+    if (h->pool.use_count() > 1) return fail("%s: the KV pages are shared with a fork", who);
+    { std::lock_guard<std::mutex> pl(h->pool->mu); for (auto &v : h->pt) for (int id : v) h->pool->unref(id); }
+    h->pool = make_pool(h->m, h->mode, h->kvc);
+    free_graphs(h);
+    return build_tables(h);
+}
+
 // A kept shell of m with this pmax and window ring, or null (caller holds g_mu).
 // Its page tables are unmapped, its scratch in the between-launch state
 // (zero accumulators and counters), its graphs still valid.
@@ -606,7 +636,7 @@ void enqueue_body(sp_kvdecode_handle *h, const StepShape &sh, TimeCb cb, void *c
         a.st = h->d_st; a.rope_cs = h->rope + ((m->gemma && !glob) ? m->HD : 0);
         a.NH = m->NH; a.NKV = m->NKV; a.HD = m->HD;
         a.win = (m->gemma && !glob) ? m->SW : -1;
-        a.max_chunks = h->max_chunks; a.mode = h->mode; a.eps = m->eps;
+        a.max_chunks = h->max_chunks; a.mode = h->mode; a.kvc = h->kvc; a.eps = m->eps;
         a.zstride = h->max_chunks * 16; a.nt = 0;
         a.base = (m->gemma && !glob) ? 10000.0f : m->base;
         a.ascale = 1.0f / sqrtf((float)m->HD);
@@ -762,7 +792,7 @@ int run_batch(sp_kvdecode_handle *h, int T, int pos0, int pos_hi, bool multi, Ti
         a.st = nullptr; a.rope_cs = b.rope + ((m->gemma && !glob) ? m->HD : 0);
         a.NH = m->NH; a.NKV = m->NKV; a.HD = m->HD;
         a.win = (m->gemma && !glob) ? m->SW : -1;
-        a.max_chunks = b.mcb; a.zstride = h->max_chunks * 16; a.mode = h->mode; a.eps = m->eps;
+        a.max_chunks = b.mcb; a.zstride = h->max_chunks * 16; a.mode = h->mode; a.kvc = h->kvc; a.eps = m->eps;
         a.base = (m->gemma && !glob) ? 10000.0f : m->base;
         a.ascale = 1.0f / sqrtf((float)m->HD);
         a.nt = T; a.pos0 = pos0; a.rope_stride = 2 * m->HD;
@@ -883,15 +913,11 @@ int sp_hipkv_open(const void *qm_opaque, int pmax, sp_kvdecode_handle **out) {
         return fail("sp_hipkv_open: no HIP device visible (this backend runs on MI355X / gfx950)%s");
     DevModel *m = model_get((const qwen3_model *)qm_opaque);
     if (!m) return 1;
-    auto new_pool = [m]() {
-        auto pool = std::make_shared<KvPool>();
-        pool->page_bytes = (size_t)2 * m->NKV * PAGE * m->HD * 4;
-        pool->pages_per_chunk = (int)std::max<size_t>(16, ((size_t)1 << 30) / pool->page_bytes);
-        return pool;
-    };
+    auto new_pool = [m]() { return make_pool(m, FLOAT, KVC_PLAIN); };
     if (sp_kvdecode_handle *sh = take_shell(m, pmax, 0)) {
         // a kept shell: reset to the open defaults, unmapped tables
         set_handle_mode(sh, FLOAT);
+        sh->kvc = KVC_PLAIN;
         sh->use_graph = 1; sh->use_batch = 1; sh->dpos = 0; sh->hwm = 0;
         sh->pool = new_pool();
         size_t tot = 0; for (int l = 0; l < m->NL; l++) tot += (size_t)sh->slots[l];
@@ -992,8 +1018,8 @@ static int decode_batch_impl(sp_kvdecode_handle *const *hs, int n, const int32_t
     for (int i = 0; i < n; i++) {
         sp_kvdecode_handle *h = hs[i];
         if (!h || h->m != m) return fail("sp_hipkv_decode_batch: handles must share one model%s");
-        if (h->mode != L->mode || h->pmax != L->pmax || h->slots != L->slots)
-            return fail("sp_hipkv_decode_batch: handles differ in mode, pmax or window ring%s");
+        if (h->mode != L->mode || h->kvc != L->kvc || h->pmax != L->pmax || h->slots != L->slots)
+            return fail("sp_hipkv_decode_batch: handles differ in mode, KV codec, pmax or window ring%s");
         if (check_tok(h, tokens[i])) return 1;
         if (h->dpos >= h->pmax) return fail("sp_hipkv_decode_batch: context full (dpos == pmax %s%lld)", "", (long long)h->pmax);
         for (int j = 0; j < i; j++)
@@ -1089,7 +1115,7 @@ int sp_hipkv_decode_batch_times(sp_kvdecode_handle *const *hs, int n, const int3
     }
     per[4] = wb(m->out) + io(m->out) + rows_n * 4.0 * m->V;
     per[8] = rows_n * ((double)(m->embd.cols / 2 + m->embd.nblk * 2) + 4.0 * m->E);
-    const double kvb = (double)KVD * 4 * 2;
+    const double kvb = (double)m->NKV * kv_row_payload(m, hs[0]->mode, hs[0]->kvc) * 2;
     for (int i = 0; i < n; i++) {
         const int pos = hs[i]->dpos;
         for (int l = 0; l < m->NL; l++) {
@@ -1136,7 +1162,19 @@ int sp_hipkv_set_mode(sp_kvdecode_handle *h, int exact) {
     // exact V-sum: weights <= 2^22, |vq| < 2^23, so int64 totals hold 2^18 positions
     if (m == EXACT && h->pmax > (1 << 18)) return fail("sp_hipkv_set_mode: exact mode holds at most %s%lld positions", "", (long long)(1 << 18));
     set_handle_mode(h, m);
-    return 0;
+    return repage(h, "sp_hipkv_set_mode");
+}
+
+int sp_hipkv_set_kv_codec(sp_kvdecode_handle *h, int codec) {
+    if (!h) return fail("sp_hipkv_set_kv_codec: null handle%s");
+    if (codec != KVC_PLAIN && codec != KVC_SPINOR) return fail("sp_hipkv_set_kv_codec: unknown codec%s");
+    if (codec == h->kvc) return 0;
+    if (h->dpos != 0) return fail("sp_hipkv_set_kv_codec: the codec is fixed once tokens are resident%s");
+    if (codec == KVC_SPINOR && h->m->HD != 64 && h->m->HD != 128 && h->m->HD != 256)
+        return fail("sp_hipkv_set_kv_codec: Spinor KV serves head_dim 64, 128 and 256%s");
+    h->kvc = codec;
+    free_graphs(h);
+    return repage(h, "sp_hipkv_set_kv_codec");
 }
 
 int sp_hipkv_set_max_rewind(sp_kvdecode_handle *h, int max_rewind) {
@@ -1182,7 +1220,7 @@ int sp_hipkv_fork(const sp_kvdecode_handle *p, sp_kvdecode_handle **out) {
             std::lock_guard<std::mutex> lk(g_mu); free_handle(h.release()); model_put(p->m); return 1;
         }
     }
-    h->pool = p->pool; h->dpos = p->dpos; h->hwm = p->hwm;
+    h->pool = p->pool; h->dpos = p->dpos; h->hwm = p->hwm; h->kvc = p->kvc;
     h->use_batch = p->use_batch; h->use_graph = p->use_graph;
     hipStreamSynchronize(p->stream);
     // share every mapped page (copy-on-write on the next append into it)
@@ -1211,6 +1249,9 @@ sp_status sp_hipkv_attach(sp_session *s, int pmax, int exact) {
     sp_kvdecode_handle *h = nullptr;
     if (sp_hipkv_open(sp_session_qwen3_model(s), pmax, &h)) return SP_EBACKEND_OOM;
     if (exact && sp_hipkv_set_mode(h, 1)) { sp_hipkv_close(h); return SP_EBADSTATE; }
+    if ((spx_session_flags(s) & (SP_KV_SPINOR | SP_KV_SPINOR_REF)) && sp_hipkv_set_kv_codec(h, KVC_SPINOR)) {
+        sp_hipkv_close(h); return SP_EUNSUPPORTED;
+    }
     sp_status st = sp_session_register_kvdecode_backend(s, h, &sp_hipkv_dispatch);
     if (st != SP_OK) { sp_hipkv_close(h); return st; }
     return spx_session_own_kvdecode(s, 1);
@@ -1276,7 +1317,7 @@ int sp_hipkv_kernel_times(sp_kvdecode_handle *h, int32_t first_token, int n, dou
     };
     for (int i = 0; i < SP_HIPKV_NCLASS; i++) { ms[i] = 0; launches[i] = 0; bytes[i] = 0; }
     const DevModel *m = h->m;
-    const double kvb = (double)m->NKV * m->HD * 4 * 2;     // K+V bytes per position per layer
+    const double kvb = (double)m->NKV * kv_row_payload(m, h->mode, h->kvc) * 2;     // K+V bytes per position per layer
     // algorithmic bytes of one GEMV: Q4B codes + f16 block scales, input and output vectors
     auto gb = [](const DevW &w) {
         return (double)w.rows * (w.cols / 2) + 2.0 * w.rows * w.nblk + 4.0 * w.cols + 4.0 * w.rows;
@@ -1319,6 +1360,13 @@ int sp_hipkv_read_kv(const sp_kvdecode_handle *h, int layer, int p0, int n, floa
     const int HD = m->HD, NKV = m->NKV, S = h->slots[layer], KVD = NKV * HD;
     HIPCHK(hipStreamSynchronize(h->stream), "kv read sync");
     std::vector<float> page(h->pool->page_bytes / 4);
+    const size_t RB = kv_row_bytes(m, h->mode, h->kvc);
+    // one stored row -> HD floats (code rows decode to code * chunk multiplier)
+    auto row_out = [&](const uint8_t *row, float *dst) {
+        if (RB == (size_t)HD * 4) { memcpy(dst, row, (size_t)HD * 4); return; }
+        const float *mul = (const float *)(row + HD);
+        for (int e = 0; e < HD; e++) dst[e] = (float)(int8_t)row[e] * mul[spn_block_of(HD, e)];
+    };
     for (int lp = p0 / PAGE; lp <= (p0 + n - 1) / PAGE && n > 0; lp++) {
         const int slot = S == h->full_pages ? lp : lp % S;
         const int id = h->pt[layer][slot];
@@ -1327,10 +1375,9 @@ int sp_hipkv_read_kv(const sp_kvdecode_handle *h, int layer, int p0, int n, floa
         const int a = std::max(p0, lp * PAGE), b = std::min(p0 + n, (lp + 1) * PAGE);
         for (int p = a; p < b; p++)
             for (int hh = 0; hh < NKV; hh++) {
-                memcpy(k + (size_t)(p - p0) * KVD + (size_t)hh * HD,
-                       page.data() + ((size_t)hh * PAGE + p % PAGE) * HD, (size_t)HD * 4);
-                memcpy(v + (size_t)(p - p0) * KVD + (size_t)hh * HD,
-                       page.data() + (size_t)NKV * PAGE * HD + ((size_t)hh * PAGE + p % PAGE) * HD, (size_t)HD * 4);
+                const uint8_t *pb = (const uint8_t *)page.data();
+                row_out(pb + ((size_t)hh * PAGE + p % PAGE) * RB, k + (size_t)(p - p0) * KVD + (size_t)hh * HD);
+                row_out(pb + ((size_t)NKV * PAGE + (size_t)hh * PAGE + p % PAGE) * RB, v + (size_t)(p - p0) * KVD + (size_t)hh * HD);
             }
     }
     return 0;
@@ -1339,7 +1386,7 @@ int sp_hipkv_read_kv(const sp_kvdecode_handle *h, int layer, int p0, int n, floa
 int sp_hipkv_info(const sp_kvdecode_handle *h, long long out[8]) {
     if (!h || !out) return fail("sp_hipkv_info: bad argument%s");
     out[0] = (long long)h->m->weight_bytes; out[1] = (long long)h->m->lm_bytes;
-    out[2] = (long long)h->m->NKV * h->m->HD * 8; out[3] = h->mode; out[4] = h->dpos;
+    out[2] = (long long)(2 * h->m->NKV * kv_row_bytes(h->m, h->mode, h->kvc)); out[3] = h->mode; out[4] = h->dpos;
     out[5] = (long long)h->pool->ptr.size(); out[6] = (long long)h->pool->page_bytes; out[7] = h->pmax;
     return 0;
 }

@@ -8,6 +8,7 @@
 #include "kvd_internal.h"
 #include "kvd_exact.h"
 #include "kvd_vec.h"
+#include "kvd_spinor.h"
 
 namespace kvd {
 
@@ -17,13 +18,14 @@ struct HeadPrep {
     float *qr;
     float *const *pages;
     int ring_pages, NH, NKV, HD, mode;
+    int kvc;                  // KVC_SPINOR: K/V pass the Spinor-63 codec
     float eps;
 };
 __device__ __forceinline__ HeadPrep head_prep_of(const AttnArgs &a) {
     HeadPrep p;
     p.q = a.q; p.k = a.k; p.v = a.v; p.q_norm = a.q_norm; p.k_norm = a.k_norm; p.rope_cs = a.rope_cs;
     p.qr = a.qr; p.pages = a.pages; p.ring_pages = a.ring_pages; p.NH = a.NH; p.NKV = a.NKV; p.HD = a.HD;
-    p.mode = a.mode; p.eps = a.eps;
+    p.mode = a.mode; p.kvc = a.kvc; p.eps = a.eps;
     return p;
 }
 
@@ -133,6 +135,41 @@ __device__ __forceinline__ int32_t kv_code_v(float v) {
     return (int32_t)r;
 }
 
+// A K or V head (lane l holds coordinates l + 64 j) through the Spinor-63
+// codec: per chunk the wave-wide max |v|, the int8 codes and v' = code * mul.
+// Float mode stores the row of codes and multipliers (row: the head's row of
+// spn_row_bytes(HD) bytes); exact mode gets v' back in place, for the int32 grid.
+template <int PER>
+__device__ __forceinline__ void spinor_head(float x[8], int lane, bool store, uint8_t *row) {
+    constexpr int HD = PER * 64, NB = spn_blocks(HD);
+    float am[NB];
+    #pragma unroll
+    for (int b = 0; b < NB; b++) am[b] = 0.0f;
+    #pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const int b = spn_block_of(HD, lane + 64 * j);
+        #pragma unroll
+        for (int bb = 0; bb < NB; bb++) if (b == bb) am[bb] = fmaxf(am[bb], fabsf(x[j]));
+    }
+    float mul_mine = 0.0f;
+    #pragma unroll
+    for (int b = 0; b < NB; b++) {
+        am[b] = spn_scale(wave_allmax(am[b]));
+        if (lane == b) mul_mine = am[b] / 127.0f;
+    }
+    #pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const int e = lane + 64 * j, b = spn_block_of(HD, e);
+        float sc = am[0];
+        #pragma unroll
+        for (int bb = 1; bb < NB; bb++) if (b == bb) sc = am[bb];
+        const int32_t c = spn_code(x[j], sc);
+        if (store) row[e] = (uint8_t)(int8_t)c;
+        else x[j] = (float)c * (sc / 127.0f);
+    }
+    if (store && lane < NB) ((float *)(row + HD))[lane] = mul_mine;
+}
+
 // hb < NH: q head hb -> qr; hb < NH + NKV: k head -> page; else v head -> page.
 // src: the head's HD projections; lane l holds elements l + 64 j.
 template <bool COHERENT, int PER>
@@ -143,6 +180,21 @@ __device__ __forceinline__ void qk_prep_head_t(const HeadPrep a, int hb, int pos
     float *page = qk_page_of(a.pages, a.ring_pages, pos);
     const int slot = pos % PAGE;
     const float *src = isq ? a.q + (size_t)h * HD : (isk ? a.k : a.v) + (size_t)h * HD;
+    if (!isq && !isk && a.kvc == KVC_SPINOR) {                  // V through the codec
+        float x[8];
+        #pragma unroll
+        for (int j = 0; j < 8; j++) if (j < per) x[j] = COHERENT ? ld_agent(&src[lane + 64 * j]) : src[lane + 64 * j];
+        if (a.mode == FLOAT) {
+            constexpr int RB = spn_row_bytes(HD);
+            spinor_head<PER>(x, lane, true, (uint8_t *)page + ((size_t)a.NKV * PAGE + (size_t)h * PAGE + slot) * RB);
+        } else {
+            spinor_head<PER>(x, lane, false, nullptr);
+            int32_t *dst = (int32_t *)page + (size_t)a.NKV * PAGE * HD + ((size_t)h * PAGE + slot) * HD;
+            #pragma unroll
+            for (int j = 0; j < 8; j++) if (j < per) dst[lane + 64 * j] = kv_code_v(x[j]);
+        }
+        return;
+    }
     if (!isq && !isk) {                                         // V: raw (exact: Q16 grid, clamped)
         float *dst = page + (size_t)a.NKV * PAGE * HD + ((size_t)h * PAGE + slot) * HD;
         #pragma unroll
@@ -159,7 +211,11 @@ __device__ __forceinline__ void qk_prep_head_t(const HeadPrep a, int hb, int pos
     if (isq) {
         #pragma unroll
         for (int j = 0; j < 8; j++) if (j < per) a.qr[(size_t)h * HD + lane + 64 * j] = out[j];
+    } else if (a.kvc == KVC_SPINOR && a.mode == FLOAT) {
+        constexpr int RB = spn_row_bytes(HD);
+        spinor_head<PER>(out, lane, true, (uint8_t *)page + ((size_t)h * PAGE + slot) * RB);
     } else {
+        if (a.kvc == KVC_SPINOR) spinor_head<PER>(out, lane, false, nullptr);
         float *dst = page + ((size_t)h * PAGE + slot) * HD;
         #pragma unroll
         for (int j = 0; j < 8; j++) {

@@ -283,6 +283,7 @@ sp_status spx_session_own_kvdecode(sp_session *s, int owned) {
     return SP_OK;
 }
 
+uint32_t spx_session_flags(const sp_session *s) { return s ? s->cfg.flags : 0u; }
 sp_kvdecode_handle *sp_session_kvdecode_backend_handle(const sp_session *s) { return s ? s->kv_h : NULL; }
 const sp_kvdecode_dispatch_fn *sp_session_kvdecode_backend_dt(const sp_session *s) { return s ? s->kv_dt : NULL; }
 const void *sp_session_qwen3_model(const sp_session *s) { return s ? (const void *)s->qm : NULL; }

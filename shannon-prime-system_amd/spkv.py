@@ -108,6 +108,7 @@ def kv():
         _sig(lib, "sp_hipkv_position", c_int, [c_void_p])
         _sig(lib, "sp_hipkv_close", None, [c_void_p])
         _sig(lib, "sp_hipkv_set_mode", c_int, [c_void_p, c_int])
+        _sig(lib, "sp_hipkv_set_kv_codec", c_int, [c_void_p, c_int])
         _sig(lib, "sp_hipkv_set_max_rewind", c_int, [c_void_p, c_int])
         _sig(lib, "sp_hipkv_set_graph", c_int, [c_void_p, c_int])
         _sig(lib, "sp_hipkv_set_batch_prefill", c_int, [c_void_p, c_int])
@@ -180,8 +181,8 @@ class Model:
 class Session:
     """sp_session over a Model; attach() registers the HIP backend (owned)."""
 
-    def __init__(self, model, max_context=0, cancel=None):
-        cfg = SessionConfig(max_context, 1, 0, 0, 0, 0)
+    def __init__(self, model, max_context=0, cancel=None, flags=0):
+        cfg = SessionConfig(max_context, 1, 0, 0, flags, 0)
         h = c_void_p()
         self.cancel = cancel
         check(l1().sp_session_create(model.h, ctypes.byref(cfg),
@@ -241,17 +242,21 @@ class Session:
 
 
 NCLASS = 9          # kernel classes of sp_hipkv_kernel_times (include/sp_hipkv.h)
+KV_PLAIN, KV_SPINOR = 0, 1                    # sp_hipkv_set_kv_codec
+SP_KV_SPINOR, SP_KV_SPINOR_REF = 1, 2         # sp_session_config.flags
 
 
 class Backend:
     """A bare section-6b handle driven through the dispatch functions directly."""
 
-    def __init__(self, qm, pmax, exact=False, graph=True, batch_prefill=True):
+    def __init__(self, qm, pmax, exact=False, graph=True, batch_prefill=True, kv_codec=KV_PLAIN):
         h = c_void_p()
         check(kv().sp_hipkv_open(qm, pmax, ctypes.byref(h)), "sp_hipkv_open")
         self.h = h
         if exact:
             check(kv().sp_hipkv_set_mode(h, 1), "sp_hipkv_set_mode")
+        if kv_codec != KV_PLAIN:
+            check(kv().sp_hipkv_set_kv_codec(h, kv_codec), "sp_hipkv_set_kv_codec")
         if not graph:
             check(kv().sp_hipkv_set_graph(h, 0), "sp_hipkv_set_graph")
         if not batch_prefill:
