@@ -42,9 +42,9 @@ KERNEL_NAMES = {
     "down_gemv_q4b": ["kvd::k_gemv<0, false, false>"],
     "lm_head_gemv_q4b": ["kvd::k_gemv<2, false, false>"],
     "gqa_decode_attn_global": ["kvd::k_attn_exact_scores<EPL, G, false, true> + kvd::k_attn_exact_vsum<EPL, G, false>",
-                               "[kvd::k_qk_prep<false> + kvd::k_attn_float<EPL, G, false>]"],
+                               "[kvd::k_qk_prep<false> + kvd::k_attn_float<EPL, G, false, SPINOR>]"],
     "gqa_decode_attn_window": ["kvd::k_attn_exact_scores<EPL, G, false, true> + kvd::k_attn_exact_vsum<EPL, G, false>",
-                               "[kvd::k_qk_prep<false> + kvd::k_attn_float<EPL, G, false>]"],
+                               "[kvd::k_qk_prep<false> + kvd::k_attn_float<EPL, G, false, SPINOR>]"],
     # float mode only: exact-mode decode prepares the heads inside the score pass
     "qk_norm_rope_append": ["[kvd::k_qk_prep<false>]"],
     "embed_rope_argmax": ["kvd::k_embed", "kvd::k_rope_table", "kvd::k_argmax"],
@@ -131,6 +131,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--workload", default="gemma3-12b-32k", choices=sorted(WORKLOADS))
     ap.add_argument("--mode", default="exact", choices=["exact", "float"])
+    ap.add_argument("--kv", default="plain", choices=["plain", "spinor"],
+                    help="session K/V codec: spinor = SP_KV_SPINOR (int8 chunk codes in float mode)")
     ap.add_argument("--cpu-steps", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-steps", type=int, default=8)
@@ -167,7 +169,7 @@ def main():
     log(f"model written {os.path.getsize(spm)/1e9:.2f} GB in {time.time()-t0:.1f}s ({threads} threads)")
     try:
         model = spkv.Model(spm, spt)
-        sess = spkv.Session(model, pmax)
+        sess = spkv.Session(model, pmax, flags=spkv.SP_KV_SPINOR if args.kv == "spinor" else 0)
         t0 = time.time()
         sess.attach(pmax, exact=exact)
         log(f"backend attached (upload) in {time.time()-t0:.1f}s, mode={args.mode}")
@@ -256,7 +258,7 @@ def main():
 
         cpu = None
         if not args.no_cpu_baseline:
-            cpu = cpu_baseline(spm, be, info, shape, exact, args.cpu_steps, tok, sess)
+            cpu = cpu_baseline(spm, be, info, shape, exact, args.cpu_steps, tok, sess, args.kv == "spinor")
 
         rec = {
             "metric": METRIC if args.workload == "gemma3-12b-32k" and ctx == 32768 else
@@ -264,11 +266,14 @@ def main():
             "value": round(value, 3), "unit": "tokens/s", "n_gpus": 1,
             "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(1e3 * wall / args.steps, 4),
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-            "dtype": "int4xint4->int64 GEMV, int32 KV (exact mode)" if exact else "int4xint4->int64 GEMV, f32 KV/attention",
+            "dtype": "int4xint4->int64 GEMV, int32 KV (exact mode)" if exact else
+                     ("int4xint4->int64 GEMV, int8 Spinor KV codes, f32 attention" if args.kv == "spinor"
+                      else "int4xint4->int64 GEMV, f32 KV/attention"),
             "data": "synthetic: seeded random-init OK_Q4B weights (SplitMix64 seed 0, N(0,0.02)), seeded uniform prompt (seed 1)",
             "config": {"workload": f"{args.workload}: {wl['shape']}-shape kvdecode, prefill {ctx} then {args.steps} greedy steps, batch 1"
                                    + (f", rewind 1-{wl['rewind_max']} tokens every {every} steps" if every else ""),
-                       "ctx": ctx, "mode": args.mode, "b_kv": 4, "pmax": pmax,
+                       "ctx": ctx, "mode": args.mode, "kv": args.kv,
+                       "b_kv": float(info[2]) / (2 * shape["n_kv_heads"] * shape["head_dim"]), "pmax": pmax,
                        **({"rewinds": rewinds, "max_rewind": max_rewind} if every else {})},
             "roofline": {"bound": "hbm", "kernel": dom["kernel"], "rocprof_kernels": dom_names,
                          "achieved": round(dom["gbs"], 1), "peak": PEAK_GBS, "unit": "GB/s",
@@ -411,7 +416,7 @@ def run_sessions(args, wl):
         kv_gb, kv_ms = sum(c["bytes"] for c in kv) / 1e9, sum(c["total_ms"] for c in kv)
         step_bytes = sum(c["bytes"] for c in cls)
         names = {"gqa_decode_attn_global": ["kvd::k_attn_exact_scores<2, 4, true> + kvd::k_attn_exact_vsum<2, 4, true>"
-                                            if exact else "kvd::k_attn_float<2, 4, true>"]}
+                                            if exact else "kvd::k_attn_float<2, 4, true, false>"]}
         rec = {
             "metric": BATCH_METRIC, "value": round(value, 3), "unit": "tokens/s", "n_gpus": 1,
             "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(1e3 * wall / args.steps, 4),
@@ -488,13 +493,13 @@ def calib_copy(nbytes):
     log(f"calibration copy of {nbytes >> 20} MiB done")
 
 
-def cpu_baseline(spm, be, info, shape, exact, n_steps, tok, sess):
+def cpu_baseline(spm, be, info, shape, exact, n_steps, tok, sess, spinor=False):
     """Oracle decode steps on the host at the same context, KV loaded from the device."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import orc
     pos = be.position()
     kvd = shape["n_kv_heads"] * shape["head_dim"]
-    o = orc.Oracle(spm, pos + n_steps + 1, orc.EXACT if exact else orc.FLOAT)
+    o = orc.Oracle(spm, pos + n_steps + 1, orc.EXACT if exact else orc.FLOAT, kv_flags=orc.KV_SPINOR if spinor else 0)
     t0 = time.time()
     win = shape.get("swa_window", 0) if shape.get("arch_id") == __import__("spkv").ARCH_GEMMA3 else 0
     for layer in range(shape["n_layers"]):

@@ -381,34 +381,91 @@ __global__ __launch_bounds__(256) void k_attn_float(AttnArgs a_in) {
         for (int j = lane; j < n; j += 64) lv += sc[g][j];
         l[g] = wsum(lv);
     }
-    float o[G][EPL];
-    #pragma unroll
-    for (int g = 0; g < G; g++)
+    if constexpr (SPN) {
+        // code rows: lane = CPR * r + col takes codes 16 col .. 16 col + 15 of
+        // row r of a group of RPL rows (one 16-byte load per lane and row
+        // group), two groups in flight per wave; the RPL row partials of a
+        // column meet by lane exchange at the end
+        constexpr int CPR = HD / 16, RPL = 64 / CPR;
+        const int rr = lane / CPR, d0 = 16 * (lane % CPR);
+        const int b0 = spn_block_of(HD, d0), bnd = spn_block_start(HD, b0 + 1);
+        const int b1 = bnd < d0 + 16 ? b0 + 1 : b0;
+        float o[G][16];
         #pragma unroll
-        for (int e = 0; e < EPL; e++) o[g][e] = 0.0f;
-    float vv[UNR][EPL], vn[UNR][EPL];
-    load_rows<EPL, float, UNR, SPN>(a, h, cs, wave * UNR, n, true, lane, vv);
-    for (int j0 = wave * UNR; j0 < n; j0 += 4 * UNR) {
-        load_rows<EPL, float, UNR, SPN>(a, h, cs, j0 + 4 * UNR, n, true, lane, vn);
-        #pragma unroll
-        for (int u = 0; u < UNR; u++) {
-            if (j0 + u >= n) break;
+        for (int g = 0; g < G; g++)
             #pragma unroll
-            for (int g = 0; g < G; g++) {
-                const float p = sc[g][j0 + u];
+            for (int t = 0; t < 16; t++) o[g][t] = 0.0f;
+        for (int j0 = wave * RPL; j0 < n; j0 += 8 * RPL) {
+            uint4 cw[2];
+            float m0[2], m1[2];
+            #pragma unroll
+            for (int k = 0; k < 2; k++) {
+                const int j = j0 + 4 * RPL * k + rr;
+                cw[k] = make_uint4(0, 0, 0, 0); m0[k] = m1[k] = 0.0f;
+                if (j < n) {
+                    const uint8_t *row = spn_row<EPL>(a, quad_page(a, cs + j0 + 4 * RPL * k, ce - 1, cs + j), h, cs + j, true);
+                    cw[k] = ld_stream((const uint4 *)(row + d0));
+                    m0[k] = ((const float *)(row + HD))[b0];
+                    m1[k] = ((const float *)(row + HD))[b1];
+                }
+            }
+            #pragma unroll
+            for (int k = 0; k < 2; k++) {
+                const int j = j0 + 4 * RPL * k + rr;
+                if (j >= n) continue;
+                float p[G];
                 #pragma unroll
-                for (int e = 0; e < EPL; e++) o[g][e] += p * vv[u][e];
+                for (int g = 0; g < G; g++) p[g] = sc[g][j];
+                const uint32_t w[4] = {cw[k].x, cw[k].y, cw[k].z, cw[k].w};
+                #pragma unroll
+                for (int t = 0; t < 16; t++) {
+                    const float x = (float)(int32_t)(int8_t)(w[t >> 2] >> (8 * (t & 3))) * (d0 + t < bnd ? m0[k] : m1[k]);
+                    #pragma unroll
+                    for (int g = 0; g < G; g++) o[g][t] += p[g] * x;
+                }
             }
         }
         #pragma unroll
-        for (int u = 0; u < UNR; u++)
+        for (int s = CPR; s < 64; s <<= 1)
             #pragma unroll
-            for (int e = 0; e < EPL; e++) vv[u][e] = vn[u][e];
-    }
-    #pragma unroll
-    for (int g = 0; g < G; g++)
+            for (int g = 0; g < G; g++)
+                #pragma unroll
+                for (int t = 0; t < 16; t++) o[g][t] += __shfl_xor(o[g][t], s, 64);
+        if (rr == 0)
+            #pragma unroll
+            for (int g = 0; g < G; g++)
+                #pragma unroll
+                for (int t = 0; t < 16; t++) ored[wave][g][d0 + t] = o[g][t];
+    } else {
+        float o[G][EPL];
         #pragma unroll
-        for (int e = 0; e < EPL; e++) ored[wave][g][lane * EPL + e] = o[g][e];
+        for (int g = 0; g < G; g++)
+            #pragma unroll
+            for (int e = 0; e < EPL; e++) o[g][e] = 0.0f;
+        float vv[UNR][EPL], vn[UNR][EPL];
+        load_rows<EPL, float, UNR, SPN>(a, h, cs, wave * UNR, n, true, lane, vv);
+        for (int j0 = wave * UNR; j0 < n; j0 += 4 * UNR) {
+            load_rows<EPL, float, UNR, SPN>(a, h, cs, j0 + 4 * UNR, n, true, lane, vn);
+            #pragma unroll
+            for (int u = 0; u < UNR; u++) {
+                if (j0 + u >= n) break;
+                #pragma unroll
+                for (int g = 0; g < G; g++) {
+                    const float p = sc[g][j0 + u];
+                    #pragma unroll
+                    for (int e = 0; e < EPL; e++) o[g][e] += p * vv[u][e];
+                }
+            }
+            #pragma unroll
+            for (int u = 0; u < UNR; u++)
+                #pragma unroll
+                for (int e = 0; e < EPL; e++) vv[u][e] = vn[u][e];
+        }
+        #pragma unroll
+        for (int g = 0; g < G; g++)
+            #pragma unroll
+            for (int e = 0; e < EPL; e++) ored[wave][g][lane * EPL + e] = o[g][e];
+    }
     __syncthreads();
     for (int i = threadIdx.x; i < G * HD; i += 256) {
         const int g = i / HD, d = i % HD;
