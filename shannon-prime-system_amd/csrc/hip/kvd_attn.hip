@@ -554,6 +554,7 @@ __device__ __forceinline__ void prep_finish(const AttnArgs &a, int h, int pos, i
         const size_t rowoff = ((size_t)h * PAGE + pos % PAGE) * HD;
         if (wave == G % 4) {
             head_norm_rope_in<EPL>(hp, in.k, lane, out);
+            if (a.kvc == KVC_SPINOR) spinor_head<EPL>(out, lane, false, nullptr);   // the codec's decoded values
             #pragma unroll
             for (int j = 0; j < EPL; j++) {
                 const int32_t ki = kv_code_k(out[j]);
@@ -563,8 +564,12 @@ __device__ __forceinline__ void prep_finish(const AttnArgs &a, int h, int pos, i
         }
         if (wave == (G + 1) % 4) {
             int32_t *dst = (int32_t *)(page + (size_t)a.NKV * PAGE * HD + rowoff);
+            float x[8];
             #pragma unroll
-            for (int j = 0; j < EPL; j++) dst[lane + 64 * j] = kv_code_v(in.v[j]);
+            for (int j = 0; j < EPL; j++) x[j] = in.v[j];
+            if (a.kvc == KVC_SPINOR) spinor_head<EPL>(x, lane, false, nullptr);
+            #pragma unroll
+            for (int j = 0; j < EPL; j++) dst[lane + 64 * j] = kv_code_v(x[j]);
         }
     }
 }
@@ -894,9 +899,9 @@ int attn_capacity(int HD, int G) {
 
 
 // The step's head preparation and attention: exact-mode decode runs the
-// preparation inside the score pass; float mode, batched tokens and the
-// Spinor codec launch k_qk_prep first.
-bool attention_fuses_prep(const AttnArgs &a) { return a.mode == EXACT && !a.nt && a.kvc == KVC_PLAIN; }
+// preparation inside the score pass; float mode and batched tokens launch
+// k_qk_prep first.
+bool attention_fuses_prep(const AttnArgs &a) { return a.mode == EXACT && !a.nt; }
 void launch_prep_attention(const AttnArgs &a, int grid_chunks, hipStream_t s) {
     if (!attention_fuses_prep(a)) launch_qk_prep(a, s);
     attention_go(a, grid_chunks, attention_fuses_prep(a), s);
