@@ -917,7 +917,7 @@ int sp_hipkv_open(const void *qm_opaque, int pmax, sp_kvdecode_handle **out) {
     if (sp_kvdecode_handle *sh = take_shell(m, pmax, 0)) {
         // a kept shell: reset to the open defaults, unmapped tables
         set_handle_mode(sh, FLOAT);
-        sh->kvc = KVC_PLAIN;
+        if (sh->kvc != KVC_PLAIN) { sh->kvc = KVC_PLAIN; free_graphs(sh); }   // graphs bake in the codec
         sh->use_graph = 1; sh->use_batch = 1; sh->dpos = 0; sh->hwm = 0;
         sh->pool = new_pool();
         size_t tot = 0; for (int l = 0; l < m->NL; l++) tot += (size_t)sh->slots[l];
@@ -1220,7 +1220,8 @@ int sp_hipkv_fork(const sp_kvdecode_handle *p, sp_kvdecode_handle **out) {
             std::lock_guard<std::mutex> lk(g_mu); free_handle(h.release()); model_put(p->m); return 1;
         }
     }
-    h->pool = p->pool; h->dpos = p->dpos; h->hwm = p->hwm; h->kvc = p->kvc;
+    if (h->kvc != p->kvc) { h->kvc = p->kvc; free_graphs(h.get()); }        // a recycled shell's graphs
+    h->pool = p->pool; h->dpos = p->dpos; h->hwm = p->hwm;
     h->use_batch = p->use_batch; h->use_graph = p->use_graph;
     hipStreamSynchronize(p->stream);
     // share every mapped page (copy-on-write on the next append into it)
