@@ -29,6 +29,7 @@ import numpy as np
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "shannon-prime-system_amd"))
+from spkv import splitmix_tokens, splitmix_u64  # noqa: E402  (seeded synthetic inputs)
 
 METRIC = "kvdecode tokens/s + KV-read HBM GB/s (% of peak), Gemma-12B shape 32k ctx"
 PEAK_GBS = 8000.0
@@ -101,17 +102,6 @@ BATCH_METRIC = "batched multi-session kvdecode tokens/s (aggregate over sessions
 
 def log(*a):
     print("[bench]", *a, file=sys.stderr, flush=True)
-
-
-def splitmix_tokens(n, vocab, seed):
-    """uniform tokens in [0, vocab) from SplitMix64 outputs (seeded prompt generator)."""
-    k = np.arange(1, n + 1, dtype=np.uint64)
-    with np.errstate(over="ignore"):
-        z = np.uint64(seed) + k * np.uint64(0x9E3779B97F4A7C15)
-        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
-        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
-        z = z ^ (z >> np.uint64(31))
-    return (z % np.uint64(vocab)).astype(np.int32)
 
 
 def cpu_model():
@@ -300,15 +290,6 @@ def main():
     finally:
         if not args.workdir:
             shutil.rmtree(work, ignore_errors=True)
-
-
-def splitmix_u64(n, seed):
-    k = np.arange(1, n + 1, dtype=np.uint64)
-    with np.errstate(over="ignore"):
-        z = np.uint64(seed) + k * np.uint64(0x9E3779B97F4A7C15)
-        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
-        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
-        return z ^ (z >> np.uint64(31))
 
 
 def run_sessions(args, wl):

@@ -62,8 +62,11 @@ int  sp_hipkv_fork(const sp_kvdecode_handle *parent, sp_kvdecode_handle **child)
  * Head dims 64, 128, 256.  Only before the first token (dpos == 0). */
 int  sp_hipkv_set_kv_codec(sp_kvdecode_handle *h, int codec);
 /* Register the backend on a session: open(sp_session_qwen3_model(s), pmax) +
- * sp_session_register_kvdecode_backend + ownership (closed with the session).
- * A session created with SP_KV_SPINOR or SP_KV_SPINOR_REF gets codec 1. */
+ * sp_session_register_kvdecode_backend + ownership (closed with the session) +
+ * lifecycle routing (spx_session_route_kv_lifecycle: prefill, rewind and clone
+ * reach the backend).  The session must be at position 0 (SP_EBADSTATE
+ * otherwise).  A session created with SP_KV_SPINOR or SP_KV_SPINOR_REF gets
+ * codec 1. */
 sp_status sp_hipkv_attach(sp_session *s, int pmax, int exact);
 
 /* Batched decode across sessions (many concurrent sessions of one model): hs[i]
@@ -110,6 +113,20 @@ int  sp_hipkv_set_graph(sp_kvdecode_handle *h, int on);
  * GEMMs, token-batched attention) or one decode step per token (0).  Both
  * leave the same K/V (bit-identical in exact mode). */
 int  sp_hipkv_set_batch_prefill(sp_kvdecode_handle *h, int on);
+/* Exact mode stores V as vq = rne(v * 2^16) clamped to +-(2^23 - 1), which
+ * keeps the exact V-sum inside int64 (|v| below 128).  This counts the V heads
+ * this handle stored with at least one clamped element since it was opened or
+ * forked (batched decodes count on the first handle of the batch); 0 means
+ * every stored V is exact.  Synchronizes the handle's stream.  No counterpart
+ * in the reference (its V slab is f32). */
+int  sp_hipkv_v_clamps(const sp_kvdecode_handle *h, long long *count);
+/* Validate a model for this backend on the host only (no device call): the
+ * checks sp_hipkv_open makes before it uploads anything -- architecture, head
+ * geometry, OK_Q4B tensors found through the arena, norm lengths, window.
+ * out: weight bytes (codes + block scales), LM-head bytes, layers, hidden,
+ * vocab, ffn, sliding window, 1 if some tensor needs the int128 GEMV path.
+ * No counterpart in the reference (a registrant's pre-flight check). */
+int  sp_hipkv_check_model(const void *qm_opaque, long long out[8]);
 /* Bytes of model weights resident in HBM and KV bytes per token per layer. */
 int  sp_hipkv_info(const sp_kvdecode_handle *h, long long out[8]);
 

@@ -134,6 +134,14 @@ const sp_kvdecode_dispatch_fn *sp_session_kvdecode_backend_dt(const sp_session *
  * sp_session_destroy and on re-registration.  Used for handles the session
  * creates itself (the fork made by sp_session_clone) and by sp_hipkv_attach. */
 sp_status spx_session_own_kvdecode(sp_session *s, int owned);
+/* Lifecycle routing of a registered section-6b table (default off, which is the
+ * reference's contract, sp_l1.h:396-399: only sp_decode_step reaches the table).
+ * On: sp_prefill_chunk runs dt->prefill plus one dt->decode_step for the last
+ * position's logits, sp_session_rewind also calls dt->rewind, and
+ * sp_session_clone forks the backend (spx_register_fork) into the clone, which
+ * inherits the routing.  Registering another table or handle turns it off.
+ * SP_EBADSTATE without a registered table.  sp_hipkv_attach turns it on. */
+sp_status spx_session_route_kv_lifecycle(sp_session *s, int on);
 /* The session's sp_session_config.flags (SP_KV_SPINOR, SP_KV_SPINOR_REF), for a
  * backend that stores the session's K/V itself.  0 for NULL. */
 uint32_t spx_session_flags(const sp_session *s);

@@ -53,6 +53,10 @@ def lib():
             ("orc_spinor_decode", c_int, [c_void_p, c_void_p, c_int]),
             ("orc_spinor_encode_vec", None, [c_void_p, c_int, c_void_p]),
             ("orc_spinor_decode_vec", c_int, [c_void_p, c_int, c_void_p]),
+            ("orc_attn_head_exact", None, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_float, c_int, c_void_p]),
+            ("orc_i128_div_to_float", c_float, [ctypes.c_int64, ctypes.c_uint64, ctypes.c_int64, c_int]),
+            ("orc_vq_of", ctypes.c_int32, [c_float, c_void_p]),
+            ("orc_v_clamps", c_int, [c_void_p]),
         ]:
             f = getattr(L, name); f.restype = res; f.argtypes = args
         _orc = L
@@ -139,6 +143,9 @@ class Oracle:
 
     def set_kv_forced(self, on):
         lib().orc_set_kv_forced(self.s, 1 if on else 0)
+
+    def v_clamps(self):
+        return lib().orc_v_clamps(self.s)
 
     def set_pos(self, p):
         return lib().orc_set_pos(self.s, p)

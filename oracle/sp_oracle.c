@@ -617,6 +617,7 @@ struct orc_sess {
     int mode, P, pos, kv_filled;
     uint32_t kv_flags;                /* ORC_KV_SPINOR / ORC_KV_SPINOR_REF: K/V pass the Spinor codec */
     int kv_forced;                    /* steps keep the K/V rows resident at pos (set by orc_kv_set) */
+    int vclamp;                       /* exact mode: V heads stored with a clamped element */
     float *kc, *vc;                   /* [NL][P][KVD]; int32 payload in exact mode */
     float *x, *nx, *q, *kn, *vn, *ao, *ap, *gg, *up, *dn, *sc;
     double *pd;
@@ -711,12 +712,24 @@ static void attn_head_exact(const float *qh, const int32_t *KC, const int32_t *V
     free(zi);
 }
 
-static int32_t vq_of(float v) {
+static int32_t vq_of(float v, int *clamped) {
     float r = rintf(v * 65536.0f);
-    if (r > 8388607.0f) r = 8388607.0f;
-    if (r < -8388607.0f) r = -8388607.0f;
+    if (r > 8388607.0f) { r = 8388607.0f; *clamped = 1; }
+    if (r < -8388607.0f) { r = -8388607.0f; *clamped = 1; }
     return (int32_t)r;
 }
+int32_t orc_vq_of(float v, int *clamped) { int c = 0; int32_t q = vq_of(v, &c); if (clamped) *clamped = c; return q; }
+void orc_attn_head_exact(const float *qh, const int32_t *KC, const int32_t *VC, int pos, int KVD, int kvh,
+                         int HD, float ascale, int win, float *out) {
+    float *sc = (float *)malloc((size_t)(pos + 1) * sizeof(float));
+    attn_head_exact(qh, KC, VC, pos, KVD, kvh, HD, ascale, win, sc, out);
+    free(sc);
+}
+float orc_i128_div_to_float(int64_t num_hi, uint64_t num_lo, int64_t den, int k) {
+    const i128 num = (i128)(((u128)(uint64_t)num_hi << 64) | num_lo);
+    return i128_div_to_float(num, den, k);
+}
+int orc_v_clamps(const orc_sess *s) { return s->vclamp; }
 
 static int step_any(orc_sess *s, int32_t tok, int pos, float *logits) {
     orc_model *m = s->m;
@@ -758,7 +771,11 @@ static int step_any(orc_sess *s, int32_t tok, int pos, float *logits) {
         if (ex) {
             int32_t *kd = (int32_t *)(kcl + (size_t)pos * KVD), *vd = (int32_t *)(vcl + (size_t)pos * KVD);
             if (!s->kv_forced)
-                for (int i = 0; i < KVD; i++) { kd[i] = (int32_t)rintf(kn[i] * 65536.0f); vd[i] = vq_of(vn[i]); }
+                for (int h = 0; h < NKV; h++) {
+                    int cl = 0;
+                    for (int i = h * HD; i < (h + 1) * HD; i++) { kd[i] = (int32_t)rintf(kn[i] * 65536.0f); vd[i] = vq_of(vn[i], &cl); }
+                    s->vclamp += cl;
+                }
             for (int h = 0; h < NH; h++)
                 attn_head_exact(q + (size_t)h * HD, (const int32_t *)kcl, (const int32_t *)vcl, pos, KVD,
                                 h / group, HD, ascale, win, sc, ao + (size_t)h * HD);

@@ -76,6 +76,17 @@ int   orc_q4b_gemv_exact(const uint8_t *codes, const uint16_t *bscale, int rows,
                          const float *x, float *y);
 void  orc_silu_exact(const float *x, int n, float *out);
 int64_t orc_rope_freq_q60(float base, int i, int d);
+/* exact-mode attention of one q head over [s0, pos] (int32 K/V slabs, KVD per
+ * position): qi = rne(q 2^16), int64 dots, the island softmax on the 2^14
+ * grid, Q22 weights, int128 V-sum, one RNE division per output */
+void  orc_attn_head_exact(const float *qh, const int32_t *KC, const int32_t *VC, int pos, int KVD, int kvh,
+                          int HD, float ascale, int win, float *out);
+/* RNE(num / (den * 2^k)) for a 128-bit num = num_hi * 2^64 + num_lo, den > 0 */
+float orc_i128_div_to_float(int64_t num_hi, uint64_t num_lo, int64_t den, int k);
+/* exact-mode V code clamp(rne(v 2^16), +-(2^23-1)); *clamped = 1 when clamped */
+int32_t orc_vq_of(float v, int *clamped);
+/* V heads this session stored with a clamped element (exact mode) */
+int   orc_v_clamps(const orc_sess *s);
 
 #ifdef __cplusplus
 }

@@ -568,8 +568,10 @@ __device__ __forceinline__ void prep_finish(const AttnArgs &a, int h, int pos, i
             #pragma unroll
             for (int j = 0; j < EPL; j++) x[j] = in.v[j];
             if (a.kvc == KVC_SPINOR) spinor_head<EPL>(x, lane, false, nullptr);
+            bool cl = false;
             #pragma unroll
-            for (int j = 0; j < EPL; j++) dst[lane + 64 * j] = kv_code_v(x[j]);
+            for (int j = 0; j < EPL; j++) dst[lane + 64 * j] = kv_code_v(x[j], cl);
+            count_v_clamp(a.vclamp, cl);
         }
     }
 }
@@ -860,9 +862,8 @@ template <int EPL, int G> static void attn_dispatch(const AttnArgs &a, int grid_
 
 static void attention_go(const AttnArgs &a, int grid_chunks, bool prep, hipStream_t s) {
     const int G = a.NH / a.NKV;
-    if (a.chunk > MAXCH || a.chunk % 16 || grid_chunks > MAXNCH) {
-        fprintf(stderr, "kvd: attention chunk %d / grid %d outside the kernel's limits\n", a.chunk, grid_chunks);
-        abort();
+    if (a.chunk > MAXCH || a.chunk % 16 || grid_chunks > MAXNCH || grid_chunks < 1) {
+        launch_fail("attention chunk or chunk count outside the kernel's limits"); return;
     }
     if (a.HD == 256 && G == 2) attn_dispatch<4, 2>(a, grid_chunks, prep, s);
     else if (a.HD == 128 && G == 2) attn_dispatch<2, 2>(a, grid_chunks, prep, s);

@@ -27,7 +27,25 @@
 
 using namespace kvd;
 
+namespace kvd {
 namespace {
+thread_local std::string t_launch_err;
+}
+void launch_fail(const char *msg) { if (t_launch_err.empty()) t_launch_err = msg; }
+const char *launch_take_error() {
+    static thread_local std::string taken;
+    if (t_launch_err.empty()) return nullptr;
+    taken.swap(t_launch_err);
+    t_launch_err.clear();
+    return taken.c_str();
+}
+}  // namespace kvd
+
+namespace {
+
+// Largest pmax a handle takes: the decode attention runs at most 4096 chunks
+// of at most 512 positions, the batched passes 4096 chunks of 256.
+constexpr int PMAX_LIMIT = 1 << 20;
 
 typedef __int128 i128;
 typedef unsigned __int128 u128;
@@ -40,6 +58,17 @@ int fail(const char *fmt, const char *a = nullptr, long long b = 0) {
     sp_set_error(buf);
     return 1;
 }
+// A launch error recorded by a launcher (shape outside a kernel's limits)
+// becomes this call's error.
+int take_launch_error(const char *who) {
+    const char *e = launch_take_error();
+    if (!e) return 0;
+    char b[300];
+    snprintf(b, sizeof b, "sp_hipkv: %s: %s", who, e);
+    sp_set_error(b);
+    return 1;
+}
+
 #define HIPCHK(call, what) do { hipError_t e_ = (call); if (e_ != hipSuccess) { \
         char b_[300]; snprintf(b_, sizeof b_, "sp_hipkv: %s: %s", (what), hipGetErrorString(e_)); \
         sp_set_error(b_); return 1; } } while (0)
@@ -186,9 +215,14 @@ int load_weight(const qwen3_model *qm, const gguf_tensor *t, int rows, int cols,
     return 0;
 }
 
-DevModel *model_get(const qwen3_model *qm) {
-    auto it = g_models.find(qm);
-    if (it != g_models.end()) { it->second->refs++; return it->second; }
+// The device model of qm: validated, then uploaded once and shared (refcounted).
+// upload = false validates only (host work, no device call) and returns a
+// DevModel without buffers that the caller deletes.
+DevModel *model_get(const qwen3_model *qm, bool upload = true) {
+    if (upload) {
+        auto it = g_models.find(qm);
+        if (it != g_models.end()) { it->second->refs++; return it->second; }
+    }
     const qwen3_config &c = qm->cfg;
     if (c.arch != SP_ARCH_QWEN3 && c.arch != SP_ARCH_GEMMA3) { fail("sp_hipkv_open: architecture %s not served (Qwen3 / Gemma3 only)", ""); return nullptr; }
     if (!qm->arena) { fail("sp_hipkv_open: model has no packed arena%s", ""); return nullptr; }
@@ -198,6 +232,14 @@ DevModel *model_get(const qwen3_model *qm) {
     const int G = (int)(c.n_head / c.n_head_kv), HD = (int)c.head_dim;
     if (!((HD == 256 && (G == 2 || G == 4)) || (HD == 128 && (G == 2 || G == 4)) || (HD == 64 && (G == 2 || G == 4)))) {
         fail("sp_hipkv_open: unsupported (head_dim, group) combination%s", ""); return nullptr;
+    }
+    if (c.n_layers == 0 || c.n_embd == 0 || c.n_vocab == 0 || c.n_ff == 0) {
+        fail("sp_hipkv_open: model has a zero dimension%s"); return nullptr;
+    }
+    if (c.n_ff % GEMV_R) { fail("sp_hipkv_open: n_ff must be a multiple of %s%lld", "", (long long)GEMV_R); return nullptr; }
+    if (c.arch == SP_ARCH_GEMMA3 && (c.sliding_window <= 0 || c.sliding_window > (4096 - 2) * 64)) {
+        // window layers run 64-position chunks, at most 4096 per launch
+        fail("sp_hipkv_open: sliding window outside [1, %s%lld]", "", (long long)((4096 - 2) * 64)); return nullptr;
     }
     std::unique_ptr<DevModel> m(new DevModel);
     m->qm = qm; m->gemma = c.arch == SP_ARCH_GEMMA3;
@@ -222,6 +264,12 @@ DevModel *model_get(const qwen3_model *qm) {
     auto addn = [&](const gguf_tensor *t, int n, const float **slot) -> int {
         const float *src = t ? sp_as_f32(qm, t) : nullptr;
         if (!src) return fail("sp_hipkv_open: missing norm tensor %s", t ? t->name : "(null)");
+        // the copy behind sp_as_f32 has the tensor's element count: both bridges
+        // (ours and sp_model_bridge.c:217-222) carry the on-disk dims
+        uint64_t ne = t->n_dims ? 1 : 0;
+        for (uint32_t d = 0; d < t->n_dims && d < GGUF_MAX_DIMS; d++) ne *= t->dims[d];
+        if (t->n_dims > GGUF_MAX_DIMS || ne != (uint64_t)n)
+            return fail("sp_hipkv_open: norm tensor %s has the wrong length", t->name);
         norm_off.push_back(up.add(src, (size_t)n * 4));
         norm_slots.push_back(slot);
         return 0;
@@ -245,11 +293,19 @@ DevModel *model_get(const qwen3_model *qm) {
     std::vector<int64_t> fg(HD / 2), fl(HD / 2);
     for (int i = 0; i < HD / 2; i++) { fg[i] = rope_freq_q60(m->base, i, HD); fl[i] = rope_freq_q60(10000.0f, i, HD); }
     const size_t o_fg = up.add(fg.data(), fg.size() * 8), o_fl = up.add(fl.data(), fl.size() * 8);
+    for (auto &pd : pend)
+        m->weight_bytes += (size_t)pd.w->rows * (pd.w->cols / 2) + (size_t)pd.w->rows * pd.w->nblk * 2;
+    const bool tied = qm->output == qm->token_embd;
+    if (tied) m->out = m->embd;
+    m->embd_bytes = (size_t)m->embd.rows * (m->embd.cols / 2) + (size_t)m->embd.rows * m->embd.nblk * 2;
+    m->lm_bytes = (size_t)m->out.rows * (m->out.cols / 2) + (size_t)m->out.rows * m->out.nblk * 2;
+    m->layer_bytes = m->weight_bytes - m->embd_bytes - (tied ? 0 : m->lm_bytes);
+    m->bytes = up.total;
+    if (!upload) return m.release();
 
     if (hipMalloc(&m->buf, up.total) != hipSuccess) {
         fail("sp_hipkv_open: hipMalloc of %s%lld weight bytes failed", "", (long long)up.total); return nullptr;
     }
-    m->bytes = up.total;
     uint8_t *base = (uint8_t *)m->buf;
     for (size_t i = 0; i < up.src.size(); i++)
         if (hipMemcpy(base + up.off[i], up.src[i].first, up.src[i].second, hipMemcpyHostToDevice) != hipSuccess) {
@@ -259,15 +315,9 @@ DevModel *model_get(const qwen3_model *qm) {
         pd.w->codes = base + pd.o[0];
         pd.w->bs = (const uint16_t *)(base + pd.o[1]);
         pd.w->ebase = (const int8_t *)(base + pd.o[2]);
-        const size_t wb = (size_t)pd.w->rows * (pd.w->cols / 2) + (size_t)pd.w->rows * pd.w->nblk * 2;
-        m->weight_bytes += wb;
     }
     for (size_t i = 0; i < norm_slots.size(); i++) *norm_slots[i] = (const float *)(base + norm_off[i]);
-    const bool tied = qm->output == qm->token_embd;
     if (tied) m->out = m->embd;
-    m->embd_bytes = (size_t)m->embd.rows * (m->embd.cols / 2) + (size_t)m->embd.rows * m->embd.nblk * 2;
-    m->lm_bytes = (size_t)m->out.rows * (m->out.cols / 2) + (size_t)m->out.rows * m->out.nblk * 2;
-    m->layer_bytes = m->weight_bytes - m->embd_bytes - (tied ? 0 : m->lm_bytes);
     m->freq_global = (int64_t *)(base + o_fg);
     m->freq_local = (int64_t *)(base + o_fl);
     const RopeConst &rc = rope_const();
@@ -345,6 +395,7 @@ struct sp_kvdecode_handle {
           *ao = nullptr, *ap = nullptr, *gg = nullptr, *uu = nullptr, *hh = nullptr, *dn = nullptr,
           *logits = nullptr, *part = nullptr, *part_ml = nullptr, *am_v = nullptr;
     int *counter = nullptr, *zscratch = nullptr, *am_i = nullptr, *am_cnt = nullptr, *gen_log = nullptr;
+    int *vclamp = nullptr;                   // exact mode: V heads stored with a clamped element
     int *tokbuf = nullptr;                   // DRIVE_STREAM tokens by absolute position
     float *rope = nullptr;                   // [2][HD] rotation table of the current step
     int64_t *vacc = nullptr, *vacc_s = nullptr;
@@ -492,7 +543,7 @@ int alloc_scratch(sp_kvdecode_handle *h) {
         {(void **)&h->am_i, (size_t)amb * 4}, {(void **)&h->am_cnt, 64}, {(void **)&h->gen_log, (size_t)h->pmax * 4 + 64},
         {(void **)&h->tokbuf, (size_t)h->pmax * 4 + 64}, {(void **)&h->rope, (size_t)m->HD * 2 * 4},
         {(void **)&h->vacc, (size_t)QD * 8 * VREP}, {(void **)&h->vacc_s, (size_t)m->NH * 8 * VREP},
-        {(void **)&h->d_st, sizeof(DState) * 4},
+        {(void **)&h->d_st, sizeof(DState) * 4}, {(void **)&h->vclamp, 64},
         {(void **)&h->stats, (size_t)m->NL * STAT_PER_LAYER * STAT_REP * sizeof(VecStat)},
     };
     size_t tot = 0;
@@ -637,7 +688,7 @@ void enqueue_body(sp_kvdecode_handle *h, const StepShape &sh, TimeCb cb, void *c
         a.NH = m->NH; a.NKV = m->NKV; a.HD = m->HD;
         a.win = (m->gemma && !glob) ? m->SW : -1;
         a.max_chunks = h->max_chunks; a.mode = h->mode; a.kvc = h->kvc; a.eps = m->eps;
-        a.zstride = h->max_chunks * 16; a.nt = 0;
+        a.zstride = h->max_chunks * 16; a.nt = 0; a.vclamp = h->vclamp;
         a.base = (m->gemma && !glob) ? 10000.0f : m->base;
         a.ascale = 1.0f / sqrtf((float)m->HD);
         a.chunk = glob ? sh.chunk_global : sh.chunk_local;
@@ -795,7 +846,7 @@ int run_batch(sp_kvdecode_handle *h, int T, int pos0, int pos_hi, bool multi, Ti
         a.max_chunks = b.mcb; a.zstride = h->max_chunks * 16; a.mode = h->mode; a.kvc = h->kvc; a.eps = m->eps;
         a.base = (m->gemma && !glob) ? 10000.0f : m->base;
         a.ascale = 1.0f / sqrtf((float)m->HD);
-        a.nt = T; a.pos0 = pos0; a.rope_stride = 2 * m->HD;
+        a.nt = T; a.pos0 = pos0; a.rope_stride = 2 * m->HD; a.vclamp = h->vclamp;
         if (multi) { a.tpos = b.tpos; a.tpages = b.tpages + (size_t)l * b.TB; }
         a.chunk = (glob || a.win < 0) ? 256 : 64;
         TM(7, true); launch_qk_prep(a, s); TM(7, false);
@@ -837,33 +888,52 @@ int run_batch(sp_kvdecode_handle *h, int T, int pos0, int pos_hi, bool multi, Ti
         launch_argmax_rows(b.logits, m->V, T, b.next, s);
         TM(4, false);
     }
+    if (take_launch_error("batched pass")) return 1;
     HIPCHK(hipGetLastError(), "batch launch");
     return 0;
 }
 
 int prefill_batch(sp_kvdecode_handle *h, int pos0, int T) { return run_batch(h, T, pos0, pos0 + T - 1, false); }
 
+constexpr size_t MAX_GRAPHS = 64;
+
+// The captured step graph of this shape, capturing it on first use.  Past
+// MAX_GRAPHS entries the cache is emptied after the stream has drained (a
+// graph exec still running must not be destroyed).
+int graph_for(sp_kvdecode_handle *h, const StepShape &sh, hipGraphExec_t *out) {
+    sp_kvdecode_handle::GKey key{sh.logits, sh.argmax, sh.grid_global, sh.grid_local, sh.chunk_global};
+    auto it = h->graphs.find(key);
+    if (it != h->graphs.end()) { *out = it->second; return 0; }
+    hipGraph_t g;
+    HIPCHK(hipStreamBeginCapture(h->stream, hipStreamCaptureModeThreadLocal), "graph capture begin");
+    enqueue_body(h, sh, nullptr, nullptr);
+    const hipError_t ec = hipStreamEndCapture(h->stream, &g);
+    if (take_launch_error("step capture")) { if (ec == hipSuccess) hipGraphDestroy(g); return 1; }
+    HIPCHK(ec, "graph capture end");
+    hipGraphExec_t ge;
+    hipError_t e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    hipGraphDestroy(g);
+    HIPCHK(e, "graph instantiate");
+    if (h->graphs.size() >= MAX_GRAPHS) {
+        const hipError_t es = hipStreamSynchronize(h->stream);
+        free_graphs(h);
+        if (es != hipSuccess) { hipGraphExecDestroy(ge); HIPCHK(es, "graph cache eviction"); }
+    }
+    h->graphs.insert({key, ge});
+    *out = ge;
+    return 0;
+}
+
 int run_body(sp_kvdecode_handle *h, const StepShape &sh) {
     if (!h->use_graph) {
         enqueue_body(h, sh, nullptr, nullptr);
+        if (take_launch_error("step launch")) return 1;
         HIPCHK(hipGetLastError(), "kernel launch");
         return 0;
     }
-    sp_kvdecode_handle::GKey key{sh.logits, sh.argmax, sh.grid_global, sh.grid_local, sh.chunk_global};
-    auto it = h->graphs.find(key);
-    if (it == h->graphs.end()) {
-        hipGraph_t g;
-        HIPCHK(hipStreamBeginCapture(h->stream, hipStreamCaptureModeThreadLocal), "graph capture begin");
-        enqueue_body(h, sh, nullptr, nullptr);
-        HIPCHK(hipStreamEndCapture(h->stream, &g), "graph capture end");
-        hipGraphExec_t ge;
-        hipError_t e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
-        hipGraphDestroy(g);
-        HIPCHK(e, "graph instantiate");
-        if (h->graphs.size() > 64) free_graphs(h);
-        it = h->graphs.insert({key, ge}).first;
-    }
-    HIPCHK(hipGraphLaunch(it->second, h->stream), "graph launch");
+    hipGraphExec_t ge;
+    if (graph_for(h, sh, &ge)) return 1;
+    HIPCHK(hipGraphLaunch(ge, h->stream), "graph launch");
     return 0;
 }
 
@@ -907,11 +977,19 @@ int sp_hipkv_open(const void *qm_opaque, int pmax, sp_kvdecode_handle **out) {
     if (!out) return fail("sp_hipkv_open: null out%s");
     *out = nullptr;
     if (!qm_opaque || pmax <= 0) return fail("sp_hipkv_open: null model or pmax <= 0%s");
+    if (pmax > PMAX_LIMIT) return fail("sp_hipkv_open: pmax exceeds the backend's limit of %s%lld positions", "", (long long)PMAX_LIMIT);
     std::lock_guard<std::mutex> lk(g_mu);
+    const qwen3_model *qm = (const qwen3_model *)qm_opaque;
+    if (!g_models.count(qm)) {
+        // the model is validated on the host before any device is touched
+        DevModel *chk = model_get(qm, false);
+        if (!chk) return 1;
+        delete chk;
+    }
     int ndev = 0;
     if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0)
         return fail("sp_hipkv_open: no HIP device visible (this backend runs on MI355X / gfx950)%s");
-    DevModel *m = model_get((const qwen3_model *)qm_opaque);
+    DevModel *m = model_get(qm);
     if (!m) return 1;
     auto new_pool = [m]() { return make_pool(m, FLOAT, KVC_PLAIN); };
     if (sp_kvdecode_handle *sh = take_shell(m, pmax, 0)) {
@@ -920,6 +998,9 @@ int sp_hipkv_open(const void *qm_opaque, int pmax, sp_kvdecode_handle **out) {
         if (sh->kvc != KVC_PLAIN) { sh->kvc = KVC_PLAIN; free_graphs(sh); }   // graphs bake in the codec
         sh->use_graph = 1; sh->use_batch = 1; sh->dpos = 0; sh->hwm = 0;
         sh->pool = new_pool();
+        if (hipMemsetAsync(sh->vclamp, 0, sizeof(int), sh->stream) != hipSuccess) {
+            free_handle(sh); model_put(m); return fail("sp_hipkv_open: clamp counter reset failed%s");
+        }
         size_t tot = 0; for (int l = 0; l < m->NL; l++) tot += (size_t)sh->slots[l];
         for (size_t i = 0; i < tot; i++) sh->h_pt[i] = nullptr;
         if (hipMemcpyAsync(sh->d_pt, sh->h_pt, tot * sizeof(float *), hipMemcpyHostToDevice, sh->stream) != hipSuccess ||
@@ -1222,6 +1303,9 @@ int sp_hipkv_fork(const sp_kvdecode_handle *p, sp_kvdecode_handle **out) {
     }
     if (h->kvc != p->kvc) { h->kvc = p->kvc; free_graphs(h.get()); }        // a recycled shell's graphs
     h->pool = p->pool; h->dpos = p->dpos; h->hwm = p->hwm;
+    if (hipMemsetAsync(h->vclamp, 0, sizeof(int), h->stream) != hipSuccess) {
+        sp_hipkv_close(h.release()); return fail("sp_hipkv_fork: clamp counter reset failed%s");
+    }
     h->use_batch = p->use_batch; h->use_graph = p->use_graph;
     hipStreamSynchronize(p->stream);
     // share every mapped page (copy-on-write on the next append into it)
@@ -1247,6 +1331,14 @@ int sp_hipkv_fork(const sp_kvdecode_handle *p, sp_kvdecode_handle **out) {
 
 sp_status sp_hipkv_attach(sp_session *s, int pmax, int exact) {
     if (!s || pmax <= 0) { sp_set_error("sp_hipkv_attach: bad argument"); return SP_EBADARG; }
+    size_t spos = 0;
+    if (sp_session_position(s, &spos) != SP_OK) return SP_EBADARG;
+    if (spos != 0) {
+        // a fresh handle starts at dpos 0: attaching it to a session with
+        // history would decode at the wrong position
+        sp_set_error("sp_hipkv_attach: the session already holds tokens (attach before the first prefill)");
+        return SP_EBADSTATE;
+    }
     sp_kvdecode_handle *h = nullptr;
     if (sp_hipkv_open(sp_session_qwen3_model(s), pmax, &h)) return SP_EBACKEND_OOM;
     if (exact && sp_hipkv_set_mode(h, 1)) { sp_hipkv_close(h); return SP_EBADSTATE; }
@@ -1255,7 +1347,8 @@ sp_status sp_hipkv_attach(sp_session *s, int pmax, int exact) {
     }
     sp_status st = sp_session_register_kvdecode_backend(s, h, &sp_hipkv_dispatch);
     if (st != SP_OK) { sp_hipkv_close(h); return st; }
-    return spx_session_own_kvdecode(s, 1);
+    st = spx_session_own_kvdecode(s, 1);
+    return st != SP_OK ? st : spx_session_route_kv_lifecycle(s, 1);
 }
 
 int sp_hipkv_greedy(sp_kvdecode_handle *h, int32_t first_token, int n, int32_t *out_tokens, double *device_ms) {
@@ -1267,22 +1360,12 @@ int sp_hipkv_greedy(sp_kvdecode_handle *h, int32_t first_token, int n, int32_t *
     if (set_state(h, h->dpos, first_token, DRIVE_GREEDY)) return 1;
     hipEvent_t e0, e1;
     HIPCHK(hipEventCreate(&e0), "event"); HIPCHK(hipEventCreate(&e1), "event");
-    // pre-instantiate the graphs this run needs so capture is outside the timed region
-    for (int w = h->dpos / 256; w <= (h->dpos + n - 1) / 256; w++) {
+    // pre-instantiate the graphs this run needs so capture is outside the timed
+    // region (runs over more windows than the cache holds re-capture later ones)
+    for (int w = h->dpos / 256; w <= (h->dpos + n - 1) / 256 && h->use_graph; w++) {
         StepShape sh = shape_for(h, std::max(h->dpos, w * 256), 1, 1);
-        if (h->use_graph) {
-            sp_kvdecode_handle::GKey key{sh.logits, sh.argmax, sh.grid_global, sh.grid_local, sh.chunk_global};
-            if (!h->graphs.count(key)) {
-                hipGraph_t g; hipGraphExec_t ge;
-                HIPCHK(hipStreamBeginCapture(h->stream, hipStreamCaptureModeThreadLocal), "capture");
-                enqueue_body(h, sh, nullptr, nullptr);
-                HIPCHK(hipStreamEndCapture(h->stream, &g), "capture end");
-                hipError_t er = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
-                hipGraphDestroy(g);
-                HIPCHK(er, "instantiate");
-                h->graphs[key] = ge;
-            }
-        }
+        hipGraphExec_t ge;
+        if (graph_for(h, sh, &ge)) return 1;
     }
     // the argmax kernel logs each position's token into gen_log[pos]
     HIPCHK(hipEventRecord(e0, h->stream), "event record");
@@ -1336,6 +1419,7 @@ int sp_hipkv_kernel_times(sp_kvdecode_handle *h, int32_t first_token, int n, dou
         const int pos = h->dpos + i;
         StepShape sh = shape_for(h, pos, 1, 1);
         enqueue_body(h, sh, cb, &c);
+        if (take_launch_error("timed step")) { hipStreamSynchronize(h->stream); return 1; }
         for (int k = 0; k < SP_HIPKV_NCLASS; k++) bytes[k] += per_step[k];
         for (int l = 0; l < m->NL; l++) {
             const bool glob = is_global(m, l);
@@ -1381,6 +1465,30 @@ int sp_hipkv_read_kv(const sp_kvdecode_handle *h, int layer, int p0, int n, floa
                 row_out(pb + ((size_t)NKV * PAGE + (size_t)hh * PAGE + p % PAGE) * RB, v + (size_t)(p - p0) * KVD + (size_t)hh * HD);
             }
     }
+    return 0;
+}
+
+int sp_hipkv_v_clamps(const sp_kvdecode_handle *h, long long *count) {
+    if (!h || !count) return fail("sp_hipkv_v_clamps: null argument%s");
+    int c = 0;
+    HIPCHK(hipStreamSynchronize(h->stream), "clamp counter sync");
+    HIPCHK(hipMemcpy(&c, h->vclamp, sizeof c, hipMemcpyDeviceToHost), "clamp counter read");
+    *count = c;
+    return 0;
+}
+
+int sp_hipkv_check_model(const void *qm_opaque, long long out[8]) {
+    if (!qm_opaque || !out) return fail("sp_hipkv_check_model: null argument%s");
+    std::lock_guard<std::mutex> lk(g_mu);
+    DevModel *m = model_get((const qwen3_model *)qm_opaque, false);
+    if (!m) return 1;
+    out[0] = (long long)m->weight_bytes; out[1] = (long long)m->lm_bytes; out[2] = m->NL;
+    out[3] = m->E; out[4] = m->V; out[5] = m->FF; out[6] = m->SW;
+    int wide = m->embd.wide | m->out.wide;
+    for (const DevLayer &d : m->L)
+        for (const DevW *w : {&d.q, &d.k, &d.v, &d.o, &d.gate, &d.up, &d.down}) wide |= w->wide;
+    out[7] = wide;
+    delete m;
     return 0;
 }
 

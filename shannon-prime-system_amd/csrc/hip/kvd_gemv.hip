@@ -414,7 +414,7 @@ void launch_gemv(const GemvArgs &a_in, int nrows_total, hipStream_t s) {
     GemvArgs a = a_in;
     // a wave's row group must not straddle segments
     for (int i = 0; i + 1 < a.nseg; i++)
-        if (a.seg[i].w.rows % GEMV_R) { fprintf(stderr, "kvd: GEMV segment rows %d not a multiple of %d\n", a.seg[i].w.rows, GEMV_R); abort(); }
+        if (a.seg[i].w.rows % GEMV_R) { launch_fail("GEMV segment rows not a multiple of the rows per wave pass"); return; }
     bool wide = false;
     for (int i = 0; i < a.nseg; i++) wide |= a.seg[i].w.wide != 0;
     const bool paired = a.act != ACT_NONE;
@@ -425,7 +425,7 @@ void launch_gemv(const GemvArgs &a_in, int nrows_total, hipStream_t s) {
     int waves = GEMV_WAVES;
     if (a.pro.kind == PRO_PLAIN && p.grid * 2 <= num_cu()) { p.grid *= 2; waves = GEMV_WAVES / 2; }
     if (p.nsplit > 1 && (!a.accbuf || !a.gcnt || nrows_total * (paired ? 2 : 1) > a.acc_rows || p.groups > a.acc_rows)) {
-        fprintf(stderr, "kvd: GEMV split accumulators missing or too small\n"); abort();
+        launch_fail("GEMV split accumulators missing or too small"); return;
     }
     a.nsplit = p.nsplit; a.bps = p.bps; a.groups = p.groups;
     const int nb = p.bps < (a.cols + 31) / 32 ? p.bps : (a.cols + 31) / 32;

@@ -95,6 +95,7 @@ struct AttnArgs {
     const int *tpos;
     float *const *const *tpages;
     VecStat *stat_out;       // decode: statistics of ao for the O GEMV (NULL: none)
+    int *vclamp;             // exact mode: +1 per stored V head with a clamped element (NULL: not counted)
 };
 
 struct Seg { DevW w; float *out; };
@@ -160,6 +161,14 @@ __device__ __forceinline__ int arrive(int *counter) {
 __device__ __forceinline__ void reset_counter(int *counter) {
     __hip_atomic_exchange(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+
+// A launcher whose arguments fall outside its kernel's limits launches nothing
+// and records the first such error of the calling thread; the step drivers
+// collect it after enqueueing (launch_take_error: the message, then clears it;
+// NULL when every launch went out).  The open-time checks keep every shape the
+// backend builds inside these limits, so this is a second line of defence.
+void launch_fail(const char *msg);
+const char *launch_take_error();
 
 // launchers (kvd_kernels.hip)
 void launch_embed(const DevW &embd, const DState *st, const int *tokbuf, float *x, float scale, hipStream_t s,

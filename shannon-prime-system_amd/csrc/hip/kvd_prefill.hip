@@ -295,7 +295,7 @@ __global__ __launch_bounds__(256) void k_gemm_q4b(GemmArgs a) {
 // ------------------------------------------------------------- launchers
 void launch_stage(const StageArgs &a, hipStream_t s) {
     const size_t lds = a.pro.kind == PRO_PLAIN ? 0 : (size_t)a.pro.n * sizeof(float);
-    if (a.pro.n % 32 || a.TP % 32 || a.T > a.TP) { fprintf(stderr, "kvd: stage shape n=%d T=%d TP=%d\n", a.pro.n, a.T, a.TP); abort(); }
+    if (a.pro.n % 32 || a.TP % 32 || a.T > a.TP) { launch_fail("GEMM staging shape outside the kernel's limits"); return; }
     switch (a.pro.kind) {
     case PRO_PLAIN: hipLaunchKernelGGL(k_stage<PRO_PLAIN>, dim3(a.TP), dim3(512), lds, s, a); break;
     case PRO_NORM:  hipLaunchKernelGGL(k_stage<PRO_NORM>, dim3(a.TP), dim3(512), lds, s, a); break;
@@ -311,12 +311,12 @@ void launch_gemm(const GemmArgs &a, int nrows_total, hipStream_t s) {
     const bool paired = a.act != ACT_NONE;
     for (int i = 0; i < a.nseg; i++)
         if (!gemm_supported(a.seg[i].w) || a.seg[i].w.cols != a.cols) {
-            fprintf(stderr, "kvd: GEMM segment %d shape %dx%d not supported\n", i, a.seg[i].w.rows, a.seg[i].w.cols); abort();
+            launch_fail("GEMM segment shape not supported"); return;
         }
-    if (nrows_total % 64 || a.TP % 32 || a.T > a.TP) { fprintf(stderr, "kvd: GEMM rows %d T %d TP %d\n", nrows_total, a.T, a.TP); abort(); }
+    if (nrows_total % 64 || a.TP % 32 || a.T > a.TP) { launch_fail("GEMM rows or token count outside the kernel's limits"); return; }
     // the kernel's buffer offsets are 32-bit: planes (3 x nblk x TP x 32 bytes)
     // and one 16-row slice of codes / scales
-    if ((size_t)3 * (a.cols / 32) * a.TP * 32 >= ((size_t)1 << 31)) { fprintf(stderr, "kvd: GEMM planes too large\n"); abort(); }
+    if ((size_t)3 * (a.cols / 32) * a.TP * 32 >= ((size_t)1 << 31)) { launch_fail("GEMM activation planes exceed 2 GiB"); return; }
     // 32-token tiles per wave (codes unpacked and scales decoded once for two
     // tiles) when that still gives >= 512 workgroups, else 16-token tiles
     // (LDS: 24 KiB per workgroup with 16-token tiles, 48 KiB with 32)

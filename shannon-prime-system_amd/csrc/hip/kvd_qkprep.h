@@ -20,12 +20,13 @@ struct HeadPrep {
     int ring_pages, NH, NKV, HD, mode;
     int kvc;                  // KVC_SPINOR: K/V pass the Spinor-63 codec
     float eps;
+    int *vclamp;              // exact mode: count of V heads stored with a clamped element
 };
 __device__ __forceinline__ HeadPrep head_prep_of(const AttnArgs &a) {
     HeadPrep p;
     p.q = a.q; p.k = a.k; p.v = a.v; p.q_norm = a.q_norm; p.k_norm = a.k_norm; p.rope_cs = a.rope_cs;
     p.qr = a.qr; p.pages = a.pages; p.ring_pages = a.ring_pages; p.NH = a.NH; p.NKV = a.NKV; p.HD = a.HD;
-    p.mode = a.mode; p.kvc = a.kvc; p.eps = a.eps;
+    p.mode = a.mode; p.kvc = a.kvc; p.eps = a.eps; p.vclamp = a.vclamp;
     return p;
 }
 
@@ -127,12 +128,20 @@ __device__ __forceinline__ void head_norm_rope(const HeadPrep &a, const float *s
 }
 
 // The stored form of a K or V element: the float itself, or in exact mode
-// K ki = rne(k * 2^16) and V vq = clamp(rne(v * 2^16), +-(2^23 - 1)).
+// K ki = rne(k * 2^16) and V vq = clamp(rne(v * 2^16), +-(2^23 - 1)) (the
+// bound keeps every V-sum product below 2^45); `clamped` is set when the
+// clamp changed the value (|v| >= 128 - 2^-17).
 __device__ __forceinline__ int32_t kv_code_k(float k) { return (int32_t)rintf(k * 65536.0f); }
-__device__ __forceinline__ int32_t kv_code_v(float v) {
-    float r = rintf(v * 65536.0f);
-    r = fminf(fmaxf(r, -8388607.0f), 8388607.0f);
-    return (int32_t)r;
+__device__ __forceinline__ int32_t kv_code_v(float v, bool &clamped) {
+    const float r = rintf(v * 65536.0f);
+    const float c = fminf(fmaxf(r, -8388607.0f), 8388607.0f);
+    clamped |= c != r;
+    return (int32_t)c;
+}
+// one count per V head (wave) that clamped an element: the caller's flag
+__device__ __forceinline__ void count_v_clamp(int *counter, bool clamped) {
+    if (counter && __any(clamped) && __lane_id() == __builtin_amdgcn_readfirstlane(__lane_id()))
+        atomicAdd(counter, 1);
 }
 
 // A K or V head (lane l holds coordinates l + 64 j) through the Spinor-63
@@ -190,20 +199,24 @@ __device__ __forceinline__ void qk_prep_head_t(const HeadPrep a, int hb, int pos
         } else {
             spinor_head<PER>(x, lane, false, nullptr);
             int32_t *dst = (int32_t *)page + (size_t)a.NKV * PAGE * HD + ((size_t)h * PAGE + slot) * HD;
+            bool cl = false;
             #pragma unroll
-            for (int j = 0; j < 8; j++) if (j < per) dst[lane + 64 * j] = kv_code_v(x[j]);
+            for (int j = 0; j < 8; j++) if (j < per) dst[lane + 64 * j] = kv_code_v(x[j], cl);
+            count_v_clamp(a.vclamp, cl);
         }
         return;
     }
     if (!isq && !isk) {                                         // V: raw (exact: Q16 grid, clamped)
         float *dst = page + (size_t)a.NKV * PAGE * HD + ((size_t)h * PAGE + slot) * HD;
+        bool cl = false;
         #pragma unroll
         for (int j = 0; j < 8; j++) {
             if (j >= per) break;
             const float v = COHERENT ? ld_agent(&src[lane + 64 * j]) : src[lane + 64 * j];
             if (a.mode == FLOAT) dst[lane + 64 * j] = v;
-            else ((int32_t *)dst)[lane + 64 * j] = kv_code_v(v);
+            else ((int32_t *)dst)[lane + 64 * j] = kv_code_v(v, cl);
         }
+        if (a.mode != FLOAT) count_v_clamp(a.vclamp, cl);
         return;
     }
     float out[8];

@@ -152,9 +152,11 @@ static int add_packed(model_bundle *b, const sp_model *sm, const char *name) {
     return 0;
 }
 
-static int add_norm(model_bundle *b, const sp_model *sm, const gguf_tensor *key) {
+/* Owned f32 copy of a norm vector of exactly n elements (a shorter tensor would
+ * let every consumer of the copy read past its end). */
+static int add_norm(model_bundle *b, const sp_model *sm, const gguf_tensor *key, uint64_t n) {
     const sp_tensor_entry *e = sp_model_find_tensor(sm, key->name);
-    if (!e || e->dtype_id != (uint32_t)SP_DT_F32 || !e->size_bytes || (e->size_bytes & 3u)) return 1;
+    if (!e || e->dtype_id != (uint32_t)SP_DT_F32 || !n || e->size_bytes != 4u * n) return 1;
     const void *src = sp_model_tensor_data(sm, e);
     float *dst = src ? (float *)malloc((size_t)e->size_bytes) : NULL;
     if (!dst) return 1;
@@ -224,11 +226,11 @@ static qwen3_model *bridge(const sp_model *sm, uint32_t want_arch, sp_arch_t arc
             snprintf(nm, sizeof nm, "blk.%u.%s.weight", L, nn[k]);
             const gguf_tensor *g = synth_for(b, sm, nm);
             *nslot[k] = g;
-            if (add_norm(b, sm, g)) FAIL(nm);
+            if (add_norm(b, sm, g, (k == 1 || k == 2) ? ai.head_dim : ai.hidden_dim)) FAIL(nm);
         }
     }
     qm->output_norm = synth_for(b, sm, "output_norm.weight");
-    if (add_norm(b, sm, qm->output_norm)) FAIL("output_norm.weight");
+    if (add_norm(b, sm, qm->output_norm, ai.hidden_dim)) FAIL("output_norm.weight");
 #undef FAIL
     int prec = (b->n_ent > 0 && b->ents[0].pt.row_prec[0] == 4u) ? 4 : 8;
     qm->arena = sp_arena_from_packed(b->ents, b->n_ent, prec);

@@ -5,17 +5,24 @@
  * :154-212, decode :725-770, clone :773-816, rewind :818-824, section-6b
  * registration :909-925), with the decode itself always done by the registered
  * section-6b backend.  This library carries no host decode: an unregistered
- * session returns SP_EUNSUPPORTED from prefill/decode (attach the HIP backend
- * with sp_hipkv_attach).
+ * session returns SP_EUNSUPPORTED from prefill/decode.  The reference's own L1
+ * keeps its host path for such sessions; the dispatch table (sp_hipkv_dispatch)
+ * is the drop-in and also runs under that L1 with a registrant that follows the
+ * sp_l1.h:386-402 contract.
  *
- * Routing beyond the reference (the frozen header is unchanged):
+ * Default routing is the reference's (sp_l1.h:396-399): sp_decode_step calls
+ * dt->decode_step and nothing else calls the table -- the registrant drives
+ * dt->prefill and dt->rewind itself, sp_session_rewind only moves the host
+ * position and sp_session_clone leaves the clone unregistered (:792-799).
+ *
+ * Lifecycle routing, opt-in per session (spx_session_route_kv_lifecycle, set
+ * by sp_hipkv_attach; the frozen header is unchanged):
  *  - sp_prefill_chunk: dt->prefill over tokens[0..n-2] then dt->decode_step on
  *    tokens[n-1] for the last-position logits (no O(n^2) re-forward);
- *  - sp_session_rewind: also calls dt->rewind when the table has one;
- *  - sp_session_clone: when the backend exports a fork (sp_hipkv_fork, looked up
- *    through the registered table), the clone gets a copy-on-write fork of the
- *    parent's device KV and owns it; otherwise it is left unregistered, as the
- *    reference does (:792-799). */
+ *  - sp_session_rewind: also calls dt->rewind;
+ *  - sp_session_clone: when the backend registered a fork (spx_register_fork),
+ *    the clone gets a copy-on-write fork of the parent's device KV, owns it and
+ *    inherits the routing; otherwise it is left unregistered. */
 #include "sp_l1_abi.h"
 #include "sp_model_abi.h"
 #include <stdio.h>
@@ -60,6 +67,7 @@ struct sp_session {
     sp_kvdecode_handle *kv_h;
     const sp_kvdecode_dispatch_fn *kv_dt;
     int                 kv_owned;   /* close kv_h on destroy / re-registration */
+    int                 kv_route;   /* lifecycle routing: prefill / rewind / clone reach the table */
 };
 
 static int cancelled(const sp_session *s) { return s->cancel && *s->cancel; }
@@ -96,7 +104,7 @@ sp_status sp_session_create(const sp_model *m, const sp_session_config *cfg,
 
 static void drop_backend(sp_session *s) {
     if (s->kv_owned && s->kv_dt && s->kv_dt->close) s->kv_dt->close(s->kv_h);
-    s->kv_h = NULL; s->kv_dt = NULL; s->kv_owned = 0;
+    s->kv_h = NULL; s->kv_dt = NULL; s->kv_owned = 0; s->kv_route = 0;
 }
 
 void sp_session_destroy(sp_session *s) {
@@ -133,6 +141,13 @@ sp_status sp_prefill_chunk(sp_session *s, const int32_t *tokens, size_t n_tokens
     if (n_tokens > s->hist_cap - s->pos) { sp_set_error("sp_prefill_chunk: context full"); return SP_ECONTEXT_FULL; }
     if (cancelled(s)) return SP_ECANCEL;
     if (!backend_ready(s, "sp_prefill_chunk")) return SP_EUNSUPPORTED;
+    if (!s->kv_route) {
+        /* the reference prefills on the host (a full forward); under the
+         * sp_l1.h contract the registrant feeds dt->prefill itself */
+        sp_set_error("sp_prefill_chunk: this library has no host prefill; drive dt->prefill from the "
+                     "registrant or enable lifecycle routing (spx_session_route_kv_lifecycle / sp_hipkv_attach)");
+        return SP_EUNSUPPORTED;
+    }
     if (n_tokens - 1u > (size_t)0x7FFFFFFF) { sp_set_error("sp_prefill_chunk: chunk too large"); return SP_EBADARG; }
 
     memcpy(s->hist + s->pos, tokens, n_tokens * sizeof(int32_t));
@@ -240,7 +255,7 @@ sp_status sp_session_clone(const sp_session *s, volatile int *cancel_flag, sp_se
     sp_session *c = *out;
     memcpy(c->hist, s->hist, s->pos * sizeof(int32_t));
     c->pos = s->pos;
-    spx_fork_fn fk = fork_for(s->kv_dt);
+    spx_fork_fn fk = s->kv_route ? fork_for(s->kv_dt) : NULL;
     if (fk && s->kv_h) {
         sp_kvdecode_handle *child = NULL;
         if (fk(s->kv_h, &child) || !child) {
@@ -249,7 +264,7 @@ sp_status sp_session_clone(const sp_session *s, volatile int *cancel_flag, sp_se
             if (!prev || !prev[0]) sp_set_error("sp_session_clone: backend fork failed");
             return SP_EBACKEND_OOM;
         }
-        c->kv_h = child; c->kv_dt = s->kv_dt; c->kv_owned = 1;
+        c->kv_h = child; c->kv_dt = s->kv_dt; c->kv_owned = 1; c->kv_route = 1;
     }
     return SP_OK;
 }
@@ -257,7 +272,7 @@ sp_status sp_session_clone(const sp_session *s, volatile int *cancel_flag, sp_se
 sp_status sp_session_rewind(sp_session *s, size_t n_tokens) {
     if (!s) { sp_set_error("sp_session_rewind: null handle"); return SP_EBADARG; }
     if (n_tokens > s->pos) { sp_set_error("sp_session_rewind: n_tokens > position"); return SP_EBADARG; }
-    if (s->kv_dt && s->kv_dt->rewind && n_tokens) {
+    if (s->kv_route && s->kv_dt && s->kv_dt->rewind && n_tokens) {
         if (n_tokens > (size_t)0x7FFFFFFF || s->kv_dt->rewind(s->kv_h, (int)n_tokens)) {
             const char *prev = sp_last_error();
             if (!prev || !prev[0]) sp_set_error("sp_session_rewind: kvdecode backend rewind failed");
@@ -272,14 +287,22 @@ sp_status sp_session_register_kvdecode_backend(sp_session *s, sp_kvdecode_handle
                                                const sp_kvdecode_dispatch_fn *dt) {
     if (!s) { sp_set_error("sp_session_register_kvdecode_backend: null session"); return SP_EBADARG; }
     if (s->kv_owned && s->kv_h != handle) drop_backend(s);
+    if (s->kv_dt != dt || s->kv_h != handle) s->kv_route = 0;   /* a new registration starts on default routing */
     s->kv_h = handle; s->kv_dt = dt;
-    if (!dt) { s->kv_h = NULL; s->kv_owned = 0; }
+    if (!dt) { s->kv_h = NULL; s->kv_owned = 0; s->kv_route = 0; }
     return SP_OK;
 }
 
 sp_status spx_session_own_kvdecode(sp_session *s, int owned) {
     if (!s) { sp_set_error("spx_session_own_kvdecode: null session"); return SP_EBADARG; }
     s->kv_owned = (owned && s->kv_dt) ? 1 : 0;
+    return SP_OK;
+}
+
+sp_status spx_session_route_kv_lifecycle(sp_session *s, int on) {
+    if (!s) { sp_set_error("spx_session_route_kv_lifecycle: null session"); return SP_EBADARG; }
+    if (on && !s->kv_dt) { sp_set_error("spx_session_route_kv_lifecycle: no kvdecode backend registered"); return SP_EBADSTATE; }
+    s->kv_route = on ? 1 : 0;
     return SP_OK;
 }
 

@@ -87,6 +87,7 @@ def l1():
         _sig(lib, "sp_session_kvdecode_backend_handle", c_void_p, [c_void_p])
         _sig(lib, "sp_session_kvdecode_backend_dt", c_void_p, [c_void_p])
         _sig(lib, "spx_session_own_kvdecode", c_int, [c_void_p, c_int])
+        _sig(lib, "spx_session_route_kv_lifecycle", c_int, [c_void_p, c_int])
         _sig(lib, "spx_decode_batch", c_int, [c_void_p, c_size_t, c_void_p, c_void_p, c_size_t, c_void_p])
         _l1 = lib
     return _l1
@@ -120,6 +121,8 @@ def kv():
         _sig(lib, "sp_hipkv_decode_batch_times", c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p])
         _sig(lib, "sp_hipkv_read_kv", c_int, [c_void_p, c_int, c_int, c_int, c_void_p, c_void_p])
         _sig(lib, "sp_hipkv_info", c_int, [c_void_p, c_void_p])
+        _sig(lib, "sp_hipkv_check_model", c_int, [c_void_p, c_void_p])
+        _sig(lib, "sp_hipkv_v_clamps", c_int, [c_void_p, ctypes.POINTER(c_longlong)])
         _kv = lib
     return _kv
 
@@ -137,6 +140,25 @@ def ptr(a):
 def check(rc, what):
     if rc != 0:
         raise RuntimeError(f"{what} failed ({rc}): {last_error()}")
+
+
+# ---------------------------------------------------------------- synthetic inputs
+def splitmix_u64(n, seed):
+    """The first n outputs of SplitMix64 seeded with `seed` (the generator of
+    the synthetic prompts, context lengths and rewind draws)."""
+    import numpy as np
+    k = np.arange(1, n + 1, dtype=np.uint64)
+    with np.errstate(over="ignore"):
+        z = np.uint64(seed) + k * np.uint64(0x9E3779B97F4A7C15)
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+        return z ^ (z >> np.uint64(31))
+
+
+def splitmix_tokens(n, vocab, seed=1):
+    """n prompt tokens uniform in [0, vocab): SplitMix64 output mod vocab."""
+    import numpy as np
+    return (splitmix_u64(n, seed) % np.uint64(vocab)).astype(np.int32)
 
 
 # ---------------------------------------------------------------- shapes
@@ -339,6 +361,11 @@ class Backend:
         v = np.zeros((n, kvd), np.float32)
         check(kv().sp_hipkv_read_kv(self.h, layer, p0, n, ptr(k), ptr(v)), "sp_hipkv_read_kv")
         return k, v
+
+    def v_clamps(self):
+        n = c_longlong()
+        check(kv().sp_hipkv_v_clamps(self.h, ctypes.byref(n)), "sp_hipkv_v_clamps")
+        return n.value
 
     def info(self):
         import numpy as np

@@ -39,3 +39,40 @@ def model_files(dirpath, name, max_context=512, seed=0):
 def prompt(n, vocab, seed=1):
     """Seeded uniform prompt tokens (SplitMix-free numpy generator; test-only)."""
     return np.random.default_rng(seed).integers(0, vocab, size=n).astype(np.int32)
+
+
+def lcg_uniform(state, rng):
+    """core/exact_islands/exact_islands_test.c:196-201 LCG: uniform in [-rng, rng]."""
+    state[0] = (state[0] * 6364136223846793005 + 1442695040888963407) & ((1 << 64) - 1)
+    u = (state[0] >> 11) / float(1 << 53)
+    return (2.0 * u - 1.0) * rng
+
+
+def island_inputs():
+    """The island test vectors: x, w (RMSNorm, E = 3840), z (softmax, 256), g (GELU, 512)."""
+    E, M, G = 3840, 256, 512
+    st = [1]
+    x = np.zeros(E, np.float32); w = np.zeros(E, np.float32)
+    for i in range(E):
+        x[i] = lcg_uniform(st, 2.0); w[i] = 1.0 + lcg_uniform(st, 0.1)
+    st = [7]; z = np.array([lcg_uniform(st, 8.0) for _ in range(M)], np.float32)
+    st = [11]; g = np.array([lcg_uniform(st, 3.0) for _ in range(G)], np.float32)
+    return x, w, z, g
+
+
+SPINOR_KS = [1, 7, 43, 55, 56, 64, 128, 200, 256, 512]
+
+
+def spinor_vectors(k, trials=40):
+    """Seeded Spinor-63 codec inputs of length k: Gaussian at magnitudes 1e-6..1e3,
+    some with zeros, all-zero, and exact half-step ties."""
+    rng = np.random.default_rng(k)
+    out = []
+    for trial in range(trials):
+        x = (rng.standard_normal(k) * (10.0 ** rng.integers(-6, 4))).astype(np.float32)
+        if trial % 5 == 1: x[rng.integers(0, k, max(1, k // 3))] = 0.0
+        if trial % 5 == 2: x[:] = 0.0
+        if trial % 5 == 3:
+            x = (rng.integers(-254, 255, k).astype(np.float32) / 2.0) * np.float32(0.125)
+        out.append(x)
+    return out

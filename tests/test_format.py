@@ -64,9 +64,11 @@ def _sha(b):
     return hashlib.sha256(b).digest()
 
 
-def build_reference_fixture():
+def build_reference_fixture(q_norm_len=None):
     """Byte-for-byte restatement of the reference's qwen3 session fixture
-    (Q8 weights, deterministic patterns, default options)."""
+    (Q8 weights, deterministic patterns, default options).  q_norm_len: write
+    the q-norm vectors with that many elements instead of head_dim (a
+    malformed but otherwise well-formed file)."""
     NL, E, FF, NH, NKV, HD, V, TOKBLOB = 2, 32, 64, 4, 2, 8, 48, 64
     # tokenizer: 128-byte header + blob i & 0xFF; CRC over [0,52) at 52
     th = struct.pack("<IHHIIIIIIIQQ", 0x4B545053, 0, 1, 128, 2, V, 1, 2, 0, 3, 128, TOKBLOB)
@@ -95,7 +97,7 @@ def build_reference_fixture():
         add_q8(f"blk.{L}.attn_k.weight", NKV * HD, E, s + 2)
         add_q8(f"blk.{L}.attn_v.weight", NKV * HD, E, s + 3)
         add_q8(f"blk.{L}.attn_output.weight", E, NH * HD, s + 4)
-        add_f32(f"blk.{L}.attn_q_norm.weight", HD)
+        add_f32(f"blk.{L}.attn_q_norm.weight", q_norm_len or HD)
         add_f32(f"blk.{L}.attn_k_norm.weight", HD)
         add_f32(f"blk.{L}.ffn_norm.weight", E)
         add_q8(f"blk.{L}.ffn_gate.weight", FF, E, s + 5)
@@ -138,6 +140,21 @@ def test_reference_fixture_known_answer(tmp_path):
     s = spkv.Session(m, 256)            # bridge: Q8 weights (served by the loader, not by the HIP path)
     assert spkv.l1().sp_session_qwen3_model(s.h)
     s.close(); m.close()
+
+
+def test_bridge_rejects_short_norm(tmp_path):
+    """A norm tensor shorter than its role's length (head_dim for q_norm) is
+    rejected when the session builds the model view, before anything reads
+    the owned copy past its end."""
+    mb, tk = build_reference_fixture(q_norm_len=6)
+    spm, spt = tmp_path / "short.spm", tmp_path / "short.spt"
+    spm.write_bytes(mb); spt.write_bytes(tk)
+    m = spkv.Model(str(spm), str(spt))                 # the file itself is well formed
+    h = ctypes.c_void_p()
+    cfg = spkv.SessionConfig(64, 1, 0, 0, 0, 0)
+    rc = spkv.l1().sp_session_create(m.h, ctypes.byref(cfg), None, ctypes.byref(h))
+    assert rc == -10 and "attn_q_norm" in spkv.last_error()
+    m.close()
 
 
 def test_reference_fixture_live_sha():

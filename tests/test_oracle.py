@@ -20,7 +20,7 @@ import pytest
 
 import orc
 import spkv
-from helpers import model_files, prompt
+from helpers import island_inputs, model_files, prompt, spinor_vectors
 
 P = orc.ptr
 
@@ -71,22 +71,8 @@ def test_float_clone_rewind_semantics(tmpdir_models):
 
 
 # ---------------------------------------------------------------- islands
-def _udev(state, rng):
-    """core/exact_islands/exact_islands_test.c:196-201 LCG uniform in [-rng, rng]."""
-    state[0] = (state[0] * 6364136223846793005 + 1442695040888963407) & ((1 << 64) - 1)
-    u = (state[0] >> 11) / float(1 << 53)
-    return (2.0 * u - 1.0) * rng
-
-
 def _island_inputs():
-    E, M, G = 3840, 256, 512
-    st = [1]
-    x = np.zeros(E, np.float32); w = np.zeros(E, np.float32)
-    for i in range(E):
-        x[i] = _udev(st, 2.0); w[i] = 1.0 + _udev(st, 0.1)
-    st = [7]; z = np.array([_udev(st, 8.0) for _ in range(M)], np.float32)
-    st = [11]; g = np.array([_udev(st, 3.0) for _ in range(G)], np.float32)
-    return x, w, z, g
+    return island_inputs()
 
 
 def test_islands_bitexact_vs_reference():
@@ -307,13 +293,7 @@ def test_spinor_codec_bitexact_vs_reference(k):
     sp_spinor_encode_vec / sp_spinor_decode_vec (core/vht2/spinor_block.c:128-149)
     on vectors with zeros, ties at half a step, tiny and large magnitudes."""
     R = _ref(); L = orc.lib()
-    rng = np.random.default_rng(k)
-    for trial in range(40):
-        x = (rng.standard_normal(k) * (10.0 ** rng.integers(-6, 4))).astype(np.float32)
-        if trial % 5 == 1: x[rng.integers(0, k, max(1, k // 3))] = 0.0
-        if trial % 5 == 2: x[:] = 0.0
-        if trial % 5 == 3:                                  # exact half-step ties
-            x = (rng.integers(-254, 255, k).astype(np.float32) / 2.0) * np.float32(0.125)
+    for trial, x in enumerate(spinor_vectors(k)):
         nb = L.orc_spinor_blocks_for(k)
         a = np.zeros(63 * nb, np.uint8); b = np.zeros(63 * nb, np.uint8)
         L.orc_spinor_encode_vec(P(x), k, P(a)); R.sp_spinor_encode_vec(P(x), k, P(b))

@@ -4,9 +4,12 @@ counting mock dispatch table (the pattern of core/session/arm_genkv_gate.c:200-2
 Pins the reference's guards and commit points (core/session/sp_session.c
 :154-212, :725-770, :773-824, :909-925): argument errors, context full, cancel
 before any mutation, backend failure -> SP_EBADSTATE with the position unchanged,
-rewind > position -> SP_EBADARG; plus this library's routing extensions (prefill
-= dt->prefill(n-1) + dt->decode_step(last), rewind -> dt->rewind, clone without a
-registered fork drops the registration as the reference does)."""
+rewind > position -> SP_EBADARG.  Default routing is the reference's contract
+(include/sp/sp_l1.h:396-399: only sp_decode_step reaches the table); with
+lifecycle routing switched on (spx_session_route_kv_lifecycle, what
+sp_hipkv_attach does) prefill = dt->prefill(n-1) + dt->decode_step(last),
+rewind -> dt->rewind, and clone without a registered fork drops the
+registration as the reference does."""
 import ctypes
 import os
 import re
@@ -69,10 +72,48 @@ def session(tmpdir_models):
     s.close(); m.close()
 
 
-def register(s, mock):
+def register(s, mock, route=True):
     L = spkv.l1()
     assert L.sp_session_register_kvdecode_backend(s.h, ctypes.c_void_p(0x1234), ctypes.byref(mock.table)) == 0
     assert L.sp_session_kvdecode_backend_handle(s.h) == 0x1234
+    if route:
+        assert L.spx_session_route_kv_lifecycle(s.h, 1) == 0
+
+
+def test_default_routing_is_the_reference_contract(session):
+    """Registered without lifecycle routing: sp_decode_step is the only verb that
+    reaches the table (sp_l1.h:396-399).  The registrant feeds dt->prefill
+    itself (here: once, directly), sp_session_rewind moves only the host
+    position, sp_prefill_chunk does not call the table (this library has no host
+    prefill), and the table sees every token exactly once."""
+    s, _ = session
+    mock = Mock(1000); register(s, mock, route=False)
+    lg = np.zeros(1000, np.float32)
+    toks = (ctypes.c_int32 * 3)(5, 6, 7)
+    assert mock._fns[1](None, toks, 3) == 0                             # the registrant's own dt->prefill
+    assert s.prefill([5, 6, 7], lg) == spkv.SP_EUNSUPPORTED
+    assert "no host prefill" in spkv.last_error()
+    assert s.decode(8, lg) == 0 and s.decode(9, lg) == 0
+    assert mock.calls == [("prefill", [5, 6, 7]), ("step", 8), ("step", 9)]
+    assert s.rewind(1) == 0 and s.position() == 1
+    assert mock.calls[-1] == ("step", 9) and mock.dpos == 5              # no dt->rewind from the session
+    c = s.clone()
+    assert spkv.l1().sp_session_kvdecode_backend_dt(c.h) is None        # reference :792-799
+    c.close()
+
+
+def test_lifecycle_routing_switch(session):
+    s, _ = session
+    L = spkv.l1()
+    assert L.spx_session_route_kv_lifecycle(s.h, 1) == spkv.SP_EBADSTATE   # nothing registered
+    assert L.spx_session_route_kv_lifecycle(None, 1) == spkv.SP_EBADARG
+    mock = Mock(1000); register(s, mock)
+    lg = np.zeros(1000, np.float32)
+    assert s.prefill([1, 2], lg) == 0 and mock.calls == [("prefill", [1]), ("step", 2)]
+    # a new registration (another handle) starts on the default routing again
+    assert L.sp_session_register_kvdecode_backend(s.h, ctypes.c_void_p(0x99), ctypes.byref(mock.table)) == 0
+    assert s.prefill([3], lg) == spkv.SP_EUNSUPPORTED
+    assert L.spx_session_route_kv_lifecycle(s.h, 0) == 0
 
 
 def test_unregistered_session_has_no_host_decode(session):
