@@ -37,8 +37,9 @@ def model_files(dirpath, name, max_context=512, seed=0):
 
 
 def prompt(n, vocab, seed=1):
-    """Seeded uniform prompt tokens (SplitMix-free numpy generator; test-only)."""
-    return np.random.default_rng(seed).integers(0, vocab, size=n).astype(np.int32)
+    """Seeded uniform prompt tokens: SplitMix64 (seed) mod vocab, the generator
+    of the benchmark configurations' prompts."""
+    return spkv.splitmix_tokens(n, vocab, seed=seed)
 
 
 def lcg_uniform(state, rng):

@@ -1,0 +1,186 @@
+"""GPU parity at the benchmark configurations' real shapes (exact mode, through
+the C ABI), against the oracle:
+
+  C2  Qwen3-0.6B, 28 layers: 4096-token prefill (SplitMix64 seed-1 prompt) and
+      256 greedy decode steps.  The device K/V of the first 64 positions equals
+      an oracle prefill; the oracle, given the device K/V of the first 4095
+      positions, reproduces the last prompt position's logits and K/V in every
+      layer; 16 decode steps are bit-exact; after 240 more device steps the
+      oracle, given the new K/V, reproduces the final step.
+  C3  Gemma-3-12B, 48 layers (8 global, 40 with a 1024 window): 32768-token
+      prefill.  K/V written by the batched prefill at a deep position and the
+      last position (written by a decode step) equal the oracle's step from the
+      device K/V before them in all 48 layers; the first decode step is
+      bit-exact; a fork that decodes, rewinds and decodes the same tokens again
+      repeats its logits bit for bit while the parent is untouched.
+  C4  Qwen3-8B, 36 layers, 64 sessions with ragged contexts (SplitMix64 seed 2,
+      shortened to U[48, 400] so the test stays short): every step each
+      session is cloned through sp_session_clone, the parent closed, the clone
+      rewound U{0..4} (seed 3) and all 64 decoded by one spx_decode_batch; the
+      last step's logits of sampled sessions equal the oracle's given that
+      session's device K/V.
+"""
+import numpy as np
+import pytest
+
+import orc
+import spkv
+from helpers import model_files, prompt
+
+pytestmark = [pytest.mark.gpu, pytest.mark.slow]
+
+
+def same_bits(a, b):
+    return np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def window_of(o, layer):
+    """Window of a layer (0: full attention): Gemma-3 layer L is global iff L % 6 == 5."""
+    return o.SW if (o.arch == spkv.ARCH_GEMMA3 and layer % 6 != 5) else 0
+
+
+def load_kv(o, be, p0, p1):
+    """Device K/V of positions [p0, p1) into the oracle (window layers: only the
+    positions the next step attends to), then the oracle's position = p1."""
+    kvd = o.NKV * o.HD
+    for layer in range(o.NL):
+        w = window_of(o, layer)
+        a = max(p0, p1 - w) if w else p0
+        if p1 > a:
+            k, v = be.read_kv(layer, a, p1 - a, kvd)
+            assert o.set_kv(layer, a, k, v) == 0
+    assert o.set_pos(p1) == 0
+
+
+def check_kv_at(o, be, p):
+    kvd = o.NKV * o.HD
+    for layer in range(o.NL):
+        kg, vg = be.read_kv(layer, p, 1, kvd)
+        kc, vc = o.kv(layer, p, 1)
+        assert same_bits(kg, kc) and same_bits(vg, vc), f"position {p} layer {layer}"
+
+
+def test_config2_qwen3_0p6b(tmp_path):
+    spm, spt = model_files(tmp_path, "qwen3-0.6b", max_context=4608)
+    m = spkv.Model(spm, spt); s = spkv.Session(m, 4608)
+    s.attach(4608, exact=True)
+    be = spkv.Backend.wrap(s.backend_handle())
+    o = orc.Oracle(spm, 4608, orc.EXACT)
+    V, kvd = o.V, o.NKV * o.HD
+    pr = prompt(4096, V)
+    lg = np.zeros(V, np.float32)
+    spkv.check(s.prefill(pr, lg), "sp_prefill_chunk")
+    for t in pr[:64]:
+        o.step(int(t), False)
+    for layer in (0, 13, 27):
+        kg, vg = be.read_kv(layer, 0, 64, kvd)
+        kc, vc = o.kv(layer, 0, 64)
+        assert same_bits(kg, kc) and same_bits(vg, vc), f"prefix layer {layer}"
+    load_kv(o, be, 64, 4095)
+    ol = o.step(int(pr[4095]))
+    assert same_bits(lg, ol), "last prompt position"
+    check_kv_at(o, be, 4095)
+    t = int(lg.argmax())
+    for k in range(16):
+        spkv.check(s.decode(t, lg), "sp_decode_step")
+        ol = o.step(t)
+        assert same_bits(lg, ol), f"decode step {k}"
+        t = int(ol.argmax())
+    for k in range(239):
+        spkv.check(s.decode(t, lg), "sp_decode_step")
+        t = int(lg.argmax())
+    pos = be.position()
+    assert pos == 4096 + 255
+    load_kv(o, be, 4096 + 16, pos)
+    spkv.check(s.decode(t, lg), "sp_decode_step")
+    assert same_bits(lg, o.step(t)), "decode step 256"
+    o.close(); s.close(); m.close()
+
+
+@pytest.fixture(scope="module")
+def gemma12b(tmp_path_factory):
+    d = tmp_path_factory.mktemp("gemma12b")
+    spm, spt = spkv.write_model(str(d / "gemma3-12b"), shape="gemma3-12b", seed=0, max_context=32768 + 128)
+    yield spm, spt
+
+
+def test_config3_gemma3_12b_32k(gemma12b):
+    spm, spt = gemma12b
+    ctx, pmax = 32768, 32768 + 64
+    m = spkv.Model(spm, spt); s = spkv.Session(m, pmax)
+    s.attach(pmax, exact=True)
+    be = spkv.Backend.wrap(s.backend_handle())
+    V = 262144
+    pr = prompt(ctx, V)
+    lg = np.zeros(V, np.float32)
+    spkv.check(s.prefill(pr, lg), "sp_prefill_chunk")
+    o = orc.Oracle(spm, pmax, orc.EXACT)
+    # a position written by the batched prefill (not the first of its batch)
+    p = 20000 + 77
+    load_kv(o, be, 0, p)
+    o.step(int(pr[p]), False)
+    check_kv_at(o, be, p)
+    # the last prompt position (a decode step) and its logits
+    load_kv(o, be, p + 1, ctx - 1)
+    ol = o.step(int(pr[ctx - 1]))
+    assert same_bits(lg, ol), "last prompt position logits"
+    check_kv_at(o, be, ctx - 1)
+    # first decode step
+    t = int(lg.argmax())
+    spkv.check(s.decode(t, lg), "sp_decode_step")
+    first = lg.copy()
+    assert same_bits(first, o.step(t)), "decode step 0"
+    o.close()
+    # fork: decode 3, rewind 3, decode the same 3 again -> the same logits; the parent is untouched
+    f = be.fork()
+    toks = [int(first.argmax()), 11, 12]
+    a = []
+    for tk in toks:
+        f.decode(tk, lg); a.append(lg.copy())
+    assert f.rewind(3) == 0
+    for i, tk in enumerate(toks):
+        f.decode(tk, lg)
+        assert same_bits(lg, a[i]), f"fork re-decode {i}"
+    f.close()
+    spkv.check(s.decode(toks[0], lg), "sp_decode_step")
+    assert same_bits(lg, a[0]), "parent after the fork"
+    s.close(); m.close()
+
+
+def test_config4_qwen3_8b_64_sessions(tmp_path):
+    spm, spt = model_files(tmp_path, "qwen3-8b", max_context=512)
+    m = spkv.Model(spm, spt)
+    S, pmax, V = 64, 512, 151936
+    ctxs = (48 + spkv.splitmix_u64(S, 2) % np.uint64(400 - 48 + 1)).astype(np.int64)
+    rew = (spkv.splitmix_u64(S * 8, 3) % np.uint64(5)).astype(np.int64)
+    prompts = prompt(int(ctxs.sum()), V)
+    sess, toks, off = [], [], 0
+    lg = np.zeros(V, np.float32)
+    for i in range(S):
+        s = spkv.Session(m, pmax)
+        s.attach(pmax, exact=True)
+        spkv.check(s.prefill(prompts[off:off + ctxs[i]], lg), "sp_prefill_chunk")
+        off += int(ctxs[i])
+        sess.append(s); toks.append(int(lg.argmax()))
+    for step in range(3):
+        for i in range(S):
+            c = sess[i].clone(); sess[i].close(); sess[i] = c
+            r = int(rew[step * S + i])
+            if r:
+                assert c.rewind(r) == 0
+        rc, lga, nxt = spkv.Session.decode_batch(sess, toks, V)
+        assert rc == 0, spkv.last_error()
+        assert [int(x) for x in nxt] == [int(r.argmax()) for r in lga]
+        if step < 2:
+            toks = [int(x) for x in nxt]
+    # the last step's logits of sampled sessions against the oracle
+    for i in (0, 37):
+        be = spkv.Backend.wrap(sess[i].backend_handle())
+        pos = be.position() - 1                       # the batched step's position
+        o = orc.Oracle(spm, pmax, orc.EXACT)
+        load_kv(o, be, 0, pos)
+        assert same_bits(lga[i], o.step(toks[i])), f"session {i}"
+        o.close()
+    for s in sess:
+        s.close()
+    m.close()

@@ -238,30 +238,35 @@ def test_spinor_codec_guards(tmpdir_models):
     s.close(); m.close()
 
 
-def test_recycled_handle_drops_codec_graphs(tmpdir_models):
+@pytest.mark.parametrize("exact", [True, False])
+def test_recycled_handle_drops_codec_graphs(tmpdir_models, exact):
     """A closed handle is kept as a shell with its captured step graphs; a
     plain handle (or fork) that reuses a Spinor handle's shell decodes as a
-    fresh plain handle does, and the other way round."""
+    fresh plain handle does, and the other way round (exact mode: bit for bit;
+    its step graphs bake the codec into the fused score pass)."""
     spm, spt = model_files(tmpdir_models, "qwen3-hd128")
     m = spkv.Model(spm, spt); s = spkv.Session(m, 128)
     qm = spkv.l1().sp_session_qwen3_model(s.h)
     V = 2048
     pr = prompt(30, V, seed=5)
-    keep = spkv.Backend(qm, 128)                  # keeps the model referenced: closed handles become shells
+    keep = spkv.Backend(qm, 128, exact=exact)     # keeps the model referenced: closed handles become shells
     ref = {}
     for codec in (spkv.KV_PLAIN, spkv.KV_SPINOR):
-        b = spkv.Backend(qm, 128, kv_codec=codec)
+        b = spkv.Backend(qm, 128, exact=exact, kv_codec=codec)
         lg = np.zeros(V, np.float32)
         b.prefill(pr[:-1]); b.decode(int(pr[-1]), lg); b.decode(7, lg)
         ref[codec] = lg.copy()
         b.close()
     assert not same_bits(ref[spkv.KV_PLAIN], ref[spkv.KV_SPINOR])
     for codec in (spkv.KV_PLAIN, spkv.KV_SPINOR, spkv.KV_PLAIN):
-        b = spkv.Backend(qm, 128, kv_codec=codec)
+        b = spkv.Backend(qm, 128, exact=exact, kv_codec=codec)
         lg = np.zeros(V, np.float32)
         b.prefill(pr[:-1]); b.decode(int(pr[-1]), lg)
         f = b.fork(); b.close()
         f.decode(7, lg)
-        assert rel(lg, ref[codec]) < 1e-6, codec
+        if exact:
+            assert same_bits(lg, ref[codec]), codec
+        else:
+            assert rel(lg, ref[codec]) < 1e-6, codec
         f.close()
     keep.close(); s.close(); m.close()
