@@ -29,6 +29,19 @@ int  sp_hipkv_prefill(sp_kvdecode_handle *h, const int32_t *tokens, int n_tok);
 /* decode_step: sp_l1.h:393-395 -- one token at dpos, logits[vocab] of the next
  * position into caller memory, dpos += 1 */
 int  sp_hipkv_decode_step(sp_kvdecode_handle *h, int32_t token, float *logits);
+/* decode_step that allocates nothing -- no counterpart in the reference; for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Same result as
+ * sp_hipkv_decode_step (bit for bit), with plain kernel launches (no graph
+ * instantiation) and the step's transient device memory (GEMV split-K
+ * accumulators and counters, attention partials, score grid, V-sum
+ * accumulators, vector statistics) in the library's static 32 MiB device
+ * buffer instead of the handle's.  Fails, with nothing changed, when the
+ * handle's model and pmax need more step scratch than that (e.g. float mode at
+ * head_dim 256 beyond ~65k positions) or when the position needs a KV page the
+ * pool would have to grow for.  All calls on one GPU share the buffer: calls
+ * that overlap on one GPU (several threads or streams) race. */
+int  sp_hipkv_decode_step_noalloc(sp_kvdecode_handle *h, int32_t token, float *logits);
 /* rewind: sp_l1.h:396 -- O(1): dpos -= n (n <= dpos) */
 int  sp_hipkv_rewind(sp_kvdecode_handle *h, int n);
 /* position: sp_l1.h:397 -- dpos, -1 on NULL */

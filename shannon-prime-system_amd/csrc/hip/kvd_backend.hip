@@ -363,13 +363,27 @@ struct KvPool {
         std::reverse(free_ids.end() - n, free_ids.end());
         return 0;
     }
-    int alloc() {
-        if (free_ids.empty() && grow(1)) return -1;
+    // may_grow = false: only pages already in the pool (no device allocation)
+    int alloc(bool may_grow = true) {
+        if (free_ids.empty() && (!may_grow || grow(1))) return -1;
         const int id = free_ids.back(); free_ids.pop_back();
         refc[id] = 1;
         return id;
     }
     void unref(int id) { if (id >= 0 && --refc[id] == 0) free_ids.push_back(id); }
+};
+
+// The transient device memory of one decode step: GEMV split-K row totals and
+// arrival counters, attention partials, chunk maxima / sums, arrival counters,
+// the exact score grid and V-sum accumulators, and the per-layer vector
+// statistics.  Every accumulator and counter is back at zero when the step's
+// kernels end; the statistics are cleared by the step's first kernel.
+struct StepScratch {
+    int64_t *gacc = nullptr; int *gcnt = nullptr; int acc_rows = 0;
+    float *part = nullptr, *part_ml = nullptr;
+    int *counter = nullptr, *zscratch = nullptr;
+    int64_t *vacc = nullptr, *vacc_s = nullptr;
+    VecStat *stats = nullptr;
 };
 
 }  // namespace
@@ -405,6 +419,7 @@ struct sp_kvdecode_handle {
     int acc_rows = 0;
     float *h_logits = nullptr;               // pinned staging
     int max_chunks = 0;
+    StepScratch ss;                          // the step scratch above, carved from `scratch` (this handle's)
     int attn_cap = 0;                        // exact decode attention workgroups resident at once
     void *scratch = nullptr;
     int built = 0;                           // tables and scratch allocated (reusable as a shell)
@@ -482,7 +497,7 @@ int build_tables(sp_kvdecode_handle *h) {
 
 // Make the pages holding positions [p0, p1) present and exclusively owned in
 // every layer (allocate on first touch, copy-on-write when shared by a fork).
-int ensure_pages(sp_kvdecode_handle *h, int p0, int p1) {
+int ensure_pages(sp_kvdecode_handle *h, int p0, int p1, bool may_grow = true) {
     const DevModel *m = h->m;
     if (p1 <= p0) return 0;
     std::lock_guard<std::mutex> lk(h->pool->mu);
@@ -495,12 +510,14 @@ int ensure_pages(sp_kvdecode_handle *h, int p0, int p1) {
             bool dirty = false;
             int &id = h->pt[l][slot];
             if (id < 0) {
-                id = h->pool->alloc();
-                if (id < 0) return fail("sp_hipkv: KV pool exhausted (hipMalloc failed)%s");
+                id = h->pool->alloc(may_grow);
+                if (id < 0) return fail(may_grow ? "sp_hipkv: KV pool exhausted (hipMalloc failed)%s"
+                                                 : "sp_hipkv: no free KV page without growing the pool%s");
                 dirty = true;
             } else if (h->pool->refc[id] > 1) {
-                const int nid = h->pool->alloc();
-                if (nid < 0) return fail("sp_hipkv: KV pool exhausted during copy-on-write%s");
+                const int nid = h->pool->alloc(may_grow);
+                if (nid < 0) return fail(may_grow ? "sp_hipkv: KV pool exhausted during copy-on-write%s"
+                                                  : "sp_hipkv: no free KV page for copy-on-write without growing the pool%s");
                 HIPCHK(hipMemcpyAsync(h->pool->ptr[nid], h->pool->ptr[id], h->pool->page_bytes,
                                       hipMemcpyDeviceToDevice, h->stream), "copy-on-write page copy");
                 h->pool->unref(id);
@@ -554,6 +571,9 @@ int alloc_scratch(sp_kvdecode_handle *h) {
     HIPCHK(hipMemsetAsync(h->scratch, 0, tot, h->stream), "scratch clear");
     size_t off = 0;
     for (auto &it : items) { *it.p = (uint8_t *)h->scratch + off; off = align_up(off + it.n, 256); }
+    h->ss.gacc = h->gacc; h->ss.gcnt = h->gcnt; h->ss.acc_rows = h->acc_rows;
+    h->ss.part = h->part; h->ss.part_ml = h->part_ml; h->ss.counter = h->counter; h->ss.zscratch = h->zscratch;
+    h->ss.vacc = h->vacc; h->ss.vacc_s = h->vacc_s; h->ss.stats = h->stats;
     HIPCHK(hipHostMalloc(&h->h_st, sizeof(DState) * 4, hipHostMallocDefault), "pinned state alloc");
     HIPCHK(hipHostMalloc(&h->h_logits, (size_t)m->V * 4, hipHostMallocDefault), "pinned logits alloc");
     h->built = 1;
@@ -647,7 +667,7 @@ int attn_chunks(const sp_kvdecode_handle *h, int pos_hi, StepShape &sh) {
 
 typedef void (*TimeCb)(void *ctx, int cls, bool begin);
 
-void enqueue_body(sp_kvdecode_handle *h, const StepShape &sh, TimeCb cb, void *ctx) {
+void enqueue_body(sp_kvdecode_handle *h, const StepShape &sh, TimeCb cb, void *ctx, const StepScratch &ss) {
     const DevModel *m = h->m;
     hipStream_t s = h->stream;
     const int QD = m->NH * m->HD, KVD = m->NKV * m->HD;
@@ -655,7 +675,7 @@ void enqueue_body(sp_kvdecode_handle *h, const StepShape &sh, TimeCb cb, void *c
     T(8, true);
     // per layer: statistics of ao, ap, hh, dn, accumulated by the kernel that
     // writes the vector and read by the GEMV that consumes it
-    VecStat *stat = h->stats;
+    VecStat *stat = ss.stats;
     auto st = [&](int l, int k) { return stat + ((size_t)l * STAT_PER_LAYER + k) * STAT_REP; };
     launch_embed(m->embd, h->d_st, h->tokbuf, h->x1, m->gemma ? sqrtf((float)m->E) : 0.0f, s,
                  stat, m->NL * STAT_PER_LAYER * STAT_REP);
@@ -666,7 +686,7 @@ void enqueue_body(sp_kvdecode_handle *h, const StepShape &sh, TimeCb cb, void *c
         const DevLayer &d = m->L[l];
         const bool glob = is_global(m, l);
         GemvArgs g{};
-        g.accbuf = h->gacc; g.gcnt = h->gcnt; g.acc_rows = h->acc_rows;
+        g.accbuf = ss.gacc; g.gcnt = ss.gcnt; g.acc_rows = ss.acc_rows;
         g.mode = h->mode; g.cols = m->E; g.act = ACT_NONE; g.nseg = 3;
         if (l == 0) { g.pro.kind = PRO_NORM; g.pro.x = h->x1; }
         else {
@@ -682,8 +702,8 @@ void enqueue_body(sp_kvdecode_handle *h, const StepShape &sh, TimeCb cb, void *c
         a.q = h->q; a.k = h->k; a.v = h->v; a.q_norm = d.q_norm; a.k_norm = d.k_norm; a.qr = h->qr;
         a.pages = h->d_pt + h->pt_off[l];
         a.ring_pages = h->slots[l] == h->full_pages ? 0 : h->slots[l];
-        a.ao = h->ao; a.part = h->part; a.part_ml = h->part_ml; a.counter = h->counter; a.zscratch = h->zscratch;
-        a.vacc = h->vacc; a.vacc_s = h->vacc_s;
+        a.ao = h->ao; a.part = ss.part; a.part_ml = ss.part_ml; a.counter = ss.counter; a.zscratch = ss.zscratch;
+        a.vacc = ss.vacc; a.vacc_s = ss.vacc_s;
         a.st = h->d_st; a.rope_cs = h->rope + ((m->gemma && !glob) ? m->HD : 0);
         a.NH = m->NH; a.NKV = m->NKV; a.HD = m->HD;
         a.win = (m->gemma && !glob) ? m->SW : -1;
@@ -702,14 +722,14 @@ void enqueue_body(sp_kvdecode_handle *h, const StepShape &sh, TimeCb cb, void *c
         }
 
         GemvArgs o{};
-        o.accbuf = h->gacc; o.gcnt = h->gcnt; o.acc_rows = h->acc_rows;
+        o.accbuf = ss.gacc; o.gcnt = ss.gcnt; o.acc_rows = ss.acc_rows;
         o.mode = h->mode; o.cols = QD; o.act = ACT_NONE; o.nseg = 1;
         o.pro.kind = PRO_PLAIN; o.pro.x = h->ao; o.pro.n = QD; o.pro.stat = st(l, STAT_AO);
         o.seg[0] = {d.o, h->ap}; o.stat_out = st(l, STAT_AP);
         T(1, true); launch_gemv(o, m->E, s); T(1, false);
 
         GemvArgs f{};
-        f.accbuf = h->gacc; f.gcnt = h->gcnt; f.acc_rows = h->acc_rows;
+        f.accbuf = ss.gacc; f.gcnt = ss.gcnt; f.acc_rows = ss.acc_rows;
         f.mode = h->mode; f.cols = m->E; f.act = m->gemma ? ACT_GELU : ACT_SILU; f.nseg = 2;
         f.pro.kind = PRO_RESID; f.pro.x = h->x1; f.pro.delta = h->ap; f.pro.post_w = d.post_attn;
         f.pro.norm_w = d.ffn_norm; f.pro.x_out = h->x0; f.pro.n = m->E; f.pro.eps = m->eps;
@@ -718,7 +738,7 @@ void enqueue_body(sp_kvdecode_handle *h, const StepShape &sh, TimeCb cb, void *c
         T(2, true); launch_gemv(f, m->FF, s); T(2, false);
 
         GemvArgs dd{};
-        dd.accbuf = h->gacc; dd.gcnt = h->gcnt; dd.acc_rows = h->acc_rows;
+        dd.accbuf = ss.gacc; dd.gcnt = ss.gcnt; dd.acc_rows = ss.acc_rows;
         dd.mode = h->mode; dd.cols = m->FF; dd.act = ACT_NONE; dd.nseg = 1;
         dd.pro.kind = PRO_PLAIN; dd.pro.x = h->hh; dd.pro.n = m->FF; dd.pro.stat = st(l, STAT_HH);
         dd.seg[0] = {d.down, h->dn}; dd.stat_out = st(l, STAT_DN);
@@ -726,7 +746,7 @@ void enqueue_body(sp_kvdecode_handle *h, const StepShape &sh, TimeCb cb, void *c
     }
     if (sh.logits) {
         GemvArgs lm{};
-        lm.accbuf = h->gacc; lm.gcnt = h->gcnt; lm.acc_rows = h->acc_rows;
+        lm.accbuf = ss.gacc; lm.gcnt = ss.gcnt; lm.acc_rows = ss.acc_rows;
         lm.mode = h->mode; lm.cols = m->E; lm.act = ACT_NONE; lm.nseg = 1;
         lm.pro.kind = PRO_RESID; lm.pro.x = h->x0; lm.pro.delta = h->dn;
         lm.pro.post_w = m->gemma ? m->L[m->NL - 1].post_ffw : nullptr;
@@ -906,7 +926,7 @@ int graph_for(sp_kvdecode_handle *h, const StepShape &sh, hipGraphExec_t *out) {
     if (it != h->graphs.end()) { *out = it->second; return 0; }
     hipGraph_t g;
     HIPCHK(hipStreamBeginCapture(h->stream, hipStreamCaptureModeThreadLocal), "graph capture begin");
-    enqueue_body(h, sh, nullptr, nullptr);
+    enqueue_body(h, sh, nullptr, nullptr, h->ss);
     const hipError_t ec = hipStreamEndCapture(h->stream, &g);
     if (take_launch_error("step capture")) { if (ec == hipSuccess) hipGraphDestroy(g); return 1; }
     HIPCHK(ec, "graph capture end");
@@ -926,7 +946,7 @@ int graph_for(sp_kvdecode_handle *h, const StepShape &sh, hipGraphExec_t *out) {
 
 int run_body(sp_kvdecode_handle *h, const StepShape &sh) {
     if (!h->use_graph) {
-        enqueue_body(h, sh, nullptr, nullptr);
+        enqueue_body(h, sh, nullptr, nullptr, h->ss);
         if (take_launch_error("step launch")) return 1;
         HIPCHK(hipGetLastError(), "kernel launch");
         return 0;
@@ -966,6 +986,45 @@ int step_one(sp_kvdecode_handle *h, int32_t tok, int want_logits) {
     StepShape sh = shape_for(h, h->dpos, want_logits, 0);
     if (run_body(h, sh)) return 1;
     return 0;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------ allocation-free decode step
+// Step scratch shared by every allocation-free decode step on a device
+// (sp_hipkv_decode_step_noalloc).  Host code reaches it only through the
+// device address hipGetSymbolAddress returns for the current device.
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)32 << 20;
+static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+__global__ void k_zero_words(uint32_t *p, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = 0u;
+}
+
+std::mutex g_scratch_mu;
+uint8_t *g_scratch_ptr[64];      // per device: the device address of `scratch`
+
+// Carve a step scratch for h out of base[0, NOALLOC_SCRATCH_BYTES); false when
+// h's shape needs more.  *used = bytes to clear.
+bool carve_noalloc(const sp_kvdecode_handle *h, uint8_t *base, StepScratch &ss, size_t *used) {
+    const DevModel *m = h->m;
+    const size_t QD = (size_t)m->NH * m->HD, mc = (size_t)h->max_chunks;
+    const bool exact = h->mode == EXACT;
+    struct Item { void **p; size_t n; };
+    Item items[] = {
+        {(void **)&ss.gacc, (size_t)h->acc_rows * 8}, {(void **)&ss.gcnt, (size_t)h->acc_rows * 4},
+        {(void **)&ss.part, exact ? 256 : (size_t)m->NH * mc * m->HD * 8}, {(void **)&ss.part_ml, (size_t)m->NH * mc * 16},
+        {(void **)&ss.zscratch, exact ? (size_t)m->NH * mc * 16 * 4 : 256}, {(void **)&ss.counter, 256},
+        {(void **)&ss.vacc, QD * 8 * VREP}, {(void **)&ss.vacc_s, (size_t)m->NH * 8 * VREP},
+        {(void **)&ss.stats, (size_t)m->NL * STAT_PER_LAYER * STAT_REP * sizeof(VecStat)},
+    };
+    size_t off = 0;
+    for (auto &it : items) { *it.p = base + off; off = align_up(off + it.n, 256); }
+    ss.acc_rows = h->acc_rows;
+    *used = off;
+    return off <= NOALLOC_SCRATCH_BYTES;
 }
 
 }  // namespace
@@ -1235,6 +1294,46 @@ int sp_hipkv_decode_step(sp_kvdecode_handle *h, int32_t token, float *logits) {
     return 0;
 }
 
+int sp_hipkv_decode_step_noalloc(sp_kvdecode_handle *h, int32_t token, float *logits) {
+    if (!h || !logits) return fail("sp_hipkv_decode_step_noalloc: null argument%s");
+    if (check_tok(h, token)) return 1;
+    if (h->dpos >= h->pmax) return fail("sp_hipkv_decode_step_noalloc: context full (dpos == pmax %s%lld)", "", (long long)h->pmax);
+    int dev = 0;
+    HIPCHK(hipGetDevice(&dev), "sp_hipkv_decode_step_noalloc: device query");
+    if (dev < 0 || dev >= 64) return fail("sp_hipkv_decode_step_noalloc: device index %s%lld out of range", "", (long long)dev);
+    uint8_t *base = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(g_scratch_mu);
+        if (!g_scratch_ptr[dev]) {
+            void *p = nullptr;
+            HIPCHK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "sp_hipkv_decode_step_noalloc: scratch address");
+            g_scratch_ptr[dev] = (uint8_t *)p;
+        }
+        base = g_scratch_ptr[dev];
+    }
+    StepScratch ss;
+    size_t used = 0;
+    if (!carve_noalloc(h, base, ss, &used))
+        return fail("sp_hipkv_decode_step_noalloc: this model and pmax need %s%lld bytes of step scratch, above the "
+                    "33554432-byte static buffer", "", (long long)used);
+    // the pages of this position must exist already (or come from free pages
+    // of the pool): nothing may grow the pool here
+    if (ensure_pages(h, h->dpos, h->dpos + 1, false)) return 1;
+    if (set_state(h, h->dpos, token, DRIVE_HOST)) return 1;
+    // accumulators and counters start at zero (a fill kernel, not a memset
+    // node, so a caller may capture the call)
+    hipLaunchKernelGGL(k_zero_words, dim3(256), dim3(256), 0, h->stream, (uint32_t *)base, used / 4);
+    enqueue_body(h, shape_for(h, h->dpos, 1, 0), nullptr, nullptr, ss);    // plain launches: no graph instantiation
+    if (take_launch_error("sp_hipkv_decode_step_noalloc")) return 1;
+    HIPCHK(hipGetLastError(), "sp_hipkv_decode_step_noalloc: launch");
+    HIPCHK(hipMemcpyAsync(h->h_logits, h->logits, (size_t)h->m->V * 4, hipMemcpyDeviceToHost, h->stream), "logits download");
+    HIPCHK(hipStreamSynchronize(h->stream), "sp_hipkv_decode_step_noalloc");
+    memcpy(logits, h->h_logits, (size_t)h->m->V * 4);
+    h->dpos++;
+    h->hwm = std::max(h->hwm, h->dpos);
+    return 0;
+}
+
 int sp_hipkv_set_mode(sp_kvdecode_handle *h, int exact) {
     if (!h) return fail("sp_hipkv_set_mode: null handle%s");
     const int m = exact ? EXACT : FLOAT;
@@ -1418,7 +1517,7 @@ int sp_hipkv_kernel_times(sp_kvdecode_handle *h, int32_t first_token, int n, dou
     for (int i = 0; i < n; i++) {
         const int pos = h->dpos + i;
         StepShape sh = shape_for(h, pos, 1, 1);
-        enqueue_body(h, sh, cb, &c);
+        enqueue_body(h, sh, cb, &c, h->ss);
         if (take_launch_error("timed step")) { hipStreamSynchronize(h->stream); return 1; }
         for (int k = 0; k < SP_HIPKV_NCLASS; k++) bytes[k] += per_step[k];
         for (int l = 0; l < m->NL; l++) {

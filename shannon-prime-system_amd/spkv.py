@@ -105,6 +105,7 @@ def kv():
         _sig(lib, "sp_hipkv_open", c_int, [c_void_p, c_int, ctypes.POINTER(c_void_p)])
         _sig(lib, "sp_hipkv_prefill", c_int, [c_void_p, c_void_p, c_int])
         _sig(lib, "sp_hipkv_decode_step", c_int, [c_void_p, c_int32, c_void_p])
+        _sig(lib, "sp_hipkv_decode_step_noalloc", c_int, [c_void_p, c_int32, c_void_p])
         _sig(lib, "sp_hipkv_rewind", c_int, [c_void_p, c_int])
         _sig(lib, "sp_hipkv_position", c_int, [c_void_p])
         _sig(lib, "sp_hipkv_close", None, [c_void_p])
