@@ -123,7 +123,7 @@ def main():
     ap.add_argument("--mode", default="exact", choices=["exact", "float"])
     ap.add_argument("--kv", default="plain", choices=["plain", "spinor"],
                     help="session K/V codec: spinor = SP_KV_SPINOR (int8 chunk codes in float mode)")
-    ap.add_argument("--cpu-steps", type=int, default=1)
+    ap.add_argument("--cpu-steps", type=int, default=8)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-steps", type=int, default=8)
     ap.add_argument("--workdir", default=None)
@@ -475,39 +475,76 @@ def calib_copy(nbytes):
 
 
 def cpu_baseline(spm, be, info, shape, exact, n_steps, tok, sess, spinor=False):
-    """Oracle decode steps on the host at the same context, KV loaded from the device."""
+    """The oracle's decode steps on the host at the same context, the K/V state
+    loaded from the device.  Rows: float mode (the reference's arithmetic) and
+    exact mode, each n_steps steps on all host cores (the row-parallel oracle:
+    GEMV rows and attention heads over threads, bit-identical to one thread)
+    and one step on one core.  In the GPU's mode every threaded oracle step is
+    compared with the GPU's logits for the same token (exact mode: bit for
+    bit).  The first row (float, all cores) is the reported value."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import orc
+    spkv = __import__("spkv")
     pos = be.position()
     kvd = shape["n_kv_heads"] * shape["head_dim"]
-    o = orc.Oracle(spm, pos + n_steps + 1, orc.EXACT if exact else orc.FLOAT, kv_flags=orc.KV_SPINOR if spinor else 0)
-    t0 = time.time()
-    win = shape.get("swa_window", 0) if shape.get("arch_id") == __import__("spkv").ARCH_GEMMA3 else 0
-    for layer in range(shape["n_layers"]):
-        # window layers attend the last `win` positions only (Gemma-3: global iff layer % 6 == 5)
-        p0 = max(0, pos - win) if (win and layer % 6 != 5) else 0
-        k, v = be.read_kv(layer, p0, pos - p0, kvd)
-        o.set_kv(layer, p0, k, v)
-        del k, v
-    o.set_pos(pos)
-    log(f"cpu baseline: KV of {pos} positions loaded in {time.time()-t0:.1f}s")
-    # the GPU's logits for the same step, through the ABI (host copy)
+    win = shape.get("swa_window", 0) if shape.get("arch_id") == spkv.ARCH_GEMMA3 else 0
+    threads = min(16, os.cpu_count() or 1)
+    rows, kv = [], None
+
+    def load(o, mode):
+        t0 = time.time()
+        for layer in range(shape["n_layers"]):
+            # window layers attend the last `win` positions only (Gemma-3: global iff layer % 6 == 5)
+            p0 = max(0, pos - win) if (win and layer % 6 != 5) else 0
+            k, v = be.read_kv(layer, p0, pos - p0, kvd)
+            # the other mode's row times its decode over the device state carried
+            # to its grid (int32 values / 2^16, or floats on the Q16 grid), not a
+            # bit-exact replay
+            if mode == "float" and exact:
+                k = k.view(np.int32).astype(np.float32) / np.float32(65536.0)
+                v = v.view(np.int32).astype(np.float32) / np.float32(65536.0)
+            elif mode == "exact" and not exact:
+                k = np.rint(k * np.float32(65536.0)).astype(np.int32).view(np.float32)
+                v = np.clip(np.rint(v * np.float32(65536.0)), -8388607, 8388607).astype(np.int32).view(np.float32)
+            o.set_kv(layer, p0, k, v)
+        o.set_pos(pos)
+        log(f"cpu baseline: KV of {pos} positions loaded in {time.time()-t0:.1f}s")
+
     glog = np.zeros(shape["vocab"], np.float32)
-    spkv_check = __import__("spkv").check
-    t0 = time.time()
-    ol = None
-    for i in range(n_steps):
-        ol = o.step(tok)
-    cpu_s = time.time() - t0
-    spkv_check(sess.decode(tok, glog), "sp_decode_step")
-    same = bool(np.array_equal(ol.view(np.uint32), glog.view(np.uint32))) if n_steps == 1 else None
-    rel = float(np.abs(ol - glog).max() / max(np.abs(ol).max(), 1e-30)) if n_steps == 1 else None
-    log(f"cpu baseline: {n_steps} step(s) in {cpu_s:.1f}s; gpu==cpu bit-exact: {same}, max rel {rel}")
-    o.close()
-    return {"value": round(n_steps / cpu_s, 5), "unit": "tokens/s", "cores": 1, "kind": "port",
-            "sample": f"{n_steps} decode step(s) of the same model at ctx {pos} ({'exact' if exact else 'float'} mode oracle, "
-                      f"KV loaded from the device), {cpu_model()}, nproc {os.cpu_count()}",
-            "gpu_logits_bitexact": same, "gpu_logits_max_rel": rel}
+    L = orc.lib()
+    for mode in ("float", "exact"):
+        gpu_mode = (mode == "exact") == exact
+        o = orc.Oracle(spm, pos + n_steps + 2, orc.EXACT if mode == "exact" else orc.FLOAT,
+                       kv_flags=orc.KV_SPINOR if spinor else 0)
+        load(o, mode)
+        L.orc_set_threads(1)                                  # one core, one step
+        t0 = time.time(); o.step(tok); one_s = time.time() - t0
+        assert o.rewind(1) == 0
+        L.orc_set_threads(threads)                            # all cores, n_steps steps
+        t_tok, cpu_s, same, worst = tok, 0.0, True, 0.0
+        for i in range(n_steps):
+            t0 = time.time(); ol = o.step(t_tok); cpu_s += time.time() - t0
+            if gpu_mode:
+                spkv.check(sess.decode(t_tok, glog), "sp_decode_step")
+                same = same and bool(np.array_equal(ol.view(np.uint32), glog.view(np.uint32)))
+                worst = max(worst, float(np.abs(ol - glog).max() / max(np.abs(ol).max(), 1e-30)))
+            t_tok = int(ol.argmax())
+        o.close()
+        row = {"mode": mode, "cores": threads, "steps": n_steps, "value": round(n_steps / cpu_s, 5),
+               "single_core_value": round(1.0 / one_s, 5)}
+        if gpu_mode:
+            row.update(gpu_logits_bitexact=same, gpu_logits_max_rel=worst)
+        log(f"cpu baseline {mode}: {n_steps} steps on {threads} threads {cpu_s:.1f}s ({row['value']} tok/s), "
+            f"1 step on 1 core {one_s:.1f}s" + (f"; gpu==cpu bit-exact {same}, max rel {worst:.2e}" if gpu_mode else ""))
+        rows.append(row)
+    first = rows[0]
+    return {"value": first["value"], "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{n_steps} decode steps of the same model at ctx {pos} (float-mode oracle, the reference's "
+                      f"arithmetic, row-parallel on {threads} threads; K/V loaded from the device), {cpu_model()}, "
+                      f"nproc {os.cpu_count()}",
+            "rows": rows,
+            "gpu_logits_bitexact": next((r.get("gpu_logits_bitexact") for r in rows if "gpu_logits_bitexact" in r), None),
+            "gpu_logits_max_rel": next((r.get("gpu_logits_max_rel") for r in rows if "gpu_logits_max_rel" in r), None)}
 
 
 if __name__ == "__main__":

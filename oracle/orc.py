@@ -57,6 +57,7 @@ def lib():
             ("orc_i128_div_to_float", c_float, [ctypes.c_int64, ctypes.c_uint64, ctypes.c_int64, c_int]),
             ("orc_vq_of", ctypes.c_int32, [c_float, c_void_p]),
             ("orc_v_clamps", c_int, [c_void_p]),
+            ("orc_set_threads", None, [c_int]), ("orc_threads", c_int, []),
         ]:
             f = getattr(L, name); f.restype = res; f.argtypes = args
         _orc = L

@@ -45,6 +45,13 @@
 typedef __int128 i128;
 typedef unsigned __int128 u128;
 
+/* Threads for the row-parallel loops (GEMV rows, attention heads): each row or
+ * head is computed exactly as in the scalar order, so results do not depend
+ * on the count.  1 = the scalar oracle. */
+static int g_threads = 1;
+void orc_set_threads(int n) { g_threads = n < 1 ? 1 : n; }
+int orc_threads(void) { return g_threads; }
+
 /* ======================= minimal .sp-model reader ======================= */
 typedef struct { char name[80]; uint32_t dtype, n_dims; uint64_t dims[8]; uint64_t off, size;
                  uint32_t bs, bc; uint8_t dig[32]; uint64_t hash; uint8_t pad[40]; } orc_entry;
@@ -210,6 +217,7 @@ static inline int nib(const uint8_t *row, int i) {
 int orc_q4b_gemv(const uint8_t *codes, const uint16_t *bs, int rows, int cols,
                  const float *x, float *y) {
     const size_t rb = (size_t)(cols + 1) / 2, nb = (size_t)(cols + 31) / 32;
+    #pragma omp parallel for schedule(static) num_threads(g_threads) if (g_threads > 1 && rows >= 64)
     for (int j = 0; j < rows; j++) {
         const uint8_t *rc = codes + (size_t)j * rb;
         const uint16_t *b = bs + (size_t)j * nb;
@@ -403,6 +411,7 @@ int orc_q4b_gemv_exact(const uint8_t *codes, const uint16_t *bs, int rows, int c
     if (sh == (1 << 20)) { for (int j = 0; j < rows; j++) y[j] = 0.0f; return 0; }
     int32_t *xq = (int32_t *)malloc((size_t)cols * sizeof(int32_t));
     for (int i = 0; i < cols; i++) xq[i] = (int32_t)rint(ldexp((double)x[i], sh));
+    #pragma omp parallel for schedule(static) num_threads(g_threads) if (g_threads > 1 && rows >= 64)
     for (int j = 0; j < rows; j++) {
         const uint8_t *rc = codes + (size_t)j * rb;
         const uint16_t *b = bs + (size_t)j * nb;
@@ -636,7 +645,7 @@ orc_sess *orc_sess_new_kv(orc_model *m, int max_ctx, int mode, uint32_t kv_flags
     s->vn = (float *)malloc(KVD * sizeof(float)); s->ao = (float *)malloc(QD * sizeof(float));
     s->ap = (float *)malloc(m->E * sizeof(float)); s->gg = (float *)malloc(m->FF * sizeof(float));
     s->up = (float *)malloc(m->FF * sizeof(float)); s->dn = (float *)malloc(m->E * sizeof(float));
-    s->sc = (float *)malloc((size_t)max_ctx * sizeof(float));
+    s->sc = (float *)malloc((size_t)m->NH * (size_t)max_ctx * sizeof(float));   /* one score row per q head */
     s->pd = (double *)malloc((size_t)max_ctx * sizeof(double));
     if (!s->kc || !s->vc || !s->sc || !s->pd) { orc_sess_free(s); return NULL; }
     return s;
@@ -776,16 +785,18 @@ static int step_any(orc_sess *s, int32_t tok, int pos, float *logits) {
                     for (int i = h * HD; i < (h + 1) * HD; i++) { kd[i] = (int32_t)rintf(kn[i] * 65536.0f); vd[i] = vq_of(vn[i], &cl); }
                     s->vclamp += cl;
                 }
+            #pragma omp parallel for schedule(static, 1) num_threads(g_threads) if (g_threads > 1 && pos >= 256)
             for (int h = 0; h < NH; h++)
                 attn_head_exact(q + (size_t)h * HD, (const int32_t *)kcl, (const int32_t *)vcl, pos, KVD,
-                                h / group, HD, ascale, win, sc, ao + (size_t)h * HD);
+                                h / group, HD, ascale, win, sc + (size_t)h * P, ao + (size_t)h * HD);
         } else {
             if (!s->kv_forced) {
                 memcpy(kcl + (size_t)pos * KVD, kn, (size_t)KVD * sizeof(float));
                 memcpy(vcl + (size_t)pos * KVD, vn, (size_t)KVD * sizeof(float));
             }
+            #pragma omp parallel for schedule(static, 1) num_threads(g_threads) if (g_threads > 1 && pos >= 256)
             for (int h = 0; h < NH; h++)
-                orc_attn_head(q + (size_t)h * HD, kcl, vcl, pos, KVD, h / group, HD, ascale, win, sc,
+                orc_attn_head(q + (size_t)h * HD, kcl, vcl, pos, KVD, h / group, HD, ascale, win, sc + (size_t)h * P,
                               ao + (size_t)h * HD);
         }
         GEMV(&ly->o, ao, ap);

@@ -25,6 +25,11 @@ typedef struct orc_sess  orc_sess;
 
 enum { ORC_FLOAT = 0, ORC_EXACT = 1 };
 
+/* threads of the row-parallel loops (GEMV rows, attention heads); results are
+ * the same for every count (each row keeps its scalar order); default 1 */
+void orc_set_threads(int n);
+int  orc_threads(void);
+
 orc_model *orc_model_load(const char *spm_path);
 void       orc_model_free(orc_model *m);
 /* arch_id, vocab, hidden, n_layers, n_heads, n_kv_heads, head_dim, n_ff, swa */

@@ -268,3 +268,22 @@ def test_exact_mode_tracks_float_mode(tmpdir_models, name):
         t = int(lf.argmax())
         lf, le = of.step(t), oe.step(t)
     of.close(); oe.close()
+
+
+@pytest.mark.parametrize("mode", [orc.FLOAT, orc.EXACT])
+def test_oracle_threads_do_not_change_results(tmpdir_models, mode):
+    """The row-parallel oracle (GEMV rows and attention heads over threads) gives
+    bit-identical logits for any thread count."""
+    spm, _ = model_files(tmpdir_models, "gemma3-hd256")
+    L = orc.lib()
+    saved = L.orc_threads()
+    out = []
+    for th in (1, 7):
+        L.orc_set_threads(th)
+        o = orc.Oracle(spm, 400, mode)
+        for i, t in enumerate(prompt(300, o.V)):
+            lg = o.step(int(t), i >= 297)
+        out.append(lg)
+        o.close()
+    L.orc_set_threads(saved)
+    assert np.array_equal(out[0].view(np.uint32), out[1].view(np.uint32))
