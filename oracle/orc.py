@@ -58,6 +58,12 @@ def lib():
             ("orc_vq_of", ctypes.c_int32, [c_float, c_void_p]),
             ("orc_v_clamps", c_int, [c_void_p]),
             ("orc_set_threads", None, [c_int]), ("orc_threads", c_int, []),
+            ("orc_arm_build_R", None, [c_void_p, c_int, c_int]),
+            ("orc_arm_project", None, [c_void_p, c_int, c_int, c_void_p, c_void_p]),
+            ("orc_arm_select", c_int, [c_void_p, c_int, c_int, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int,
+                                       c_void_p, c_void_p]),
+            ("orc_set_recall", c_int, [c_void_p, c_int, c_int, c_int, c_int]),
+            ("orc_recall_sidecar", c_int, [c_void_p, c_int, c_int, c_int, c_void_p]),
         ]:
             f = getattr(L, name); f.restype = res; f.argtypes = args
         _orc = L
@@ -89,6 +95,14 @@ def ref_lib():
             f = getattr(L, name); f.restype = None; f.argtypes = [c_void_p, c_void_p, c_int, c_void_p] if name == "sp_rmsnorm_exact" else [c_void_p, c_int, c_void_p]
         L.sp_softmax_exact.restype = None
         L.sp_softmax_exact.argtypes = [c_void_p, c_int, c_void_p]
+        L.refh_ppl_recall.restype = c_int
+        L.refh_ppl_recall.argtypes = [ctypes.c_char_p, ctypes.c_char_p, c_void_p, c_int, c_int, c_int, c_int, c_int,
+                                      c_int, ctypes.POINTER(c_double)]
+        L.sp_arm_build_R.restype = None
+        L.sp_arm_build_R.argtypes = [c_void_p, c_int, c_int]
+        L.sp_arm_select.restype = c_int
+        L.sp_arm_select.argtypes = [c_void_p, c_int, c_int, c_void_p, c_void_p, ctypes.c_size_t, c_int, c_int, c_int,
+                                    c_int, c_int, c_int, c_int, c_void_p, c_void_p]
         _ref = L
     return _ref
 
@@ -144,6 +158,10 @@ class Oracle:
 
     def set_kv_forced(self, on):
         lib().orc_set_kv_forced(self.s, 1 if on else 0)
+
+    def set_recall(self, B, W=64, sink=4, r=16):
+        if lib().orc_set_recall(self.s, B, W, sink, r):
+            raise RuntimeError("orc_set_recall failed")
 
     def v_clamps(self):
         return lib().orc_v_clamps(self.s)

@@ -5,7 +5,9 @@
 #include "sp/sp_l1.h"
 #include "sp/sp_model.h"
 #include "sp/sp_hash.h"
+#include "sp/model.h"
 #include "qwen3_fixture.h"
+#include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -66,4 +68,35 @@ int refh_qwen3_fixture_sha(uint8_t out[32], size_t *len) {
     *len = info.model_len;
     free(mb); free(tb);
     return 0;
+}
+
+/* The reference's decode-path perplexity (core/forward/decode.c
+ * qwen3_ppl_decode) on a Qwen3 .sp-model with the ARM recall knobs
+ * SP_RECALL_B / _W / _SINK / _R set for the call (B = 0: recall off); the
+ * other knobs are cleared.  Returns 0 and *ppl on success. */
+int refh_ppl_recall(const char *spm, const char *spt, const int32_t *toks, int n, int n_warm,
+                    int B, int W, int sink, int r, double *ppl) {
+    static const char *off[] = {"SP_RING2", "SP_RING2_DISK", "SP_RECALL_DECODE_ONLY", "SP_RECALL_FUSE", "SP_NTT_KV",
+                                "SP_RECALL_BITS", "SP_RECALL_KVSEL", "SP_REPLAY", "SP_ENGINE_NTT_ATTN",
+                                "SP_KV_SPINOR", "SP_KV_SPINOR_REF"};
+    for (size_t i = 0; i < sizeof off / sizeof off[0]; i++) unsetenv(off[i]);
+    char b[32];
+    snprintf(b, sizeof b, "%d", B); setenv("SP_RECALL_B", b, 1);
+    snprintf(b, sizeof b, "%d", W); setenv("SP_RECALL_W", b, 1);
+    snprintf(b, sizeof b, "%d", sink); setenv("SP_RECALL_SINK", b, 1);
+    snprintf(b, sizeof b, "%d", r); setenv("SP_RECALL_R", b, 1);
+    sp_model *m = NULL;
+    if (sp_model_load(spm, spt, &m) != SP_OK) return -1;
+    struct qwen3_model *qm = sp_model_to_qwen3(m);
+    int rc = -2;
+    if (qm) {
+        int32_t *t = (int32_t *)malloc((size_t)n * sizeof(int32_t));
+        memcpy(t, toks, (size_t)n * sizeof(int32_t));
+        rc = qwen3_ppl_decode(qm, t, n, n_warm, ppl, NULL) ? -3 : 0;
+        free(t);
+        qwen3_free(qm);
+    }
+    sp_model_unload(m);
+    unsetenv("SP_RECALL_B");
+    return rc;
 }

@@ -620,6 +620,110 @@ static void spinor_roundtrip(float *v, int k) {
     (void)orc_spinor_decode_vec(blk, k, v);
 }
 
+/* ======================= ARM recall router =======================
+ * Restates core/arm/arm.c: the frozen +-1 projection (SplitMix64 from the seed
+ * of include/sp/arm.h:49, :17-27), the sequential float projection (:31-45),
+ * the descending median-of-three quickselect (:49-76) and the selection
+ * sinks u top-(B-W-sink) u recent-W (:110-160), with the sidecar layout
+ * projk[((L*P + s)*NKV + kvh)*r + p] of arm.h:60-67. */
+#define ORC_ARM_SEED 0x5350524F4A2BULL
+typedef struct { float s; int i; } orc_sidx;
+static uint64_t arm_splitmix(uint64_t *st) {
+    uint64_t z = (*st += 0x9E3779B97F4A7C15ULL);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+    return z ^ (z >> 31);
+}
+void orc_arm_build_R(signed char *R, int r, int hd) {
+    uint64_t st = ORC_ARM_SEED;
+    for (int i = 0; i < r * hd; i++) R[i] = (arm_splitmix(&st) & 1) ? 1 : -1;
+}
+void orc_arm_project(const signed char *R, int r, int hd, const float *vec, float *proj) {
+    for (int p = 0; p < r; p++) {
+        float a = 0.0f;
+        for (int d = 0; d < hd; d++) a += (float)R[(size_t)p * hd + d] * vec[d];
+        proj[p] = a;
+    }
+}
+static void sidx_swap(orc_sidx *a, int i, int j) { orc_sidx t = a[i]; a[i] = a[j]; a[j] = t; }
+static int qsel_partition(orc_sidx *a, int lo, int hi) {
+    const int mid = lo + (hi - lo) / 2;
+    if (a[mid].s > a[lo].s) sidx_swap(a, lo, mid);
+    if (a[hi].s > a[lo].s) sidx_swap(a, lo, hi);
+    if (a[hi].s > a[mid].s) sidx_swap(a, mid, hi);
+    const float pivot = a[mid].s;
+    sidx_swap(a, mid, hi);
+    int store = lo;
+    for (int j = lo; j < hi; j++) if (a[j].s > pivot) { sidx_swap(a, j, store); store++; }
+    sidx_swap(a, store, hi);
+    return store;
+}
+static void qsel_topk(orc_sidx *a, int n, int k) {
+    if (k <= 0 || k >= n) return;
+    int lo = 0, hi = n - 1;
+    while (lo < hi) {
+        const int p = qsel_partition(a, lo, hi);
+        if (p == k) break;
+        else if (p < k) lo = p + 1;
+        else hi = p - 1;
+    }
+}
+/* one head's recall set into ri (returns its size): [0, pos] when B <= 0 or
+ * the context is within budget, else sinks u top-(B-W-sink) u recent-W;
+ * pk: this layer's sidecar rows for kv head kvh, stride nkv*r floats */
+int orc_arm_select(const signed char *R, int r, int hd, const float *qh, const float *pk, int nkv,
+                   int B, int W0, int sink0, int pos, void *cand_v, int *ri) {
+    orc_sidx *cand = (orc_sidx *)cand_v;
+    if (B <= 0 || pos + 1 <= B) { for (int s = 0; s <= pos; s++) ri[s] = s; return pos + 1; }
+    float pq[64];
+    orc_arm_project(R, r, hd, qh, pq);
+    int W = W0 > pos + 1 ? pos + 1 : W0;
+    int sink = sink0 > pos + 1 ? pos + 1 : sink0;
+    int cand_hi = pos + 1 - W;
+    if (cand_hi < sink) cand_hi = sink;
+    if (cand_hi > pos + 1) cand_hi = pos + 1;
+    int topk = B - W - sink; if (topk < 0) topk = 0;
+    if (topk > cand_hi - sink) topk = cand_hi - sink;
+    int nc = 0;
+    for (int s = sink; s < cand_hi; s++) {
+        const float *k = pk + (size_t)s * nkv * r;
+        float a = 0.0f;
+        for (int p = 0; p < r; p++) a += pq[p] * k[p];
+        cand[nc].s = a; cand[nc].i = s; nc++;
+    }
+    if (topk > nc) topk = nc;
+    qsel_topk(cand, nc, topk);
+    int m = 0;
+    for (int s2 = 0; s2 < sink; s2++) ri[m++] = s2;
+    for (int t = 0; t < topk; t++) ri[m++] = cand[t].i;
+    for (int s2 = cand_hi; s2 <= pos; s2++) ri[m++] = s2;
+    return m;
+}
+
+/* float attention of one head over the positions ri[0, mm) in that order
+ * (core/forward/decode.c:755-790: scores, max, exp-sum and V-sum in ri order) */
+static void attn_head_list(const float *qh, const float *KC, const float *VC, const int *ri, int mm, int KVD,
+                           int kvh, int HD, float ascale, float *sc, float *out) {
+    float maxs = -INFINITY;
+    for (int jj = 0; jj < mm; jj++) {
+        const float *kh = KC + (size_t)ri[jj] * KVD + (size_t)kvh * HD;
+        float acc = 0.0f;
+        for (int i = 0; i < HD; i++) acc += qh[i] * kh[i];
+        const float d = acc * ascale;
+        sc[jj] = d;
+        if (d > maxs) maxs = d;
+    }
+    float sum = 0.0f;
+    for (int jj = 0; jj < mm; jj++) { sc[jj] = expf(sc[jj] - maxs); sum += sc[jj]; }
+    const float inv = 1.0f / sum;
+    for (int i = 0; i < HD; i++) out[i] = 0.0f;
+    for (int jj = 0; jj < mm; jj++) {
+        const float w = sc[jj] * inv;
+        const float *vh = VC + (size_t)ri[jj] * KVD + (size_t)kvh * HD;
+        for (int i = 0; i < HD; i++) out[i] += w * vh[i];
+    }
+}
+
 /* ======================= session + steps ======================= */
 struct orc_sess {
     orc_model *m;
@@ -627,6 +731,14 @@ struct orc_sess {
     uint32_t kv_flags;                /* ORC_KV_SPINOR / ORC_KV_SPINOR_REF: K/V pass the Spinor codec */
     int kv_forced;                    /* steps keep the K/V rows resident at pos (set by orc_kv_set) */
     int vclamp;                       /* exact mode: V heads stored with a clamped element */
+    /* ARM recall (orc_set_recall): budget B, window W, sinks, projection rows r;
+     * R [r][HD] frozen +-1 projection, projk [NL][P][NKV][r] sidecar, per-head
+     * selection scratch ri / cand [NH][P] */
+    int rec_B, rec_W, rec_sink, rec_r;
+    signed char *rec_R;
+    float *projk;
+    int *rec_ri;
+    void *rec_cand;
     float *kc, *vc;                   /* [NL][P][KVD]; int32 payload in exact mode */
     float *x, *nx, *q, *kn, *vn, *ao, *ap, *gg, *up, *dn, *sc;
     double *pd;
@@ -653,7 +765,29 @@ orc_sess *orc_sess_new_kv(orc_model *m, int max_ctx, int mode, uint32_t kv_flags
 void orc_sess_free(orc_sess *s) {
     if (!s) return;
     free(s->kc); free(s->vc); free(s->x); free(s->nx); free(s->q); free(s->kn); free(s->vn);
-    free(s->ao); free(s->ap); free(s->gg); free(s->up); free(s->dn); free(s->sc); free(s->pd); free(s);
+    free(s->ao); free(s->ap); free(s->gg); free(s->up); free(s->dn); free(s->sc); free(s->pd);
+    free(s->rec_R); free(s->projk); free(s->rec_ri); free(s->rec_cand); free(s);
+}
+int orc_set_recall(orc_sess *s, int B, int W, int sink, int r) {
+    if (!s || B < 0 || W < 0 || sink < 0 || r < 1 || r > 64) return 1;
+    free(s->rec_R); free(s->projk); free(s->rec_ri); free(s->rec_cand);
+    s->rec_R = NULL; s->projk = NULL; s->rec_ri = NULL; s->rec_cand = NULL;
+    s->rec_B = B; s->rec_W = W; s->rec_sink = sink; s->rec_r = r;
+    if (!B) return 0;
+    const orc_model *m = s->m;
+    s->rec_R = (signed char *)malloc((size_t)r * m->HD);
+    s->projk = (float *)calloc((size_t)m->NL * s->P * m->NKV * r, sizeof(float));
+    s->rec_ri = (int *)malloc((size_t)m->NH * s->P * sizeof(int));
+    s->rec_cand = malloc((size_t)m->NH * s->P * sizeof(orc_sidx));
+    if (!s->rec_R || !s->projk || !s->rec_ri || !s->rec_cand) return 1;
+    orc_arm_build_R(s->rec_R, r, (int)m->HD);
+    return 0;
+}
+int orc_recall_sidecar(const orc_sess *s, int layer, int p0, int n, float *out) {
+    if (!s || !s->projk || layer < 0 || layer >= (int)s->m->NL || p0 < 0 || n < 0 || p0 + n > s->P) return 1;
+    const size_t row = (size_t)s->m->NKV * s->rec_r;
+    memcpy(out, s->projk + ((size_t)layer * s->P + p0) * row, (size_t)n * row * sizeof(float));
+    return 0;
 }
 int orc_pos(const orc_sess *s) { return s->pos; }
 void orc_set_kv_forced(orc_sess *s, int on) { s->kv_forced = on ? 1 : 0; }
@@ -673,6 +807,10 @@ orc_sess *orc_clone(const orc_sess *s) {
     const size_t kv = (size_t)s->m->NL * (size_t)s->P * s->m->NKV * s->m->HD;
     memcpy(c->kc, s->kc, kv * sizeof(float)); memcpy(c->vc, s->vc, kv * sizeof(float));
     c->pos = s->pos; c->kv_filled = s->kv_filled;
+    if (s->rec_B > 0) {
+        if (orc_set_recall(c, s->rec_B, s->rec_W, s->rec_sink, s->rec_r)) { orc_sess_free(c); return NULL; }
+        memcpy(c->projk, s->projk, (size_t)s->m->NL * s->P * s->m->NKV * s->rec_r * sizeof(float));
+    }
     return c;
 }
 int orc_kv_get(const orc_sess *s, int layer, int p0, int n, float *k, float *v) {
@@ -692,33 +830,43 @@ int orc_kv_set(orc_sess *s, int layer, int p0, int n, const float *k, const floa
     return 0;
 }
 
-/* exact-mode attention for one q-head over [s0, pos]; K/V slabs hold int32 */
-static void attn_head_exact(const float *qh, const int32_t *KC, const int32_t *VC, int pos, int KVD,
-                            int kvh, int HD, float ascale, int win, float *sc, float *out) {
-    int s0 = (win >= 0 && pos - win + 1 > 0) ? pos - win + 1 : 0;
+/* exact-mode attention for one q-head over [s0, pos] -- or, with a position
+ * list ri[0, mm), over those positions (recall); K/V slabs hold int32.  Every
+ * sum is an integer, so the list's order does not matter. */
+static void attn_head_exact_sel(const float *qh, const int32_t *KC, const int32_t *VC, int pos, int KVD,
+                                int kvh, int HD, float ascale, int win, const int *ri, int mm, float *out) {
+    const int s0 = (win >= 0 && pos - win + 1 > 0) ? pos - win + 1 : 0;
+    const int n = ri ? mm : pos + 1 - s0;
     int32_t qi[1024];
     for (int i = 0; i < HD; i++) qi[i] = (int32_t)rintf(qh[i] * 65536.0f);
     int64_t mx = INT64_MIN;
-    int64_t *zi = (int64_t *)malloc((size_t)(pos + 1) * sizeof(int64_t));
-    for (int s = s0; s <= pos; s++) {
+    int64_t *zi = (int64_t *)malloc((size_t)(n > 0 ? n : 1) * sizeof(int64_t));
+    for (int j = 0; j < n; j++) {
+        const int s = ri ? ri[j] : s0 + j;
         const int32_t *kh = KC + (size_t)s * KVD + (size_t)kvh * HD;
         int64_t ip = 0;
         for (int i = 0; i < HD; i++) ip += (int64_t)qi[i] * kh[i];
-        sc[s] = (float)((double)ip / 4294967296.0) * ascale;
-        zi[s] = (int64_t)llround((double)sc[s] * 16384.0);
-        if (zi[s] > mx) mx = zi[s];
+        const float scv = (float)((double)ip / 4294967296.0) * ascale;
+        zi[j] = (int64_t)llround((double)scv * 16384.0);
+        if (zi[j] > mx) mx = zi[j];
     }
     int64_t S = 0;
     i128 acc[1024];
     for (int i = 0; i < HD; i++) acc[i] = 0;
-    for (int s = s0; s <= pos; s++) {
-        int64_t e = exp_fixed(((zi[s] - mx) * ONE) >> 14) >> 8;
+    for (int j = 0; j < n; j++) {
+        const int s = ri ? ri[j] : s0 + j;
+        int64_t e = exp_fixed(((zi[j] - mx) * ONE) >> 14) >> 8;
         S += e;
         const int32_t *vh = VC + (size_t)s * KVD + (size_t)kvh * HD;
         for (int i = 0; i < HD; i++) acc[i] += (i128)((int64_t)e * vh[i]);
     }
     for (int i = 0; i < HD; i++) out[i] = i128_div_to_float(acc[i], S, 16);
     free(zi);
+}
+static void attn_head_exact(const float *qh, const int32_t *KC, const int32_t *VC, int pos, int KVD,
+                            int kvh, int HD, float ascale, int win, float *sc, float *out) {
+    (void)sc;
+    attn_head_exact_sel(qh, KC, VC, pos, KVD, kvh, HD, ascale, win, NULL, 0, out);
 }
 
 static int32_t vq_of(float v, int *clamped) {
@@ -771,6 +919,10 @@ static int step_any(orc_sess *s, int32_t tok, int pos, float *logits) {
             if (ex) { orc_rmsnorm_exact(kh, ly->k_norm, HD, kh); orc_rope_exact(kh, HD, pos, rbase); }
             else { rmsnorm_head(kh, ly->k_norm, HD, eps); orc_rope_neox(kh, HD, pos, rbase); }
         }
+        if (s->rec_B > 0 && !s->kv_forced)            /* recall sidecar of the new position (decode.c:493-503) */
+            for (int h = 0; h < NKV; h++)
+                orc_arm_project(s->rec_R, s->rec_r, HD, kn + (size_t)h * HD,
+                                s->projk + (((size_t)L * P + pos) * NKV + h) * (size_t)s->rec_r);
         if (s->kv_forced) { /* the caller's rows at pos stand */ }
         else if (s->kv_flags & (ORC_KV_SPINOR | ORC_KV_SPINOR_REF))
             /* sp_session.c:298-320: the block cache (mode 1) and the in-place
@@ -786,18 +938,40 @@ static int step_any(orc_sess *s, int32_t tok, int pos, float *logits) {
                     s->vclamp += cl;
                 }
             #pragma omp parallel for schedule(static, 1) num_threads(g_threads) if (g_threads > 1 && pos >= 256)
-            for (int h = 0; h < NH; h++)
-                attn_head_exact(q + (size_t)h * HD, (const int32_t *)kcl, (const int32_t *)vcl, pos, KVD,
-                                h / group, HD, ascale, win, sc + (size_t)h * P, ao + (size_t)h * HD);
+            for (int h = 0; h < NH; h++) {
+                if (s->rec_B > 0 && win < 0) {           /* recall: the head's selected positions */
+                    int *ri = s->rec_ri + (size_t)h * P;
+                    const int mm = orc_arm_select(s->rec_R, s->rec_r, HD, q + (size_t)h * HD,
+                                                  s->projk + ((size_t)L * P * NKV + h / group) * s->rec_r, NKV,
+                                                  s->rec_B, s->rec_W, s->rec_sink, pos,
+                                                  (orc_sidx *)s->rec_cand + (size_t)h * P, ri);
+                    attn_head_exact_sel(q + (size_t)h * HD, (const int32_t *)kcl, (const int32_t *)vcl, pos, KVD,
+                                        h / group, HD, ascale, -1, ri, mm, ao + (size_t)h * HD);
+                } else {
+                    attn_head_exact(q + (size_t)h * HD, (const int32_t *)kcl, (const int32_t *)vcl, pos, KVD,
+                                    h / group, HD, ascale, win, sc + (size_t)h * P, ao + (size_t)h * HD);
+                }
+            }
         } else {
             if (!s->kv_forced) {
                 memcpy(kcl + (size_t)pos * KVD, kn, (size_t)KVD * sizeof(float));
                 memcpy(vcl + (size_t)pos * KVD, vn, (size_t)KVD * sizeof(float));
             }
             #pragma omp parallel for schedule(static, 1) num_threads(g_threads) if (g_threads > 1 && pos >= 256)
-            for (int h = 0; h < NH; h++)
-                orc_attn_head(q + (size_t)h * HD, kcl, vcl, pos, KVD, h / group, HD, ascale, win, sc + (size_t)h * P,
-                              ao + (size_t)h * HD);
+            for (int h = 0; h < NH; h++) {
+                if (s->rec_B > 0 && win < 0) {           /* recall: decode.c:740-790 */
+                    int *ri = s->rec_ri + (size_t)h * P;
+                    const int mm = orc_arm_select(s->rec_R, s->rec_r, HD, q + (size_t)h * HD,
+                                                  s->projk + ((size_t)L * P * NKV + h / group) * s->rec_r, NKV,
+                                                  s->rec_B, s->rec_W, s->rec_sink, pos,
+                                                  (orc_sidx *)s->rec_cand + (size_t)h * P, ri);
+                    attn_head_list(q + (size_t)h * HD, kcl, vcl, ri, mm, KVD, h / group, HD, ascale,
+                                   sc + (size_t)h * P, ao + (size_t)h * HD);
+                } else {
+                    orc_attn_head(q + (size_t)h * HD, kcl, vcl, pos, KVD, h / group, HD, ascale, win, sc + (size_t)h * P,
+                                  ao + (size_t)h * HD);
+                }
+            }
         }
         GEMV(&ly->o, ao, ap);
         if (gemma) { NORM(ap, ly->post_attn, E, nx); for (int i = 0; i < E; i++) x[i] += nx[i]; }

@@ -90,6 +90,23 @@ void  orc_attn_head_exact(const float *qh, const int32_t *KC, const int32_t *VC,
 float orc_i128_div_to_float(int64_t num_hi, uint64_t num_lo, int64_t den, int k);
 /* exact-mode V code clamp(rne(v 2^16), +-(2^23-1)); *clamped = 1 when clamped */
 int32_t orc_vq_of(float v, int *clamped);
+/* ---- ARM recall router (core/arm/arm.c, include/sp/arm.h) ---- */
+/* R[r*hd] = +-1 from the frozen SplitMix64 seed */
+void  orc_arm_build_R(signed char *R, int r, int hd);
+/* proj[p] = sum_d R[p,d] * vec[d], sequential float */
+void  orc_arm_project(const signed char *R, int r, int hd, const float *vec, float *proj);
+/* one head's recall set (sp_arm_select semantics): pk = the layer's sidecar for
+ * kv head kvh (stride nkv*r floats per position), cand = (pos+1) {float, int}
+ * scratch; returns the set size, ri in the reference's order */
+int   orc_arm_select(const signed char *R, int r, int hd, const float *qh, const float *pk, int nkv,
+                     int B, int W, int sink, int pos, void *cand, int *ri);
+/* Recall decode (core/forward/decode.c:740-790 with SP_RECALL_B/W/SINK/R):
+ * every full-attention layer attends each q head's recall set; the K
+ * projection sidecar is kept per position.  B = 0 switches it off.  Before the
+ * first token. */
+int   orc_set_recall(orc_sess *s, int B, int W, int sink, int r);
+/* sidecar rows [p0, p0+n) of a layer: NKV*r floats per position */
+int   orc_recall_sidecar(const orc_sess *s, int layer, int p0, int n, float *out);
 /* V heads this session stored with a clamped element (exact mode) */
 int   orc_v_clamps(const orc_sess *s);
 

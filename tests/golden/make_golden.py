@@ -14,6 +14,9 @@ core/session/sp_session.c sp_prefill_chunk :154-212 + sp_decode_step :725-770):
   * cases: the tiny shapes of the tests (Qwen3, Gemma3 with clipping windows,
     an untied head, head_dim 256), the Spinor-63 K/V codec flags, and config 1
     (one Qwen3-0.6B layer, vocab 151936, 512-token prompt, 64 decode steps).
+Recall: the reference's decode-path perplexity (core/forward/decode.c
+qwen3_ppl_decode, through oracle/ref_harness.c refh_ppl_recall) with the ARM
+recall knobs SP_RECALL_B/W/SINK/R, as the exact double (hex).
 Also the reference's exact islands (core/exact_islands/exact_islands.c) on the
 island test vectors and its Spinor-63 codec (core/vht2/spinor_block.c:128-149)
 on seeded vectors, as SHA-256 of the outputs.
@@ -52,6 +55,10 @@ CASES = [
     ("gemma3-tiny", 64, 20, 8, spkv.SP_KV_SPINOR_REF),
     ("qwen3-0.6b-1layer", 1024, 512, 64, 0),
 ]
+
+
+# (B, W, sink, r) of the recall cases; B = 0 is the plain decode path
+RECALL = [(0, 64, 4, 16), (16, 8, 2, 16), (24, 4, 3, 8), (12, 4, 0, 32)]
 
 
 def sha(b):
@@ -95,6 +102,19 @@ def main():
                 "last_logits_head": [float(v).hex() for v in lg[-1][:8]],
             })
             print(f"{name} flags={flags}: {time.time() - t0:.1f}s", file=sys.stderr)
+
+    out["recall"] = []
+    with tempfile.TemporaryDirectory() as d:
+        for name in ("qwen3-tiny", "qwen3-g4"):
+            spm, spt = model(d, name, 64)
+            V = int(SMALL[name]["vocab"])
+            toks = spkv.splitmix_tokens(48, V, seed=1)
+            for B, W, sink, r in RECALL:
+                ppl = ctypes.c_double()
+                if R.refh_ppl_recall(spm.encode(), spt.encode(), P(toks), len(toks), 4, B, W, sink, r, ctypes.byref(ppl)):
+                    sys.exit(f"reference recall decode failed for {name}")
+                out["recall"].append({"model": name, "max_context": 64, "n": 48, "n_warm": 4, "prompt_seed": 1,
+                                      "B": B, "W": W, "sink": sink, "r": r, "ppl_hex": ppl.value.hex()})
 
     x, w, z, g = island_inputs()
     a = np.zeros_like(x); R.sp_rmsnorm_exact(P(x), P(w), x.size, P(a))

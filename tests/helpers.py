@@ -77,3 +77,32 @@ def spinor_vectors(k, trials=40):
             x = (rng.integers(-254, 255, k).astype(np.float32) / 2.0) * np.float32(0.125)
         out.append(x)
     return out
+
+
+def oracle_ppl(o, toks, n_warm):
+    """The decode-path perplexity of core/forward/decode.c qwen3_ppl_decode
+    (:859-874) from an oracle session's logits: for positions pos in
+    [n_warm, n-2], -log softmax(logits_pos)[toks[pos+1]] with the max taken in
+    float, the exp-sum sequential in double (libm exp / log), then
+    exp(mean).  n_warm is clamped to [1, n-2] as the reference does."""
+    import math
+    n = len(toks)
+    n_warm = min(max(n_warm, 1), n - 2)
+    nll, ns = 0.0, 0
+    for pos, t in enumerate(toks):
+        want = pos + 1 < n and pos >= n_warm
+        lg = o.step(int(t), want)
+        if not want:
+            continue
+        tgt = int(toks[pos + 1])
+        m = lg[0]
+        for j in range(1, len(lg)):
+            if lg[j] > m:
+                m = lg[j]
+        maxl = float(m)
+        se = 0.0
+        for v in lg.tolist():
+            se += math.exp(v - maxl)
+        nll += -(float(lg[tgt]) - maxl - math.log(se))
+        ns += 1
+    return math.exp(nll / ns)

@@ -10,7 +10,10 @@ C sources).
     logits come from a full forward that keeps no K/V and carries no codec),
     including config 1 (one Qwen3-0.6B layer, vocab 151936, 512 + 64);
   * the exact islands and the Spinor-63 codec reproduce the reference's output
-    hashes on the shared test vectors.
+    hashes on the shared test vectors;
+  * the oracle's decode with the ARM recall router reproduces the reference's
+    decode-path perplexity (qwen3_ppl_decode with SP_RECALL_B/W/SINK/R) as the
+    exact double.
 """
 import hashlib
 import json
@@ -21,7 +24,7 @@ import pytest
 
 import orc
 import spkv
-from helpers import SMALL, SPINOR_KS, island_inputs, spinor_vectors
+from helpers import SMALL, SPINOR_KS, island_inputs, oracle_ppl, spinor_vectors
 
 GOLDEN = json.load(open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "reference_decode.json")))
 P = orc.ptr
@@ -88,3 +91,15 @@ def test_spinor_codec_matches_reference_golden(k):
         enc.update(b.tobytes()); dec.update(y.tobytes())
     want = GOLDEN["spinor"]["k"][str(k)]
     assert enc.hexdigest() == want["blocks_sha256"] and dec.hexdigest() == want["decoded_sha256"]
+
+
+@pytest.mark.parametrize("case", GOLDEN["recall"], ids=lambda c: f'{c["model"]}-B{c["B"]}-W{c["W"]}-s{c["sink"]}-r{c["r"]}')
+def test_oracle_recall_decode_matches_reference_golden(tmpdir_models, case):
+    c = dict(case, seed=0, flags=0)
+    spm, _ = _files(tmpdir_models, c)
+    o = orc.Oracle(spm, case["max_context"])
+    if case["B"]:
+        o.set_recall(case["B"], case["W"], case["sink"], case["r"])
+    toks = spkv.splitmix_tokens(case["n"], o.V, seed=case["prompt_seed"])
+    assert oracle_ppl(o, toks, case["n_warm"]).hex() == case["ppl_hex"]
+    o.close()

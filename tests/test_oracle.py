@@ -330,3 +330,65 @@ def test_float_decode_spinor_kv_bitexact_vs_reference(tmpdir_models, name, flags
         ol = o.step(int(fed[k]))
         assert np.array_equal(ol.view(np.uint32), lg[k].view(np.uint32)), f"decode step {k}"
     o.close()
+
+
+# ---------------------------------------------------------------- ARM recall router
+def test_recall_projection_matrix_matches_reference():
+    R = _ref(); L = orc.lib()
+    for r, hd in ((16, 128), (8, 64), (32, 256)):
+        a = np.zeros(r * hd, np.int8); b = np.zeros(r * hd, np.int8)
+        L.orc_arm_build_R(P(a), r, hd); R.sp_arm_build_R(P(b), r, hd)
+        assert np.array_equal(a, b) and set(np.unique(a)) == {-1, 1}
+
+
+@pytest.mark.parametrize("ties", [False, True])
+def test_recall_selection_matches_reference(ties):
+    """orc_arm_select against the reference's sp_arm_select (core/arm/arm.c:
+    110-160): the same positions in the same order, including the
+    quickselect's arrangement when projected scores tie (duplicated sidecar
+    rows), for budgets below and above the context, windows and sinks."""
+    R = _ref(); L = orc.lib()
+    rng = np.random.default_rng(8 + ties)
+    for trial in range(40):
+        hd, r, nkv = (64, 16, 2) if trial % 2 else (128, 8, 4)
+        P_, layer = 300, int(rng.integers(0, 3))
+        Rm = np.zeros(r * hd, np.int8); L.orc_arm_build_R(P(Rm), r, hd)
+        projk = rng.standard_normal((3, P_, nkv, r)).astype(np.float32)
+        if ties:
+            src = rng.integers(0, P_, 40)
+            projk[layer, rng.integers(0, P_, 40)] = projk[layer, src]
+        q = rng.standard_normal(hd).astype(np.float32)
+        pos = int(rng.integers(1, P_))
+        B, W, sink, kvh = int(rng.integers(0, 120)), int(rng.integers(0, 40)), int(rng.integers(0, 6)), int(rng.integers(0, nkv))
+        cand_a = np.zeros(2 * P_, np.int32); ri_a = np.zeros(P_, np.int32)
+        cand_b = np.zeros(2 * P_, np.int32); ri_b = np.zeros(P_, np.int32)
+        flat = np.ascontiguousarray(projk)
+        pk = flat[layer, :, kvh, :]                         # this head's rows, stride nkv*r
+        base = flat.ctypes.data + ((layer * P_ * nkv + kvh) * r) * 4
+        ma = L.orc_arm_select(P(Rm), r, hd, P(q), ctypes.c_void_p(base), nkv, B, W, sink, pos, P(cand_a), P(ri_a))
+        mb = R.sp_arm_select(P(Rm), r, hd, P(q), P(flat), layer, P_, nkv, kvh, B, W, sink, pos, P(cand_b), P(ri_b))
+        assert ma == mb and np.array_equal(ri_a[:ma], ri_b[:mb]), trial
+        assert pk.shape == (P_, r)
+
+
+@pytest.mark.parametrize("cfg", [(0, 64, 4, 16), (16, 8, 2, 16), (24, 4, 3, 8), (12, 4, 0, 32)])
+def test_recall_decode_matches_reference_ppl(tmpdir_models, cfg):
+    """Teacher-forced decode with the ARM recall router (the reference's
+    qwen3_ppl_decode with SP_RECALL_B/W/SINK/R, core/forward/decode.c:740-790,
+    :859-874): the oracle's float decode with the same recall settings gives
+    the same perplexity to the last bit of the double -- every scored logit,
+    every selected set and the order of every float sum agree."""
+    from helpers import oracle_ppl
+    R = _ref()
+    B, W, sink, r = cfg
+    for name in ("qwen3-tiny", "qwen3-g4"):
+        spm, spt = model_files(tmpdir_models, name)
+        o = orc.Oracle(spm, 64)
+        toks = prompt(48, o.V)
+        if B:
+            o.set_recall(B, W, sink, r)
+        mine = oracle_ppl(o, toks, 4)
+        o.close()
+        ref = ctypes.c_double()
+        assert R.refh_ppl_recall(spm.encode(), spt.encode(), P(toks), len(toks), 4, B, W, sink, r, ctypes.byref(ref)) == 0
+        assert mine.hex() == ref.value.hex(), (name, mine, ref.value)
