@@ -74,6 +74,21 @@ int  sp_hipkv_fork(const sp_kvdecode_handle *parent, sp_kvdecode_handle **child)
  * padded to 16, for 4 HD); exact mode keeps the decoded values' int32 grid.
  * Head dims 64, 128, 256.  Only before the first token (dpos == 0). */
 int  sp_hipkv_set_kv_codec(sp_kvdecode_handle *h, int codec);
+/* ARM recall router on the global-attention layers (replaces the reference's
+ * SP_RECALL_B / SP_RECALL_W / SP_RECALL_SINK / SP_RECALL_R knobs with
+ * SP_RECALL_DECODE_ONLY=1, core/forward/decode.c:85-98 and :561, router
+ * core/arm/arm.c:17-160): every appended K head is projected on the frozen
+ * +-1 matrix (r rows, seed of include/sp/arm.h:49) into a sidecar kept in the
+ * KV pages; at each decode step each q head attends only over sinks u
+ * top-(B-W-sink) by projected score u the recent W positions (all positions
+ * while the context holds at most B).  Prefill attends densely and writes the
+ * sidecar.  B = 0 switches recall off.  r in [1, 64]; head dims 64, 128, 256;
+ * not with Spinor code rows in float mode.  Only before the first token
+ * (dpos == 0).  Forks inherit it; batched decodes step such handles one by one. */
+int  sp_hipkv_set_recall(sp_kvdecode_handle *h, int B, int W, int sink, int r);
+/* The recall sidecar of a global layer for positions [p0, p0+n): [n][n_kv_heads][r]
+ * floats (the reference's projk rows, include/sp/arm.h:60-67). */
+int  sp_hipkv_read_recall_sidecar(const sp_kvdecode_handle *h, int layer, int p0, int n, float *out);
 /* Register the backend on a session: open(sp_session_qwen3_model(s), pmax) +
  * sp_session_register_kvdecode_backend + ownership (closed with the session) +
  * lifecycle routing (spx_session_route_kv_lifecycle: prefill, rewind and clone

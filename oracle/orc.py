@@ -64,6 +64,7 @@ def lib():
                                        c_void_p, c_void_p]),
             ("orc_set_recall", c_int, [c_void_p, c_int, c_int, c_int, c_int]),
             ("orc_recall_sidecar", c_int, [c_void_p, c_int, c_int, c_int, c_void_p]),
+            ("orc_set_recall_dense", None, [c_void_p, c_int]),
         ]:
             f = getattr(L, name); f.restype = res; f.argtypes = args
         _orc = L
@@ -98,6 +99,9 @@ def ref_lib():
         L.refh_ppl_recall.restype = c_int
         L.refh_ppl_recall.argtypes = [ctypes.c_char_p, ctypes.c_char_p, c_void_p, c_int, c_int, c_int, c_int, c_int,
                                       c_int, ctypes.POINTER(c_double)]
+        L.refh_generate_recall.restype = c_int
+        L.refh_generate_recall.argtypes = [ctypes.c_char_p, ctypes.c_char_p, c_void_p, c_int, c_int, c_int, c_int,
+                                           c_int, c_int, c_int]
         L.sp_arm_build_R.restype = None
         L.sp_arm_build_R.argtypes = [c_void_p, c_int, c_int]
         L.sp_arm_select.restype = c_int
@@ -162,6 +166,17 @@ class Oracle:
     def set_recall(self, B, W=64, sink=4, r=16):
         if lib().orc_set_recall(self.s, B, W, sink, r):
             raise RuntimeError("orc_set_recall failed")
+        self.rec_r = r
+
+    def set_recall_dense(self, on):
+        lib().orc_set_recall_dense(self.s, 1 if on else 0)
+
+    def recall_sidecar(self, layer, p0, n):
+        import numpy as np
+        out = np.zeros((n, self.NKV, self.rec_r), np.float32)
+        if lib().orc_recall_sidecar(self.s, layer, p0, n, ptr(out)):
+            raise RuntimeError("orc_recall_sidecar failed")
+        return out
 
     def v_clamps(self):
         return lib().orc_v_clamps(self.s)

@@ -100,3 +100,32 @@ int refh_ppl_recall(const char *spm, const char *spt, const int32_t *toks, int n
     unsetenv("SP_RECALL_B");
     return rc;
 }
+
+/* qwen3_generate_kv (decode.c:909-912) greedy over n_gen tokens after the
+ * prompt with the ARM recall knobs; decode_only sets SP_RECALL_DECODE_ONLY=1
+ * (dense prompt, the router at the generated positions).  seq: n_prompt +
+ * n_gen ints, the prompt in front; returns the number generated or < 0. */
+int refh_generate_recall(const char *spm, const char *spt, int32_t *seq, int n_prompt, int n_gen,
+                         int B, int W, int sink, int r, int decode_only) {
+    static const char *off[] = {"SP_RING2", "SP_RING2_DISK", "SP_RECALL_DECODE_ONLY", "SP_RECALL_FUSE", "SP_NTT_KV",
+                                "SP_RECALL_BITS", "SP_RECALL_KVSEL", "SP_REPLAY", "SP_ENGINE_NTT_ATTN",
+                                "SP_KV_SPINOR", "SP_KV_SPINOR_REF"};
+    for (size_t i = 0; i < sizeof off / sizeof off[0]; i++) unsetenv(off[i]);
+    char b[32];
+    snprintf(b, sizeof b, "%d", B); setenv("SP_RECALL_B", b, 1);
+    snprintf(b, sizeof b, "%d", W); setenv("SP_RECALL_W", b, 1);
+    snprintf(b, sizeof b, "%d", sink); setenv("SP_RECALL_SINK", b, 1);
+    snprintf(b, sizeof b, "%d", r); setenv("SP_RECALL_R", b, 1);
+    if (decode_only) setenv("SP_RECALL_DECODE_ONLY", "1", 1);
+    sp_model *m = NULL;
+    if (sp_model_load(spm, spt, &m) != SP_OK) return -1;
+    struct qwen3_model *qm = sp_model_to_qwen3(m);
+    int rc = -2;
+    if (qm) {
+        rc = qwen3_generate_kv(qm, seq, n_prompt, n_gen, -1);
+        qwen3_free(qm);
+    }
+    sp_model_unload(m);
+    unsetenv("SP_RECALL_B"); unsetenv("SP_RECALL_DECODE_ONLY");
+    return rc;
+}

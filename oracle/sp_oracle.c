@@ -735,6 +735,7 @@ struct orc_sess {
      * R [r][HD] frozen +-1 projection, projk [NL][P][NKV][r] sidecar, per-head
      * selection scratch ri / cand [NH][P] */
     int rec_B, rec_W, rec_sink, rec_r;
+    int rec_dense;                    /* orc_set_recall_dense: effective budget 0 (identity lists) */
     signed char *rec_R;
     float *projk;
     int *rec_ri;
@@ -783,6 +784,7 @@ int orc_set_recall(orc_sess *s, int B, int W, int sink, int r) {
     orc_arm_build_R(s->rec_R, r, (int)m->HD);
     return 0;
 }
+void orc_set_recall_dense(orc_sess *s, int on) { s->rec_dense = on ? 1 : 0; }
 int orc_recall_sidecar(const orc_sess *s, int layer, int p0, int n, float *out) {
     if (!s || !s->projk || layer < 0 || layer >= (int)s->m->NL || p0 < 0 || n < 0 || p0 + n > s->P) return 1;
     const size_t row = (size_t)s->m->NKV * s->rec_r;
@@ -811,6 +813,7 @@ orc_sess *orc_clone(const orc_sess *s) {
         if (orc_set_recall(c, s->rec_B, s->rec_W, s->rec_sink, s->rec_r)) { orc_sess_free(c); return NULL; }
         memcpy(c->projk, s->projk, (size_t)s->m->NL * s->P * s->m->NKV * s->rec_r * sizeof(float));
     }
+    c->rec_dense = s->rec_dense;
     return c;
 }
 int orc_kv_get(const orc_sess *s, int layer, int p0, int n, float *k, float *v) {
@@ -943,7 +946,7 @@ static int step_any(orc_sess *s, int32_t tok, int pos, float *logits) {
                     int *ri = s->rec_ri + (size_t)h * P;
                     const int mm = orc_arm_select(s->rec_R, s->rec_r, HD, q + (size_t)h * HD,
                                                   s->projk + ((size_t)L * P * NKV + h / group) * s->rec_r, NKV,
-                                                  s->rec_B, s->rec_W, s->rec_sink, pos,
+                                                  s->rec_dense ? 0 : s->rec_B, s->rec_W, s->rec_sink, pos,
                                                   (orc_sidx *)s->rec_cand + (size_t)h * P, ri);
                     attn_head_exact_sel(q + (size_t)h * HD, (const int32_t *)kcl, (const int32_t *)vcl, pos, KVD,
                                         h / group, HD, ascale, -1, ri, mm, ao + (size_t)h * HD);
@@ -963,7 +966,7 @@ static int step_any(orc_sess *s, int32_t tok, int pos, float *logits) {
                     int *ri = s->rec_ri + (size_t)h * P;
                     const int mm = orc_arm_select(s->rec_R, s->rec_r, HD, q + (size_t)h * HD,
                                                   s->projk + ((size_t)L * P * NKV + h / group) * s->rec_r, NKV,
-                                                  s->rec_B, s->rec_W, s->rec_sink, pos,
+                                                  s->rec_dense ? 0 : s->rec_B, s->rec_W, s->rec_sink, pos,
                                                   (orc_sidx *)s->rec_cand + (size_t)h * P, ri);
                     attn_head_list(q + (size_t)h * HD, kcl, vcl, ri, mm, KVD, h / group, HD, ascale,
                                    sc + (size_t)h * P, ao + (size_t)h * HD);

@@ -105,6 +105,10 @@ int   orc_arm_select(const signed char *R, int r, int hd, const float *qh, const
  * projection sidecar is kept per position.  B = 0 switches it off.  Before the
  * first token. */
 int   orc_set_recall(orc_sess *s, int B, int W, int sink, int r);
+/* Dense recall steps (SP_RECALL_DECODE_ONLY=1 during the prompt, decode.c:561:
+ * the effective budget is 0, so each q head attends every position through the
+ * identity list) while on; the sidecar is still written.  Off by default. */
+void  orc_set_recall_dense(orc_sess *s, int on);
 /* sidecar rows [p0, p0+n) of a layer: NKV*r floats per position */
 int   orc_recall_sidecar(const orc_sess *s, int layer, int p0, int n, float *out);
 /* V heads this session stored with a clamped element (exact mode) */

@@ -902,7 +902,7 @@ int attn_capacity(int HD, int G) {
 // The step's head preparation and attention: exact-mode decode runs the
 // preparation inside the score pass; float mode and batched tokens launch
 // k_qk_prep first.
-bool attention_fuses_prep(const AttnArgs &a) { return a.mode == EXACT && !a.nt; }
+bool attention_fuses_prep(const AttnArgs &a) { return a.mode == EXACT && !a.nt && !a.rec_r; }
 void launch_prep_attention(const AttnArgs &a, int grid_chunks, hipStream_t s) {
     if (!attention_fuses_prep(a)) launch_qk_prep(a, s);
     attention_go(a, grid_chunks, attention_fuses_prep(a), s);

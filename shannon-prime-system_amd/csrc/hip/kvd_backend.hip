@@ -420,6 +420,19 @@ struct sp_kvdecode_handle {
     float *h_logits = nullptr;               // pinned staging
     int max_chunks = 0;
     StepScratch ss;                          // the step scratch above, carved from `scratch` (this handle's)
+    // ARM recall (sp_hipkv_set_recall): budget B, window W, sinks, projection
+    // rows r (B = 0: off).  The K sidecar lives in the KV pages (forks,
+    // copy-on-write and rewind carry it); the router's buffers live here and
+    // are back at zero (accumulators, counters) between launches.
+    struct Recall {
+        int B = 0, W = 0, sink = 0, r = 0;
+        void *buf = nullptr;
+        uint32_t *Rb = nullptr, *keys = nullptr;
+        int *lists = nullptr, *counts = nullptr, *zs = nullptr, *cmax = nullptr, *counter = nullptr;
+        int64_t *vacc = nullptr, *vs = nullptr;
+        float *part = nullptr, *psum = nullptr;
+        int lstride = 0, mchunks = 0;
+    } rec;
     int attn_cap = 0;                        // exact decode attention workgroups resident at once
     void *scratch = nullptr;
     int built = 0;                           // tables and scratch allocated (reusable as a shell)
@@ -437,8 +450,8 @@ struct sp_kvdecode_handle {
         void *hstage = nullptr;              // pinned upload staging for toks/tpos/tpages
     } b;
     // graph cache: key (logits?, argmax?, grid_global, grid_local, chunk_global)
-    struct GKey { int lg, am, gg, gl, cg; bool operator<(const GKey &o) const {
-        return std::tie(lg, am, gg, gl, cg) < std::tie(o.lg, o.am, o.gg, o.gl, o.cg); } };
+    struct GKey { int lg, am, gg, gl, cg, rt; bool operator<(const GKey &o) const {
+        return std::tie(lg, am, gg, gl, cg, rt) < std::tie(o.lg, o.am, o.gg, o.gl, o.cg, o.rt); } };
     std::map<GKey, hipGraphExec_t> graphs;
 };
 
@@ -465,9 +478,14 @@ size_t kv_row_bytes(const DevModel *m, int mode, int kvc) {
 double kv_row_payload(const DevModel *m, int mode, int kvc) {
     return mode == FLOAT && kvc == KVC_SPINOR ? (double)(m->HD + 4 * spn_blocks(m->HD)) : 4.0 * m->HD;
 }
-std::shared_ptr<KvPool> make_pool(const DevModel *m, int mode, int kvc) {
+// A page: K and V rows of PAGE positions of every kv head, then with recall
+// (r > 0) the K sidecar [NKV][PAGE][r] floats.
+size_t page_bytes_of(const DevModel *m, int mode, int kvc, int r) {
+    return (size_t)2 * m->NKV * PAGE * kv_row_bytes(m, mode, kvc) + (size_t)recall_page_floats(m->NKV, r) * 4;
+}
+std::shared_ptr<KvPool> make_pool(const DevModel *m, int mode, int kvc, int r) {
     auto pool = std::make_shared<KvPool>();
-    pool->page_bytes = (size_t)2 * m->NKV * PAGE * kv_row_bytes(m, mode, kvc);
+    pool->page_bytes = page_bytes_of(m, mode, kvc, r);
     pool->pages_per_chunk = (int)std::max<size_t>(16, ((size_t)1 << 30) / pool->page_bytes);
     return pool;
 }
@@ -598,13 +616,67 @@ void set_handle_mode(sp_kvdecode_handle *h, int mode) {
 // A fresh pool when the stored row format changes (mode or codec, only before
 // the first token): unmaps every page and rebuilds the empty tables.
 int repage(sp_kvdecode_handle *h, const char *who) {
-    const size_t want = (size_t)2 * h->m->NKV * PAGE * kv_row_bytes(h->m, h->mode, h->kvc);
+    const size_t want = page_bytes_of(h->m, h->mode, h->kvc, h->rec.r);
     if (h->pool->page_bytes == want) return 0;
     if (h->pool.use_count() > 1) return fail("%s: the KV pages are shared with a fork", who);
     { std::lock_guard<std::mutex> pl(h->pool->mu); for (auto &v : h->pt) for (int id : v) h->pool->unref(id); }
-    h->pool = make_pool(h->m, h->mode, h->kvc);
+    h->pool = make_pool(h->m, h->mode, h->kvc, h->rec.r);
     free_graphs(h);
     return build_tables(h);
+}
+
+void free_recall(sp_kvdecode_handle *h) {
+    if (h->rec.buf) { hipStreamSynchronize(h->stream); hipFree(h->rec.buf); }
+    h->rec = sp_kvdecode_handle::Recall{};
+}
+
+// The frozen +-1 projection of core/arm/arm.c:17-27 (SplitMix64 from the seed
+// of include/sp/arm.h:49, element i = p * HD + d of R is +1 when the low bit of
+// the i-th draw is set) as sign bits, row p at [p * HD/32].
+std::vector<uint32_t> recall_sign_bits(int r, int HD) {
+    std::vector<uint32_t> bits((size_t)r * HD / 32, 0u);
+    uint64_t st = 0x5350524F4A2BULL;
+    for (int i = 0; i < r * HD; i++) {
+        uint64_t z = (st += 0x9E3779B97F4A7C15ULL);
+        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+        z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+        z ^= z >> 31;
+        if (z & 1) bits[(size_t)i / 32] |= 1u << (i % 32);
+    }
+    return bits;
+}
+
+// The router's buffers for budget B (> 0), window W, sinks, r rows.  A recall
+// set holds at most max(B, W + sink) positions (and at most pmax).
+int alloc_recall(sp_kvdecode_handle *h, int B, int W, int sink, int r) {
+    free_recall(h);
+    if (B <= 0) return 0;
+    const DevModel *m = h->m;
+    auto &R = h->rec;
+    const int P = h->pmax;
+    R.lstride = std::min(P, std::max(std::min(B, P), std::min(W, P) + std::min(sink, P)));
+    R.mchunks = (R.lstride + RECALL_CHUNK - 1) / RECALL_CHUNK;
+    const size_t NH = m->NH, HD = m->HD, mc = R.mchunks, ls = R.lstride;
+    struct Item { void **p; size_t n; };
+    Item items[] = {
+        {(void **)&R.Rb, (size_t)r * HD / 8}, {(void **)&R.keys, NH * P * 4}, {(void **)&R.lists, NH * ls * 4},
+        {(void **)&R.zs, NH * ls * 4}, {(void **)&R.counts, NH * 4}, {(void **)&R.cmax, NH * mc * 4},
+        {(void **)&R.counter, NH * 4}, {(void **)&R.vacc, NH * HD * 8}, {(void **)&R.vs, NH * 8},
+        {(void **)&R.part, NH * mc * HD * 4}, {(void **)&R.psum, NH * mc * 4},
+    };
+    size_t tot = 0;
+    for (auto &it : items) tot = align_up(tot + it.n, 256);
+    void *buf = nullptr;
+    HIPCHK(hipMalloc(&buf, tot), "recall buffers alloc");
+    R.buf = buf;
+    size_t off = 0;
+    for (auto &it : items) { *it.p = (uint8_t *)buf + off; off = align_up(off + it.n, 256); }
+    const std::vector<uint32_t> bits = recall_sign_bits(r, (int)HD);
+    HIPCHK(hipMemsetAsync(buf, 0, tot, h->stream), "recall buffers clear");
+    HIPCHK(hipMemcpyAsync(R.Rb, bits.data(), bits.size() * 4, hipMemcpyHostToDevice, h->stream), "recall projection upload");
+    HIPCHK(hipStreamSynchronize(h->stream), "recall buffers");
+    R.B = B; R.W = W; R.sink = sink; R.r = r;
+    return 0;
 }
 
 // A kept shell of m with this pmax and window ring, or null (caller holds g_mu).
@@ -625,6 +697,7 @@ constexpr size_t MAX_SHELLS = 256;
 void free_handle(sp_kvdecode_handle *h) {
     if (h->stream) hipStreamSynchronize(h->stream);
     free_graphs(h);
+    if (h->rec.buf) hipFree(h->rec.buf);
     if (h->d_pt) hipFree(h->d_pt);
     if (h->h_pt) hipHostFree(h->h_pt);
     if (h->scratch) hipFree(h->scratch);
@@ -638,7 +711,9 @@ void free_handle(sp_kvdecode_handle *h) {
 }
 
 // ------------------------------------------------------------ one step body
-struct StepShape { int logits, argmax, grid_global, grid_local, chunk_global, chunk_local; };
+// route: global layers attend over the recall router's positions (decode
+// steps of a handle with recall on; prefill attends densely)
+struct StepShape { int logits, argmax, grid_global, grid_local, chunk_global, chunk_local, route; };
 
 int attn_chunks(const sp_kvdecode_handle *h, int pos_hi, StepShape &sh) {
     const DevModel *m = h->m;
@@ -666,6 +741,20 @@ int attn_chunks(const sp_kvdecode_handle *h, int pos_hi, StepShape &sh) {
 }
 
 typedef void (*TimeCb)(void *ctx, int cls, bool begin);
+
+RecallArgs recall_args(const sp_kvdecode_handle *h, float *const *pages, VecStat *stat_out) {
+    const DevModel *m = h->m;
+    const auto &R = h->rec;
+    RecallArgs rc{};
+    rc.Rb = R.Rb; rc.qr = h->qr; rc.pages = pages; rc.st = h->d_st; rc.ao = h->ao; rc.stat_out = stat_out;
+    rc.keys = R.keys; rc.lists = R.lists; rc.counts = R.counts; rc.zs = R.zs; rc.cmax = R.cmax;
+    rc.vacc = R.vacc; rc.vs = R.vs; rc.part = R.part; rc.psum = R.psum; rc.counter = R.counter;
+    rc.kstride = h->pmax; rc.lstride = R.lstride; rc.mchunks = R.mchunks;
+    rc.score_blocks = std::min(RECALL_SCORE_BLOCKS, (h->pmax + 255) / 256);
+    rc.NH = m->NH; rc.NKV = m->NKV; rc.HD = m->HD; rc.r = R.r; rc.B = R.B; rc.W = R.W; rc.sink = R.sink;
+    rc.mode = h->mode; rc.ascale = 1.0f / sqrtf((float)m->HD);
+    return rc;
+}
 
 void enqueue_body(sp_kvdecode_handle *h, const StepShape &sh, TimeCb cb, void *ctx, const StepScratch &ss) {
     const DevModel *m = h->m;
@@ -713,8 +802,12 @@ void enqueue_body(sp_kvdecode_handle *h, const StepShape &sh, TimeCb cb, void *c
         a.ascale = 1.0f / sqrtf((float)m->HD);
         a.chunk = glob ? sh.chunk_global : sh.chunk_local;
         a.stat_out = st(l, STAT_AO);
+        if (h->rec.B > 0 && a.win < 0) { a.rec_R = h->rec.Rb; a.rec_r = h->rec.r; }
         const int cls = (glob || a.win < 0) ? 5 : 6, grid = glob ? sh.grid_global : sh.grid_local;
-        if (attention_fuses_prep(a)) {
+        if (sh.route && a.rec_r) {
+            T(7, true); launch_qk_prep(a, s); T(7, false);
+            T(cls, true); launch_recall_attention(recall_args(h, a.pages, a.stat_out), s); T(cls, false);
+        } else if (attention_fuses_prep(a)) {
             T(cls, true); launch_prep_attention(a, grid, s); T(cls, false);
         } else {
             T(7, true); launch_qk_prep(a, s); T(7, false);
@@ -868,6 +961,7 @@ int run_batch(sp_kvdecode_handle *h, int T, int pos0, int pos_hi, bool multi, Ti
         a.ascale = 1.0f / sqrtf((float)m->HD);
         a.nt = T; a.pos0 = pos0; a.rope_stride = 2 * m->HD; a.vclamp = h->vclamp;
         if (multi) { a.tpos = b.tpos; a.tpages = b.tpages + (size_t)l * b.TB; }
+        else if (h->rec.B > 0 && a.win < 0) { a.rec_R = h->rec.Rb; a.rec_r = h->rec.r; }   // prefill: the sidecar
         a.chunk = (glob || a.win < 0) ? 256 : 64;
         TM(7, true); launch_qk_prep(a, s); TM(7, false);
         // chunks of the batch's longest span: a window of W positions covers at
@@ -921,7 +1015,7 @@ constexpr size_t MAX_GRAPHS = 64;
 // MAX_GRAPHS entries the cache is emptied after the stream has drained (a
 // graph exec still running must not be destroyed).
 int graph_for(sp_kvdecode_handle *h, const StepShape &sh, hipGraphExec_t *out) {
-    sp_kvdecode_handle::GKey key{sh.logits, sh.argmax, sh.grid_global, sh.grid_local, sh.chunk_global};
+    sp_kvdecode_handle::GKey key{sh.logits, sh.argmax, sh.grid_global, sh.grid_local, sh.chunk_global, sh.route};
     auto it = h->graphs.find(key);
     if (it != h->graphs.end()) { *out = it->second; return 0; }
     hipGraph_t g;
@@ -958,9 +1052,9 @@ int run_body(sp_kvdecode_handle *h, const StepShape &sh) {
 }
 
 // round the attention grids up so one captured graph serves a run of positions
-StepShape shape_for(const sp_kvdecode_handle *h, int pos, int logits, int argmax) {
+StepShape shape_for(const sp_kvdecode_handle *h, int pos, int logits, int argmax, bool decode = true) {
     StepShape sh{};
-    sh.logits = logits; sh.argmax = argmax;
+    sh.logits = logits; sh.argmax = argmax; sh.route = decode && h->rec.B > 0;
     const int hi = std::min(h->pmax - 1, ((pos / 256) + 1) * 256 - 1);
     attn_chunks(h, h->use_graph ? hi : pos, sh);
     return sh;
@@ -1050,12 +1144,13 @@ int sp_hipkv_open(const void *qm_opaque, int pmax, sp_kvdecode_handle **out) {
         return fail("sp_hipkv_open: no HIP device visible (this backend runs on MI355X / gfx950)%s");
     DevModel *m = model_get(qm);
     if (!m) return 1;
-    auto new_pool = [m]() { return make_pool(m, FLOAT, KVC_PLAIN); };
+    auto new_pool = [m]() { return make_pool(m, FLOAT, KVC_PLAIN, 0); };
     if (sp_kvdecode_handle *sh = take_shell(m, pmax, 0)) {
         // a kept shell: reset to the open defaults, unmapped tables
         set_handle_mode(sh, FLOAT);
         if (sh->kvc != KVC_PLAIN) { sh->kvc = KVC_PLAIN; free_graphs(sh); }   // graphs bake in the codec
         sh->use_graph = 1; sh->use_batch = 1; sh->dpos = 0; sh->hwm = 0;
+        if (sh->rec.B) { free_recall(sh); free_graphs(sh); }
         sh->pool = new_pool();
         if (hipMemsetAsync(sh->vclamp, 0, sizeof(int), sh->stream) != hipSuccess) {
             free_handle(sh); model_put(m); return fail("sp_hipkv_open: clamp counter reset failed%s");
@@ -1136,7 +1231,7 @@ int sp_hipkv_prefill(sp_kvdecode_handle *h, const int32_t *tokens, int n_tok) {
     } else {
         if (set_state(h, h->dpos, 0, DRIVE_STREAM)) return 1;
         for (int i = 0; i < n_tok; i++) {
-            StepShape sh = shape_for(h, h->dpos + i, 0, 0);
+            StepShape sh = shape_for(h, h->dpos + i, 0, 0, false);
             if (run_body(h, sh)) return 1;
         }
     }
@@ -1165,9 +1260,11 @@ static int decode_batch_impl(sp_kvdecode_handle *const *hs, int n, const int32_t
         for (int j = 0; j < i; j++)
             if (hs[j] == h) return fail("sp_hipkv_decode_batch: a handle appears twice%s");
     }
-    const bool batched = batch_supported(L) && gemm_supported(m->out);
-    if (!batched) {                                   // shapes the GEMM does not take: one step each
-        if (cb) return fail("sp_hipkv_decode_batch_times: this model shape has no batched path%s");
+    bool routed = false;
+    for (int i = 0; i < n; i++) routed |= hs[i]->rec.B > 0;
+    const bool batched = batch_supported(L) && gemm_supported(m->out) && !routed;
+    if (!batched) {                                   // shapes the GEMM does not take, recall: one step each
+        if (cb) return fail("sp_hipkv_decode_batch_times: no batched path for this model shape or with recall%s");
         for (int i = 0; i < n; i++) {
             if (step_one(hs[i], tokens[i], 1)) return 1;
             if (logits) HIPCHK(hipMemcpyAsync(logits + (size_t)i * m->V, hs[i]->logits, (size_t)m->V * 4,
@@ -1341,6 +1438,8 @@ int sp_hipkv_set_mode(sp_kvdecode_handle *h, int exact) {
     if (h->dpos != 0) return fail("sp_hipkv_set_mode: the mode is fixed once tokens are resident%s");
     // exact V-sum: weights <= 2^22, |vq| < 2^23, so int64 totals hold 2^18 positions
     if (m == EXACT && h->pmax > (1 << 18)) return fail("sp_hipkv_set_mode: exact mode holds at most %s%lld positions", "", (long long)(1 << 18));
+    if (m == FLOAT && h->kvc == KVC_SPINOR && h->rec.B > 0)
+        return fail("sp_hipkv_set_mode: recall in float mode reads plain K/V rows (not Spinor code rows)%s");
     set_handle_mode(h, m);
     return repage(h, "sp_hipkv_set_mode");
 }
@@ -1352,6 +1451,8 @@ int sp_hipkv_set_kv_codec(sp_kvdecode_handle *h, int codec) {
     if (h->dpos != 0) return fail("sp_hipkv_set_kv_codec: the codec is fixed once tokens are resident%s");
     if (codec == KVC_SPINOR && h->m->HD != 64 && h->m->HD != 128 && h->m->HD != 256)
         return fail("sp_hipkv_set_kv_codec: Spinor KV serves head_dim 64, 128 and 256%s");
+    if (codec == KVC_SPINOR && h->mode == FLOAT && h->rec.B > 0)
+        return fail("sp_hipkv_set_kv_codec: recall in float mode reads plain K/V rows (not Spinor code rows)%s");
     h->kvc = codec;
     free_graphs(h);
     return repage(h, "sp_hipkv_set_kv_codec");
@@ -1379,6 +1480,47 @@ int sp_hipkv_set_batch_prefill(sp_kvdecode_handle *h, int on) {
     return 0;
 }
 
+int sp_hipkv_set_recall(sp_kvdecode_handle *h, int B, int W, int sink, int r) {
+    if (!h) return fail("sp_hipkv_set_recall: null handle%s");
+    if (B < 0 || W < 0 || sink < 0) return fail("sp_hipkv_set_recall: negative budget, window or sink count%s");
+    if (B > 0 && (r < 1 || r > 64)) return fail("sp_hipkv_set_recall: projection rows r must lie in [1, 64]%s");
+    if (B == 0) r = 0;
+    if (B == h->rec.B && W == h->rec.W && sink == h->rec.sink && r == h->rec.r) return 0;
+    if (h->dpos != 0) return fail("sp_hipkv_set_recall: recall is fixed once tokens are resident%s");
+    if (B > 0 && h->m->HD != 64 && h->m->HD != 128 && h->m->HD != 256)
+        return fail("sp_hipkv_set_recall: recall serves head_dim 64, 128 and 256%s");
+    if (B > 0 && h->mode == FLOAT && h->kvc == KVC_SPINOR)
+        return fail("sp_hipkv_set_recall: recall in float mode reads plain K/V rows (not Spinor code rows)%s");
+    if (h->pool.use_count() > 1) return fail("sp_hipkv_set_recall: the KV pages are shared with a fork%s");
+    free_graphs(h);
+    if (alloc_recall(h, B, W, sink, r)) return 1;
+    return repage(h, "sp_hipkv_set_recall");
+}
+
+int sp_hipkv_read_recall_sidecar(const sp_kvdecode_handle *h, int layer, int p0, int n, float *out) {
+    if (!h || !out || layer < 0 || layer >= h->m->NL || p0 < 0 || n < 0 || p0 + n > h->dpos)
+        return fail("sp_hipkv_read_recall_sidecar: bad argument%s");
+    if (h->rec.B <= 0) return fail("sp_hipkv_read_recall_sidecar: recall is off%s");
+    const DevModel *m = h->m;
+    if (!is_global(m, layer)) return fail("sp_hipkv_read_recall_sidecar: window layers keep no sidecar%s");
+    const int NKV = m->NKV, r = h->rec.r;
+    const size_t side0 = page_bytes_of(m, h->mode, h->kvc, 0);          // the sidecar follows K and V
+    HIPCHK(hipStreamSynchronize(h->stream), "sidecar read sync");
+    std::vector<float> side((size_t)recall_page_floats(NKV, r));
+    for (int lp = p0 / PAGE; lp <= (p0 + n - 1) / PAGE && n > 0; lp++) {
+        const int id = h->pt[layer][lp];
+        if (id < 0) return fail("sp_hipkv_read_recall_sidecar: position not resident%s");
+        HIPCHK(hipMemcpy(side.data(), (const uint8_t *)h->pool->ptr[id] + side0, side.size() * 4, hipMemcpyDeviceToHost),
+               "sidecar page read");
+        const int a = std::max(p0, lp * PAGE), b = std::min(p0 + n, (lp + 1) * PAGE);
+        for (int p = a; p < b; p++)
+            for (int kh = 0; kh < NKV; kh++)
+                memcpy(out + ((size_t)(p - p0) * NKV + kh) * r, side.data() + ((size_t)kh * PAGE + p % PAGE) * r,
+                       (size_t)r * 4);
+    }
+    return 0;
+}
+
 int sp_hipkv_fork(const sp_kvdecode_handle *p, sp_kvdecode_handle **out) {
     if (!p || !out) return fail("sp_hipkv_fork: null argument%s");
     *out = nullptr;
@@ -1401,6 +1543,12 @@ int sp_hipkv_fork(const sp_kvdecode_handle *p, sp_kvdecode_handle **out) {
         }
     }
     if (h->kvc != p->kvc) { h->kvc = p->kvc; free_graphs(h.get()); }        // a recycled shell's graphs
+    if (h->rec.B != p->rec.B || h->rec.W != p->rec.W || h->rec.sink != p->rec.sink || h->rec.r != p->rec.r) {
+        free_graphs(h.get());
+        if (alloc_recall(h.get(), p->rec.B, p->rec.W, p->rec.sink, p->rec.r)) {
+            sp_hipkv_close(h.release()); return 1;
+        }
+    }
     h->pool = p->pool; h->dpos = p->dpos; h->hwm = p->hwm;
     if (hipMemsetAsync(h->vclamp, 0, sizeof(int), h->stream) != hipSuccess) {
         sp_hipkv_close(h.release()); return fail("sp_hipkv_fork: clamp counter reset failed%s");

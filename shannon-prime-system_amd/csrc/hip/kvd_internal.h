@@ -96,7 +96,37 @@ struct AttnArgs {
     float *const *const *tpages;
     VecStat *stat_out;       // decode: statistics of ao for the O GEMV (NULL: none)
     int *vclamp;             // exact mode: +1 per stored V head with a clamped element (NULL: not counted)
+    // recall sidecar: rec_r > 0 writes each new K head's projection on the
+    // frozen +-1 matrix (sign bits rec_R [rec_r][HD/32]) into its page
+    const uint32_t *rec_R;
+    int rec_r;
 };
+
+// ARM recall over one global layer's pages (decode): the router picks each q
+// head's positions from the K sidecar, the attention reads only those.
+struct RecallArgs {
+    const uint32_t *Rb;      // [r][HD/32] sign bits of the frozen projection (bit set: +1)
+    const float *qr;         // rotated, normed q [NH*HD]
+    float *const *pages;     // this layer's page table (full: no ring)
+    const DState *st;
+    float *ao;               // output [NH*HD]
+    VecStat *stat_out;       // statistics of ao for the O GEMV
+    uint32_t *keys;          // [NH][kstride] order keys of the candidates' projected scores
+    int *lists;              // [NH][lstride] recalled positions
+    int *counts;             // [NH] recall set sizes
+    int *zs;                 // [NH][lstride] exact: Q14 score grid; float: score bits
+    int *cmax;               // [NH][mchunks] chunk maxima (exact: int; float: float bits)
+    int64_t *vacc, *vs;      // exact: V-sum totals [NH][HD] and denominators [NH] (zero between launches)
+    float *part, *psum;      // float: chunk V-sums [NH][mchunks][HD] and weight sums [NH][mchunks]
+    int *counter;            // [NH] arrival counters (self-resetting)
+    int kstride, lstride, mchunks, score_blocks;
+    int NH, NKV, HD, r, B, W, sink, mode;
+    float ascale;
+};
+void launch_recall_attention(const RecallArgs &rc, hipStream_t s);
+constexpr int RECALL_CHUNK = 64;        // recalled positions per attention workgroup
+constexpr int RECALL_SCORE_BLOCKS = 32; // router scoring workgroups per q head (grid-stride)
+int recall_page_floats(int NKV, int r); // sidecar floats per page
 
 struct Seg { DevW w; float *out; };
 enum Act { ACT_NONE = 0, ACT_GELU = 1, ACT_SILU = 2 };

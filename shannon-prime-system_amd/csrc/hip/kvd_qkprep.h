@@ -21,12 +21,15 @@ struct HeadPrep {
     int kvc;                  // KVC_SPINOR: K/V pass the Spinor-63 codec
     float eps;
     int *vclamp;              // exact mode: count of V heads stored with a clamped element
+    const uint32_t *rec_R;    // recall sidecar projection sign bits [rec_r][HD/32]
+    int rec_r;                // 0: no sidecar
 };
 __device__ __forceinline__ HeadPrep head_prep_of(const AttnArgs &a) {
     HeadPrep p;
     p.q = a.q; p.k = a.k; p.v = a.v; p.q_norm = a.q_norm; p.k_norm = a.k_norm; p.rope_cs = a.rope_cs;
     p.qr = a.qr; p.pages = a.pages; p.ring_pages = a.ring_pages; p.NH = a.NH; p.NKV = a.NKV; p.HD = a.HD;
     p.mode = a.mode; p.kvc = a.kvc; p.eps = a.eps; p.vclamp = a.vclamp;
+    p.rec_R = a.rec_R; p.rec_r = a.rec_r;
     return p;
 }
 
@@ -179,6 +182,30 @@ __device__ __forceinline__ void spinor_head(float x[8], int lane, bool store, ui
     if (store && lane < NB) ((float *)(row + HD))[lane] = mul_mine;
 }
 
+// The recall sidecar of one K head (core/arm/arm.c:31-45): lane p < r gets
+// sum_d R[p][d] * k[d] as a sequential float sum in d (R = +-1, so each
+// product is +-k[d] exactly and only the additions round, as on the CPU).
+// The wave holds k at lanes l + 64 j in out[j]; readlane broadcasts each
+// element in turn.
+template <int PER>
+__device__ __forceinline__ void recall_sidecar(const uint32_t *Rb, int r, const float out[8], float *dst, int lane) {
+    constexpr int NW = PER * 2;                    // sign words per row (HD / 32)
+    const int p = lane < r ? lane : 0;
+    uint32_t bits[NW];
+    #pragma unroll
+    for (int w = 0; w < NW; w++) bits[w] = Rb[(size_t)p * NW + w];
+    float acc = 0.0f;
+    #pragma unroll
+    for (int w = 0; w < NW; w++) {
+        const int src = __float_as_int(out[w >> 1]);
+        for (int b = 0; b < 32; b++) {
+            const float kd = __int_as_float(__builtin_amdgcn_readlane(src, (w & 1) * 32 + b));
+            acc = __fadd_rn(acc, ((bits[w] >> b) & 1u) ? kd : -kd);
+        }
+    }
+    if (lane < r) dst[lane] = acc;
+}
+
 // hb < NH: q head hb -> qr; hb < NH + NKV: k head -> page; else v head -> page.
 // src: the head's HD projections; lane l holds elements l + 64 j.
 template <bool COHERENT, int PER>
@@ -224,7 +251,12 @@ __device__ __forceinline__ void qk_prep_head_t(const HeadPrep a, int hb, int pos
     if (isq) {
         #pragma unroll
         for (int j = 0; j < 8; j++) if (j < per) a.qr[(size_t)h * HD + lane + 64 * j] = out[j];
-    } else if (a.kvc == KVC_SPINOR && a.mode == FLOAT) {
+        return;
+    }
+    if (a.rec_r)                                                // sidecar from the K before any codec
+        recall_sidecar<PER>(a.rec_R, a.rec_r, out,
+                            page + (size_t)2 * a.NKV * PAGE * HD + ((size_t)h * PAGE + slot) * a.rec_r, lane);
+    if (a.kvc == KVC_SPINOR && a.mode == FLOAT) {
         constexpr int RB = spn_row_bytes(HD);
         spinor_head<PER>(out, lane, true, (uint8_t *)page + ((size_t)h * PAGE + slot) * RB);
     } else {

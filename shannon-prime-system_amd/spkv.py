@@ -124,6 +124,8 @@ def kv():
         _sig(lib, "sp_hipkv_info", c_int, [c_void_p, c_void_p])
         _sig(lib, "sp_hipkv_check_model", c_int, [c_void_p, c_void_p])
         _sig(lib, "sp_hipkv_v_clamps", c_int, [c_void_p, ctypes.POINTER(c_longlong)])
+        _sig(lib, "sp_hipkv_set_recall", c_int, [c_void_p, c_int, c_int, c_int, c_int])
+        _sig(lib, "sp_hipkv_read_recall_sidecar", c_int, [c_void_p, c_int, c_int, c_int, c_void_p])
         _kv = lib
     return _kv
 
@@ -362,6 +364,16 @@ class Backend:
         v = np.zeros((n, kvd), np.float32)
         check(kv().sp_hipkv_read_kv(self.h, layer, p0, n, ptr(k), ptr(v)), "sp_hipkv_read_kv")
         return k, v
+
+    def set_recall(self, B, W=64, sink=4, r=16):
+        """ARM recall on the global layers (decode steps route, prefill is dense)."""
+        check(kv().sp_hipkv_set_recall(self.h, B, W, sink, r), "sp_hipkv_set_recall")
+
+    def recall_sidecar(self, layer, p0, n, nkv, r):
+        import numpy as np
+        out = np.zeros((n, nkv, r), np.float32)
+        check(kv().sp_hipkv_read_recall_sidecar(self.h, layer, p0, n, ptr(out)), "sp_hipkv_read_recall_sidecar")
+        return out
 
     def v_clamps(self):
         n = c_longlong()

@@ -17,6 +17,10 @@ core/session/sp_session.c sp_prefill_chunk :154-212 + sp_decode_step :725-770):
 Recall: the reference's decode-path perplexity (core/forward/decode.c
 qwen3_ppl_decode, through oracle/ref_harness.c refh_ppl_recall) with the ARM
 recall knobs SP_RECALL_B/W/SINK/R, as the exact double (hex).
+Recall generation: the reference's greedy decode (qwen3_generate_kv through
+oracle/ref_harness.c refh_generate_recall) with the recall knobs, with and
+without SP_RECALL_DECODE_ONLY=1 (dense prompt, router at the generated
+positions), as the generated token sequence; B = 0 is the plain decode.
 Also the reference's exact islands (core/exact_islands/exact_islands.c) on the
 island test vectors and its Spinor-63 codec (core/vht2/spinor_block.c:128-149)
 on seeded vectors, as SHA-256 of the outputs.
@@ -59,6 +63,8 @@ CASES = [
 
 # (B, W, sink, r) of the recall cases; B = 0 is the plain decode path
 RECALL = [(0, 64, 4, 16), (16, 8, 2, 16), (24, 4, 3, 8), (12, 4, 0, 32)]
+# (B, W, sink, r, decode_only) of the recall generation cases (24-token prompt, 32 generated)
+RECALL_GEN = [(0, 64, 4, 16, 0), (16, 8, 2, 16, 1), (12, 4, 0, 32, 1), (16, 8, 2, 16, 0), (24, 4, 3, 8, 0)]
 
 
 def sha(b):
@@ -115,6 +121,22 @@ def main():
                     sys.exit(f"reference recall decode failed for {name}")
                 out["recall"].append({"model": name, "max_context": 64, "n": 48, "n_warm": 4, "prompt_seed": 1,
                                       "B": B, "W": W, "sink": sink, "r": r, "ppl_hex": ppl.value.hex()})
+
+    out["recall_generate"] = []
+    with tempfile.TemporaryDirectory() as d:
+        for name in ("qwen3-tiny", "qwen3-g4"):
+            spm, spt = model(d, name, 64)
+            V = int(SMALL[name]["vocab"])
+            for B, W, sink, r, dec_only in RECALL_GEN:
+                n_prompt, n_gen = 24, 32
+                seq = np.zeros(n_prompt + n_gen, np.int32)
+                seq[:n_prompt] = spkv.splitmix_tokens(n_prompt, V, seed=1)
+                if R.refh_generate_recall(spm.encode(), spt.encode(), P(seq), n_prompt, n_gen, B, W, sink, r,
+                                          dec_only) != n_prompt + n_gen:
+                    sys.exit(f"reference recall generation failed for {name}")
+                out["recall_generate"].append({
+                    "model": name, "max_context": 64, "n_prompt": n_prompt, "prompt_seed": 1, "B": B, "W": W,
+                    "sink": sink, "r": r, "decode_only": dec_only, "generated": [int(t) for t in seq[n_prompt:]]})
 
     x, w, z, g = island_inputs()
     a = np.zeros_like(x); R.sp_rmsnorm_exact(P(x), P(w), x.size, P(a))

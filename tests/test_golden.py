@@ -13,7 +13,10 @@ C sources).
     hashes on the shared test vectors;
   * the oracle's decode with the ARM recall router reproduces the reference's
     decode-path perplexity (qwen3_ppl_decode with SP_RECALL_B/W/SINK/R) as the
-    exact double.
+    exact double, and its greedy sequences (qwen3_generate_kv) with the router
+    on the whole sequence and with SP_RECALL_DECODE_ONLY=1 (dense prompt steps,
+    orc_set_recall_dense); the recall sequences differ from the plain one, so
+    the pin sees the router.
 """
 import hashlib
 import json
@@ -103,3 +106,32 @@ def test_oracle_recall_decode_matches_reference_golden(tmpdir_models, case):
     toks = spkv.splitmix_tokens(case["n"], o.V, seed=case["prompt_seed"])
     assert oracle_ppl(o, toks, case["n_warm"]).hex() == case["ppl_hex"]
     o.close()
+
+
+@pytest.mark.parametrize("case", GOLDEN["recall_generate"],
+                         ids=lambda c: f'{c["model"]}-B{c["B"]}-W{c["W"]}-s{c["sink"]}-r{c["r"]}-d{c["decode_only"]}')
+def test_oracle_recall_generation_matches_reference_golden(tmpdir_models, case):
+    c = dict(case, seed=0, flags=0)
+    spm, _ = _files(tmpdir_models, c)
+    o = orc.Oracle(spm, case["max_context"])
+    if case["B"]:
+        o.set_recall(case["B"], case["W"], case["sink"], case["r"])
+    o.set_recall_dense(case["decode_only"])
+    pr = spkv.splitmix_tokens(case["n_prompt"], o.V, seed=case["prompt_seed"])
+    for t in pr:
+        lg = o.step(int(t))
+    o.set_recall_dense(0)
+    out = []
+    for k in range(len(case["generated"])):
+        out.append(int(lg.argmax()))
+        if k + 1 < len(case["generated"]):
+            lg = o.step(out[-1])
+    assert out == case["generated"]
+    o.close()
+
+
+def test_recall_generation_goldens_see_the_router():
+    plain = {c["model"]: c["generated"] for c in GOLDEN["recall_generate"] if c["B"] == 0}
+    for c in GOLDEN["recall_generate"]:
+        if c["B"]:
+            assert c["generated"] != plain[c["model"]], c
