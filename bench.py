@@ -130,6 +130,8 @@ def main():
     ap.add_argument("--ctx", type=int, default=None, help="override the workload's prefill length")
     ap.add_argument("--no-graph", action="store_true", help="plain kernel launches instead of one HIP graph per step")
     ap.add_argument("--no-batch-prefill", action="store_true", help="prefill one decode step per token")
+    ap.add_argument("--recall", default=None, metavar="B,W,SINK,R",
+                    help="ARM recall on the global layers (sp_hipkv_set_recall): budget, window, sinks, projection rows")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="run one device-to-device copy of this many MiB first (HBM counter calibration)")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("CSV", "COUNTER"), default=None,
@@ -168,6 +170,9 @@ def main():
             spkv.check(spkv.kv().sp_hipkv_set_graph(be.h, 0), "sp_hipkv_set_graph")
         if args.no_batch_prefill:
             spkv.check(spkv.kv().sp_hipkv_set_batch_prefill(be.h, 0), "sp_hipkv_set_batch_prefill")
+        recall = tuple(int(x) for x in args.recall.split(",")) if args.recall else None
+        if recall:
+            be.set_recall(*recall)
         every = wl.get("rewind_every", 0)
         if every:
             # the window ring must hold every position a rewind can return to:
@@ -248,11 +253,12 @@ def main():
 
         cpu = None
         if not args.no_cpu_baseline:
-            cpu = cpu_baseline(spm, be, info, shape, exact, args.cpu_steps, tok, sess, args.kv == "spinor")
+            cpu = cpu_baseline(spm, be, info, shape, exact, args.cpu_steps, tok, sess, args.kv == "spinor", recall)
 
         rec = {
-            "metric": METRIC if args.workload == "gemma3-12b-32k" and ctx == 32768 else
-                      f"kvdecode tokens/s + KV-read HBM GB/s (% of peak), {args.workload} at ctx {ctx}",
+            "metric": METRIC if args.workload == "gemma3-12b-32k" and ctx == 32768 and not recall else
+                      f"kvdecode tokens/s + KV-read HBM GB/s (% of peak), {args.workload} at ctx {ctx}"
+                      + (f", ARM recall B={recall[0]} W={recall[1]} sink={recall[2]} r={recall[3]}" if recall else ""),
             "value": round(value, 3), "unit": "tokens/s", "n_gpus": 1,
             "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(1e3 * wall / args.steps, 4),
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
@@ -263,6 +269,7 @@ def main():
             "config": {"workload": f"{args.workload}: {wl['shape']}-shape kvdecode, prefill {ctx} then {args.steps} greedy steps, batch 1"
                                    + (f", rewind 1-{wl['rewind_max']} tokens every {every} steps" if every else ""),
                        "ctx": ctx, "mode": args.mode, "kv": args.kv,
+                       **({"recall": dict(zip(("B", "W", "sink", "r"), recall))} if recall else {}),
                        "b_kv": float(info[2]) / (2 * shape["n_kv_heads"] * shape["head_dim"]), "pmax": pmax,
                        **({"rewinds": rewinds, "max_rewind": max_rewind} if every else {})},
             "roofline": {"bound": "hbm", "kernel": dom["kernel"], "rocprof_kernels": dom_names,
@@ -474,7 +481,7 @@ def calib_copy(nbytes):
     log(f"calibration copy of {nbytes >> 20} MiB done")
 
 
-def cpu_baseline(spm, be, info, shape, exact, n_steps, tok, sess, spinor=False):
+def cpu_baseline(spm, be, info, shape, exact, n_steps, tok, sess, spinor=False, recall=None):
     """The oracle's decode steps on the host at the same context, the K/V state
     loaded from the device.  Rows: float mode (the reference's arithmetic) and
     exact mode, each n_steps steps on all host cores (the row-parallel oracle:
@@ -507,6 +514,9 @@ def cpu_baseline(spm, be, info, shape, exact, n_steps, tok, sess, spinor=False):
                 k = np.rint(k * np.float32(65536.0)).astype(np.int32).view(np.float32)
                 v = np.clip(np.rint(v * np.float32(65536.0)), -8388607, 8388607).astype(np.int32).view(np.float32)
             o.set_kv(layer, p0, k, v)
+            if recall and (not win or layer % 6 == 5):
+                # the global layers' recall sidecar (window layers keep none)
+                o.set_recall_sidecar(layer, 0, be.recall_sidecar(layer, 0, pos, shape["n_kv_heads"], recall[3]))
         o.set_pos(pos)
         log(f"cpu baseline: KV of {pos} positions loaded in {time.time()-t0:.1f}s")
 
@@ -516,6 +526,8 @@ def cpu_baseline(spm, be, info, shape, exact, n_steps, tok, sess, spinor=False):
         gpu_mode = (mode == "exact") == exact
         o = orc.Oracle(spm, pos + n_steps + 2, orc.EXACT if mode == "exact" else orc.FLOAT,
                        kv_flags=orc.KV_SPINOR if spinor else 0)
+        if recall:
+            o.set_recall(*recall)
         load(o, mode)
         L.orc_set_threads(1)                                  # one core, one step
         t0 = time.time(); o.step(tok); one_s = time.time() - t0

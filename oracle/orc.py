@@ -65,6 +65,7 @@ def lib():
             ("orc_set_recall", c_int, [c_void_p, c_int, c_int, c_int, c_int]),
             ("orc_recall_sidecar", c_int, [c_void_p, c_int, c_int, c_int, c_void_p]),
             ("orc_set_recall_dense", None, [c_void_p, c_int]),
+            ("orc_recall_sidecar_set", c_int, [c_void_p, c_int, c_int, c_int, c_void_p]),
         ]:
             f = getattr(L, name); f.restype = res; f.argtypes = args
         _orc = L
@@ -177,6 +178,12 @@ class Oracle:
         if lib().orc_recall_sidecar(self.s, layer, p0, n, ptr(out)):
             raise RuntimeError("orc_recall_sidecar failed")
         return out
+
+    def set_recall_sidecar(self, layer, p0, rows):
+        import numpy as np
+        rows = np.ascontiguousarray(rows, np.float32)
+        if lib().orc_recall_sidecar_set(self.s, layer, p0, rows.shape[0], ptr(rows)):
+            raise RuntimeError("orc_recall_sidecar_set failed")
 
     def v_clamps(self):
         return lib().orc_v_clamps(self.s)

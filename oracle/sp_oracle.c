@@ -785,6 +785,12 @@ int orc_set_recall(orc_sess *s, int B, int W, int sink, int r) {
     return 0;
 }
 void orc_set_recall_dense(orc_sess *s, int on) { s->rec_dense = on ? 1 : 0; }
+int orc_recall_sidecar_set(orc_sess *s, int layer, int p0, int n, const float *in) {
+    if (!s || !s->projk || layer < 0 || layer >= (int)s->m->NL || p0 < 0 || n < 0 || p0 + n > s->P) return 1;
+    const size_t row = (size_t)s->m->NKV * s->rec_r;
+    memcpy(s->projk + ((size_t)layer * s->P + p0) * row, in, (size_t)n * row * sizeof(float));
+    return 0;
+}
 int orc_recall_sidecar(const orc_sess *s, int layer, int p0, int n, float *out) {
     if (!s || !s->projk || layer < 0 || layer >= (int)s->m->NL || p0 < 0 || n < 0 || p0 + n > s->P) return 1;
     const size_t row = (size_t)s->m->NKV * s->rec_r;

@@ -111,6 +111,8 @@ int   orc_set_recall(orc_sess *s, int B, int W, int sink, int r);
 void  orc_set_recall_dense(orc_sess *s, int on);
 /* sidecar rows [p0, p0+n) of a layer: NKV*r floats per position */
 int   orc_recall_sidecar(const orc_sess *s, int layer, int p0, int n, float *out);
+/* overwrite sidecar rows [p0, p0+n) of a layer (a state loaded from elsewhere) */
+int   orc_recall_sidecar_set(orc_sess *s, int layer, int p0, int n, const float *in);
 /* V heads this session stored with a clamped element (exact mode) */
 int   orc_v_clamps(const orc_sess *s);
 

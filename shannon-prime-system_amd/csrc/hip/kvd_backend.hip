@@ -430,8 +430,8 @@ struct sp_kvdecode_handle {
         uint32_t *Rb = nullptr, *keys = nullptr;
         int *lists = nullptr, *counts = nullptr, *zs = nullptr, *cmax = nullptr, *counter = nullptr;
         int64_t *vacc = nullptr, *vs = nullptr;
-        float *part = nullptr, *psum = nullptr;
-        int lstride = 0, mchunks = 0;
+        float *part = nullptr, *psum = nullptr, *pq = nullptr;
+        int lstride = 0, mchunks = 0, kstride = 0;
     } rec;
     int attn_cap = 0;                        // exact decode attention workgroups resident at once
     void *scratch = nullptr;
@@ -656,10 +656,12 @@ int alloc_recall(sp_kvdecode_handle *h, int B, int W, int sink, int r) {
     const int P = h->pmax;
     R.lstride = std::min(P, std::max(std::min(B, P), std::min(W, P) + std::min(sink, P)));
     R.mchunks = (R.lstride + RECALL_CHUNK - 1) / RECALL_CHUNK;
+    R.kstride = (int)align_up((size_t)P, 64);
     const size_t NH = m->NH, HD = m->HD, mc = R.mchunks, ls = R.lstride;
     struct Item { void **p; size_t n; };
     Item items[] = {
-        {(void **)&R.Rb, (size_t)r * HD / 8}, {(void **)&R.keys, NH * P * 4}, {(void **)&R.lists, NH * ls * 4},
+        {(void **)&R.Rb, (size_t)r * HD / 8}, {(void **)&R.keys, NH * R.kstride * 4}, {(void **)&R.pq, NH * r * 4},
+        {(void **)&R.lists, NH * ls * 4},
         {(void **)&R.zs, NH * ls * 4}, {(void **)&R.counts, NH * 4}, {(void **)&R.cmax, NH * mc * 4},
         {(void **)&R.counter, NH * 4}, {(void **)&R.vacc, NH * HD * 8}, {(void **)&R.vs, NH * 8},
         {(void **)&R.part, NH * mc * HD * 4}, {(void **)&R.psum, NH * mc * 4},
@@ -677,6 +679,20 @@ int alloc_recall(sp_kvdecode_handle *h, int B, int W, int sink, int r) {
     HIPCHK(hipStreamSynchronize(h->stream), "recall buffers");
     R.B = B; R.W = W; R.sink = sink; R.r = r;
     return 0;
+}
+
+// The recall set's geometry at position pos (the device router's sel_geom,
+// sp_arm_select's clamps): identity, sinks, candidate end, top-k, set size.
+struct RecallGeom { bool ident; int sink, cand_hi, topk, m; };
+RecallGeom recall_geom(const sp_kvdecode_handle::Recall &R, int pos) {
+    RecallGeom g;
+    g.ident = R.B <= 0 || pos + 1 <= R.B;
+    const int W = std::min(R.W, pos + 1);
+    g.sink = std::min(R.sink, pos + 1);
+    g.cand_hi = std::min(std::max(pos + 1 - W, g.sink), pos + 1);
+    g.topk = std::min(std::max(R.B - W - g.sink, 0), g.cand_hi - g.sink);
+    g.m = g.ident ? pos + 1 : g.sink + g.topk + (pos + 1 - g.cand_hi);
+    return g;
 }
 
 // A kept shell of m with this pmax and window ring, or null (caller holds g_mu).
@@ -746,10 +762,10 @@ RecallArgs recall_args(const sp_kvdecode_handle *h, float *const *pages, VecStat
     const DevModel *m = h->m;
     const auto &R = h->rec;
     RecallArgs rc{};
-    rc.Rb = R.Rb; rc.qr = h->qr; rc.pages = pages; rc.st = h->d_st; rc.ao = h->ao; rc.stat_out = stat_out;
+    rc.pq = R.pq; rc.qr = h->qr; rc.pages = pages; rc.st = h->d_st; rc.ao = h->ao; rc.stat_out = stat_out;
     rc.keys = R.keys; rc.lists = R.lists; rc.counts = R.counts; rc.zs = R.zs; rc.cmax = R.cmax;
     rc.vacc = R.vacc; rc.vs = R.vs; rc.part = R.part; rc.psum = R.psum; rc.counter = R.counter;
-    rc.kstride = h->pmax; rc.lstride = R.lstride; rc.mchunks = R.mchunks;
+    rc.kstride = R.kstride; rc.lstride = R.lstride; rc.mchunks = R.mchunks;
     rc.score_blocks = std::min(RECALL_SCORE_BLOCKS, (h->pmax + 255) / 256);
     rc.NH = m->NH; rc.NKV = m->NKV; rc.HD = m->HD; rc.r = R.r; rc.B = R.B; rc.W = R.W; rc.sink = R.sink;
     rc.mode = h->mode; rc.ascale = 1.0f / sqrtf((float)m->HD);
@@ -805,6 +821,7 @@ void enqueue_body(sp_kvdecode_handle *h, const StepShape &sh, TimeCb cb, void *c
         if (h->rec.B > 0 && a.win < 0) { a.rec_R = h->rec.Rb; a.rec_r = h->rec.r; }
         const int cls = (glob || a.win < 0) ? 5 : 6, grid = glob ? sh.grid_global : sh.grid_local;
         if (sh.route && a.rec_r) {
+            a.rec_pq = h->rec.pq;                       // the router's query projections
             T(7, true); launch_qk_prep(a, s); T(7, false);
             T(cls, true); launch_recall_attention(recall_args(h, a.pages, a.stat_out), s); T(cls, false);
         } else if (attention_fuses_prep(a)) {
@@ -1489,6 +1506,8 @@ int sp_hipkv_set_recall(sp_kvdecode_handle *h, int B, int W, int sink, int r) {
     if (h->dpos != 0) return fail("sp_hipkv_set_recall: recall is fixed once tokens are resident%s");
     if (B > 0 && h->m->HD != 64 && h->m->HD != 128 && h->m->HD != 256)
         return fail("sp_hipkv_set_recall: recall serves head_dim 64, 128 and 256%s");
+    if (B > 0 && h->m->NH / h->m->NKV > RECALL_MAX_GROUP)
+        return fail("sp_hipkv_set_recall: recall serves at most 8 q heads per kv head%s");
     if (B > 0 && h->mode == FLOAT && h->kvc == KVC_SPINOR)
         return fail("sp_hipkv_set_recall: recall in float mode reads plain K/V rows (not Spinor code rows)%s");
     if (h->pool.use_count() > 1) return fail("sp_hipkv_set_recall: the KV pages are shared with a fork%s");
@@ -1670,6 +1689,14 @@ int sp_hipkv_kernel_times(sp_kvdecode_handle *h, int32_t first_token, int n, dou
         for (int k = 0; k < SP_HIPKV_NCLASS; k++) bytes[k] += per_step[k];
         for (int l = 0; l < m->NL; l++) {
             const bool glob = is_global(m, l);
+            if (glob && h->rec.B > 0) {
+                // recall: each q head scans its kv head's sidecar over the
+                // candidates and reads the K and V rows of its recall set
+                const RecallGeom g = recall_geom(h->rec, pos);
+                const double scan = (g.ident || !g.topk) ? 0.0 : (double)(g.cand_hi - g.sink) * h->rec.r * 4.0;
+                bytes[5] += (double)m->NH * (scan + (double)g.m * kv_row_payload(m, h->mode, h->kvc) * 2);
+                continue;
+            }
             const int s0 = (!glob && m->SW > 0 && pos - m->SW + 1 > 0) ? pos - m->SW + 1 : 0;
             bytes[(glob || m->SW <= 0) ? 5 : 6] += kvb * (pos - s0 + 1);
         }

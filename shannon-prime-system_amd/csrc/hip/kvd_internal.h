@@ -100,12 +100,13 @@ struct AttnArgs {
     // frozen +-1 matrix (sign bits rec_R [rec_r][HD/32]) into its page
     const uint32_t *rec_R;
     int rec_r;
+    float *rec_pq;           // routed step: each q head's projection [NH][rec_r] (NULL: not needed)
 };
 
 // ARM recall over one global layer's pages (decode): the router picks each q
 // head's positions from the K sidecar, the attention reads only those.
 struct RecallArgs {
-    const uint32_t *Rb;      // [r][HD/32] sign bits of the frozen projection (bit set: +1)
+    const float *pq;         // each q head's projection [NH][r] (written by the head preparation)
     const float *qr;         // rotated, normed q [NH*HD]
     float *const *pages;     // this layer's page table (full: no ring)
     const DState *st;
@@ -119,13 +120,14 @@ struct RecallArgs {
     int64_t *vacc, *vs;      // exact: V-sum totals [NH][HD] and denominators [NH] (zero between launches)
     float *part, *psum;      // float: chunk V-sums [NH][mchunks][HD] and weight sums [NH][mchunks]
     int *counter;            // [NH] arrival counters (self-resetting)
-    int kstride, lstride, mchunks, score_blocks;
+    int kstride, lstride, mchunks, score_blocks;   // kstride: a multiple of 4, >= pmax
     int NH, NKV, HD, r, B, W, sink, mode;
     float ascale;
 };
 void launch_recall_attention(const RecallArgs &rc, hipStream_t s);
 constexpr int RECALL_CHUNK = 64;        // recalled positions per attention workgroup
-constexpr int RECALL_SCORE_BLOCKS = 32; // router scoring workgroups per q head (grid-stride)
+constexpr int RECALL_SCORE_BLOCKS = 64; // router scoring workgroups per kv head (grid-stride)
+constexpr int RECALL_MAX_GROUP = 8;     // q heads per kv head the router serves
 int recall_page_floats(int NKV, int r); // sidecar floats per page
 
 struct Seg { DevW w; float *out; };

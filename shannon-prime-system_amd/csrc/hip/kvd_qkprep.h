@@ -23,13 +23,14 @@ struct HeadPrep {
     int *vclamp;              // exact mode: count of V heads stored with a clamped element
     const uint32_t *rec_R;    // recall sidecar projection sign bits [rec_r][HD/32]
     int rec_r;                // 0: no sidecar
+    float *rec_pq;            // routed step: q heads' projections [NH][rec_r]
 };
 __device__ __forceinline__ HeadPrep head_prep_of(const AttnArgs &a) {
     HeadPrep p;
     p.q = a.q; p.k = a.k; p.v = a.v; p.q_norm = a.q_norm; p.k_norm = a.k_norm; p.rope_cs = a.rope_cs;
     p.qr = a.qr; p.pages = a.pages; p.ring_pages = a.ring_pages; p.NH = a.NH; p.NKV = a.NKV; p.HD = a.HD;
     p.mode = a.mode; p.kvc = a.kvc; p.eps = a.eps; p.vclamp = a.vclamp;
-    p.rec_R = a.rec_R; p.rec_r = a.rec_r;
+    p.rec_R = a.rec_R; p.rec_r = a.rec_r; p.rec_pq = a.rec_pq;
     return p;
 }
 
@@ -182,7 +183,8 @@ __device__ __forceinline__ void spinor_head(float x[8], int lane, bool store, ui
     if (store && lane < NB) ((float *)(row + HD))[lane] = mul_mine;
 }
 
-// The recall sidecar of one K head (core/arm/arm.c:31-45): lane p < r gets
+// The recall projection of one K head (the sidecar) or q head (the router's
+// query), core/arm/arm.c:31-45: lane p < r gets
 // sum_d R[p][d] * k[d] as a sequential float sum in d (R = +-1, so each
 // product is +-k[d] exactly and only the additions round, as on the CPU).
 // The wave holds k at lanes l + 64 j in out[j]; readlane broadcasts each
@@ -251,6 +253,8 @@ __device__ __forceinline__ void qk_prep_head_t(const HeadPrep a, int hb, int pos
     if (isq) {
         #pragma unroll
         for (int j = 0; j < 8; j++) if (j < per) a.qr[(size_t)h * HD + lane + 64 * j] = out[j];
+        if (a.rec_pq)                                           // the router's query projection
+            recall_sidecar<PER>(a.rec_R, a.rec_r, out, a.rec_pq + (size_t)h * a.rec_r, lane);
         return;
     }
     if (a.rec_r)                                                // sidecar from the K before any codec
