@@ -880,7 +880,10 @@ static void attention_go(const AttnArgs &a, int grid_chunks, bool prep, hipStrea
     else if (a.HD == 256 && G == 4) attn_dispatch<4, 4>(a, grid_chunks, prep, s);
     else if (a.HD == 64 && G == 4) attn_dispatch<1, 4>(a, grid_chunks, prep, s);
 }
-void launch_attention(const AttnArgs &a, int grid_chunks, hipStream_t s) { attention_go(a, grid_chunks, false, s); }
+void launch_attention(const AttnArgs &a, int grid_chunks, hipStream_t s) {
+    if (prefill_attention_tiled(a)) return launch_prefill_attention(a, s);
+    attention_go(a, grid_chunks, false, s);
+}
 
 // Workgroups of the exact decode attention (score pass and V-sum) the device
 // holds at once, the smaller of the two (0: no such instance).  The host sizes

@@ -125,6 +125,10 @@ struct RecallArgs {
     float ascale;
 };
 void launch_recall_attention(const RecallArgs &rc, hipStream_t s);
+// exact-mode attention of one session's batched prefill on global layers
+// (token-shared K/V reads, the score pass on the int8 matrix cores)
+bool prefill_attention_tiled(const AttnArgs &a);
+void launch_prefill_attention(const AttnArgs &a, hipStream_t s);
 constexpr int RECALL_CHUNK = 64;        // recalled positions per attention workgroup
 constexpr int RECALL_SCORE_BLOCKS = 64; // router scoring workgroups per kv head (grid-stride)
 constexpr int RECALL_MAX_GROUP = 8;     // q heads per kv head the router serves

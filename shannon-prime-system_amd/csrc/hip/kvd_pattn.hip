@@ -1,0 +1,373 @@
+// kvd_pattn.hip -- exact-mode attention of one session's batched prefill on
+// the global (full-context) layers: the batch's tokens share every K and V row
+// they read instead of each token streaming the whole context.
+//
+// The arithmetic is the decode attention's (kvd_attn.hip), so every token's
+// scores, weights and output are bit-identical to a decode step's:
+//   ip = <qi, ki> exact, qi = rne(q 2^16), ki the stored int32 K;
+//   z = llround(((float)((double)ip / 2^32) * ascale) * 2^14);
+//   w = exp_fixed(((z - M) 2^30) >> 14) >> 8 (Q22), M the token-head's max;
+//   out = RNE(sum_p w vq / (sum_p w * 2^16)).
+//
+// Score pass, on the int8 matrix cores: qi and ki are split into four balanced
+// base-256 digits; every digit pair (a, b) is one int8 MFMA product with an
+// exact int32 sum (|sum| <= HD 2^14), and ip = sum_{a,b} 2^(8(a+b)) P_ab in
+// int64 -- the same integer as the decode kernels' int64 dot product.  A
+// workgroup scores 64 positions for 64 token-heads (one 16 x 16 tile row per
+// wave); the positions' K digits are staged once in LDS.  A workgroup whose q
+// or K values do not fit four balanced digits (|x| > 127 (1 + 2^8 + 2^16 +
+// 2^24)) scores its tile on the vector units instead, with the same result.
+//
+// V-sum pass: a workgroup takes a 512-position chunk for a group of tokens:
+// each V row is read once for all of the group's token-heads (FP64 FMAs on
+// integers below 2^53, as in decode), partial sums go to the tokens' int64
+// totals by order-free atomics, and the group's last workgroup divides.
+#include "kvd_internal.h"
+#include "kvd_exact.h"
+#include "kvd_vec.h"
+#include "kvd_spinor.h"
+
+namespace kvd {
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+constexpr int PS_CH = 64;            // positions per score workgroup (and per chunk maximum)
+constexpr int PV_CH = 512;           // positions per V-sum workgroup (128 rows per wave: FP64 sums below 2^52)
+constexpr int DIG_MAX = 127 * (1 + 256 + 65536 + 16777216);   // largest |x| of four balanced digits
+
+__device__ __forceinline__ const float *pg(const AttnArgs &a, int pos) { return a.pages[pos / PAGE]; }
+
+// x = d0 + 2^8 d1 + 2^16 d2 + 2^24 d3, d in [-128, 127] (|x| <= DIG_MAX)
+__device__ __forceinline__ void digits4(int32_t x, int32_t d[4]) {
+    #pragma unroll
+    for (int k = 0; k < 4; k++) {
+        d[k] = ((x + 128) & 255) - 128;
+        x = (x - d[k]) >> 8;
+    }
+}
+
+// ---------------------------------------------------------------- score pass
+// grid: (token groups of 64 / G tokens, 64-position chunks, kv heads); the
+// token group runs fastest, so the groups reading one chunk's K run together.
+// zscratch and the chunk maxima are laid out per token as for the decode
+// kernels: token t's scores at zscratch + t NH zstride, its maximum of chunk c
+// of token-head q at part_ml + t NH max_chunks 4 + (q max_chunks + c) 4.
+template <int EPL, int G>
+__global__ __launch_bounds__(256) void k_pattn_scores(AttnArgs a) {
+    constexpr int HD = EPL * 64, KS = HD / 32, TPW = 16 / G, TWG = 4 * TPW, KROW = HD + 16;
+    const int tg = blockIdx.x, c = blockIdx.y, h = blockIdx.z;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int t0 = tg * TWG;
+    const int tend = t0 + TWG < a.nt ? t0 + TWG : a.nt;
+    const int pos_hi = a.pos0 + tend - 1;               // the group's last token attends up to here
+    const int cs = c * PS_CH;
+    if (t0 >= a.nt || cs > pos_hi) return;
+    const int np = pos_hi - cs + 1 < PS_CH ? pos_hi - cs + 1 : PS_CH;
+    __shared__ __align__(16) int8_t kd[4][PS_CH][KROW];   // K digits [digit][position][dim]
+    __shared__ int s_wide;
+    if (threadIdx.x == 0) s_wide = 0;
+    const size_t QD = (size_t)a.NH * HD;
+    // this wave's 16 token-heads: lane row m = lane % 16 -> token t0 + wave TPW + m / G, head h G + m % G
+    const int m = lane & 15, j = lane >> 4;
+    const int tq = t0 + wave * TPW + m / G;
+    const float *qp = a.qr + (size_t)(tq < a.nt ? tq : 0) * QD + (size_t)(h * G + m % G) * HD + 8 * j;
+    int32_t qi[KS][8];
+    bool wide = false;
+    #pragma unroll
+    for (int ks = 0; ks < KS; ks++) {
+        const float4 v0 = *(const float4 *)(qp + 32 * ks), v1 = *(const float4 *)(qp + 32 * ks + 4);
+        const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+        #pragma unroll
+        for (int e = 0; e < 8; e++) {
+            qi[ks][e] = tq < a.nt ? (int32_t)rintf(v[e] * 65536.0f) : 0;
+            wide |= qi[ks][e] > DIG_MAX || qi[ks][e] < -DIG_MAX;
+        }
+    }
+    __syncthreads();                                    // s_wide is cleared
+    // K rows of the chunk as digit planes: thread i takes 16 consecutive dims of a row
+    for (int i = threadIdx.x; i < PS_CH * (HD / 16); i += 256) {
+        const int pl = i / (HD / 16), d0 = (i % (HD / 16)) * 16, p = cs + pl;
+        int32_t x[16];
+        if (pl < np) {
+            const int32_t *row = (const int32_t *)pg(a, p) + ((size_t)h * PAGE + (p & (PAGE - 1))) * HD + d0;
+            #pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int4 v = *(const int4 *)(row + 4 * q);
+                x[4 * q] = v.x; x[4 * q + 1] = v.y; x[4 * q + 2] = v.z; x[4 * q + 3] = v.w;
+            }
+        } else {
+            #pragma unroll
+            for (int e = 0; e < 16; e++) x[e] = 0;
+        }
+        uint32_t w[4][4] = {};
+        #pragma unroll
+        for (int e = 0; e < 16; e++) {
+            wide |= x[e] > DIG_MAX || x[e] < -DIG_MAX;
+            int32_t d[4];
+            digits4(x[e], d);
+            #pragma unroll
+            for (int b = 0; b < 4; b++) w[b][e >> 2] |= (uint32_t)(d[b] & 255) << (8 * (e & 3));
+        }
+        #pragma unroll
+        for (int b = 0; b < 4; b++) *(uint4 *)&kd[b][pl][d0] = make_uint4(w[b][0], w[b][1], w[b][2], w[b][3]);
+    }
+    if (__any(wide) && lane == 0) s_wide = 1;
+    __syncthreads();
+    const bool mfma = s_wide == 0;
+
+    // this wave's A operands: digit a of qi at dims 32 ks + 8 j .. +8 (byte e = dim 8 j + e)
+    long A[4][KS];
+    #pragma unroll
+    for (int ks = 0; ks < KS; ks++) {
+        uint32_t lo[4] = {}, hi[4] = {};
+        #pragma unroll
+        for (int e = 0; e < 8; e++) {
+            int32_t d[4];
+            digits4(qi[ks][e], d);
+            #pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const uint32_t byte = (uint32_t)(d[b] & 255) << (8 * (e & 3));
+                if (e < 4) lo[b] |= byte; else hi[b] |= byte;
+            }
+        }
+        #pragma unroll
+        for (int b = 0; b < 4; b++) A[b][ks] = (long)(((uint64_t)hi[b] << 32) | lo[b]);
+    }
+    int mx[4] = {INT32_MIN, INT32_MIN, INT32_MIN, INT32_MIN};
+    const int rowq = 4 * j;                              // output rows 4 j .. 4 j + 3 of the tile
+    for (int nt = 0; nt < PS_CH / 16; nt++) {
+        if (nt * 16 >= np) break;
+        const int p = cs + nt * 16 + m;                  // this lane's output column (position)
+        int64_t ip[4] = {0, 0, 0, 0};
+        if (mfma) {
+            v4i acc[16];
+            #pragma unroll
+            for (int k = 0; k < 16; k++) acc[k] = (v4i){0, 0, 0, 0};
+            #pragma unroll
+            for (int ks = 0; ks < KS; ks++) {
+                long B[4];
+                #pragma unroll
+                for (int b = 0; b < 4; b++) B[b] = *(const long *)&kd[b][nt * 16 + m][32 * ks + 8 * j];
+                #pragma unroll
+                for (int a2 = 0; a2 < 4; a2++)
+                    #pragma unroll
+                    for (int b = 0; b < 4; b++)
+                        acc[a2 * 4 + b] = __builtin_amdgcn_mfma_i32_16x16x32_i8(A[a2][ks], B[b], acc[a2 * 4 + b], 0, 0, 0);
+            }
+            #pragma unroll
+            for (int i = 0; i < 4; i++)
+                #pragma unroll
+                for (int a2 = 0; a2 < 4; a2++)
+                    #pragma unroll
+                    for (int b = 0; b < 4; b++) ip[i] += (int64_t)acc[a2 * 4 + b][i] * ((int64_t)1 << (8 * (a2 + b)));
+        } else {
+            // out-of-range magnitudes: the tile on the vector units, from the
+            // digits (x = sum_b 2^(8b) d_b exactly holds only in range, so the
+            // int32 values are rebuilt from the rows themselves)
+            #pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int mm = rowq + i;
+                const int tt = t0 + wave * TPW + mm / G;
+                if (tt >= a.nt || p > pos_hi) continue;
+                const float *q2 = a.qr + (size_t)tt * QD + (size_t)(h * G + mm % G) * HD;
+                const int32_t *krow = (const int32_t *)pg(a, p) + ((size_t)h * PAGE + (p & (PAGE - 1))) * HD;
+                int64_t s = 0;
+                for (int d = 0; d < HD; d++) s += (int64_t)(int32_t)rintf(q2[d] * 65536.0f) * krow[d];
+                ip[i] = s;
+            }
+        }
+        #pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int mm = rowq + i;
+            const int tt = t0 + wave * TPW + mm / G;
+            if (tt < a.nt && p <= a.pos0 + tt) {
+                const float scv = (float)((double)ip[i] / 4294967296.0) * a.ascale;
+                const int32_t z = (int32_t)llround_pow2<14>(scv);
+                a.zscratch[(size_t)tt * a.NH * a.zstride + (size_t)(h * G + mm % G) * a.zstride + p] = z;
+                mx[i] = z > mx[i] ? z : mx[i];
+            }
+        }
+    }
+    // chunk maxima: over the 16 lanes of a row group
+    #pragma unroll
+    for (int i = 0; i < 4; i++) {
+        int v = mx[i];
+        #pragma unroll
+        for (int o = 1; o < 16; o <<= 1) { const int w = __shfl_xor(v, o, 64); v = w > v ? w : v; }
+        mx[i] = v;
+    }
+    if (m == 0) {
+        #pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int mm = rowq + i;
+            const int tt = t0 + wave * TPW + mm / G;
+            if (tt < a.nt && cs <= a.pos0 + tt)
+                ((int32_t *)a.part_ml)[(size_t)tt * a.NH * a.max_chunks * 4 + ((size_t)(h * G + mm % G) * a.max_chunks + c) * 4] = mx[i];
+        }
+    }
+}
+
+// --------------------------------------------------------------- V-sum pass
+// grid: (token groups of TT tokens, 512-position chunks, kv heads).  NQ =
+// TT G token-heads share each V row.  Token t's totals are its decode-layout
+// accumulators (vacc + t QD VREP, vacc_s + t NH VREP, replica 0) and its
+// group's arrivals count on counter[t0 NKV + h].
+template <int EPL, int G, int TT>
+__global__ __launch_bounds__(256) void k_pattn_vsum(AttnArgs a) {
+    constexpr int HD = EPL * 64, NQ = TT * G, UV = 4;
+    const int tg = blockIdx.x, c = blockIdx.y, h = blockIdx.z;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int t0 = tg * TT;
+    const int tend = t0 + TT < a.nt ? t0 + TT : a.nt;
+    const int pos_hi = a.pos0 + tend - 1;
+    const int nch = pos_hi / PV_CH + 1;                 // chunks of this group (the arrival count)
+    const int cs = c * PV_CH;
+    if (t0 >= a.nt || c >= nch) return;
+    const int np = pos_hi - cs + 1 < PV_CH ? pos_hi - cs + 1 : PV_CH;
+    const size_t QD = (size_t)a.NH * HD;
+    __shared__ int32_t ew[NQ][PV_CH];                    // island weights (Q22), 0 where masked
+    __shared__ int s_M[NQ];
+    __shared__ int64_t ored[NQ][HD];                      // the waves' partials, added in LDS (order-free)
+    __shared__ int64_t sred[NQ];
+    __shared__ int is_last;
+    for (int i = threadIdx.x; i < NQ * HD; i += 256) ored[i / HD][i % HD] = 0;
+    // each token-head's maximum over its 64-position chunk maxima (wave w: token-heads w, w+4, ..)
+    for (int q = wave; q < NQ; q += 4) {
+        const int tt = t0 + q / G;
+        int t = INT32_MIN;
+        if (tt < a.nt) {
+            const int n64 = (a.pos0 + tt) / PS_CH + 1;
+            const int32_t *pml = (const int32_t *)a.part_ml + (size_t)tt * a.NH * a.max_chunks * 4 +
+                                 (size_t)(h * G + q % G) * a.max_chunks * 4;
+            for (int k = lane; k < n64; k += 64) { const int v = pml[(size_t)k * 4]; t = v > t ? v : t; }
+        }
+        t = wave_allmax_i(t);
+        if (lane == 0) s_M[q] = t;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < NQ * PV_CH; i += 256) {
+        const int q = i / PV_CH, jj = i % PV_CH, tt = t0 + q / G, p = cs + jj;
+        int32_t w = 0;
+        if (jj < np && tt < a.nt && p <= a.pos0 + tt) {
+            const int32_t z = a.zscratch[(size_t)tt * a.NH * a.zstride + (size_t)(h * G + q % G) * a.zstride + p];
+            w = (int32_t)(exp_fixed((((int64_t)z - (int64_t)s_M[q]) * ONE) >> 14) >> 8);
+        }
+        ew[q][jj] = w;
+    }
+    __syncthreads();
+    // FP64 V-sum: a wave's rows (<= 128) keep every partial an integer below 2^53
+    double o[NQ][EPL];
+    #pragma unroll
+    for (int q = 0; q < NQ; q++)
+        #pragma unroll
+        for (int e = 0; e < EPL; e++) o[q][e] = 0.0;
+    for (int j0 = wave * UV; j0 < np; j0 += 4 * UV) {
+        int32_t v[UV][EPL];
+        #pragma unroll
+        for (int u = 0; u < UV; u++) {
+            const int jj = j0 + u;
+            if (jj < np) {
+                const int p = cs + jj;
+                const int32_t *row = (const int32_t *)pg(a, p) + (size_t)a.NKV * PAGE * HD +
+                                     ((size_t)h * PAGE + (p & (PAGE - 1))) * HD + lane * EPL;
+                #pragma unroll
+                for (int e = 0; e < EPL; e++) v[u][e] = row[e];
+            } else {
+                #pragma unroll
+                for (int e = 0; e < EPL; e++) v[u][e] = 0;
+            }
+        }
+        #pragma unroll
+        for (int u = 0; u < UV; u++) {
+            const int jj = j0 + u < PV_CH ? j0 + u : 0;
+            #pragma unroll
+            for (int q = 0; q < NQ; q++) {
+                const double w = (double)ew[q][jj];
+                #pragma unroll
+                for (int e = 0; e < EPL; e++) o[q][e] = fma(w, (double)v[u][e], o[q][e]);
+            }
+        }
+    }
+    #pragma unroll
+    for (int q = 0; q < NQ; q++)
+        #pragma unroll
+        for (int e = 0; e < EPL; e++) atomicAdd((unsigned long long *)&ored[q][lane * EPL + e], (unsigned long long)(int64_t)o[q][e]);
+    __syncthreads();
+    // denominators of this chunk
+    for (int q = wave; q < NQ; q += 4) {
+        int64_t s = 0;
+        for (int jj = lane; jj < PV_CH; jj += 64) s += ew[q][jj];
+        s = wave_allsum(s);
+        if (lane == 0) sred[q] = s;
+    }
+    for (int i = threadIdx.x; i < NQ * HD; i += 256) {
+        const int q = i / HD, d = i % HD, tt = t0 + q / G;
+        if (tt >= a.nt) continue;
+        const int64_t t = ored[q][d];
+        atomicAdd((unsigned long long *)&a.vacc[(size_t)tt * QD * VREP + (size_t)(h * G + q % G) * HD + d], (unsigned long long)t);
+    }
+    __syncthreads();
+    if (threadIdx.x < NQ) {
+        const int q = threadIdx.x, tt = t0 + q / G;
+        if (tt < a.nt)
+            atomicAdd((unsigned long long *)&a.vacc_s[(size_t)tt * a.NH * VREP + h * G + q % G], (unsigned long long)sred[q]);
+    }
+    mem_complete();
+    __syncthreads();
+    if (threadIdx.x == 0) is_last = (arrive(&a.counter[(size_t)t0 * a.NKV + h]) == nch - 1);
+    __syncthreads();
+    if (!is_last) return;
+    // the group's totals are read and cleared for the next launch in one atomic step
+    __shared__ int64_t Sg[NQ];
+    if (threadIdx.x < NQ) {
+        const int q = threadIdx.x, tt = t0 + q / G;
+        Sg[q] = tt < a.nt ? (int64_t)__hip_atomic_exchange((unsigned long long *)&a.vacc_s[(size_t)tt * a.NH * VREP + h * G + q % G],
+                                                           0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 1;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < NQ * HD; i += 256) {
+        const int q = i / HD, d = i % HD, tt = t0 + q / G;
+        if (tt >= a.nt) continue;
+        const int64_t tot = (int64_t)__hip_atomic_exchange(
+            (unsigned long long *)&a.vacc[(size_t)tt * QD * VREP + (size_t)(h * G + q % G) * HD + d], 0ull,
+            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        a.ao[(size_t)tt * QD + (size_t)(h * G + q % G) * HD + d] = rne_div_to_float((i128)tot, Sg[q], 16);
+    }
+    if (threadIdx.x == 0) reset_counter(&a.counter[(size_t)t0 * a.NKV + h]);
+}
+
+template <int EPL, int G>
+void pattn_go(const AttnArgs &a, hipStream_t s) {
+    constexpr int TPW = 16 / G, TWG = 4 * TPW, TT = 8 / G;
+    const int pos_hi = a.pos0 + a.nt - 1;
+    const dim3 g1((a.nt + TWG - 1) / TWG, pos_hi / PS_CH + 1, a.NKV);
+    hipLaunchKernelGGL((k_pattn_scores<EPL, G>), g1, dim3(256), 0, s, a);
+    const dim3 g2((a.nt + TT - 1) / TT, pos_hi / PV_CH + 1, a.NKV);
+    hipLaunchKernelGGL((k_pattn_vsum<EPL, G, TT>), g2, dim3(256), 0, s, a);
+}
+
+}  // namespace
+
+bool prefill_attention_tiled(const AttnArgs &a) {
+    const int G = a.NH / a.NKV;
+    return a.mode == EXACT && a.nt > 0 && !a.tpages && !a.tpos && a.win < 0 && a.ring_pages == 0 &&
+           a.kvc == KVC_PLAIN && (a.HD == 64 || a.HD == 128 || a.HD == 256) && (G == 2 || G == 4);
+}
+
+void launch_prefill_attention(const AttnArgs &a, hipStream_t s) {
+    const int G = a.NH / a.NKV;
+    const int pos_hi = a.pos0 + a.nt - 1;
+    // the chunk maxima and score rows must hold every position of the batch
+    if (!prefill_attention_tiled(a) || pos_hi / PS_CH + 1 > a.max_chunks || pos_hi >= a.zstride)
+        return launch_fail("tiled prefill attention: arguments outside the kernels' limits");
+    if (a.HD == 256 && G == 2) pattn_go<4, 2>(a, s);
+    else if (a.HD == 256) pattn_go<4, 4>(a, s);
+    else if (a.HD == 128 && G == 2) pattn_go<2, 2>(a, s);
+    else if (a.HD == 128) pattn_go<2, 4>(a, s);
+    else if (G == 2) pattn_go<1, 2>(a, s);
+    else pattn_go<1, 4>(a, s);
+}
+
+}  // namespace kvd
