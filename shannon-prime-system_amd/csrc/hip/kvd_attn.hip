@@ -119,9 +119,18 @@ __device__ __forceinline__ void tok_select(AttnArgs &a, int t, int &pos) {
 // launches put the token first, (token, chunk, kv head): the batch's tokens
 // that read one chunk's K/V rows are dispatched together and share them
 // through the caches, instead of each token streaming the whole span alone.
-template <bool BATCH> __device__ __forceinline__ int grid_token() { return BATCH ? (int)blockIdx.x : 0; }
-template <bool BATCH> __device__ __forceinline__ int grid_chunk() { return BATCH ? (int)blockIdx.y : (int)blockIdx.x; }
-template <bool BATCH> __device__ __forceinline__ int grid_head() { return BATCH ? (int)blockIdx.z : (int)blockIdx.y; }
+// A batched decode over sessions with a work list: (item, kv head), the item
+// naming the token and chunk, so no workgroup is launched for a chunk past its
+// session's position.
+template <bool BATCH> __device__ __forceinline__ int grid_token(const AttnArgs &a) {
+    return BATCH ? (a.work ? a.work[blockIdx.x].x : (int)blockIdx.x) : 0;
+}
+template <bool BATCH> __device__ __forceinline__ int grid_chunk(const AttnArgs &a) {
+    return BATCH ? (a.work ? a.work[blockIdx.x].y : (int)blockIdx.y) : (int)blockIdx.x;
+}
+template <bool BATCH> __device__ __forceinline__ int grid_head(const AttnArgs &a) {
+    return BATCH ? (a.work ? (int)blockIdx.y : (int)blockIdx.z) : (int)blockIdx.y;
+}
 
 // ------------------------------------------------------------------ qk_prep
 // grid.x = NH (q heads) + NKV (k heads) + NKV (v heads), one wave each
@@ -286,8 +295,8 @@ template <int EPL, int G, bool BATCH, bool SPN>
 __global__ __launch_bounds__(256) void k_attn_float(AttnArgs a_in) {
     AttnArgs a = a_in;
     int pos;
-    tok_select<BATCH>(a, grid_token<BATCH>(), pos);
-    const int HD = EPL * 64, c = grid_chunk<BATCH>(), h = grid_head<BATCH>();
+    tok_select<BATCH>(a, grid_token<BATCH>(a_in), pos);
+    const int HD = EPL * 64, c = grid_chunk<BATCH>(a_in), h = grid_head<BATCH>(a_in);
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     int cs, ce, nch;
     chunk_range(a, pos, c, cs, ce, nch);
@@ -596,8 +605,8 @@ __global__ __launch_bounds__(256) void k_attn_exact_scores(AttnArgs a_in) {
     static_assert(!(BATCH && PREP), "head preparation is fused for decode only");
     AttnArgs a = a_in;
     int pos;
-    tok_select<BATCH>(a, grid_token<BATCH>(), pos);
-    const int HD = EPL * 64, c = grid_chunk<BATCH>(), h = grid_head<BATCH>();
+    tok_select<BATCH>(a, grid_token<BATCH>(a_in), pos);
+    const int HD = EPL * 64, c = grid_chunk<BATCH>(a_in), h = grid_head<BATCH>(a_in);
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     int cs, ce, nch;
     chunk_range(a, pos, c, cs, ce, nch);
@@ -695,8 +704,8 @@ template <int EPL, int G, bool BATCH, int UV>
 __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a_in) {
     AttnArgs a = a_in;
     int pos;
-    tok_select<BATCH>(a, grid_token<BATCH>(), pos);
-    const int HD = EPL * 64, c = grid_chunk<BATCH>(), h = grid_head<BATCH>();
+    tok_select<BATCH>(a, grid_token<BATCH>(a_in), pos);
+    const int HD = EPL * 64, c = grid_chunk<BATCH>(a_in), h = grid_head<BATCH>(a_in);
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     int cs, ce, nch;
     chunk_range(a, pos, c, cs, ce, nch);
@@ -854,7 +863,7 @@ __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a_in) {
 // decode (B = false: position from the step state) and batched prefill
 // (B = true: token grid dimension) are separate instances
 template <int EPL, int G, bool B> static void attn_dispatch_b(const AttnArgs &a, int grid_chunks, bool prep, hipStream_t s) {
-    const dim3 grid = B ? dim3(a.nt, grid_chunks, a.NKV) : dim3(grid_chunks, a.NKV, 1);
+    const dim3 grid = B ? (a.work ? dim3(a.nwork, a.NKV, 1) : dim3(a.nt, grid_chunks, a.NKV)) : dim3(grid_chunks, a.NKV, 1);
     if (a.mode == FLOAT && a.kvc == KVC_SPINOR) hipLaunchKernelGGL((k_attn_float<EPL, G, B, true>), grid, dim3(256), 0, s, a);
     else if (a.mode == FLOAT) hipLaunchKernelGGL((k_attn_float<EPL, G, B, false>), grid, dim3(256), 0, s, a);
     else {

@@ -447,6 +447,7 @@ struct sp_kvdecode_handle {
         // greedy tokens, per-token token / position / per-layer page tables
         void *dbuf = nullptr;
         float *logits; int *next, *toks, *tpos; float *const **tpages;
+        int2 *work; int nwork = 0, wcap = 0;   // full-context layers' (token, chunk) work items
         void *hstage = nullptr;              // pinned upload staging for toks/tpos/tpages
     } b;
     // graph cache: key (logits?, argmax?, grid_global, grid_local, chunk_global)
@@ -977,9 +978,14 @@ int run_batch(sp_kvdecode_handle *h, int T, int pos0, int pos_hi, bool multi, Ti
         a.base = (m->gemma && !glob) ? 10000.0f : m->base;
         a.ascale = 1.0f / sqrtf((float)m->HD);
         a.nt = T; a.pos0 = pos0; a.rope_stride = 2 * m->HD; a.vclamp = h->vclamp;
-        if (multi) { a.tpos = b.tpos; a.tpages = b.tpages + (size_t)l * b.TB; }
+        if (multi) {
+            a.tpos = b.tpos; a.tpages = b.tpages + (size_t)l * b.TB;
+            if (glob || a.win < 0) { a.work = b.work; a.nwork = b.nwork; }
+        }
         else if (h->rec.B > 0 && a.win < 0) { a.rec_R = h->rec.Rb; a.rec_r = h->rec.r; }   // prefill: the sidecar
-        a.chunk = (glob || a.win < 0) ? 256 : 64;
+        // batched decode over sessions: the longest chunks the kernels take,
+        // so that the many sessions' rows make fewer, longer workgroups
+        a.chunk = (glob || a.win < 0) ? (multi ? ATTN_MAXCH : 256) : 64;
         TM(7, true); launch_qk_prep(a, s); TM(7, false);
         // chunks of the batch's longest span: a window of W positions covers at
         // most (W-1)/chunk + 2 chunks whatever its alignment
@@ -1302,30 +1308,39 @@ static int decode_batch_impl(sp_kvdecode_handle *const *hs, int n, const int32_t
     const int TB = b.TB;
     if (!b.dbuf) {
         const size_t lb = (size_t)TB * m->V * 4, nb = (size_t)TB * 4, pb = (size_t)m->NL * TB * sizeof(void *);
-        HIPCHK(hipMalloc(&b.dbuf, align_up(lb, 256) + 3 * align_up(nb, 256) + pb), "batch decode alloc");
+        b.wcap = TB * (L->pmax / ATTN_MAXCH + 2);
+        const size_t wb = (size_t)b.wcap * sizeof(int2);
+        HIPCHK(hipMalloc(&b.dbuf, align_up(lb, 256) + 3 * align_up(nb, 256) + align_up(pb, 256) + wb), "batch decode alloc");
         uint8_t *p = (uint8_t *)b.dbuf;
         b.logits = (float *)p; p += align_up(lb, 256);
         b.next = (int *)p; p += align_up(nb, 256);
         b.toks = (int *)p; p += align_up(nb, 256);
         b.tpos = (int *)p; p += align_up(nb, 256);
-        b.tpages = (float *const **)p;
-        HIPCHK(hipHostMalloc(&b.hstage, 2 * nb + pb, hipHostMallocDefault), "batch decode staging");
+        b.tpages = (float *const **)p; p += align_up(pb, 256);
+        b.work = (int2 *)p;
+        HIPCHK(hipHostMalloc(&b.hstage, 2 * nb + pb + wb, hipHostMallocDefault), "batch decode staging");
     }
     for (int g0 = 0; g0 < n; g0 += TB) {
         const int T = std::min(TB, n - g0);
         int *htok = (int *)b.hstage, *hpos = htok + TB;
         float *const **hpg = (float *const **)(hpos + TB);
+        int2 *hwork = (int2 *)(hpg + (size_t)m->NL * TB);
         int pos_hi = 0;
+        b.nwork = 0;
         for (int t = 0; t < T; t++) {
             sp_kvdecode_handle *h = hs[g0 + t];
             htok[t] = tokens[g0 + t]; hpos[t] = h->dpos;
             pos_hi = std::max(pos_hi, h->dpos);
             for (int l = 0; l < m->NL; l++) hpg[(size_t)l * TB + t] = h->d_pt + h->pt_off[l];
+            // full-context layers: ATTN_MAXCH-position chunks up to this session's position
+            for (int c = 0; c <= h->dpos / ATTN_MAXCH && b.nwork < b.wcap; c++) hwork[b.nwork++] = make_int2(t, c);
         }
         HIPCHK(hipMemcpyAsync(b.toks, htok, (size_t)TB * 4, hipMemcpyHostToDevice, L->stream), "batch tokens");
         HIPCHK(hipMemcpyAsync(b.tpos, hpos, (size_t)TB * 4, hipMemcpyHostToDevice, L->stream), "batch positions");
         HIPCHK(hipMemcpyAsync((void *)b.tpages, hpg, (size_t)m->NL * TB * sizeof(void *), hipMemcpyHostToDevice, L->stream),
                "batch page tables");
+        HIPCHK(hipMemcpyAsync(b.work, hwork, (size_t)b.nwork * sizeof(int2), hipMemcpyHostToDevice, L->stream),
+               "batch work items");
         if (run_batch(L, T, 0, pos_hi, true, cb, ctx)) return 1;
         if (logits) HIPCHK(hipMemcpyAsync(logits + (size_t)g0 * m->V, b.logits, (size_t)T * m->V * 4,
                                           hipMemcpyDeviceToHost, L->stream), "batch logits download");

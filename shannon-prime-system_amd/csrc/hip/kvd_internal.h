@@ -96,6 +96,10 @@ struct AttnArgs {
     float *const *const *tpages;
     VecStat *stat_out;       // decode: statistics of ao for the O GEMV (NULL: none)
     int *vclamp;             // exact mode: +1 per stored V head with a clamped element (NULL: not counted)
+    // batched decode over sessions, full-context layers: the (token, chunk)
+    // work items, one workgroup each per kv head (NULL: the token x chunk grid)
+    const int2 *work;
+    int nwork;
     // recall sidecar: rec_r > 0 writes each new K head's projection on the
     // frozen +-1 matrix (sign bits rec_R [rec_r][HD/32]) into its page
     const uint32_t *rec_R;

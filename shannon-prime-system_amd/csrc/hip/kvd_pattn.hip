@@ -18,7 +18,7 @@
 // or K values do not fit four balanced digits (|x| > 127 (1 + 2^8 + 2^16 +
 // 2^24)) scores its tile on the vector units instead, with the same result.
 //
-// V-sum pass: a workgroup takes a 512-position chunk for a group of tokens:
+// V-sum pass: a workgroup takes a 2048-position chunk for a group of tokens:
 // each V row is read once for all of the group's token-heads (FP64 FMAs on
 // integers below 2^53, as in decode), partial sums go to the tokens' int64
 // totals by order-free atomics, and the group's last workgroup divides.
@@ -34,7 +34,8 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int PS_CH = 64;            // positions per score workgroup (and per chunk maximum)
-constexpr int PV_CH = 512;           // positions per V-sum workgroup (128 rows per wave: FP64 sums below 2^52)
+constexpr int PV_CH = 2048;          // positions per V-sum workgroup
+constexpr int PV_SUB = 512;          // ... in sub-chunks of 128 rows per wave (FP64 sums below 2^53)
 constexpr int DIG_MAX = 127 * (1 + 256 + 65536 + 16777216);   // largest |x| of four balanced digits
 
 __device__ __forceinline__ const float *pg(const AttnArgs &a, int pos) { return a.pages[pos / PAGE]; }
@@ -210,7 +211,7 @@ __global__ __launch_bounds__(256) void k_pattn_scores(AttnArgs a) {
 }
 
 // --------------------------------------------------------------- V-sum pass
-// grid: (token groups of TT tokens, 512-position chunks, kv heads).  NQ =
+// grid: (token groups of TT tokens, 2048-position chunks, kv heads).  NQ =
 // TT G token-heads share each V row.  Token t's totals are its decode-layout
 // accumulators (vacc + t QD VREP, vacc_s + t NH VREP, replica 0) and its
 // group's arrivals count on counter[t0 NKV + h].
@@ -227,12 +228,13 @@ __global__ __launch_bounds__(256) void k_pattn_vsum(AttnArgs a) {
     if (t0 >= a.nt || c >= nch) return;
     const int np = pos_hi - cs + 1 < PV_CH ? pos_hi - cs + 1 : PV_CH;
     const size_t QD = (size_t)a.NH * HD;
-    __shared__ int32_t ew[NQ][PV_CH];                    // island weights (Q22), 0 where masked
+    __shared__ int32_t ew[NQ][PV_SUB];                   // island weights (Q22) of a sub-chunk, 0 where masked
     __shared__ int s_M[NQ];
     __shared__ int64_t ored[NQ][HD];                      // the waves' partials, added in LDS (order-free)
     __shared__ int64_t sred[NQ];
     __shared__ int is_last;
     for (int i = threadIdx.x; i < NQ * HD; i += 256) ored[i / HD][i % HD] = 0;
+    if (threadIdx.x < NQ) sred[threadIdx.x] = 0;
     // each token-head's maximum over its 64-position chunk maxima (wave w: token-heads w, w+4, ..)
     for (int q = wave; q < NQ; q += 4) {
         const int tt = t0 + q / G;
@@ -247,60 +249,64 @@ __global__ __launch_bounds__(256) void k_pattn_vsum(AttnArgs a) {
         if (lane == 0) s_M[q] = t;
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < NQ * PV_CH; i += 256) {
-        const int q = i / PV_CH, jj = i % PV_CH, tt = t0 + q / G, p = cs + jj;
-        int32_t w = 0;
-        if (jj < np && tt < a.nt && p <= a.pos0 + tt) {
-            const int32_t z = a.zscratch[(size_t)tt * a.NH * a.zstride + (size_t)(h * G + q % G) * a.zstride + p];
-            w = (int32_t)(exp_fixed((((int64_t)z - (int64_t)s_M[q]) * ONE) >> 14) >> 8);
-        }
-        ew[q][jj] = w;
-    }
-    __syncthreads();
-    // FP64 V-sum: a wave's rows (<= 128) keep every partial an integer below 2^53
-    double o[NQ][EPL];
-    #pragma unroll
-    for (int q = 0; q < NQ; q++)
-        #pragma unroll
-        for (int e = 0; e < EPL; e++) o[q][e] = 0.0;
-    for (int j0 = wave * UV; j0 < np; j0 += 4 * UV) {
-        int32_t v[UV][EPL];
-        #pragma unroll
-        for (int u = 0; u < UV; u++) {
-            const int jj = j0 + u;
-            if (jj < np) {
-                const int p = cs + jj;
-                const int32_t *row = (const int32_t *)pg(a, p) + (size_t)a.NKV * PAGE * HD +
-                                     ((size_t)h * PAGE + (p & (PAGE - 1))) * HD + lane * EPL;
-                #pragma unroll
-                for (int e = 0; e < EPL; e++) v[u][e] = row[e];
-            } else {
-                #pragma unroll
-                for (int e = 0; e < EPL; e++) v[u][e] = 0;
+    for (int sb = 0; sb < np; sb += PV_SUB) {
+        const int ns = np - sb < PV_SUB ? np - sb : PV_SUB;
+        for (int i = threadIdx.x; i < NQ * PV_SUB; i += 256) {
+            const int q = i / PV_SUB, jj = i % PV_SUB, tt = t0 + q / G, p = cs + sb + jj;
+            int32_t w = 0;
+            if (jj < ns && tt < a.nt && p <= a.pos0 + tt) {
+                const int32_t z = a.zscratch[(size_t)tt * a.NH * a.zstride + (size_t)(h * G + q % G) * a.zstride + p];
+                w = (int32_t)(exp_fixed((((int64_t)z - (int64_t)s_M[q]) * ONE) >> 14) >> 8);
             }
+            ew[q][jj] = w;
         }
+        __syncthreads();
+        // FP64 V-sum of the sub-chunk: a wave's rows (<= 128) keep every
+        // partial an integer below 2^53; the partials then add in int64
+        double o[NQ][EPL];
         #pragma unroll
-        for (int u = 0; u < UV; u++) {
-            const int jj = j0 + u < PV_CH ? j0 + u : 0;
+        for (int q = 0; q < NQ; q++)
             #pragma unroll
-            for (int q = 0; q < NQ; q++) {
-                const double w = (double)ew[q][jj];
+            for (int e = 0; e < EPL; e++) o[q][e] = 0.0;
+        for (int j0 = wave * UV; j0 < ns; j0 += 4 * UV) {
+            int32_t v[UV][EPL];
+            #pragma unroll
+            for (int u = 0; u < UV; u++) {
+                const int jj = j0 + u;
+                if (jj < ns) {
+                    const int p = cs + sb + jj;
+                    const int32_t *row = (const int32_t *)pg(a, p) + (size_t)a.NKV * PAGE * HD +
+                                         ((size_t)h * PAGE + (p & (PAGE - 1))) * HD + lane * EPL;
+                    #pragma unroll
+                    for (int e = 0; e < EPL; e++) v[u][e] = row[e];
+                } else {
+                    #pragma unroll
+                    for (int e = 0; e < EPL; e++) v[u][e] = 0;
+                }
+            }
+            #pragma unroll
+            for (int u = 0; u < UV; u++) {
+                const int jj = j0 + u < PV_SUB ? j0 + u : 0;
                 #pragma unroll
-                for (int e = 0; e < EPL; e++) o[q][e] = fma(w, (double)v[u][e], o[q][e]);
+                for (int q = 0; q < NQ; q++) {
+                    const double w = (double)ew[q][jj];
+                    #pragma unroll
+                    for (int e = 0; e < EPL; e++) o[q][e] = fma(w, (double)v[u][e], o[q][e]);
+                }
             }
         }
-    }
-    #pragma unroll
-    for (int q = 0; q < NQ; q++)
         #pragma unroll
-        for (int e = 0; e < EPL; e++) atomicAdd((unsigned long long *)&ored[q][lane * EPL + e], (unsigned long long)(int64_t)o[q][e]);
-    __syncthreads();
-    // denominators of this chunk
-    for (int q = wave; q < NQ; q += 4) {
-        int64_t s = 0;
-        for (int jj = lane; jj < PV_CH; jj += 64) s += ew[q][jj];
-        s = wave_allsum(s);
-        if (lane == 0) sred[q] = s;
+        for (int q = 0; q < NQ; q++)
+            #pragma unroll
+            for (int e = 0; e < EPL; e++) atomicAdd((unsigned long long *)&ored[q][lane * EPL + e], (unsigned long long)(int64_t)o[q][e]);
+        // denominators of the sub-chunk
+        for (int q = wave; q < NQ; q += 4) {
+            int64_t sum = 0;
+            for (int jj = lane; jj < PV_SUB; jj += 64) sum += ew[q][jj];
+            sum = wave_allsum(sum);
+            if (lane == 0) atomicAdd((unsigned long long *)&sred[q], (unsigned long long)sum);
+        }
+        __syncthreads();                                 // ew is consumed
     }
     for (int i = threadIdx.x; i < NQ * HD; i += 256) {
         const int q = i / HD, d = i % HD, tt = t0 + q / G;
