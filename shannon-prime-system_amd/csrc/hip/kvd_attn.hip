@@ -91,11 +91,11 @@ template <typename T> __device__ __forceinline__ T ld_stream(const T *p) {
     typedef typename std::conditional<sizeof(T) == 16, int __attribute__((ext_vector_type(4))),
                                       int __attribute__((ext_vector_type(2)))>::type V;
     static_assert(sizeof(T) == sizeof(V), "8- or 16-byte rows");
-    return __builtin_bit_cast(T, __builtin_nontemporal_load((const V *)p));
+    return __builtin_bit_cast(T, __builtin_nontemporal_load(gmem((const V *)p)));
 }
 __device__ __forceinline__ float *page_of(float *const *pages, int ring, int pos) {
     const int lp = pos / PAGE;
-    return pages[ring ? lp % ring : lp];
+    return gmem(pages)[ring ? lp % ring : lp];
 }
 
 // Decode: the position comes from the step state.  Batched prefill: token t of
@@ -104,7 +104,7 @@ template <bool BATCH>
 __device__ __forceinline__ void tok_select(AttnArgs &a, int t, int &pos) {
     if constexpr (!BATCH) { pos = a.st->pos; return; }
     pos = a.tpos ? a.tpos[t] : a.pos0 + t;
-    if (a.tpages) a.pages = a.tpages[t];
+    if (a.tpages) a.pages = gmem(a.tpages)[t];
     const size_t QD = (size_t)a.NH * a.HD, KVD = (size_t)a.NKV * a.HD;
     a.q += t * QD; a.k += t * KVD; a.v += t * KVD; a.qr += t * QD; a.ao += t * QD;
     a.part += t * (size_t)a.NH * a.max_chunks * a.HD;
@@ -215,7 +215,7 @@ __device__ __forceinline__ void load_row(const AttnArgs &a, int h, int p, bool v
         const v2 t = ld_stream((const v2 *)src); out[0] = t.x; out[1] = t.y;
     } else {
         #pragma unroll
-        for (int e = 0; e < EPL; e++) out[e] = src[e];
+        for (int e = 0; e < EPL; e++) out[e] = gmem(src)[e];
     }
 }
 
@@ -235,12 +235,12 @@ __device__ __forceinline__ void load_row_spn(const AttnArgs &a, int h, int p, bo
     const uint8_t *row = spn_row<EPL>(a, page_of(a.pages, a.ring_pages, pu), hu, pu, vpart);
     const int e0 = lane * EPL, b0 = spn_block_of(HD, e0), b1 = spn_block_of(HD, e0 + EPL - 1);
     const float *mul = (const float *)(row + HD);
-    const float m0 = mul[b0], m1 = mul[b1];
+    const float m0 = gmem(mul)[b0], m1 = gmem(mul)[b1];
     const int bnd = spn_block_start(HD, b0 + 1);
     uint32_t w[(EPL + 3) / 4];
-    if constexpr (EPL == 1) w[0] = __builtin_nontemporal_load(row + e0);
-    else if constexpr (EPL == 2) w[0] = __builtin_nontemporal_load((const uint16_t *)(row + e0));
-    else if constexpr (EPL == 4) w[0] = __builtin_nontemporal_load((const uint32_t *)(row + e0));
+    if constexpr (EPL == 1) w[0] = __builtin_nontemporal_load(gmem(row + e0));
+    else if constexpr (EPL == 2) w[0] = __builtin_nontemporal_load(gmem((const uint16_t *)(row + e0)));
+    else if constexpr (EPL == 4) w[0] = __builtin_nontemporal_load(gmem((const uint32_t *)(row + e0)));
     else { const uint2 t = ld_stream((const uint2 *)(row + e0)); w[0] = t.x; w[1] = t.y; }
     #pragma unroll
     for (int e = 0; e < EPL; e++)
@@ -330,7 +330,7 @@ __global__ __launch_bounds__(256) void k_attn_float(AttnArgs a_in) {
             float mu[4 * NM4];
             #pragma unroll
             for (int t = 0; t < NM4; t++) {
-                const float4 m4 = *(const float4 *)(row + HD + 16 * t);
+                const float4 m4 = *gmem((const float4 *)(row + HD + 16 * t));
                 mu[4 * t] = m4.x; mu[4 * t + 1] = m4.y; mu[4 * t + 2] = m4.z; mu[4 * t + 3] = m4.w;
             }
             #pragma unroll
@@ -422,8 +422,8 @@ __global__ __launch_bounds__(256) void k_attn_float(AttnArgs a_in) {
                 if (j < n) {
                     const uint8_t *row = spn_row<EPL>(a, quad_page(a, cs + j0 + 4 * RPL * k, ce - 1, cs + j), h, cs + j, true);
                     cw[k] = ld_stream((const uint4 *)(row + d0));
-                    m0[k] = ((const float *)(row + HD))[b0];
-                    m1[k] = ((const float *)(row + HD))[b1];
+                    m0[k] = gmem((const float *)(row + HD))[b0];
+                    m1[k] = gmem((const float *)(row + HD))[b1];
                 }
             }
             #pragma unroll
@@ -575,7 +575,7 @@ __device__ __forceinline__ void prep_finish(const AttnArgs &a, int h, int pos, i
             #pragma unroll
             for (int j = 0; j < EPL; j++) {
                 const int32_t ki = kv_code_k(out[j]);
-                ((int32_t *)(page + rowoff))[lane + 64 * j] = ki;
+                gmem((int32_t *)(page + rowoff))[lane + 64 * j] = ki;
                 ((int *)kn)[lane + 64 * j] = ki;
             }
         }
@@ -587,7 +587,7 @@ __device__ __forceinline__ void prep_finish(const AttnArgs &a, int h, int pos, i
             if (a.kvc == KVC_SPINOR) spinor_head<EPL>(x, lane, false, nullptr);
             bool cl = false;
             #pragma unroll
-            for (int j = 0; j < EPL; j++) dst[lane + 64 * j] = kv_code_v(x[j], cl);
+            for (int j = 0; j < EPL; j++) gmem(dst)[lane + 64 * j] = kv_code_v(x[j], cl);
             count_v_clamp(a.vclamp, cl);
         }
     }
@@ -600,7 +600,11 @@ __device__ __forceinline__ void prep_finish(const AttnArgs &a, int h, int pos, i
 // appends the new K (after norm and RoPE) and V rows to the paged store and
 // scores position pos from the new K row it keeps in LDS (its own loads of
 // that row may predate the append).  Same arithmetic as k_qk_prep.
-template <int EPL, int G, bool BATCH, bool PREP>
+// LPR lanes per row, 16 bytes each per load: a load instruction takes LPR * 16
+// contiguous bytes of each of the wave's RPW = 64 / LPR rows.  8 lanes read
+// a whole 128-byte line of a row per load (long chunks: half the line requests
+// of 4 lanes); 4 lanes let the four waves cover a 64-position chunk in one pass.
+template <int EPL, int G, bool BATCH, bool PREP, int LPR>
 __global__ __launch_bounds__(256) void k_attn_exact_scores(AttnArgs a_in) {
     static_assert(!(BATCH && PREP), "head preparation is fused for decode only");
     AttnArgs a = a_in;
@@ -614,7 +618,9 @@ __global__ __launch_bounds__(256) void k_attn_exact_scores(AttnArgs a_in) {
     __shared__ int zmax[4][G];
     __shared__ int4 qs[G][EPL * 16];                 // qi = rne(q * 2^16), 4 dims per entry
     __shared__ int4 kn[PREP ? EPL * 16 : 1];         // PREP, last chunk: the new K row (ki)
-    const int r = lane >> 2, k4 = lane & 3;
+    static_assert(LPR == 4 || LPR == 8, "4 or 8 lanes per row");
+    constexpr int RPW = 64 / LPR, NLD = EPL * 16 / LPR;
+    const int r = lane / LPR, k4 = lane % LPR;
     const int n = ce - cs;
     const bool holds_pos = PREP && c == nch - 1;     // chunk ranges end at pos
     // The head preparation's inputs are requested first, then the wave's first
@@ -622,13 +628,13 @@ __global__ __launch_bounds__(256) void k_attn_exact_scores(AttnArgs a_in) {
     PrepIn<EPL> pin;
     if constexpr (PREP) prep_load<EPL, G>(a, h, pos, wave, lane, holds_pos, pin);
     __builtin_amdgcn_sched_barrier(0);
-    int4 kv[4 * EPL];
+    int4 kv[NLD];
     {
-        const int j = wave * 16 + r;
+        const int j = wave * RPW + r;
         if (j < n) {
-            const int32_t *row = quad_row<EPL, int32_t>(a, h, cs + wave * 16, ce - 1, cs + j, false) + 4 * k4;
+            const int32_t *row = quad_row<EPL, int32_t>(a, h, cs + wave * RPW, ce - 1, cs + j, false) + 4 * k4;
             #pragma unroll
-            for (int i = 0; i < 4 * EPL; i++) kv[i] = ld_stream((const int4 *)(row + 16 * i));
+            for (int i = 0; i < NLD; i++) kv[i] = ld_stream((const int4 *)(row + 4 * LPR * i));
         }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -644,32 +650,32 @@ __global__ __launch_bounds__(256) void k_attn_exact_scores(AttnArgs a_in) {
     }
     __syncthreads();
     int mx = INT32_MIN;                              // lane with k4 == g tracks head g
-    for (int j0 = wave * 16; j0 < n; j0 += 64) {
+    for (int j0 = wave * RPW; j0 < n; j0 += 4 * RPW) {
         const int j = j0 + r;
         int64_t acc[G];
         #pragma unroll
         for (int g = 0; g < G; g++) acc[g] = 0;
         if (j < n) {
-            if (j0 != wave * 16) {
+            if (j0 != wave * RPW) {
                 const int32_t *row = quad_row<EPL, int32_t>(a, h, cs + j0, ce - 1, cs + j, false) + 4 * k4;
                 #pragma unroll
-                for (int i = 0; i < 4 * EPL; i++) kv[i] = ld_stream((const int4 *)(row + 16 * i));
+                for (int i = 0; i < NLD; i++) kv[i] = ld_stream((const int4 *)(row + 4 * LPR * i));
             }
             if (holds_pos && cs + j == pos) {
                 #pragma unroll
-                for (int i = 0; i < 4 * EPL; i++) kv[i] = kn[4 * i + k4];
+                for (int i = 0; i < NLD; i++) kv[i] = kn[LPR * i + k4];
             }
             #pragma unroll
-            for (int i = 0; i < 4 * EPL; i++)
+            for (int i = 0; i < NLD; i++)
                 #pragma unroll
                 for (int g = 0; g < G; g++) {
-                    const int4 q = qs[g][4 * i + k4];
+                    const int4 q = qs[g][LPR * i + k4];
                     acc[g] += (int64_t)q.x * kv[i].x + (int64_t)q.y * kv[i].y + (int64_t)q.z * kv[i].z + (int64_t)q.w * kv[i].w;
                 }
         }
         #pragma unroll
         for (int g = 0; g < G; g++) {
-            acc[g] = quad_sum(acc[g]);
+            acc[g] = group_sum<LPR>(acc[g]);
         }
         if (j < n && k4 < G) {
             int64_t tot = acc[0];
@@ -867,8 +873,14 @@ template <int EPL, int G, bool B> static void attn_dispatch_b(const AttnArgs &a,
     if (a.mode == FLOAT && a.kvc == KVC_SPINOR) hipLaunchKernelGGL((k_attn_float<EPL, G, B, true>), grid, dim3(256), 0, s, a);
     else if (a.mode == FLOAT) hipLaunchKernelGGL((k_attn_float<EPL, G, B, false>), grid, dim3(256), 0, s, a);
     else {
-        if (!B && prep) hipLaunchKernelGGL((k_attn_exact_scores<EPL, G, B, !B>), grid, dim3(256), 0, s, a);
-        else hipLaunchKernelGGL((k_attn_exact_scores<EPL, G, B, false>), grid, dim3(256), 0, s, a);
+        const bool wide = a.chunk > 64;
+        if (!B && prep) {
+            if (wide) hipLaunchKernelGGL((k_attn_exact_scores<EPL, G, B, !B, 8>), grid, dim3(256), 0, s, a);
+            else hipLaunchKernelGGL((k_attn_exact_scores<EPL, G, B, !B, 4>), grid, dim3(256), 0, s, a);
+        } else {
+            if (wide) hipLaunchKernelGGL((k_attn_exact_scores<EPL, G, B, false, 8>), grid, dim3(256), 0, s, a);
+            else hipLaunchKernelGGL((k_attn_exact_scores<EPL, G, B, false, 4>), grid, dim3(256), 0, s, a);
+        }
         hipLaunchKernelGGL((k_attn_exact_vsum<EPL, G, B, 2 * UNR>), grid, dim3(256), 0, s, a);
     }
 }
@@ -899,7 +911,7 @@ void launch_attention(const AttnArgs &a, int grid_chunks, hipStream_t s) {
 // global-layer chunks so that a launch is one round of them where it can.
 template <int EPL, int G> static int attn_cap_t() {
     int a = 0, b = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&a, k_attn_exact_scores<EPL, G, false, true>, 256, 0) != hipSuccess ||
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&a, k_attn_exact_scores<EPL, G, false, true, 8>, 256, 0) != hipSuccess ||
         hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, k_attn_exact_vsum<EPL, G, false, 2 * UNR>, 256, 0) != hipSuccess)
         return 0;
     return a < b ? a : b;

@@ -202,6 +202,20 @@ __device__ __forceinline__ void reset_counter(int *counter) {
     __hip_atomic_exchange(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Loads through a pointer read from memory (a page table entry): the compiler
+// cannot tell its address space and would issue flat loads, which count with
+// the LDS operations too, so that every wait for an LDS read in the same loop
+// would also wait for the rows still streaming in.  KV pages are device
+// memory, so the global-space view keeps the address.
+// (The host pass of these device functions has no such address space.)
+#if defined(__HIP_DEVICE_COMPILE__)
+#define KVD_GLOBAL __attribute__((address_space(1)))
+#else
+#define KVD_GLOBAL
+#endif
+template <typename T> __device__ __forceinline__ const KVD_GLOBAL T *gmem(const T *p) { return (const KVD_GLOBAL T *)p; }
+template <typename T> __device__ __forceinline__ KVD_GLOBAL T *gmem(T *p) { return (KVD_GLOBAL T *)p; }
+
 // A launcher whose arguments fall outside its kernel's limits launches nothing
 // and records the first such error of the calling thread; the step drivers
 // collect it after enqueueing (launch_take_error: the message, then clears it;

@@ -38,7 +38,7 @@ constexpr int PV_CH = 2048;          // positions per V-sum workgroup
 constexpr int PV_SUB = 512;          // ... in sub-chunks of 128 rows per wave (FP64 sums below 2^53)
 constexpr int DIG_MAX = 127 * (1 + 256 + 65536 + 16777216);   // largest |x| of four balanced digits
 
-__device__ __forceinline__ const float *pg(const AttnArgs &a, int pos) { return a.pages[pos / PAGE]; }
+__device__ __forceinline__ const float *pg(const AttnArgs &a, int pos) { return gmem(a.pages)[pos / PAGE]; }
 
 // x = d0 + 2^8 d1 + 2^16 d2 + 2^24 d3, d in [-128, 127] (|x| <= DIG_MAX)
 __device__ __forceinline__ void digits4(int32_t x, int32_t d[4]) {
@@ -95,7 +95,7 @@ __global__ __launch_bounds__(256) void k_pattn_scores(AttnArgs a) {
             const int32_t *row = (const int32_t *)pg(a, p) + ((size_t)h * PAGE + (p & (PAGE - 1))) * HD + d0;
             #pragma unroll
             for (int q = 0; q < 4; q++) {
-                const int4 v = *(const int4 *)(row + 4 * q);
+                const int4 v = *gmem((const int4 *)(row + 4 * q));
                 x[4 * q] = v.x; x[4 * q + 1] = v.y; x[4 * q + 2] = v.z; x[4 * q + 3] = v.w;
             }
         } else {
@@ -175,7 +175,7 @@ __global__ __launch_bounds__(256) void k_pattn_scores(AttnArgs a) {
                 const float *q2 = a.qr + (size_t)tt * QD + (size_t)(h * G + mm % G) * HD;
                 const int32_t *krow = (const int32_t *)pg(a, p) + ((size_t)h * PAGE + (p & (PAGE - 1))) * HD;
                 int64_t s = 0;
-                for (int d = 0; d < HD; d++) s += (int64_t)(int32_t)rintf(q2[d] * 65536.0f) * krow[d];
+                for (int d = 0; d < HD; d++) s += (int64_t)(int32_t)rintf(q2[d] * 65536.0f) * gmem(krow)[d];
                 ip[i] = s;
             }
         }
@@ -278,7 +278,7 @@ __global__ __launch_bounds__(256) void k_pattn_vsum(AttnArgs a) {
                     const int32_t *row = (const int32_t *)pg(a, p) + (size_t)a.NKV * PAGE * HD +
                                          ((size_t)h * PAGE + (p & (PAGE - 1))) * HD + lane * EPL;
                     #pragma unroll
-                    for (int e = 0; e < EPL; e++) v[u][e] = row[e];
+                    for (int e = 0; e < EPL; e++) v[u][e] = gmem(row)[e];
                 } else {
                     #pragma unroll
                     for (int e = 0; e < EPL; e++) v[u][e] = 0;

@@ -36,7 +36,7 @@ __device__ __forceinline__ HeadPrep head_prep_of(const AttnArgs &a) {
 
 __device__ __forceinline__ float *qk_page_of(float *const *pages, int ring, int pos) {
     const int lp = pos / PAGE;
-    return pages[ring ? lp % ring : lp];
+    return gmem(pages)[ring ? lp % ring : lp];
 }
 
 // The global inputs of one head's preparation, loaded by head_load so that a

@@ -30,7 +30,7 @@ int recall_page_floats(int NKV, int r) { return NKV * PAGE * r; }
 
 namespace {
 
-__device__ __forceinline__ const float *rc_page(const RecallArgs &rc, int pos) { return rc.pages[pos / PAGE]; }
+__device__ __forceinline__ const float *rc_page(const RecallArgs &rc, int pos) { return gmem(rc.pages)[pos / PAGE]; }
 // row of position s of kv head kvh: K (vpart = 0) or V (vpart = 1)
 __device__ __forceinline__ const int32_t *rc_row(const RecallArgs &rc, int kvh, int s, int vpart) {
     return (const int32_t *)rc_page(rc, s) + (size_t)vpart * rc.NKV * PAGE * rc.HD +
@@ -82,7 +82,7 @@ __global__ __launch_bounds__(256) void k_recall_score(RecallArgs rc) {
         if constexpr (RT) {
             #pragma unroll
             for (int q = 0; q < RT / 4; q++) {
-                const float4 v = *(const float4 *)(side + 4 * q);
+                const float4 v = *gmem((const float4 *)(side + 4 * q));
                 row[4 * q] = v.x; row[4 * q + 1] = v.y; row[4 * q + 2] = v.z; row[4 * q + 3] = v.w;
             }
         }
@@ -92,7 +92,7 @@ __global__ __launch_bounds__(256) void k_recall_score(RecallArgs rc) {
                 #pragma unroll
                 for (int p = 0; p < RT; p++) a = __fadd_rn(a, __fmul_rn(pq[gh * RT + p], row[p]));
             } else {
-                for (int p = 0; p < r; p++) a = __fadd_rn(a, __fmul_rn(pq[gh * r + p], side[p]));
+                for (int p = 0; p < r; p++) a = __fadd_rn(a, __fmul_rn(pq[gh * r + p], gmem(side)[p]));
             }
             rc.keys[(size_t)(kvh * G + gh) * rc.kstride + s] = order_key(a);
         }
@@ -382,7 +382,7 @@ __global__ __launch_bounds__(256) void k_recall_scores(RecallArgs rc) {
         const int32_t *row = rc_row(rc, kvh, s, 0) + 4 * k4;
         #pragma unroll
         for (int i = 0; i < 4 * EPL; i++) {
-            const int4 kv = *(const int4 *)(row + 16 * i);
+            const int4 kv = *gmem((const int4 *)(row + 16 * i));
             if constexpr (EXACT_MODE) {
                 const int4 q = qi[4 * i + k4];
                 ai += (int64_t)q.x * kv.x + (int64_t)q.y * kv.y + (int64_t)q.z * kv.z + (int64_t)q.w * kv.w;
@@ -431,9 +431,9 @@ __global__ __launch_bounds__(256) void k_recall_scores(RecallArgs rc) {
 template <int EPL>
 __device__ __forceinline__ void rc_vrow(const RecallArgs &rc, int kvh, int s, int lane, int32_t out[EPL]) {
     const int32_t *src = rc_row(rc, kvh, s, 1) + lane * EPL;
-    if constexpr (EPL == 4) { const int4 t = *(const int4 *)src; out[0] = t.x; out[1] = t.y; out[2] = t.z; out[3] = t.w; }
-    else if constexpr (EPL == 2) { const int2 t = *(const int2 *)src; out[0] = t.x; out[1] = t.y; }
-    else out[0] = src[0];
+    if constexpr (EPL == 4) { const int4 t = *gmem((const int4 *)src); out[0] = t.x; out[1] = t.y; out[2] = t.z; out[3] = t.w; }
+    else if constexpr (EPL == 2) { const int2 t = *gmem((const int2 *)src); out[0] = t.x; out[1] = t.y; }
+    else out[0] = *gmem(src);
 }
 
 // ---- attention pass 2 (exact): island weights, exact V-sum (FP64 FMAs on

@@ -86,6 +86,13 @@ template <typename T> __device__ __forceinline__ T quad_sum(T v) {
     v = v + sw(v, std::integral_constant<int, 0xB1>{});      // quad_perm 1,0,3,2
     return v + sw(v, std::integral_constant<int, 0x4E>{});   // quad_perm 2,3,0,1
 }
+// Sum over aligned groups of N = 4 or 8 lanes (all lanes of a group get it).
+template <int N, typename T> __device__ __forceinline__ T group_sum(T v) {
+    static_assert(N == 4 || N == 8, "groups of 4 or 8 lanes");
+    v = quad_sum(v);
+    if constexpr (N == 8) v += __shfl_xor(v, 4, 64);
+    return v;
+}
 
 // Block-wide reductions through one LDS slot array per reduction: lane 63 of
 // each wave posts its wave total, one barrier, every thread combines the
