@@ -443,6 +443,7 @@ struct sp_kvdecode_handle {
         float *x0, *x1, *q, *k, *v, *qr, *ao, *ap, *gg, *uu, *hh, *dn, *rope, *part, *part_ml;
         int8_t *planes; int *sh, *counter, *zs;
         int64_t *vacc, *vacc_s;
+        int64_t *gpart; int *gcnt;           // GEMM split-K partial slices and tile arrival counters
         // batched decode over sessions (allocated on first use): logits rows,
         // greedy tokens, per-token token / position / per-layer page tables
         void *dbuf = nullptr;
@@ -881,6 +882,8 @@ void enqueue_body(sp_kvdecode_handle *h, const StepShape &sh, TimeCb cb, void *c
 // attention kernels with a token grid dimension.  Each token's K/V and every
 // intermediate are the same integers/floats a decode step computes.
 constexpr int PREFILL_TB = 128;
+constexpr size_t GEMM_PART_BYTES = (size_t)64 << 20;    // split-K partials of the batched GEMMs
+constexpr int GEMM_TILE_COUNTERS = 8192;
 
 bool batch_supported(const sp_kvdecode_handle *h) {
     const DevModel *m = h->m;
@@ -914,6 +917,7 @@ int alloc_batch(sp_kvdecode_handle *h) {
         {(void **)&b.part_ml, TB * m->NH * (size_t)b.mcb * 16},
         {(void **)&b.part, h->mode == FLOAT ? TB * m->NH * (size_t)b.mcb * m->HD * 4 : 256},
         {(void **)&b.vacc, TB * QD * 8 * VREP}, {(void **)&b.vacc_s, TB * m->NH * 8 * VREP},
+        {(void **)&b.gpart, GEMM_PART_BYTES}, {(void **)&b.gcnt, GEMM_TILE_COUNTERS * 4},
     };
     size_t tot = 0;
     for (auto &it : items) tot = align_up(tot + it.n, 256);
@@ -952,6 +956,7 @@ int run_batch(sp_kvdecode_handle *h, int T, int pos0, int pos_hi, bool multi, Ti
     auto gemm = [&](int cols) {
         GemmArgs g{};
         g.cols = cols; g.planes = b.planes; g.sh = b.sh; g.T = T; g.TP = TP; g.mode = h->mode; g.act = ACT_NONE;
+        g.part = b.gpart; g.part_cap = GEMM_PART_BYTES / 8; g.cnt = b.gcnt; g.cnt_cap = GEMM_TILE_COUNTERS;
         return g;
     };
     for (int l = 0; l < m->NL; l++) {

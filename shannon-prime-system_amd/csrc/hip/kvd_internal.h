@@ -176,6 +176,15 @@ struct GemmArgs {
     int  act;
     float *act_out;
     int  mode;
+    // split K (the launcher picks the split count): each split's exact int64
+    // partials [TP][arows] (arows: the launch's rows, paired: gate rows then up
+    // rows) in its own slice of part, one arrival counter per output tile in
+    // cnt (zero between launches).  NULL: no split.
+    int64_t *part;
+    int *cnt;
+    size_t part_cap;   // int64 elements of part
+    int cnt_cap;       // counters in cnt
+    int arows;
 };
 
 // Hand-off between workgroups of one launch without cache-wide fences: all data

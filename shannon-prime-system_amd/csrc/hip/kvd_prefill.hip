@@ -117,6 +117,7 @@ __device__ __forceinline__ void transpose4(uint4 &v) {
 
 constexpr int GEMM_KC = 8;                // 32-column blocks per pipeline chunk
 constexpr int GEMM_AG = GEMM_KC / 4;      // 16-byte code loads per lane and chunk
+constexpr int GEMM_SPLIT_TARGET = 2048;   // workgroups a split-K launch aims for
 
 // A wave's own operands of one chunk: the codes of its 16 rows (a lane loads
 // 16 bytes = 4 blocks of its row; transpose4 turns that into one dword per
@@ -154,7 +155,10 @@ __global__ __launch_bounds__(256) void k_gemm_q4b(GemmArgs a) {
     const DevW &wa = a.seg[s].w;
     const DevW &wb = a.seg[PAIRED ? 1 : s].w;
     const int nblk = wa.nblk, TP = a.TP, rb = wa.cols / 2;
-    const int nck = nblk / KC;
+    // split K: this workgroup's chunks [ckb, ckb + nck) of the nblk / KC
+    const int kper = (nblk / KC + (int)gridDim.z - 1) / (int)gridDim.z;
+    const int ckb = (int)blockIdx.z * kper;
+    const int nck = nblk / KC - ckb < kper ? nblk / KC - ckb : kper;
     const int rbase = tile_row + wave * 16, t0 = blockIdx.y * 16 * TT, row = rbase + c16;
     const __amdgpu_buffer_rsrc_t rca = buf_rsrc(wa.codes + (size_t)rbase * rb, 16u * rb);
     const __amdgpu_buffer_rsrc_t rcb = buf_rsrc(wb.codes + (size_t)rbase * rb, 16u * rb);
@@ -174,7 +178,7 @@ __global__ __launch_bounds__(256) void k_gemm_q4b(GemmArgs a) {
         goff[r] = p * pstride + (kb * TP + 16 * j) * 32 + (q % 32) * 16;
     }
     auto stage_load = [&](uint4 (&st)[PPT], int ck) {
-        const int so = __builtin_amdgcn_readfirstlane(ck * KC * TP * 32);
+        const int so = __builtin_amdgcn_readfirstlane((ckb + ck) * KC * TP * 32);
         #pragma unroll
         for (int r = 0; r < PPT; r++) st[r] = buf_ld128(rpl, goff[r], so);
     };
@@ -183,7 +187,7 @@ __global__ __launch_bounds__(256) void k_gemm_q4b(GemmArgs a) {
         for (int r = 0; r < PPT; r++) Bs[buf][tid + 256 * r] = st[r];
     };
     auto wave_load = [&](WaveChunk<PAIRED> &w, int ck) {
-        const int b0 = __builtin_amdgcn_readfirstlane(ck * KC);
+        const int b0 = __builtin_amdgcn_readfirstlane((ckb + ck) * KC);
         #pragma unroll
         for (int q = 0; q < AG; q++) {
             w.A[q] = buf_ld128(rca, lo_c, (b0 + 4 * q) * 16);
@@ -272,6 +276,42 @@ __global__ __launch_bounds__(256) void k_gemm_q4b(GemmArgs a) {
         stage_store(st0, 0);
         __syncthreads();
     }
+    if (gridDim.z > 1) {
+        // split K: every split stores its exact partials in its own slice
+        // (agent-scope stores, coherent across the XCDs' L2s); the last split
+        // of the tile to arrive adds the others' to its own
+        const int grow = (int)blockIdx.x * 64 + wave * 16 + c16;   // the row among the launch's rows
+        const size_t zs = (size_t)TP * a.arows;
+        int64_t *mine = a.part + blockIdx.z * zs;
+        #pragma unroll
+        for (int j = 0; j < TT; j++)
+            #pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int t = t0 + 16 * j + 4 * g + i;
+                st_agent(&mine[(size_t)t * a.arows + grow], acc_a[j][i]);
+                if constexpr (PAIRED) st_agent(&mine[(size_t)t * a.arows + a.arows / 2 + grow], acc_b[j][i]);
+            }
+        mem_complete();
+        __shared__ int last;
+        __syncthreads();
+        int *cnt = a.cnt + blockIdx.y * gridDim.x + blockIdx.x;
+        if (threadIdx.x == 0) last = arrive(cnt) == (int)gridDim.z - 1;
+        __syncthreads();
+        if (!last) return;
+        for (int z = 0; z < (int)gridDim.z; z++) {
+            if (z == (int)blockIdx.z) continue;
+            const int64_t *other = a.part + z * zs;
+            #pragma unroll
+            for (int j = 0; j < TT; j++)
+                #pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int t = t0 + 16 * j + 4 * g + i;
+                    acc_a[j][i] += ld_agent(&other[(size_t)t * a.arows + grow]);
+                    if constexpr (PAIRED) acc_b[j][i] += ld_agent(&other[(size_t)t * a.arows + a.arows / 2 + grow]);
+                }
+        }
+        if (threadIdx.x == 0) reset_counter(cnt);
+    }
     // outputs: lane holds row `row` for tokens t0 + 16j + 4g + i
     #pragma unroll
     for (int j = 0; j < TT; j++)
@@ -320,14 +360,31 @@ void launch_gemm(const GemmArgs &a, int nrows_total, hipStream_t s) {
     // 32-token tiles per wave (codes unpacked and scales decoded once for two
     // tiles) when that still gives >= 512 workgroups, else 16-token tiles
     // (LDS: 24 KiB per workgroup with 16-token tiles, 48 KiB with 32)
-    if ((nrows_total / 64) * (a.TP / 32) < 512) {
-        const dim3 grid(nrows_total / 64, a.TP / 16);
-        if (paired) hipLaunchKernelGGL((k_gemm_q4b<true, 1>), grid, dim3(256), 0, s, a);
-        else        hipLaunchKernelGGL((k_gemm_q4b<false, 1>), grid, dim3(256), 0, s, a);
+    const bool tt2 = (nrows_total / 64) * (a.TP / 32) >= 512;
+    dim3 grid(nrows_total / 64, a.TP / (tt2 ? 32 : 16), 1);
+    // split K where the tiles alone leave the device under two workgroups per
+    // CU (about eight wanted), with at least two chunks per split and the
+    // splits' partial slices inside the buffer
+    GemmArgs g = a;
+    g.arows = nrows_total * (paired ? 2 : 1);
+    const int nck = a.cols / 32 / GEMM_KC, tiles = (int)(grid.x * grid.y);
+    int ks = 1;
+    if (a.part && a.cnt && tiles <= a.cnt_cap && tiles < GEMM_SPLIT_TARGET / 4) {
+        ks = (GEMM_SPLIT_TARGET + tiles - 1) / tiles;
+        if (ks > nck / 2) ks = nck / 2;
+        const size_t slice = (size_t)a.TP * g.arows;
+        if (ks > 1 && (size_t)ks * slice > a.part_cap) ks = (int)(a.part_cap / slice);
+        if (ks < 1) ks = 1;
+        const int kper = (nck + ks - 1) / ks;
+        ks = (nck + kper - 1) / kper;                  // every split holds chunks
+    }
+    grid.z = ks;
+    if (paired) {
+        if (tt2) hipLaunchKernelGGL((k_gemm_q4b<true, 2>), grid, dim3(256), 0, s, g);
+        else     hipLaunchKernelGGL((k_gemm_q4b<true, 1>), grid, dim3(256), 0, s, g);
     } else {
-        const dim3 grid(nrows_total / 64, a.TP / 32);
-        if (paired) hipLaunchKernelGGL((k_gemm_q4b<true, 2>), grid, dim3(256), 0, s, a);
-        else        hipLaunchKernelGGL((k_gemm_q4b<false, 2>), grid, dim3(256), 0, s, a);
+        if (tt2) hipLaunchKernelGGL((k_gemm_q4b<false, 2>), grid, dim3(256), 0, s, g);
+        else     hipLaunchKernelGGL((k_gemm_q4b<false, 1>), grid, dim3(256), 0, s, g);
     }
 }
 
