@@ -22,6 +22,12 @@
 // each V row is read once for all of the group's token-heads (FP64 FMAs on
 // integers below 2^53, as in decode), partial sums go to the tokens' int64
 // totals by order-free atomics, and the group's last workgroup divides.
+//
+// Sliding-window layers (win >= 0): token t attends [s0(t), pos(t)], s0(t) =
+// max(0, pos(t) - win + 1), as in decode; chunks are absolute position ranges
+// from the batch's lowest window start, each pass masks a token's positions
+// below s0(t), and a workgroup whose chunk lies below its token group's
+// earliest window start does nothing.
 #include "kvd_internal.h"
 #include "kvd_exact.h"
 #include "kvd_vec.h"
@@ -34,11 +40,19 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int PS_CH = 64;            // positions per score workgroup (and per chunk maximum)
-constexpr int PV_CH = 2048;          // positions per V-sum workgroup
+constexpr int PV_CH = 2048;          // positions per V-sum workgroup (full-context layers)
 constexpr int PV_SUB = 512;          // ... in sub-chunks of 128 rows per wave (FP64 sums below 2^53)
 constexpr int DIG_MAX = 127 * (1 + 256 + 65536 + 16777216);   // largest |x| of four balanced digits
 
-__device__ __forceinline__ const float *pg(const AttnArgs &a, int pos) { return gmem(a.pages)[pos / PAGE]; }
+__device__ __forceinline__ const float *pg(const AttnArgs &a, int pos) {
+    const int lp = pos / PAGE;
+    return gmem(a.pages)[a.ring_pages ? lp % a.ring_pages : lp];
+}
+// the first position token t of the batch attends
+__host__ __device__ __forceinline__ int win_start(const AttnArgs &a, int t) {
+    const int q = a.pos0 + t - a.win + 1;
+    return a.win >= 0 && q > 0 ? q : 0;
+}
 
 // x = d0 + 2^8 d1 + 2^16 d2 + 2^24 d3, d in [-128, 127] (|x| <= DIG_MAX)
 __device__ __forceinline__ void digits4(int32_t x, int32_t d[4]) {
@@ -58,13 +72,13 @@ __device__ __forceinline__ void digits4(int32_t x, int32_t d[4]) {
 template <int EPL, int G>
 __global__ __launch_bounds__(256) void k_pattn_scores(AttnArgs a) {
     constexpr int HD = EPL * 64, KS = HD / 32, TPW = 16 / G, TWG = 4 * TPW, KROW = HD + 16;
-    const int tg = blockIdx.x, c = blockIdx.y, h = blockIdx.z;
+    const int tg = blockIdx.x, c = win_start(a, 0) / PS_CH + (int)blockIdx.y, h = blockIdx.z;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int t0 = tg * TWG;
     const int tend = t0 + TWG < a.nt ? t0 + TWG : a.nt;
     const int pos_hi = a.pos0 + tend - 1;               // the group's last token attends up to here
     const int cs = c * PS_CH;
-    if (t0 >= a.nt || cs > pos_hi) return;
+    if (t0 >= a.nt || cs > pos_hi || cs + PS_CH <= win_start(a, t0)) return;
     const int np = pos_hi - cs + 1 < PS_CH ? pos_hi - cs + 1 : PS_CH;
     __shared__ __align__(16) int8_t kd[4][PS_CH][KROW];   // K digits [digit][position][dim]
     __shared__ int s_wide;
@@ -183,7 +197,7 @@ __global__ __launch_bounds__(256) void k_pattn_scores(AttnArgs a) {
         for (int i = 0; i < 4; i++) {
             const int mm = rowq + i;
             const int tt = t0 + wave * TPW + mm / G;
-            if (tt < a.nt && p <= a.pos0 + tt) {
+            if (tt < a.nt && p <= a.pos0 + tt && p >= win_start(a, tt)) {
                 const float scv = (float)((double)ip[i] / 4294967296.0) * a.ascale;
                 const int32_t z = (int32_t)llround_pow2<14>(scv);
                 a.zscratch[(size_t)tt * a.NH * a.zstride + (size_t)(h * G + mm % G) * a.zstride + p] = z;
@@ -204,7 +218,7 @@ __global__ __launch_bounds__(256) void k_pattn_scores(AttnArgs a) {
         for (int i = 0; i < 4; i++) {
             const int mm = rowq + i;
             const int tt = t0 + wave * TPW + mm / G;
-            if (tt < a.nt && cs <= a.pos0 + tt)
+            if (tt < a.nt && cs <= a.pos0 + tt && cs + PS_CH > win_start(a, tt))
                 ((int32_t *)a.part_ml)[(size_t)tt * a.NH * a.max_chunks * 4 + ((size_t)(h * G + mm % G) * a.max_chunks + c) * 4] = mx[i];
         }
     }
@@ -215,35 +229,41 @@ __global__ __launch_bounds__(256) void k_pattn_scores(AttnArgs a) {
 // TT G token-heads share each V row.  Token t's totals are its decode-layout
 // accumulators (vacc + t QD VREP, vacc_s + t NH VREP, replica 0) and its
 // group's arrivals count on counter[t0 NKV + h].
-template <int EPL, int G, int TT>
-__global__ __launch_bounds__(256) void k_pattn_vsum(AttnArgs a) {
-    constexpr int HD = EPL * 64, NQ = TT * G, UV = 4;
-    const int tg = blockIdx.x, c = blockIdx.y, h = blockIdx.z;
+// WIN (sliding-window layers): one 8-wave workgroup per (token group, kv
+// head) takes the group's whole span (at most win + TT - 1 rows), adds the
+// waves' partials in LDS and divides: no cross-workgroup exchange.
+template <int EPL, int G, int TT, bool WIN>
+__global__ __launch_bounds__(WIN ? 512 : 256) void k_pattn_vsum(AttnArgs a) {
+    constexpr int HD = EPL * 64, NQ = TT * G, UV = WIN ? 8 : 4, NW = WIN ? 8 : 4, NT = 64 * NW;
+    const int VC = PV_CH;
+    const int tg = blockIdx.x, c = win_start(a, 0) / VC + (int)blockIdx.y, h = blockIdx.z;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int t0 = tg * TT;
     const int tend = t0 + TT < a.nt ? t0 + TT : a.nt;
     const int pos_hi = a.pos0 + tend - 1;
-    const int nch = pos_hi / PV_CH + 1;                 // chunks of this group (the arrival count)
-    const int cs = c * PV_CH;
-    if (t0 >= a.nt || c >= nch) return;
-    const int np = pos_hi - cs + 1 < PV_CH ? pos_hi - cs + 1 : PV_CH;
+    const int s0g = win_start(a, t0);                   // the group's lowest window start
+    const int nch = WIN ? 1 : pos_hi / VC - s0g / VC + 1;   // chunks of this group (the arrival count)
+    if (t0 >= a.nt || (!WIN && (c < s0g / VC || c > pos_hi / VC))) return;
+    // this workgroup's rows: [cs, cs + np) within the chunk and the group's span
+    const int cs = WIN ? s0g : (c * VC > s0g ? c * VC : s0g);
+    const int np = WIN ? pos_hi - s0g + 1 : (pos_hi < c * VC + VC - 1 ? pos_hi : c * VC + VC - 1) - cs + 1;
     const size_t QD = (size_t)a.NH * HD;
     __shared__ int32_t ew[NQ][PV_SUB];                   // island weights (Q22) of a sub-chunk, 0 where masked
     __shared__ int s_M[NQ];
     __shared__ int64_t ored[NQ][HD];                      // the waves' partials, added in LDS (order-free)
     __shared__ int64_t sred[NQ];
     __shared__ int is_last;
-    for (int i = threadIdx.x; i < NQ * HD; i += 256) ored[i / HD][i % HD] = 0;
+    for (int i = threadIdx.x; i < NQ * HD; i += NT) ored[i / HD][i % HD] = 0;
     if (threadIdx.x < NQ) sred[threadIdx.x] = 0;
     // each token-head's maximum over its 64-position chunk maxima (wave w: token-heads w, w+4, ..)
-    for (int q = wave; q < NQ; q += 4) {
+    for (int q = wave; q < NQ; q += NW) {
         const int tt = t0 + q / G;
         int t = INT32_MIN;
         if (tt < a.nt) {
             const int n64 = (a.pos0 + tt) / PS_CH + 1;
             const int32_t *pml = (const int32_t *)a.part_ml + (size_t)tt * a.NH * a.max_chunks * 4 +
                                  (size_t)(h * G + q % G) * a.max_chunks * 4;
-            for (int k = lane; k < n64; k += 64) { const int v = pml[(size_t)k * 4]; t = v > t ? v : t; }
+            for (int k = win_start(a, tt) / PS_CH + lane; k < n64; k += 64) { const int v = pml[(size_t)k * 4]; t = v > t ? v : t; }
         }
         t = wave_allmax_i(t);
         if (lane == 0) s_M[q] = t;
@@ -251,10 +271,10 @@ __global__ __launch_bounds__(256) void k_pattn_vsum(AttnArgs a) {
     __syncthreads();
     for (int sb = 0; sb < np; sb += PV_SUB) {
         const int ns = np - sb < PV_SUB ? np - sb : PV_SUB;
-        for (int i = threadIdx.x; i < NQ * PV_SUB; i += 256) {
+        for (int i = threadIdx.x; i < NQ * PV_SUB; i += NT) {
             const int q = i / PV_SUB, jj = i % PV_SUB, tt = t0 + q / G, p = cs + sb + jj;
             int32_t w = 0;
-            if (jj < ns && tt < a.nt && p <= a.pos0 + tt) {
+            if (jj < ns && tt < a.nt && p <= a.pos0 + tt && p >= win_start(a, tt)) {
                 const int32_t z = a.zscratch[(size_t)tt * a.NH * a.zstride + (size_t)(h * G + q % G) * a.zstride + p];
                 w = (int32_t)(exp_fixed((((int64_t)z - (int64_t)s_M[q]) * ONE) >> 14) >> 8);
             }
@@ -268,8 +288,10 @@ __global__ __launch_bounds__(256) void k_pattn_vsum(AttnArgs a) {
         for (int q = 0; q < NQ; q++)
             #pragma unroll
             for (int e = 0; e < EPL; e++) o[q][e] = 0.0;
-        for (int j0 = wave * UV; j0 < ns; j0 += 4 * UV) {
-            int32_t v[UV][EPL];
+        // UV rows per wave and step (rows past ns read as zeros); WIN requests
+        // the next step's rows before this step's FMAs (the full-context
+        // instances keep their registers for occupancy instead)
+        auto load_v = [&](int j0, int32_t (&v)[UV][EPL]) {
             #pragma unroll
             for (int u = 0; u < UV; u++) {
                 const int jj = j0 + u;
@@ -284,6 +306,12 @@ __global__ __launch_bounds__(256) void k_pattn_vsum(AttnArgs a) {
                     for (int e = 0; e < EPL; e++) v[u][e] = 0;
                 }
             }
+        };
+        int32_t v[UV][EPL], vn[UV][EPL];
+        if constexpr (WIN) load_v(wave * UV, v);
+        for (int j0 = wave * UV; j0 < ns; j0 += NW * UV) {
+            if constexpr (WIN) load_v(j0 + NW * UV, vn);
+            else load_v(j0, v);
             #pragma unroll
             for (int u = 0; u < UV; u++) {
                 const int jj = j0 + u < PV_SUB ? j0 + u : 0;
@@ -294,13 +322,18 @@ __global__ __launch_bounds__(256) void k_pattn_vsum(AttnArgs a) {
                     for (int e = 0; e < EPL; e++) o[q][e] = fma(w, (double)v[u][e], o[q][e]);
                 }
             }
+            if constexpr (WIN)
+                #pragma unroll
+                for (int u = 0; u < UV; u++)
+                    #pragma unroll
+                    for (int e = 0; e < EPL; e++) v[u][e] = vn[u][e];
         }
         #pragma unroll
         for (int q = 0; q < NQ; q++)
             #pragma unroll
             for (int e = 0; e < EPL; e++) atomicAdd((unsigned long long *)&ored[q][lane * EPL + e], (unsigned long long)(int64_t)o[q][e]);
         // denominators of the sub-chunk
-        for (int q = wave; q < NQ; q += 4) {
+        for (int q = wave; q < NQ; q += NW) {
             int64_t sum = 0;
             for (int jj = lane; jj < PV_SUB; jj += 64) sum += ew[q][jj];
             sum = wave_allsum(sum);
@@ -308,7 +341,15 @@ __global__ __launch_bounds__(256) void k_pattn_vsum(AttnArgs a) {
         }
         __syncthreads();                                 // ew is consumed
     }
-    for (int i = threadIdx.x; i < NQ * HD; i += 256) {
+    if constexpr (WIN) {
+        // the whole span was this workgroup's: divide the totals
+        for (int i = threadIdx.x; i < NQ * HD; i += NT) {
+            const int q = i / HD, d = i % HD, tt = t0 + q / G;
+            if (tt < a.nt) a.ao[(size_t)tt * QD + (size_t)(h * G + q % G) * HD + d] = rne_div_to_float((i128)ored[q][d], sred[q], 16);
+        }
+        return;
+    }
+    for (int i = threadIdx.x; i < NQ * HD; i += NT) {
         const int q = i / HD, d = i % HD, tt = t0 + q / G;
         if (tt >= a.nt) continue;
         const int64_t t = ored[q][d];
@@ -333,7 +374,7 @@ __global__ __launch_bounds__(256) void k_pattn_vsum(AttnArgs a) {
                                                            0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 1;
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < NQ * HD; i += 256) {
+    for (int i = threadIdx.x; i < NQ * HD; i += NT) {
         const int q = i / HD, d = i % HD, tt = t0 + q / G;
         if (tt >= a.nt) continue;
         const int64_t tot = (int64_t)__hip_atomic_exchange(
@@ -347,18 +388,22 @@ __global__ __launch_bounds__(256) void k_pattn_vsum(AttnArgs a) {
 template <int EPL, int G>
 void pattn_go(const AttnArgs &a, hipStream_t s) {
     constexpr int TPW = 16 / G, TWG = 4 * TPW, TT = 8 / G;
-    const int pos_hi = a.pos0 + a.nt - 1;
-    const dim3 g1((a.nt + TWG - 1) / TWG, pos_hi / PS_CH + 1, a.NKV);
+    const int pos_hi = a.pos0 + a.nt - 1, lo = win_start(a, 0);
+    const dim3 g1((a.nt + TWG - 1) / TWG, pos_hi / PS_CH - lo / PS_CH + 1, a.NKV);
     hipLaunchKernelGGL((k_pattn_scores<EPL, G>), g1, dim3(256), 0, s, a);
-    const dim3 g2((a.nt + TT - 1) / TT, pos_hi / PV_CH + 1, a.NKV);
-    hipLaunchKernelGGL((k_pattn_vsum<EPL, G, TT>), g2, dim3(256), 0, s, a);
+    if (a.win >= 0) {
+        hipLaunchKernelGGL((k_pattn_vsum<EPL, G, TT, true>), dim3((a.nt + TT - 1) / TT, 1, a.NKV), dim3(512), 0, s, a);
+    } else {
+        const dim3 g2((a.nt + TT - 1) / TT, pos_hi / PV_CH - lo / PV_CH + 1, a.NKV);
+        hipLaunchKernelGGL((k_pattn_vsum<EPL, G, TT, false>), g2, dim3(256), 0, s, a);
+    }
 }
 
 }  // namespace
 
 bool prefill_attention_tiled(const AttnArgs &a) {
     const int G = a.NH / a.NKV;
-    return a.mode == EXACT && a.nt > 0 && !a.tpages && !a.tpos && a.win < 0 && a.ring_pages == 0 &&
+    return a.mode == EXACT && a.nt > 0 && !a.tpages && !a.tpos &&
            a.kvc == KVC_PLAIN && (a.HD == 64 || a.HD == 128 || a.HD == 256) && (G == 2 || G == 4);
 }
 
