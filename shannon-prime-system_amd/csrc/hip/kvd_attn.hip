@@ -270,6 +270,44 @@ __device__ __forceinline__ void load_rows(const AttnArgs &a, int h, int cs, int 
     }
 }
 
+// EPL consecutive int32 of a row for this lane (16, 8 or 4 bytes), streamed
+template <int EPL> __device__ __forceinline__ void ld_lane_row(const int32_t *src, int32_t out[EPL]) {
+    if constexpr (EPL == 4) {
+        typedef int32_t v4 __attribute__((ext_vector_type(4)));
+        const v4 t = ld_stream((const v4 *)src); out[0] = t.x; out[1] = t.y; out[2] = t.z; out[3] = t.w;
+    } else if constexpr (EPL == 2) {
+        typedef int32_t v2 __attribute__((ext_vector_type(2)));
+        const v2 t = ld_stream((const v2 *)src); out[0] = t.x; out[1] = t.y;
+    } else {
+        out[0] = __builtin_nontemporal_load(gmem(src));
+    }
+}
+
+// Rows j0 .. j0+R-1 of the chunk starting at cs (n rows) for the exact passes.
+// Rows past the chunk are clamped to its last row, so every load is issued
+// whatever n is: a load under a condition is not counted by the compiler's
+// waits, and the first use of anything loaded before it would then wait for
+// every row in flight (loads complete in order).  The R <= PAGE consecutive
+// positions span at most two pages, looked up once per group.
+template <int EPL, int R>
+__device__ __forceinline__ void load_rows_c(const AttnArgs &a, int h, int cs, int n, int j0, bool vpart, int lane,
+                                            int32_t out[R][EPL]) {
+    static_assert(R <= PAGE, "a row group spans at most two pages");
+    constexpr int HD = EPL * 64;
+    const int p0 = __builtin_amdgcn_readfirstlane(cs + (j0 < n ? j0 : n - 1));
+    const int p1 = __builtin_amdgcn_readfirstlane(cs + (j0 + R - 1 < n ? j0 + R - 1 : n - 1));
+    // the row base is uniform (scalar), only the lane offset is per lane
+    const size_t off = (vpart ? (size_t)a.NKV * PAGE * HD : 0) + (size_t)__builtin_amdgcn_readfirstlane(h) * PAGE * HD;
+    const int32_t *b0 = (const int32_t *)page_of(a.pages, a.ring_pages, p0) + off;
+    const int32_t *b1 = (const int32_t *)page_of(a.pages, a.ring_pages, p1) + off;
+    #pragma unroll
+    for (int u = 0; u < R; u++) {
+        const int p = cs + (j0 + u < n ? j0 + u : n - 1);
+        const int32_t *row = (p / PAGE == p0 / PAGE ? b0 : b1) + (size_t)(p & (PAGE - 1)) * HD;
+        ld_lane_row<EPL>(row + lane * EPL, out[u]);
+    }
+}
+
 // Row-quad layout for the score passes: a wave takes 16 consecutive positions
 // at a time, lane = 4 * row + quarter; in load i a quarter reads 16 B at
 // byte 64 i + 16 quarter of its row (each row's four lanes read 64
@@ -289,6 +327,17 @@ __device__ __forceinline__ const T *quad_row(const AttnArgs &a, int h, int p0, i
     const float *pg = quad_page(a, p0, plast, p);
     const int HD = EPL * 64;
     return (const T *)(pg + (vpart ? (size_t)a.NKV * PAGE * HD : 0) + ((size_t)h * PAGE + (p & (PAGE - 1))) * HD);
+}
+// One row group of the exact score pass (LPR lanes per row, 64 / LPR rows
+// from j0): row j0 + r, clamped to the chunk's last row like load_rows_c, so
+// the loads are issued unconditionally.
+template <int EPL, int LPR>
+__device__ __forceinline__ void load_kgroup(const AttnArgs &a, int h, int cs, int n, int j0, int r, int k4,
+                                            int4 kv[EPL * 16 / LPR]) {
+    const int jc = j0 < n ? j0 : n - 1, j = j0 + r < n ? j0 + r : n - 1;
+    const int32_t *row = quad_row<EPL, int32_t>(a, h, cs + jc, cs + n - 1, cs + j, false) + 4 * k4;
+    #pragma unroll
+    for (int i = 0; i < EPL * 16 / LPR; i++) kv[i] = ld_stream((const int4 *)(row + 4 * LPR * i));
 }
 
 template <int EPL, int G, bool BATCH, bool SPN>
@@ -629,14 +678,7 @@ __global__ __launch_bounds__(256) void k_attn_exact_scores(AttnArgs a_in) {
     if constexpr (PREP) prep_load<EPL, G>(a, h, pos, wave, lane, holds_pos, pin);
     __builtin_amdgcn_sched_barrier(0);
     int4 kv[NLD];
-    {
-        const int j = wave * RPW + r;
-        if (j < n) {
-            const int32_t *row = quad_row<EPL, int32_t>(a, h, cs + wave * RPW, ce - 1, cs + j, false) + 4 * k4;
-            #pragma unroll
-            for (int i = 0; i < NLD; i++) kv[i] = ld_stream((const int4 *)(row + 4 * LPR * i));
-        }
-    }
+    load_kgroup<EPL, LPR>(a, h, cs, n, wave * RPW, r, k4, kv);
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (PREP) {
         prep_finish<EPL, G>(a, h, pos, wave, lane, holds_pos, pin, qs, kn);
@@ -652,15 +694,11 @@ __global__ __launch_bounds__(256) void k_attn_exact_scores(AttnArgs a_in) {
     int mx = INT32_MIN;                              // lane with k4 == g tracks head g
     for (int j0 = wave * RPW; j0 < n; j0 += 4 * RPW) {
         const int j = j0 + r;
+        if (j0 != wave * RPW) load_kgroup<EPL, LPR>(a, h, cs, n, j0, r, k4, kv);
         int64_t acc[G];
         #pragma unroll
         for (int g = 0; g < G; g++) acc[g] = 0;
         if (j < n) {
-            if (j0 != wave * RPW) {
-                const int32_t *row = quad_row<EPL, int32_t>(a, h, cs + j0, ce - 1, cs + j, false) + 4 * k4;
-                #pragma unroll
-                for (int i = 0; i < NLD; i++) kv[i] = ld_stream((const int4 *)(row + 4 * LPR * i));
-            }
             if (holds_pos && cs + j == pos) {
                 #pragma unroll
                 for (int i = 0; i < NLD; i++) kv[i] = kn[LPR * i + k4];
@@ -716,7 +754,7 @@ __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a_in) {
     int cs, ce, nch;
     chunk_range(a, pos, c, cs, ce, nch);
     if (c >= nch) return;
-    __shared__ int32_t ew[G][MAXCH];                // island weights in Q22 (<= 2^22)
+    __shared__ int32_t ew[G][MAXCH + UV];           // island weights in Q22 (<= 2^22), 0 past the chunk
     __shared__ int64_t ored[4][G][EPL * 64];
     __shared__ int redi[4][G];
     __shared__ int64_t redl[4][G];
@@ -724,23 +762,27 @@ __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a_in) {
     const int n = ce - cs;
     // This chunk's scores and the chunk maxima are requested first, then the
     // first UV V rows of each wave: the global-max reduction and the weights
-    // then overlap the rows' latency.
+    // then overlap the rows' latency.  Every one of these loads is issued
+    // (indices past the end clamped, the values unused), so that the waits
+    // for the scores leave the rows in flight.
     constexpr int ZPT = G * MAXCH / 256;              // score slots per thread
-    int32_t zr[ZPT];
+    int32_t zr[ZPT];                                  // slot j >= n: unused
     #pragma unroll
     for (int k = 0; k < ZPT; k++) {
         const int i = threadIdx.x + 256 * k;
         const int g = i / MAXCH, j = i % MAXCH;
-        zr[k] = j < n ? a.zscratch[(size_t)(h * G + g) * a.zstride + (size_t)(cs + j)] : 0;
+        zr[k] = a.zscratch[(size_t)(h * G + g) * a.zstride + (size_t)(cs + (j < n ? j : n - 1))];
     }
     const int32_t *pml = (const int32_t *)a.part_ml;
     int pm0[G];
     #pragma unroll
-    for (int g = 0; g < G; g++)
-        pm0[g] = (int)threadIdx.x < nch ? pml[((size_t)(h * G + g) * a.max_chunks + threadIdx.x) * 4] : INT32_MIN;
+    for (int g = 0; g < G; g++) {
+        const int v = pml[((size_t)(h * G + g) * a.max_chunks + ((int)threadIdx.x < nch ? threadIdx.x : 0)) * 4];
+        pm0[g] = (int)threadIdx.x < nch ? v : INT32_MIN;
+    }
     __builtin_amdgcn_sched_barrier(0);
-    int32_t vv[UV][EPL];
-    load_rows<EPL, int32_t, UV>(a, h, cs, wave * UV, n, true, lane, vv);
+    int32_t va[UV][EPL], vb[UV][EPL];                 // row groups in flight, alternating
+    load_rows_c<EPL, UV>(a, h, cs, n, wave * UV, true, lane, va);
     __builtin_amdgcn_sched_barrier(0);
     // global max of the attended window over every chunk's maximum
     int M[G];
@@ -767,6 +809,7 @@ __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a_in) {
         const int g = i / MAXCH, j = i % MAXCH;
         if (j < n) ew[g][j] = (int32_t)(exp_fixed((((int64_t)zr[k] - (int64_t)M[g]) * ONE) >> 14) >> 8);
     }
+    if ((int)threadIdx.x < G * UV) ew[threadIdx.x / UV][n + threadIdx.x % UV] = 0;
     __syncthreads();
     // The V-sum of this wave's rows in FP64, exactly: weights are Q22 (<= 2^22)
     // and |vq| < 2^23, so every product and every partial sum of a wave's rows
@@ -777,23 +820,31 @@ __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a_in) {
     for (int g = 0; g < G; g++)
         #pragma unroll
         for (int e = 0; e < EPL; e++) o[g][e] = 0.0;
-    int32_t vn[UV][EPL];
-    for (int j0 = wave * UV; j0 < n; j0 += 4 * UV) {
-        load_rows<EPL, int32_t, UV>(a, h, cs, j0 + 4 * UV, n, true, lane, vn);
+    // every row of the group is read, without conditions (rows past the end
+    // meet the zero weights after the chunk's, which add exactly nothing): a
+    // row left unread on some path would count as still in flight, and
+    // reusing its registers would wait for every load
+    auto vsum = [&](const int32_t (&v)[UV][EPL], int j0) {
         #pragma unroll
         for (int u = 0; u < UV; u++) {
-            if (j0 + u >= n) break;
             #pragma unroll
             for (int g = 0; g < G; g++) {
                 const double w = (double)ew[g][j0 + u];
                 #pragma unroll
-                for (int e = 0; e < EPL; e++) o[g][e] = fma(w, (double)vv[u][e], o[g][e]);
+                for (int e = 0; e < EPL; e++) o[g][e] = fma(w, (double)v[u][e], o[g][e]);
             }
         }
-        #pragma unroll
-        for (int u = 0; u < UV; u++)
-            #pragma unroll
-            for (int e = 0; e < EPL; e++) vv[u][e] = vn[u][e];
+    };
+    // the next row group is requested before the current one is summed, into
+    // the other buffer (no register copies, whose waits would be total)
+    for (int j0 = wave * UV; j0 < n; j0 += 8 * UV) {
+        load_rows_c<EPL, UV>(a, h, cs, n, j0 + 4 * UV, true, lane, vb);
+        __builtin_amdgcn_sched_barrier(0);
+        vsum(va, j0);
+        if (j0 + 4 * UV >= n) break;
+        load_rows_c<EPL, UV>(a, h, cs, n, j0 + 8 * UV, true, lane, va);
+        __builtin_amdgcn_sched_barrier(0);
+        vsum(vb, j0 + 4 * UV);
     }
     #pragma unroll
     for (int g = 0; g < G; g++)
