@@ -237,7 +237,7 @@ __global__ __launch_bounds__(WIN ? 512 : 256) void k_pattn_vsum(AttnArgs a) {
     constexpr int HD = EPL * 64, NQ = TT * G, UV = WIN ? 8 : 4, NW = WIN ? 8 : 4, NT = 64 * NW;
     const int VC = PV_CH;
     const int tg = blockIdx.x, c = win_start(a, 0) / VC + (int)blockIdx.y, h = blockIdx.z;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int t0 = tg * TT;
     const int tend = t0 + TT < a.nt ? t0 + TT : a.nt;
     const int pos_hi = a.pos0 + tend - 1;
@@ -248,13 +248,14 @@ __global__ __launch_bounds__(WIN ? 512 : 256) void k_pattn_vsum(AttnArgs a) {
     const int cs = WIN ? s0g : (c * VC > s0g ? c * VC : s0g);
     const int np = WIN ? pos_hi - s0g + 1 : (pos_hi < c * VC + VC - 1 ? pos_hi : c * VC + VC - 1) - cs + 1;
     const size_t QD = (size_t)a.NH * HD;
-    __shared__ int32_t ew[NQ][PV_SUB];                   // island weights (Q22) of a sub-chunk, 0 where masked
+    __shared__ int32_t ew[NQ][PV_SUB + UV];              // island weights (Q22) of a sub-chunk, 0 where masked and past it
     __shared__ int s_M[NQ];
     __shared__ int64_t ored[NQ][HD];                      // the waves' partials, added in LDS (order-free)
     __shared__ int64_t sred[NQ];
     __shared__ int is_last;
     for (int i = threadIdx.x; i < NQ * HD; i += NT) ored[i / HD][i % HD] = 0;
     if (threadIdx.x < NQ) sred[threadIdx.x] = 0;
+    if (threadIdx.x < NQ * UV) ew[threadIdx.x / UV][PV_SUB + threadIdx.x % UV] = 0;
     // each token-head's maximum over its 64-position chunk maxima (wave w: token-heads w, w+4, ..)
     for (int q = wave; q < NQ; q += NW) {
         const int tt = t0 + q / G;
@@ -271,13 +272,25 @@ __global__ __launch_bounds__(WIN ? 512 : 256) void k_pattn_vsum(AttnArgs a) {
     __syncthreads();
     for (int sb = 0; sb < np; sb += PV_SUB) {
         const int ns = np - sb < PV_SUB ? np - sb : PV_SUB;
-        for (int i = threadIdx.x; i < NQ * PV_SUB; i += NT) {
-            const int q = i / PV_SUB, jj = i % PV_SUB, tt = t0 + q / G, p = cs + sb + jj;
+        // the sub-chunk's scores: every slot's load is issued first (token and
+        // position clamped into range, masked slots' values unused), then the
+        // weights are formed -- one round trip, not one per slot
+        static_assert(NQ * PV_SUB % NT == 0, "whole slots per thread");
+        constexpr int FPT = NQ * PV_SUB / NT;
+        int32_t zz[FPT];
+        #pragma unroll
+        for (int k = 0; k < FPT; k++) {
+            const int i = threadIdx.x + NT * k, q = i / PV_SUB, jj = i % PV_SUB;
+            const int tt = t0 + q / G < a.nt ? t0 + q / G : a.nt - 1;
+            const int p = cs + sb + (jj < ns ? jj : ns - 1);
+            zz[k] = a.zscratch[(size_t)tt * a.NH * a.zstride + (size_t)(h * G + q % G) * a.zstride + p];
+        }
+        #pragma unroll
+        for (int k = 0; k < FPT; k++) {
+            const int i = threadIdx.x + NT * k, q = i / PV_SUB, jj = i % PV_SUB, tt = t0 + q / G, p = cs + sb + jj;
             int32_t w = 0;
-            if (jj < ns && tt < a.nt && p <= a.pos0 + tt && p >= win_start(a, tt)) {
-                const int32_t z = a.zscratch[(size_t)tt * a.NH * a.zstride + (size_t)(h * G + q % G) * a.zstride + p];
-                w = (int32_t)(exp_fixed((((int64_t)z - (int64_t)s_M[q]) * ONE) >> 14) >> 8);
-            }
+            if (jj < ns && tt < a.nt && p <= a.pos0 + tt && p >= win_start(a, tt))
+                w = (int32_t)(exp_fixed((((int64_t)zz[k] - (int64_t)s_M[q]) * ONE) >> 14) >> 8);
             ew[q][jj] = w;
         }
         __syncthreads();
@@ -288,45 +301,54 @@ __global__ __launch_bounds__(WIN ? 512 : 256) void k_pattn_vsum(AttnArgs a) {
         for (int q = 0; q < NQ; q++)
             #pragma unroll
             for (int e = 0; e < EPL; e++) o[q][e] = 0.0;
-        // UV rows per wave and step (rows past ns read as zeros); WIN requests
-        // the next step's rows before this step's FMAs (the full-context
-        // instances keep their registers for occupancy instead)
+        // UV rows per wave and step, every load issued (rows past ns clamped to
+        // the last row; they meet zero weights), the step's at most two pages
+        // looked up once; the next step's rows are requested before this
+        // step's FMAs, into the other buffer (no register copies)
+        const size_t voff = (size_t)a.NKV * PAGE * HD + (size_t)h * PAGE * HD;
         auto load_v = [&](int j0, int32_t (&v)[UV][EPL]) {
+            const int pa = __builtin_amdgcn_readfirstlane(cs + sb + (j0 < ns ? j0 : ns - 1));
+            const int pb = __builtin_amdgcn_readfirstlane(cs + sb + (j0 + UV - 1 < ns ? j0 + UV - 1 : ns - 1));
+            const int32_t *ba = (const int32_t *)pg(a, pa) + voff, *bb = (const int32_t *)pg(a, pb) + voff;
             #pragma unroll
             for (int u = 0; u < UV; u++) {
-                const int jj = j0 + u;
-                if (jj < ns) {
-                    const int p = cs + sb + jj;
-                    const int32_t *row = (const int32_t *)pg(a, p) + (size_t)a.NKV * PAGE * HD +
-                                         ((size_t)h * PAGE + (p & (PAGE - 1))) * HD + lane * EPL;
-                    #pragma unroll
-                    for (int e = 0; e < EPL; e++) v[u][e] = gmem(row)[e];
+                const int p = __builtin_amdgcn_readfirstlane(cs + sb + (j0 + u < ns ? j0 + u : ns - 1));
+                const int32_t *row = (p / PAGE == pa / PAGE ? ba : bb) + (size_t)(p & (PAGE - 1)) * HD;
+                const int32_t *src = row + lane * EPL;
+                if constexpr (EPL == 4) {
+                    const int4 t = *gmem((const int4 *)src); v[u][0] = t.x; v[u][1] = t.y; v[u][2] = t.z; v[u][3] = t.w;
+                } else if constexpr (EPL == 2) {
+                    const int2 t = *gmem((const int2 *)src); v[u][0] = t.x; v[u][1] = t.y;
                 } else {
-                    #pragma unroll
-                    for (int e = 0; e < EPL; e++) v[u][e] = 0;
+                    v[u][0] = *gmem(src);
                 }
             }
         };
-        int32_t v[UV][EPL], vn[UV][EPL];
-        if constexpr (WIN) load_v(wave * UV, v);
-        for (int j0 = wave * UV; j0 < ns; j0 += NW * UV) {
-            if constexpr (WIN) load_v(j0 + NW * UV, vn);
-            else load_v(j0, v);
+        // one row at a time (the scheduler would otherwise hoist every
+        // weight of the step into registers ahead of the FMAs)
+        auto vrows = [&](const int32_t (&v)[UV][EPL], int j0) {
             #pragma unroll
             for (int u = 0; u < UV; u++) {
-                const int jj = j0 + u < PV_SUB ? j0 + u : 0;
                 #pragma unroll
                 for (int q = 0; q < NQ; q++) {
-                    const double w = (double)ew[q][jj];
+                    const double w = (double)ew[q][j0 + u];
                     #pragma unroll
                     for (int e = 0; e < EPL; e++) o[q][e] = fma(w, (double)v[u][e], o[q][e]);
                 }
+                __builtin_amdgcn_sched_barrier(0);
             }
-            if constexpr (WIN)
-                #pragma unroll
-                for (int u = 0; u < UV; u++)
-                    #pragma unroll
-                    for (int e = 0; e < EPL; e++) v[u][e] = vn[u][e];
+        };
+        int32_t va[UV][EPL], vb[UV][EPL];
+        load_v(wave * UV, va);
+        __builtin_amdgcn_sched_barrier(0);
+        for (int j0 = wave * UV; j0 < ns; j0 += 2 * NW * UV) {
+            load_v(j0 + NW * UV, vb);
+            __builtin_amdgcn_sched_barrier(0);
+            vrows(va, j0);
+            if (j0 + NW * UV >= ns) break;
+            load_v(j0 + 2 * NW * UV, va);
+            __builtin_amdgcn_sched_barrier(0);
+            vrows(vb, j0 + NW * UV);
         }
         #pragma unroll
         for (int q = 0; q < NQ; q++)
