@@ -360,7 +360,7 @@ __global__ __launch_bounds__(256) void k_recall_scores(RecallArgs rc) {
     const int m = rc.counts[h];
     const int j0 = c * RECALL_CHUNK;
     if (j0 >= m) return;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, e = lane >> 2, k4 = lane & 3;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), e = lane >> 2, k4 = lane & 3;
     __shared__ int4 qi[EPL * 16];
     __shared__ float4 qf[EPL * 16];
     __shared__ int wmi[4];
@@ -446,31 +446,37 @@ __global__ __launch_bounds__(256) void k_recall_vsum_exact(RecallArgs rc) {
     const int m = rc.counts[h];
     const int nact = (m + RECALL_CHUNK - 1) / RECALL_CHUNK;
     if (c >= nact) return;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     __shared__ int s_M;
     __shared__ int64_t ored[4][HD];
     __shared__ int64_t sred[4];
     __shared__ int is_last;
     __shared__ int64_t Sg;
-    // this wave's 16 list entries: positions and scores first (lanes 0..15),
-    // then every row requested before the weights are formed
+    // Wave 0 requests the chunk maxima first; every wave then requests its 16
+    // list entries (positions and scores, lanes 0..15) and all 16 rows.
+    // Entries past the list are clamped to its last one and weighted 0, so
+    // every load is issued and the waits for the maxima and the scores leave
+    // the rows in flight.
     const int jw = c * RECALL_CHUNK + wave * 16;
     const int nw = m - jw < 0 ? 0 : (m - jw > 16 ? 16 : m - jw);
-    int s_l = 0, z_l = 0;
-    if (lane < nw) { s_l = rc.lists[(size_t)h * rc.lstride + jw + lane]; z_l = rc.zs[(size_t)h * rc.lstride + jw + lane]; }
+    int cm = INT32_MIN;
+    if (wave == 0) {
+        const int x = rc.cmax[(size_t)h * rc.mchunks + (lane < nact ? lane : nact - 1)];
+        cm = lane < nact ? x : INT32_MIN;
+    }
+    const int jl = jw + lane < m ? jw + lane : m - 1;
+    const int s_l = rc.lists[(size_t)h * rc.lstride + jl], z_l = rc.zs[(size_t)h * rc.lstride + jl];
     int32_t v[16][EPL];
     #pragma unroll
-    for (int u = 0; u < 16; u++) {
-        if (u < nw) rc_vrow<EPL>(rc, kvh, __builtin_amdgcn_readlane(s_l, u), lane, v[u]);
-    }
-    if (threadIdx.x < 64) {
-        int t = INT32_MIN;
-        for (int k = threadIdx.x; k < nact; k += 64) {
+    for (int u = 0; u < 16; u++) rc_vrow<EPL>(rc, kvh, __builtin_amdgcn_readlane(s_l, u), lane, v[u]);
+    if (wave == 0) {
+        int t = cm;
+        for (int k = 64 + lane; k < nact; k += 64) {
             const int x = rc.cmax[(size_t)h * rc.mchunks + k];
             t = x > t ? x : t;
         }
         t = wave_allmax_i(t);
-        if (threadIdx.x == 0) s_M = t;
+        if (lane == 0) s_M = t;
     }
     __syncthreads();
     const int64_t M = s_M;
@@ -479,12 +485,10 @@ __global__ __launch_bounds__(256) void k_recall_vsum_exact(RecallArgs rc) {
     #pragma unroll
     for (int e = 0; e < EPL; e++) o[e] = 0.0;
     #pragma unroll
-    for (int u = 0; u < 16; u++) {
-        if (u < nw) {
-            const double w = (double)__shfl(w_l, u, 64);
-            #pragma unroll
-            for (int e = 0; e < EPL; e++) o[e] = fma(w, (double)v[u][e], o[e]);
-        }
+    for (int u = 0; u < 16; u++) {                  // entries past the list: weight 0, adds exactly nothing
+        const double w = (double)__shfl(w_l, u, 64);
+        #pragma unroll
+        for (int e = 0; e < EPL; e++) o[e] = fma(w, (double)v[u][e], o[e]);
     }
     const int64_t S = wave_allsum(w_l);
     #pragma unroll
@@ -530,27 +534,32 @@ __global__ __launch_bounds__(256) void k_recall_vsum_float(RecallArgs rc) {
     const int m = rc.counts[h];
     const int nact = (m + RECALL_CHUNK - 1) / RECALL_CHUNK;
     if (c >= nact) return;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     __shared__ float s_M;
     __shared__ float ored[4][HD];
     __shared__ float sred[4];
     __shared__ int is_last;
     __shared__ float Sg;
+    // loads ordered and clamped as in the exact pass; entries past the list
+    // are skipped in the sums
     const int jw = c * RECALL_CHUNK + wave * 16;
     const int nw = m - jw < 0 ? 0 : (m - jw > 16 ? 16 : m - jw);
-    int s_l = 0;
-    float z_l = 0.0f;
-    if (lane < nw) { s_l = rc.lists[(size_t)h * rc.lstride + jw + lane]; z_l = __int_as_float(rc.zs[(size_t)h * rc.lstride + jw + lane]); }
+    float cm = -INFINITY;
+    if (wave == 0) {
+        const float x = __int_as_float(rc.cmax[(size_t)h * rc.mchunks + (lane < nact ? lane : nact - 1)]);
+        cm = lane < nact ? x : -INFINITY;
+    }
+    const int jl = jw + lane < m ? jw + lane : m - 1;
+    const int s_l = rc.lists[(size_t)h * rc.lstride + jl];
+    const float z_l = __int_as_float(rc.zs[(size_t)h * rc.lstride + jl]);
     int32_t v[16][EPL];
     #pragma unroll
-    for (int u = 0; u < 16; u++) {
-        if (u < nw) rc_vrow<EPL>(rc, kvh, __builtin_amdgcn_readlane(s_l, u), lane, v[u]);
-    }
-    if (threadIdx.x < 64) {
-        float t = -INFINITY;
-        for (int k = threadIdx.x; k < nact; k += 64) t = fmaxf(t, __int_as_float(rc.cmax[(size_t)h * rc.mchunks + k]));
+    for (int u = 0; u < 16; u++) rc_vrow<EPL>(rc, kvh, __builtin_amdgcn_readlane(s_l, u), lane, v[u]);
+    if (wave == 0) {
+        float t = cm;
+        for (int k = 64 + lane; k < nact; k += 64) t = fmaxf(t, __int_as_float(rc.cmax[(size_t)h * rc.mchunks + k]));
         t = wave_allmax(t);
-        if (threadIdx.x == 0) s_M = t;
+        if (lane == 0) s_M = t;
     }
     __syncthreads();
     const float w_l = lane < nw ? expf(z_l - s_M) : 0.0f;
