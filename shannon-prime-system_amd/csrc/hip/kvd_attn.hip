@@ -197,28 +197,6 @@ __device__ __forceinline__ void chunk_range(const AttnArgs &a, int pos, int c, i
     if (ce > pos + 1) ce = pos + 1;
 }
 
-// 16 B-per-lane row loads of one head's HD elements at absolute position p
-template <int EPL, typename T>
-__device__ __forceinline__ void load_row(const AttnArgs &a, int h, int p, bool vpart, int lane, T out[EPL]) {
-    // row and head are wave-uniform: the page pointer and the row base are
-    // scalar work, only the lane offset is per lane
-    const int pu = __builtin_amdgcn_readfirstlane(p), hu = __builtin_amdgcn_readfirstlane(h);
-    const float *page = page_of(a.pages, a.ring_pages, pu);
-    const int HD = EPL * 64;
-    const T *row = (const T *)(page + (vpart ? (size_t)a.NKV * PAGE * HD : 0) + ((size_t)hu * PAGE + (pu & (PAGE - 1))) * HD);
-    const T *src = row + lane * EPL;
-    if constexpr (EPL == 4) {
-        typedef T v4 __attribute__((ext_vector_type(4)));
-        const v4 t = ld_stream((const v4 *)src); out[0] = t.x; out[1] = t.y; out[2] = t.z; out[3] = t.w;
-    } else if constexpr (EPL == 2) {
-        typedef T v2 __attribute__((ext_vector_type(2)));
-        const v2 t = ld_stream((const v2 *)src); out[0] = t.x; out[1] = t.y;
-    } else {
-        #pragma unroll
-        for (int e = 0; e < EPL; e++) out[e] = gmem(src)[e];
-    }
-}
-
 // Spinor-63 code rows (float mode with KVC_SPINOR): row p of kv-head h holds
 // HD int8 codes and the chunk multipliers (kvd_spinor.h).  v' = code * mul of
 // the coordinate's chunk; a lane's consecutive coordinates cross at most one
@@ -228,47 +206,9 @@ __device__ __forceinline__ const uint8_t *spn_row(const AttnArgs &a, const float
     constexpr int RB = spn_row_bytes(EPL * 64);
     return (const uint8_t *)page + ((vpart ? (size_t)a.NKV * PAGE : 0) + (size_t)h * PAGE + (p & (PAGE - 1))) * RB;
 }
-template <int EPL>
-__device__ __forceinline__ void load_row_spn(const AttnArgs &a, int h, int p, bool vpart, int lane, float out[EPL]) {
-    constexpr int HD = EPL * 64;
-    const int pu = __builtin_amdgcn_readfirstlane(p), hu = __builtin_amdgcn_readfirstlane(h);
-    const uint8_t *row = spn_row<EPL>(a, page_of(a.pages, a.ring_pages, pu), hu, pu, vpart);
-    const int e0 = lane * EPL, b0 = spn_block_of(HD, e0), b1 = spn_block_of(HD, e0 + EPL - 1);
-    const float *mul = (const float *)(row + HD);
-    const float m0 = gmem(mul)[b0], m1 = gmem(mul)[b1];
-    const int bnd = spn_block_start(HD, b0 + 1);
-    uint32_t w[(EPL + 3) / 4];
-    if constexpr (EPL == 1) w[0] = __builtin_nontemporal_load(gmem(row + e0));
-    else if constexpr (EPL == 2) w[0] = __builtin_nontemporal_load(gmem((const uint16_t *)(row + e0)));
-    else if constexpr (EPL == 4) w[0] = __builtin_nontemporal_load(gmem((const uint32_t *)(row + e0)));
-    else { const uint2 t = ld_stream((const uint2 *)(row + e0)); w[0] = t.x; w[1] = t.y; }
-    #pragma unroll
-    for (int e = 0; e < EPL; e++)
-        out[e] = (float)(int32_t)(int8_t)(w[e >> 2] >> (8 * (e & 3))) * (e0 + e < bnd ? m0 : m1);
-}
-
 constexpr int MAXCH = ATTN_MAXCH;   // positions per chunk (LDS score buffer)
 constexpr int MAXNCH = 4096;     // chunks per kv-head (combine weight buffer)
 constexpr int UNR = 4;           // positions in flight per wave
-
-// UNR rows j0.. of the chunk (zeros past n); the loops below load the next
-// UNR rows before working on the current ones, so a wave always has a row
-// group in flight
-template <int EPL, typename T, int R = UNR, bool SPN = false>
-__device__ __forceinline__ void load_rows(const AttnArgs &a, int h, int cs, int j0, int n, bool vpart, int lane,
-                                          T out[R][EPL]) {
-    #pragma unroll
-    for (int u = 0; u < R; u++) {
-        if (j0 + u < n) {
-            if constexpr (SPN) load_row_spn<EPL>(a, h, cs + j0 + u, vpart, lane, out[u]);
-            else load_row<EPL>(a, h, cs + j0 + u, vpart, lane, out[u]);
-        }
-        else {
-            #pragma unroll
-            for (int e = 0; e < EPL; e++) out[u][e] = (T)0;
-        }
-    }
-}
 
 // EPL consecutive int32 of a row for this lane (16, 8 or 4 bytes), streamed
 template <int EPL> __device__ __forceinline__ void ld_lane_row(const int32_t *src, int32_t out[EPL]) {
@@ -350,7 +290,7 @@ __global__ __launch_bounds__(256) void k_attn_float(AttnArgs a_in) {
     int cs, ce, nch;
     chunk_range(a, pos, c, cs, ce, nch);
     if (c >= nch) return;
-    __shared__ float sc[G][MAXCH];
+    __shared__ float sc[G][MAXCH + UNR];             // 0 past the chunk (plain rows' V-sum)
     __shared__ float ored[4][G][EPL * 64];
     __shared__ float wk[MAXNCH];
     __shared__ float redf[4];
@@ -440,6 +380,7 @@ __global__ __launch_bounds__(256) void k_attn_float(AttnArgs a_in) {
         const int g = i / n, j = i % n;
         sc[g][j] = expf(sc[g][j] - m[g]);
     }
+    if ((int)threadIdx.x < G * UNR) sc[threadIdx.x / UNR][n + threadIdx.x % UNR] = 0.0f;
     __syncthreads();
     #pragma unroll
     for (int g = 0; g < G; g++) {
@@ -508,24 +449,31 @@ __global__ __launch_bounds__(256) void k_attn_float(AttnArgs a_in) {
         for (int g = 0; g < G; g++)
             #pragma unroll
             for (int e = 0; e < EPL; e++) o[g][e] = 0.0f;
-        float vv[UNR][EPL], vn[UNR][EPL];
-        load_rows<EPL, float, UNR, SPN>(a, h, cs, wave * UNR, n, true, lane, vv);
-        for (int j0 = wave * UNR; j0 < n; j0 += 4 * UNR) {
-            load_rows<EPL, float, UNR, SPN>(a, h, cs, j0 + 4 * UNR, n, true, lane, vn);
+        // rows as in the exact V-sum: every load issued (rows past the chunk
+        // clamped, meeting the zero numerators after it), the next group in
+        // the other buffer; rows are added in the same order as before
+        int32_t va[UNR][EPL], vb[UNR][EPL];
+        auto vsum = [&](const int32_t (&v)[UNR][EPL], int j0) {
             #pragma unroll
             for (int u = 0; u < UNR; u++) {
-                if (j0 + u >= n) break;
                 #pragma unroll
                 for (int g = 0; g < G; g++) {
                     const float p = sc[g][j0 + u];
                     #pragma unroll
-                    for (int e = 0; e < EPL; e++) o[g][e] += p * vv[u][e];
+                    for (int e = 0; e < EPL; e++) o[g][e] += p * __int_as_float(v[u][e]);
                 }
             }
-            #pragma unroll
-            for (int u = 0; u < UNR; u++)
-                #pragma unroll
-                for (int e = 0; e < EPL; e++) vv[u][e] = vn[u][e];
+        };
+        load_rows_c<EPL, UNR>(a, h, cs, n, wave * UNR, true, lane, va);
+        __builtin_amdgcn_sched_barrier(0);
+        for (int j0 = wave * UNR; j0 < n; j0 += 8 * UNR) {
+            load_rows_c<EPL, UNR>(a, h, cs, n, j0 + 4 * UNR, true, lane, vb);
+            __builtin_amdgcn_sched_barrier(0);
+            vsum(va, j0);
+            if (j0 + 4 * UNR >= n) break;
+            load_rows_c<EPL, UNR>(a, h, cs, n, j0 + 8 * UNR, true, lane, va);
+            __builtin_amdgcn_sched_barrier(0);
+            vsum(vb, j0 + 4 * UNR);
         }
         #pragma unroll
         for (int g = 0; g < G; g++)
