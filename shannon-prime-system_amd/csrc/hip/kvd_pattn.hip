@@ -101,20 +101,36 @@ __global__ __launch_bounds__(256) void k_pattn_scores(AttnArgs a) {
         }
     }
     __syncthreads();                                    // s_wide is cleared
-    // K rows of the chunk as digit planes: thread i takes 16 consecutive dims of a row
-    for (int i = threadIdx.x; i < PS_CH * (HD / 16); i += 256) {
-        const int pl = i / (HD / 16), d0 = (i % (HD / 16)) * 16, p = cs + pl;
+    // K rows of the chunk as digit planes: thread i takes 16 consecutive dims of
+    // a row.  The chunk is one page (PS_CH == PAGE, chunks aligned), looked up
+    // once; every row load is requested before the first is used, rows past
+    // the group's last position clamped to it (their scores are never stored,
+    // and a copy of a row changes no range check)
+    static_assert(PS_CH == PAGE && PS_CH * (HD / 16) % 256 == 0, "one page per chunk, whole row pieces per thread");
+    constexpr int KIT = PS_CH * (HD / 16) / 256;
+    const int32_t *kpage = (const int32_t *)pg(a, cs) + (size_t)h * PAGE * HD;
+    int4 kx[KIT][4];
+    #pragma unroll
+    for (int it = 0; it < KIT; it++) {
+        const int i = threadIdx.x + 256 * it, pl = i / (HD / 16), d0 = (i % (HD / 16)) * 16;
+        const int32_t *row = kpage + (size_t)(pl < np ? pl : np - 1) * HD + d0;
+        #pragma unroll
+        for (int q = 0; q < 4; q++) kx[it][q] = *gmem((const int4 *)(row + 4 * q));
+    }
+    // every row is requested before any is used: the conversion below takes
+    // its inputs through a zero the compiler cannot see through, produced
+    // after the loads (otherwise it hoists the conversion between them, and
+    // each iteration waits for its own rows before the next is requested)
+    int32_t after_loads;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(after_loads) : : "memory");
+    #pragma unroll
+    for (int it = 0; it < KIT; it++) {
+        const int i = threadIdx.x + 256 * it, pl = i / (HD / 16), d0 = (i % (HD / 16)) * 16;
         int32_t x[16];
-        if (pl < np) {
-            const int32_t *row = (const int32_t *)pg(a, p) + ((size_t)h * PAGE + (p & (PAGE - 1))) * HD + d0;
-            #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const int4 v = *gmem((const int4 *)(row + 4 * q));
-                x[4 * q] = v.x; x[4 * q + 1] = v.y; x[4 * q + 2] = v.z; x[4 * q + 3] = v.w;
-            }
-        } else {
-            #pragma unroll
-            for (int e = 0; e < 16; e++) x[e] = 0;
+        #pragma unroll
+        for (int q = 0; q < 4; q++) {
+            x[4 * q] = kx[it][q].x ^ after_loads; x[4 * q + 1] = kx[it][q].y ^ after_loads;
+            x[4 * q + 2] = kx[it][q].z ^ after_loads; x[4 * q + 3] = kx[it][q].w ^ after_loads;
         }
         uint32_t w[4][4] = {};
         #pragma unroll
