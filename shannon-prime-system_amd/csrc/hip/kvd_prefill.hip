@@ -141,7 +141,7 @@ template <bool PAIRED> struct WaveChunk {
 // back with ds_read_b64.  Each wave loads its own codes 16 bytes per lane and
 // its scales 16 bytes per lane (8 blocks) one chunk ahead.  All buffer
 // offsets are 32-bit (checked by the launcher).
-template <bool PAIRED, int TT>
+template <bool PAIRED, int TT, bool SPLIT>
 __global__ __launch_bounds__(256) void k_gemm_q4b(GemmArgs a) {
     constexpr int KC = GEMM_KC, AG = GEMM_AG;
     constexpr int SEG = 3 * TT;                        // 512-byte tiles per block (planes x token tiles)
@@ -255,28 +255,36 @@ __global__ __launch_bounds__(256) void k_gemm_q4b(GemmArgs a) {
     // wave's codes and scales are requested right after their registers' use.
     // Every buffer write is separated from the previous reads of that buffer
     // by the barrier that published the other buffer.
+    // Without split K the loads for chunks past the last are issued too, as
+    // repeats of the last chunk (cache hits, values unused): a load under a
+    // condition is not counted by the compiler's waits, and the waits for the
+    // chunk being computed would then wait for the next chunk's loads as well.
+    // A split's few chunks end in a hand-off that waits for every load, so
+    // there the extra loads would only delay it: they stay conditional.
+    auto cl = [&](int ck) { return ck < nck ? ck : nck - 1; };
+    auto want = [&](int ck) { return !SPLIT || ck < nck; };
     uint4 st0[PPT], st1[PPT];
     WaveChunk<PAIRED> w0, w1;
     stage_load(st0, 0);
     wave_load(w0, 0);
-    if (nck > 1) { stage_load(st1, 1); wave_load(w1, 1); }
+    if (want(1)) { stage_load(st1, cl(1)); wave_load(w1, cl(1)); }
     stage_store(st0, 0);
     __syncthreads();
     for (int ck = 0; ck < nck; ck += 2) {
-        if (ck + 2 < nck) stage_load(st0, ck + 2);
+        if (want(ck + 2)) stage_load(st0, cl(ck + 2));
         compute(w0, 0);
-        if (ck + 2 < nck) wave_load(w0, ck + 2);
+        if (want(ck + 2)) wave_load(w0, cl(ck + 2));
         if (ck + 1 >= nck) break;
         stage_store(st1, 1);
         __syncthreads();
-        if (ck + 3 < nck) stage_load(st1, ck + 3);
+        if (want(ck + 3)) stage_load(st1, cl(ck + 3));
         compute(w1, 1);
-        if (ck + 3 < nck) wave_load(w1, ck + 3);
+        if (want(ck + 3)) wave_load(w1, cl(ck + 3));
         if (ck + 2 >= nck) break;
         stage_store(st0, 0);
         __syncthreads();
     }
-    if (gridDim.z > 1) {
+    if constexpr (SPLIT) {
         // split K: every split stores its exact partials in its own slice
         // (agent-scope stores, coherent across the XCDs' L2s); the last split
         // of the tile to arrive adds the others' to its own
@@ -379,12 +387,16 @@ void launch_gemm(const GemmArgs &a, int nrows_total, hipStream_t s) {
         ks = (nck + kper - 1) / kper;                  // every split holds chunks
     }
     grid.z = ks;
-    if (paired) {
-        if (tt2) hipLaunchKernelGGL((k_gemm_q4b<true, 2>), grid, dim3(256), 0, s, g);
-        else     hipLaunchKernelGGL((k_gemm_q4b<true, 1>), grid, dim3(256), 0, s, g);
-    } else {
-        if (tt2) hipLaunchKernelGGL((k_gemm_q4b<false, 2>), grid, dim3(256), 0, s, g);
-        else     hipLaunchKernelGGL((k_gemm_q4b<false, 1>), grid, dim3(256), 0, s, g);
+    const int inst = (paired ? 4 : 0) + (tt2 ? 2 : 0) + (ks > 1 ? 1 : 0);
+    switch (inst) {
+    case 0: hipLaunchKernelGGL((k_gemm_q4b<false, 1, false>), grid, dim3(256), 0, s, g); break;
+    case 1: hipLaunchKernelGGL((k_gemm_q4b<false, 1, true>), grid, dim3(256), 0, s, g); break;
+    case 2: hipLaunchKernelGGL((k_gemm_q4b<false, 2, false>), grid, dim3(256), 0, s, g); break;
+    case 3: hipLaunchKernelGGL((k_gemm_q4b<false, 2, true>), grid, dim3(256), 0, s, g); break;
+    case 4: hipLaunchKernelGGL((k_gemm_q4b<true, 1, false>), grid, dim3(256), 0, s, g); break;
+    case 5: hipLaunchKernelGGL((k_gemm_q4b<true, 1, true>), grid, dim3(256), 0, s, g); break;
+    case 6: hipLaunchKernelGGL((k_gemm_q4b<true, 2, false>), grid, dim3(256), 0, s, g); break;
+    default: hipLaunchKernelGGL((k_gemm_q4b<true, 2, true>), grid, dim3(256), 0, s, g); break;
     }
 }
 
