@@ -699,7 +699,12 @@ __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a_in) {
     tok_select<BATCH>(a, grid_token<BATCH>(a_in), pos);
     const int HD = EPL * 64, c = grid_chunk<BATCH>(a_in), h = grid_head<BATCH>(a_in);
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    int cs, ce, nch;
+    // decode may sum V over longer chunks than the score pass's (vchunk, a
+    // multiple of chunk): fewer workgroups arrive on each kv head's counter.
+    // The maxima stay per score chunk (nsc of them).
+    int cs, ce, nch, nsc;
+    chunk_range(a, pos, 0, cs, ce, nsc);
+    if (!BATCH && a.vchunk > a.chunk) a.chunk = a.vchunk;
     chunk_range(a, pos, c, cs, ce, nch);
     if (c >= nch) return;
     __shared__ int32_t ew[G][MAXCH + UV];           // island weights in Q22 (<= 2^22), 0 past the chunk
@@ -725,8 +730,8 @@ __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a_in) {
     int pm0[G];
     #pragma unroll
     for (int g = 0; g < G; g++) {
-        const int v = pml[((size_t)(h * G + g) * a.max_chunks + ((int)threadIdx.x < nch ? threadIdx.x : 0)) * 4];
-        pm0[g] = (int)threadIdx.x < nch ? v : INT32_MIN;
+        const int v = pml[((size_t)(h * G + g) * a.max_chunks + ((int)threadIdx.x < nsc ? threadIdx.x : 0)) * 4];
+        pm0[g] = (int)threadIdx.x < nsc ? v : INT32_MIN;
     }
     __builtin_amdgcn_sched_barrier(0);
     int32_t va[UV][EPL], vb[UV][EPL];                 // row groups in flight, alternating
@@ -737,7 +742,7 @@ __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a_in) {
     #pragma unroll
     for (int g = 0; g < G; g++) {
         int t = pm0[g];
-        for (int k = threadIdx.x + 256; k < nch; k += 256) {
+        for (int k = threadIdx.x + 256; k < nsc; k += 256) {
             const int v = pml[((size_t)(h * G + g) * a.max_chunks + k) * 4];
             t = v > t ? v : t;
         }
@@ -880,7 +885,11 @@ template <int EPL, int G, bool B> static void attn_dispatch_b(const AttnArgs &a,
             if (wide) hipLaunchKernelGGL((k_attn_exact_scores<EPL, G, B, false, 8>), grid, dim3(256), 0, s, a);
             else hipLaunchKernelGGL((k_attn_exact_scores<EPL, G, B, false, 4>), grid, dim3(256), 0, s, a);
         }
-        hipLaunchKernelGGL((k_attn_exact_vsum<EPL, G, B, 2 * UNR>), grid, dim3(256), 0, s, a);
+        dim3 gv = grid;
+        // V-sum chunks of vchunk positions: the span of grid_chunks score
+        // chunks meets at most grid_chunks * chunk / vchunk + 2 of them
+        if (!B && a.vchunk > a.chunk) gv.x = grid_chunks * a.chunk / a.vchunk + 2;
+        hipLaunchKernelGGL((k_attn_exact_vsum<EPL, G, B, 2 * UNR>), gv, dim3(256), 0, s, a);
     }
 }
 template <int EPL, int G> static void attn_dispatch(const AttnArgs &a, int grid_chunks, bool prep, hipStream_t s) {
@@ -892,6 +901,9 @@ static void attention_go(const AttnArgs &a, int grid_chunks, bool prep, hipStrea
     const int G = a.NH / a.NKV;
     if (a.chunk > MAXCH || a.chunk % 16 || grid_chunks > MAXNCH || grid_chunks < 1) {
         launch_fail("attention chunk or chunk count outside the kernel's limits"); return;
+    }
+    if (a.vchunk && (a.vchunk > MAXCH || a.vchunk % a.chunk)) {
+        launch_fail("V-sum chunk not a multiple of the score chunk within the kernel's limits"); return;
     }
     if (a.HD == 256 && G == 2) attn_dispatch<4, 2>(a, grid_chunks, prep, s);
     else if (a.HD == 128 && G == 2) attn_dispatch<2, 2>(a, grid_chunks, prep, s);

@@ -731,7 +731,7 @@ void free_handle(sp_kvdecode_handle *h) {
 // ------------------------------------------------------------ one step body
 // route: global layers attend over the recall router's positions (decode
 // steps of a handle with recall on; prefill attends densely)
-struct StepShape { int logits, argmax, grid_global, grid_local, chunk_global, chunk_local, route; };
+struct StepShape { int logits, argmax, grid_global, grid_local, chunk_global, chunk_local, route, vchunk_global; };
 
 int attn_chunks(const sp_kvdecode_handle *h, int pos_hi, StepShape &sh) {
     const DevModel *m = h->m;
@@ -753,6 +753,14 @@ int attn_chunks(const sp_kvdecode_handle *h, int pos_hi, StepShape &sh) {
     while ((pos_hi / cg + 1) > 4096) cg *= 2;
     sh.chunk_global = cg;
     sh.grid_global = pos_hi / cg + 1;
+    // exact-mode V-sum: a head with many short score chunks sums V over k of
+    // them per workgroup (about 24 V-sum workgroups per head, at most
+    // ATTN_MAXCH positions), so fewer workgroups arrive on each head's
+    // counter.  Qwen3-0.6B shape, 4 352 positions, 64-position score chunks:
+    // V-sum chunks of 192 took the attention 19.4 -> 17.0 us (128: 17.5, 256:
+    // 17.6); the Gemma-3-12B shape's 272- and 512-position chunks gain nothing.
+    const int k = std::min(ATTN_MAXCH / cg, (sh.grid_global + 12) / 24);
+    sh.vchunk_global = k >= 2 ? k * cg : 0;
     // window layers: 64-position chunks; a window of W positions touches at most
     // (W-1)/64 + 2 of them whatever its alignment
     const int cl = 64;
@@ -823,6 +831,7 @@ void enqueue_body(sp_kvdecode_handle *h, const StepShape &sh, TimeCb cb, void *c
         a.base = (m->gemma && !glob) ? 10000.0f : m->base;
         a.ascale = 1.0f / sqrtf((float)m->HD);
         a.chunk = glob ? sh.chunk_global : sh.chunk_local;
+        a.vchunk = glob ? sh.vchunk_global : 0;
         a.stat_out = st(l, STAT_AO);
         if (h->rec.B > 0 && a.win < 0) { a.rec_R = h->rec.Rb; a.rec_r = h->rec.r; }
         const int cls = (glob || a.win < 0) ? 5 : 6, grid = glob ? sh.grid_global : sh.grid_local;

@@ -84,6 +84,7 @@ struct AttnArgs {
     const DState *st;
     const float *rope_cs;    // this step's rotation table for the layer's base: cos[HD/2], sin[HD/2]
     int NH, NKV, HD, win, max_chunks, chunk, mode;
+    int vchunk;              // exact decode: positions per V-sum chunk, a multiple of chunk (0: chunk)
     int kvc;                 // KV codec: 0 plain, 1 Spinor-63 (float mode: code rows)
     float eps, base, ascale;
     int zstride;             // positions per q-head row of zscratch (>= pmax)
