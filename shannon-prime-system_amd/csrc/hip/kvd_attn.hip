@@ -804,9 +804,9 @@ __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a_in) {
         #pragma unroll
         for (int e = 0; e < EPL; e++) ored[wave][g][lane * EPL + e] = (int64_t)o[g][e];
     __syncthreads();
-    // exact, order-free accumulation of this chunk into the kv-head's totals;
-    // VREP replicas (chunk c adds into replica c % VREP) spread the same-address
-    // atomics, the last workgroup sums them
+    // exact, order-free accumulation of this chunk into the kv-head's totals
+    // (VREP replicas, chunk c adding into replica c % VREP); the last
+    // workgroup sums them
     const size_t QDh = (size_t)a.NH * HD;
     int64_t *vrep = a.vacc + (size_t)(c % VREP) * QDh;
     int64_t *srep = a.vacc_s + (size_t)(c % VREP) * a.NH;
