@@ -41,10 +41,14 @@ __device__ void cordic_q62(int64_t th, int64_t &co, int64_t &si) {
     int quad = 0;
     while (th >= HALF_PI_Q60 && quad < 3) { th -= HALF_PI_Q60; quad++; }
     int64_t x = g_kinv_q62, y = 0, z = th;
+    // branch-free rotation direction: sm = -1 where z < 0, and (v ^ sm) - sm
+    // is v or -v; the same integer steps as the two-sided update
+    #pragma unroll 2
     for (int i = 0; i < 62; i++) {
-        const int64_t xs = x >> i, ys = y >> i;
-        if (z >= 0) { x -= ys; y += xs; z -= g_atan_q60[i]; }
-        else        { x += ys; y -= xs; z += g_atan_q60[i]; }
+        const int64_t xs = x >> i, ys = y >> i, sm = z >> 63;
+        x -= (ys ^ sm) - sm;
+        y += (xs ^ sm) - sm;
+        z -= (g_atan_q60[i] ^ sm) - sm;
     }
     switch (quad) {
         case 0: co = x;  si = y;  break;
