@@ -102,6 +102,44 @@ def test_config2_qwen3_0p6b(tmp_path):
     o.close(); s.close(); m.close()
 
 
+@pytest.mark.parametrize("name,graph", [("qwen3-hd128", False), ("gemma3-hd256", True)])
+def test_long_context_vsum_over_score_chunks(tmp_path, name, graph):
+    """At 3 900 positions a full-context layer has about 61 score chunks of 64
+    positions per kv head, and the exact V-sum then sums three of them per
+    workgroup.  Prefill on the device; the first 64 positions' K/V equal the
+    oracle's; the oracle is then seeded from the device K/V and 8 decode steps
+    (graph-captured or plain launches) are bit-exact."""
+    spm, spt = model_files(tmp_path, name, max_context=4352)
+    m = spkv.Model(spm, spt); s = spkv.Session(m, 4352)
+    s.attach(4352, exact=True)
+    if not graph:
+        spkv.check(spkv.kv().sp_hipkv_set_graph(s.backend_handle(), 0), "set_graph")
+    be = spkv.Backend.wrap(s.backend_handle())
+    o = orc.Oracle(spm, 4352, orc.EXACT)
+    V, kvd = o.V, o.NKV * o.HD
+    pr = prompt(3900, V, seed=7)
+    lg = np.zeros(V, np.float32)
+    spkv.check(s.prefill(pr, lg), "sp_prefill_chunk")
+    for t in pr[:64]:
+        o.step(int(t), False)
+    for layer in range(o.NL):
+        if window_of(o, layer):
+            continue                           # window layers keep a ring of recent positions
+        kg, vg = be.read_kv(layer, 0, 64, kvd)
+        kc, vc = o.kv(layer, 0, 64)
+        assert same_bits(kg, kc) and same_bits(vg, vc), f"prefix layer {layer}"
+    load_kv(o, be, 64, 3899)
+    assert same_bits(lg, o.step(int(pr[3899]))), "last prompt position"
+    check_kv_at(o, be, 3899)
+    t = int(lg.argmax())
+    for k in range(8):
+        spkv.check(s.decode(t, lg), "sp_decode_step")
+        ol = o.step(t)
+        assert same_bits(lg, ol), f"decode step {k}"
+        t = int(ol.argmax())
+    o.close(); s.close(); m.close()
+
+
 @pytest.fixture(scope="module")
 def gemma12b(tmp_path_factory):
     d = tmp_path_factory.mktemp("gemma12b")
