@@ -286,10 +286,14 @@ sp_status sp_session_rewind(sp_session *s, size_t n_tokens) {
 sp_status sp_session_register_kvdecode_backend(sp_session *s, sp_kvdecode_handle *handle,
                                                const sp_kvdecode_dispatch_fn *dt) {
     if (!s) { sp_set_error("sp_session_register_kvdecode_backend: null session"); return SP_EBADARG; }
-    if (s->kv_owned && s->kv_h != handle) drop_backend(s);
+    /* an owned backend that is replaced or unregistered is closed here */
+    if (s->kv_owned && (s->kv_h != handle || !dt)) drop_backend(s);
     if (s->kv_dt != dt || s->kv_h != handle) s->kv_route = 0;   /* a new registration starts on default routing */
+    /* both fields are stored as given, as the reference does (sp_session.c:913-914):
+     * a NULL dt unregisters (sp_decode_step no longer routes) while the handle
+     * readback still returns the handle passed */
     s->kv_h = handle; s->kv_dt = dt;
-    if (!dt) { s->kv_h = NULL; s->kv_owned = 0; s->kv_route = 0; }
+    if (!dt) { s->kv_owned = 0; s->kv_route = 0; }
     return SP_OK;
 }
 
