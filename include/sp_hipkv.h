@@ -30,17 +30,20 @@ int  sp_hipkv_prefill(sp_kvdecode_handle *h, const int32_t *tokens, int n_tok);
  * position into caller memory, dpos += 1 */
 int  sp_hipkv_decode_step(sp_kvdecode_handle *h, int32_t token, float *logits);
 /* decode_step that allocates nothing -- no counterpart in the reference; for
- * callers that cannot allocate device memory (code under HIP graph capture,
- * tight serving loops, harnesses that forbid hipMalloc).  Same result as
- * sp_hipkv_decode_step (bit for bit), with plain kernel launches (no graph
- * instantiation) and the step's transient device memory (GEMV split-K
- * accumulators and counters, attention partials, score grid, V-sum
- * accumulators, vector statistics) in the library's static 32 MiB device
- * buffer instead of the handle's.  Fails, with nothing changed, when the
- * handle's model and pmax need more step scratch than that (e.g. float mode at
- * head_dim 256 beyond ~65k positions) or when the position needs a KV page the
- * pool would have to grow for.  All calls on one GPU share the buffer: calls
- * that overlap on one GPU (several threads or streams) race. */
+ * callers that cannot allocate device memory (tight serving loops, harnesses
+ * that forbid hipMalloc).  Same result as sp_hipkv_decode_step (bit for bit),
+ * with plain kernel launches (no graph instantiation) and the step's transient
+ * device memory (GEMV split-K accumulators and counters, attention partials,
+ * score grid, V-sum accumulators, vector statistics) in the library's static
+ * 32 MiB device buffer instead of the handle's.  Fails, with nothing changed,
+ * when the handle's model and pmax need more step scratch than that (e.g.
+ * float mode at head_dim 256 beyond ~65k positions) or when the position needs
+ * more KV pages (new, or copies of pages shared with a fork) than the pool has
+ * free without growing.  Like sp_hipkv_decode_step it waits for the step and
+ * copies the logits to the host, so it cannot be called under stream capture.
+ * All calls on one GPU share the buffer; a per-device lock makes such calls
+ * (from several threads, on several handles and streams) run one after
+ * another, each finished before the next starts. */
 int  sp_hipkv_decode_step_noalloc(sp_kvdecode_handle *h, int32_t token, float *logits);
 /* rewind: sp_l1.h:396 -- O(1): dpos -= n (n <= dpos) */
 int  sp_hipkv_rewind(sp_kvdecode_handle *h, int n);
@@ -62,6 +65,14 @@ int  sp_hipkv_set_mode(sp_kvdecode_handle *h, int exact);
  * ever written, since the ring has overwritten part of that position's window.
  * Only before the first token (dpos == 0).  0 = full table (default). */
 int  sp_hipkv_set_max_rewind(sp_kvdecode_handle *h, int max_rewind);
+/* Pages the KV pool allocates (one hipMalloc) when it has no free page left:
+ * 0 = about 1 GiB of pages, at least 16 (default).  Applies to the pool this
+ * handle shares with its forks, from the next growth on; a mode, codec or
+ * recall change before the first token keeps the setting.  A serving caller
+ * that packs many sessions into HBM uses it to grow in smaller steps.  No
+ * counterpart in the reference (its KV slab is one malloc per session,
+ * core/session/sp_session.c:240-245). */
+int  sp_hipkv_set_pool_growth(sp_kvdecode_handle *h, int pages);
 /* Copy-on-write fork of the resident cache (no counterpart in sp_l1.h: the
  * table has no fork row; sp_session_clone uses it through spx_register_fork). */
 int  sp_hipkv_fork(const sp_kvdecode_handle *parent, sp_kvdecode_handle **child);

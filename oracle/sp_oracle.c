@@ -693,6 +693,29 @@ int orc_arm_select(const signed char *R, int r, int hd, const float *qh, const f
     }
     if (topk > nc) topk = nc;
     qsel_topk(cand, nc, topk);
+    /* Ties at the k-th score: the quickselect keeps whichever equal candidates
+     * its partitions leave in front, an artefact of its order.  The rule here
+     * (and on the device) keeps the lowest positions among the candidates equal
+     * to the k-th score; without such a tie the set is the quickselect's.
+     * (-0.0 == +0.0, as in the reference's comparisons.)  Parity unpinned
+     * against the reference for exact ties at the k-th score. */
+    if (topk > 0 && topk < nc) {
+        float th = cand[0].s;
+        for (int t = 1; t < topk; t++) if (cand[t].s < th) th = cand[t].s;
+        int tied_out = 0;
+        for (int t = topk; t < nc; t++) if (cand[t].s == th) { tied_out = 1; break; }
+        if (tied_out) {
+            int above = 0;                 /* selected strictly above th, kept in place */
+            for (int t = 0; t < topk; t++) if (cand[t].s > th) sidx_swap(cand, t, above++);
+            /* the remaining slots: candidates equal to th, lowest positions first */
+            for (int t = above; t < topk; t++) {
+                int best = -1;
+                for (int u = t; u < nc; u++)
+                    if (cand[u].s == th && (best < 0 || cand[u].i < cand[best].i)) best = u;
+                sidx_swap(cand, t, best);
+            }
+        }
+    }
     int m = 0;
     for (int s2 = 0; s2 < sink; s2++) ri[m++] = s2;
     for (int t = 0; t < topk; t++) ri[m++] = cand[t].i;

@@ -160,7 +160,8 @@ __global__ __launch_bounds__(256) void k_rope_table(const DState *st, int pos0, 
         const int t = idx / half, i = idx % half;
         float c, s;
         if (mode == FLOAT) {
-            const float freq = powf(t ? base_l : base_g, -2.0f * (float)i / (float)HD);
+            // the host-formed powf(base, -2i/d) after the HD/2 Q60 entries
+            const float freq = ((const float *)((t ? fq_l : fq_g) + half))[i];
             const float theta = (float)pos * freq;
             c = cosf(theta); s = sinf(theta);
         } else {

@@ -289,9 +289,21 @@ DevModel *model_get(const qwen3_model *qm, bool upload = true) {
         d.post_attn = d.post_ffw = nullptr;
         if (m->gemma && (addn(y.post_attn_norm, m->E, &d.post_attn) || addn(y.post_ffw_norm, m->E, &d.post_ffw))) return nullptr;
     }
-    // exact-mode RoPE frequency tables (global base, and 1e4 for Gemma window layers)
-    std::vector<int64_t> fg(HD / 2), fl(HD / 2);
-    for (int i = 0; i < HD / 2; i++) { fg[i] = rope_freq_q60(m->base, i, HD); fl[i] = rope_freq_q60(10000.0f, i, HD); }
+    // RoPE frequency tables (global base, and 1e4 for Gemma window layers): per
+    // base HD/2 exact-mode frequencies in Q60, then HD/2 float-mode frequencies
+    // powf(base, -2i/d), formed here by the host's libm as the reference forms
+    // them (core/forward_kernels/forward_kernels.c:34): theta = p * freq is then
+    // the reference's float, where a one-ulp difference in freq would move
+    // theta by p ulps (2e-3 rad at p = 32767)
+    const int half = HD / 2;
+    std::vector<int64_t> fg(HD), fl(HD);
+    for (int i = 0; i < half; i++) {
+        fg[i] = rope_freq_q60(m->base, i, HD); fl[i] = rope_freq_q60(10000.0f, i, HD);
+        const float e = -2.0f * (float)i / (float)HD;
+        const float pg = powf(m->base, e), pl = powf(10000.0f, e);
+        memcpy((float *)(fg.data() + half) + i, &pg, 4);
+        memcpy((float *)(fl.data() + half) + i, &pl, 4);
+    }
     const size_t o_fg = up.add(fg.data(), fg.size() * 8), o_fl = up.add(fl.data(), fl.size() * 8);
     for (auto &pd : pend)
         m->weight_bytes += (size_t)pd.w->rows * (pd.w->cols / 2) + (size_t)pd.w->rows * pd.w->nblk * 2;
@@ -396,6 +408,7 @@ struct sp_kvdecode_handle {
     int kvc = KVC_PLAIN;                     // KV codec (KVC_SPINOR: SP_KV_SPINOR sessions)
     int use_batch = 1;                       // batched (MFMA) prefill where the shapes allow it
     int max_rewind = 0;                      // 0: full tables for window layers
+    int pool_growth = 0;                     // pages per pool growth (0: ~1 GiB)
     int full_pages = 0, ring_pages = 0;
     std::vector<std::vector<int>> pt;        // [NL][slots] page ids (-1 = unmapped)
     std::vector<int> slots;                  // per layer: number of slots
@@ -485,10 +498,15 @@ double kv_row_payload(const DevModel *m, int mode, int kvc) {
 size_t page_bytes_of(const DevModel *m, int mode, int kvc, int r) {
     return (size_t)2 * m->NKV * PAGE * kv_row_bytes(m, mode, kvc) + (size_t)recall_page_floats(m->NKV, r) * 4;
 }
-std::shared_ptr<KvPool> make_pool(const DevModel *m, int mode, int kvc, int r) {
+// growth: pages per device allocation when the pool grows (0: about 1 GiB of
+// pages, at least 16)
+int pool_growth_pages(size_t page_bytes, int growth) {
+    return growth > 0 ? growth : (int)std::max<size_t>(16, ((size_t)1 << 30) / page_bytes);
+}
+std::shared_ptr<KvPool> make_pool(const DevModel *m, int mode, int kvc, int r, int growth) {
     auto pool = std::make_shared<KvPool>();
     pool->page_bytes = page_bytes_of(m, mode, kvc, r);
-    pool->pages_per_chunk = (int)std::max<size_t>(16, ((size_t)1 << 30) / pool->page_bytes);
+    pool->pages_per_chunk = pool_growth_pages(pool->page_bytes, growth);
     return pool;
 }
 
@@ -517,44 +535,65 @@ int build_tables(sp_kvdecode_handle *h) {
 
 // Make the pages holding positions [p0, p1) present and exclusively owned in
 // every layer (allocate on first touch, copy-on-write when shared by a fork).
+//
+// Two phases, so that a failure changes nothing: first the pages the call
+// needs (unmapped slots plus slots shared with a fork) are counted and taken
+// from the pool's free list, growing the pool once when allowed; only then are
+// the tables changed, and the changed span is uploaded before any return.
 int ensure_pages(sp_kvdecode_handle *h, int p0, int p1, bool may_grow = true) {
     const DevModel *m = h->m;
     if (p1 <= p0) return 0;
     std::lock_guard<std::mutex> lk(h->pool->mu);
-    size_t lo = SIZE_MAX, hi = 0;                // changed entries of the concatenated table
+    KvPool &pool = *h->pool;
+    const int lp0 = p0 / PAGE, lp1 = (p1 - 1) / PAGE;
+    // the distinct slots of [lp0, lp1] in layer l: a ring visits at most S of them
+    auto slots_of = [&](int l, int &n) { const int S = h->slots[l]; n = std::min(lp1 - lp0 + 1, S); return S; };
+    size_t need = 0;
     for (int l = 0; l < m->NL; l++) {
-        const int S = h->slots[l];
-        const int lp0 = p0 / PAGE, lp1 = (p1 - 1) / PAGE;
-        for (int lp = lp0; lp <= lp1; lp++) {
-            const int slot = (S == h->full_pages) ? lp : lp % S;
-            bool dirty = false;
+        int n = 0;
+        const int S = slots_of(l, n);
+        for (int i = 0; i < n; i++) {
+            const int lp = lp0 + i, slot = (S == h->full_pages) ? lp : lp % S;
+            const int id = h->pt[l][slot];
+            if (id < 0 || pool.refc[id] > 1) need++;
+        }
+    }
+    if (need > pool.free_ids.size()) {
+        if (!may_grow)
+            return fail("sp_hipkv: %s%lld free KV pages needed without growing the pool (nothing changed)", "",
+                        (long long)need);
+        if (pool.grow((int)(need - pool.free_ids.size())))
+            return fail("sp_hipkv: KV pool exhausted (hipMalloc failed; nothing changed)%s");
+    }
+    size_t lo = SIZE_MAX, hi = 0;                // changed entries of the concatenated table
+    hipError_t err = hipSuccess;
+    for (int l = 0; l < m->NL && err == hipSuccess; l++) {
+        int n = 0;
+        const int S = slots_of(l, n);
+        for (int i = 0; i < n; i++) {
+            const int lp = lp0 + i, slot = (S == h->full_pages) ? lp : lp % S;
             int &id = h->pt[l][slot];
-            if (id < 0) {
-                id = h->pool->alloc(may_grow);
-                if (id < 0) return fail(may_grow ? "sp_hipkv: KV pool exhausted (hipMalloc failed)%s"
-                                                 : "sp_hipkv: no free KV page without growing the pool%s");
-                dirty = true;
-            } else if (h->pool->refc[id] > 1) {
-                const int nid = h->pool->alloc(may_grow);
-                if (nid < 0) return fail(may_grow ? "sp_hipkv: KV pool exhausted during copy-on-write%s"
-                                                  : "sp_hipkv: no free KV page for copy-on-write without growing the pool%s");
-                HIPCHK(hipMemcpyAsync(h->pool->ptr[nid], h->pool->ptr[id], h->pool->page_bytes,
-                                      hipMemcpyDeviceToDevice, h->stream), "copy-on-write page copy");
-                h->pool->unref(id);
-                id = nid;
-                dirty = true;
+            if (id >= 0 && pool.refc[id] <= 1) continue;
+            const int nid = pool.alloc(false);   // reserved above: cannot fail
+            if (id >= 0) {                       // shared with a fork: copy, then drop this handle's reference
+                err = hipMemcpyAsync(pool.ptr[nid], pool.ptr[id], pool.page_bytes, hipMemcpyDeviceToDevice, h->stream);
+                if (err != hipSuccess) { pool.unref(nid); break; }
+                pool.unref(id);
             }
-            h->h_pt[h->pt_off[l] + slot] = h->pool->ptr[id];
-            if (dirty) { lo = std::min(lo, h->pt_off[l] + slot); hi = std::max(hi, h->pt_off[l] + slot + 1); }
+            id = nid;
+            h->h_pt[h->pt_off[l] + slot] = pool.ptr[nid];
+            lo = std::min(lo, h->pt_off[l] + slot); hi = std::max(hi, h->pt_off[l] + slot + 1);
         }
     }
     if (hi > lo) {
-        // one upload of the changed span (the pinned mirror is authoritative);
-        // the wait also covers the copy-on-write copies issued above
+        // one upload of the changed span (the pinned mirror is authoritative),
+        // also after a failed copy so the device table matches the host's; the
+        // wait also covers the copy-on-write copies issued above
         HIPCHK(hipMemcpyAsync(h->d_pt + lo, h->h_pt + lo, (hi - lo) * sizeof(float *), hipMemcpyHostToDevice, h->stream),
                "page table update");
         HIPCHK(hipStreamSynchronize(h->stream), "page table update sync");
     }
+    HIPCHK(err, "copy-on-write page copy");
     return 0;
 }
 
@@ -622,7 +661,7 @@ int repage(sp_kvdecode_handle *h, const char *who) {
     if (h->pool->page_bytes == want) return 0;
     if (h->pool.use_count() > 1) return fail("%s: the KV pages are shared with a fork", who);
     { std::lock_guard<std::mutex> pl(h->pool->mu); for (auto &v : h->pt) for (int id : v) h->pool->unref(id); }
-    h->pool = make_pool(h->m, h->mode, h->kvc, h->rec.r);
+    h->pool = make_pool(h->m, h->mode, h->kvc, h->rec.r, h->pool_growth);
     free_graphs(h);
     return build_tables(h);
 }
@@ -1138,8 +1177,12 @@ __global__ void k_zero_words(uint32_t *p, size_t n) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = 0u;
 }
 
+constexpr int NOALLOC_MAX_DEVICES = 64;
 std::mutex g_scratch_mu;
-uint8_t *g_scratch_ptr[64];      // per device: the device address of `scratch`
+uint8_t *g_scratch_ptr[NOALLOC_MAX_DEVICES];        // per device: the device address of `scratch`
+// per device: held by an allocation-free step from carving the scratch to its
+// final synchronize, so calls that share a GPU's array run one after another
+std::mutex g_noalloc_mu[NOALLOC_MAX_DEVICES];
 
 // Carve a step scratch for h out of base[0, NOALLOC_SCRATCH_BYTES); false when
 // h's shape needs more.  *used = bytes to clear.
@@ -1185,12 +1228,12 @@ int sp_hipkv_open(const void *qm_opaque, int pmax, sp_kvdecode_handle **out) {
         return fail("sp_hipkv_open: no HIP device visible (this backend runs on MI355X / gfx950)%s");
     DevModel *m = model_get(qm);
     if (!m) return 1;
-    auto new_pool = [m]() { return make_pool(m, FLOAT, KVC_PLAIN, 0); };
+    auto new_pool = [m]() { return make_pool(m, FLOAT, KVC_PLAIN, 0, 0); };
     if (sp_kvdecode_handle *sh = take_shell(m, pmax, 0)) {
         // a kept shell: reset to the open defaults, unmapped tables
         set_handle_mode(sh, FLOAT);
         if (sh->kvc != KVC_PLAIN) { sh->kvc = KVC_PLAIN; free_graphs(sh); }   // graphs bake in the codec
-        sh->use_graph = 1; sh->use_batch = 1; sh->dpos = 0; sh->hwm = 0;
+        sh->use_graph = 1; sh->use_batch = 1; sh->dpos = 0; sh->hwm = 0; sh->pool_growth = 0;
         if (sh->rec.B) { free_recall(sh); free_graphs(sh); }
         sh->pool = new_pool();
         if (hipMemsetAsync(sh->vclamp, 0, sizeof(int), sh->stream) != hipSuccess) {
@@ -1447,7 +1490,12 @@ int sp_hipkv_decode_step_noalloc(sp_kvdecode_handle *h, int32_t token, float *lo
     if (h->dpos >= h->pmax) return fail("sp_hipkv_decode_step_noalloc: context full (dpos == pmax %s%lld)", "", (long long)h->pmax);
     int dev = 0;
     HIPCHK(hipGetDevice(&dev), "sp_hipkv_decode_step_noalloc: device query");
-    if (dev < 0 || dev >= 64) return fail("sp_hipkv_decode_step_noalloc: device index %s%lld out of range", "", (long long)dev);
+    if (dev < 0 || dev >= NOALLOC_MAX_DEVICES)
+        return fail("sp_hipkv_decode_step_noalloc: device index %s%lld out of range", "", (long long)dev);
+    // every call on this device shares its array: the lock orders them, and
+    // each call has finished on the device (its final synchronize) before the
+    // next one clears the array
+    std::lock_guard<std::mutex> serial(g_noalloc_mu[dev]);
     uint8_t *base = nullptr;
     {
         std::lock_guard<std::mutex> lk(g_scratch_mu);
@@ -1467,8 +1515,8 @@ int sp_hipkv_decode_step_noalloc(sp_kvdecode_handle *h, int32_t token, float *lo
     // of the pool): nothing may grow the pool here
     if (ensure_pages(h, h->dpos, h->dpos + 1, false)) return 1;
     if (set_state(h, h->dpos, token, DRIVE_HOST)) return 1;
-    // accumulators and counters start at zero (a fill kernel, not a memset
-    // node, so a caller may capture the call)
+    // accumulators and counters start at zero (the previous call on this
+    // device left its own contents)
     hipLaunchKernelGGL(k_zero_words, dim3(256), dim3(256), 0, h->stream, (uint32_t *)base, used / 4);
     enqueue_body(h, shape_for(h, h->dpos, 1, 0), nullptr, nullptr, ss);    // plain launches: no graph instantiation
     if (take_launch_error("sp_hipkv_decode_step_noalloc")) return 1;
@@ -1515,6 +1563,14 @@ int sp_hipkv_set_max_rewind(sp_kvdecode_handle *h, int max_rewind) {
     h->max_rewind = max_rewind;
     free_graphs(h);
     return build_tables(h);
+}
+
+int sp_hipkv_set_pool_growth(sp_kvdecode_handle *h, int pages) {
+    if (!h || pages < 0) return fail("sp_hipkv_set_pool_growth: bad argument%s");
+    h->pool_growth = pages;
+    std::lock_guard<std::mutex> pl(h->pool->mu);
+    h->pool->pages_per_chunk = pool_growth_pages(h->pool->page_bytes, pages);
+    return 0;
 }
 
 int sp_hipkv_set_graph(sp_kvdecode_handle *h, int on) {
@@ -1605,7 +1661,7 @@ int sp_hipkv_fork(const sp_kvdecode_handle *p, sp_kvdecode_handle **out) {
     if (hipMemsetAsync(h->vclamp, 0, sizeof(int), h->stream) != hipSuccess) {
         sp_hipkv_close(h.release()); return fail("sp_hipkv_fork: clamp counter reset failed%s");
     }
-    h->use_batch = p->use_batch; h->use_graph = p->use_graph;
+    h->use_batch = p->use_batch; h->use_graph = p->use_graph; h->pool_growth = p->pool_growth;
     hipStreamSynchronize(p->stream);
     // share every mapped page (copy-on-write on the next append into it)
     {

@@ -37,9 +37,12 @@ __device__ __forceinline__ const int32_t *rc_row(const RecallArgs &rc, int kvh, 
            ((size_t)kvh * PAGE + (s & (PAGE - 1))) * rc.HD;
 }
 
-// float -> unsigned key with the float order (larger float, larger key), and back
+// float -> unsigned key with the float order (larger float, larger key), and
+// back.  -0.0 takes +0.0's key: equal floats get equal keys, as the
+// reference's comparisons (`>`, core/arm/arm.c:49-76) treat them.
 __device__ __forceinline__ uint32_t order_key(float f) {
-    const uint32_t b = __float_as_uint(f);
+    uint32_t b = __float_as_uint(f);
+    if (b == 0x80000000u) b = 0u;
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 __device__ __forceinline__ float key_float(uint32_t k) {

@@ -113,6 +113,7 @@ def kv():
         _sig(lib, "sp_hipkv_set_kv_codec", c_int, [c_void_p, c_int])
         _sig(lib, "sp_hipkv_set_max_rewind", c_int, [c_void_p, c_int])
         _sig(lib, "sp_hipkv_set_graph", c_int, [c_void_p, c_int])
+        _sig(lib, "sp_hipkv_set_pool_growth", c_int, [c_void_p, c_int])
         _sig(lib, "sp_hipkv_set_batch_prefill", c_int, [c_void_p, c_int])
         _sig(lib, "sp_hipkv_fork", c_int, [c_void_p, ctypes.POINTER(c_void_p)])
         _sig(lib, "sp_hipkv_attach", c_int, [c_void_p, c_int, c_int])

@@ -269,6 +269,84 @@ def test_decode_batch_matches_per_session(tmpdir_models, name, exact):
     close_all(s, m)
 
 
+def oracle_from_device(spm, pmax, exact, be, pos, window):
+    """An oracle session whose K/V of positions [0, pos) are the device's (window
+    layers: only the positions the next step attends to), at position pos."""
+    o = orc.Oracle(spm, pmax, orc.EXACT if exact else orc.FLOAT)
+    kvd = o.NKV * o.HD
+    for layer in range(o.NL):
+        w = window(o, layer)
+        a = max(0, pos - w) if w else 0
+        if pos > a:
+            k, v = be.read_kv(layer, a, pos - a, kvd)
+            assert o.set_kv(layer, a, k, v) == 0
+    assert o.set_pos(pos) == 0
+    return o
+
+
+@pytest.mark.parametrize("name", ["qwen3-hd128", "gemma3-hd256"])
+@pytest.mark.parametrize("exact", [True, False])
+def test_decode_batch_across_chunks(tmpdir_models, name, exact):
+    """The batched decode's full-context layers split each session into
+    512-position chunks, one (session, chunk) work item per workgroup and kv
+    head, merged per session by its last arriving workgroup.  Ragged contexts
+    around and across the chunk boundaries (100 .. 1700 positions: one to four
+    chunks, a session ending on a boundary, one past it); three steps, each a
+    copy-on-write fork of every session rewound 0-4 tokens.  Every row equals an
+    independent handle's sp_hipkv_decode_step (exact mode bit for bit, float
+    mode rel <= 1e-3, same argmax), and the longest and a one-chunk session
+    equal the oracle given the device K/V."""
+    pmax = 2048
+    spm, spt = model_files(tmpdir_models, name, max_context=pmax)
+    m = spkv.Model(spm, spt); s = spkv.Session(m, pmax)
+    qm = spkv.l1().sp_session_qwen3_model(s.h)
+    V = 2048
+    lens = [100, 511, 512, 513, 600, 1100, 1536, 1700]
+    rew = [[0] * len(lens), [4, 1, 0, 2, 3, 0, 1, 4], [1, 0, 4, 1, 0, 2, 3, 0]]
+    A, B, toks = [], [], []
+    for i, n in enumerate(lens):
+        pr = prompt(n, V, seed=40 + i)
+        a = spkv.Backend(qm, pmax, exact=exact)
+        a.prefill(pr[:-1])
+        A.append(a); B.append(a.fork())
+        toks.append(int(pr[-1]))
+    lg = np.zeros(V, np.float32)
+    for step in range(3):
+        A2, B2 = [], []
+        for i in range(len(lens)):
+            a, b = A[i].fork(), B[i].fork()
+            A[i].close(); B[i].close()
+            if rew[step][i]:
+                assert a.rewind(rew[step][i]) == 0 and b.rewind(rew[step][i]) == 0
+            A2.append(a); B2.append(b)
+        A, B = A2, B2
+        lga, nxt = spkv.Backend.decode_batch(A, toks, V)
+        for i in range(len(lens)):
+            B[i].decode(toks[i], lg)
+            if exact:
+                assert same_bits(lga[i], lg), f"step {step} session {i} (ctx {lens[i]})"
+            else:
+                assert rel(lga[i], lg) < FLOAT_TOL and int(lga[i].argmax()) == int(lg.argmax()), \
+                    f"step {step} session {i}: rel {rel(lga[i], lg):.3e}"
+            assert int(nxt[i]) == int(lga[i].argmax())
+            assert A[i].position() == B[i].position()
+        last = toks
+        toks = [int(t) for t in nxt]
+    window = lambda o, layer: o.SW if (o.arch == spkv.ARCH_GEMMA3 and layer % 6 != 5) else 0
+    for i in (len(lens) - 1, 0):
+        pos = A[i].position() - 1                      # the last batched step's position
+        o = oracle_from_device(spm, pmax, exact, A[i], pos, window)
+        ol = o.step(last[i])
+        if exact:
+            assert same_bits(lga[i], ol), f"session {i} vs the oracle"
+        else:
+            assert rel(lga[i], ol) < FLOAT_TOL and int(lga[i].argmax()) == int(ol.argmax())
+        o.close()
+    for x in A + B:
+        x.close()
+    close_all(s, m)
+
+
 def test_decode_batch_errors(tmpdir_models):
     spm, spt = model_files(tmpdir_models, "qwen3-hd128")
     m = spkv.Model(spm, spt); s = spkv.Session(m, 64)

@@ -341,14 +341,51 @@ def test_recall_projection_matrix_matches_reference():
         assert np.array_equal(a, b) and set(np.unique(a)) == {-1, 1}
 
 
+def _sel_geom(B, W, sink, pos):
+    """sp_arm_select's clamps (core/arm/arm.c:110-160): identity?, sinks, candidate end, top-k."""
+    if B <= 0 or pos + 1 <= B:
+        return True, 0, 0, 0
+    W = min(W, pos + 1); sink = min(sink, pos + 1)
+    hi = min(max(pos + 1 - W, sink), pos + 1)
+    return False, sink, hi, min(max(B - W - sink, 0), hi - sink)
+
+
+def _check_selection(ri_a, ma, ri_b, mb, cand_a, B, W, sink, pos):
+    """The oracle's list against the reference's: identical, or -- only when
+    candidates equal to the k-th projected score straddle the cut, where the
+    reference's quickselect keeps whichever its partitions leave in front --
+    the same sinks, window and above-threshold positions, the tied slots filled
+    with the lowest tied positions.  Returns True when the tie rule applied."""
+    assert ma == mb
+    if np.array_equal(ri_a[:ma], ri_b[:mb]):
+        return False
+    ident, sk, hi, topk = _sel_geom(B, W, sink, pos)
+    assert not ident and 0 < topk < hi - sk
+    nc = hi - sk
+    pairs = cand_a[:2 * nc].reshape(nc, 2)
+    score = {int(p): float(v) for v, p in zip(pairs[:, 0].view(np.float32), pairs[:, 1])}
+    th = sorted(score.values(), reverse=True)[topk - 1]
+    above = {p for p, v in score.items() if v > th}
+    tied = sorted(p for p, v in score.items() if v == th)
+    mine, ref = ri_a[sk:sk + topk], ri_b[sk:sk + topk]
+    assert np.array_equal(ri_a[:sk], ri_b[:sk]) and np.array_equal(ri_a[sk + topk:ma], ri_b[sk + topk:mb])
+    assert above <= set(mine.tolist()) and above <= set(ref.tolist())
+    assert set(mine.tolist()) - above == set(tied[:topk - len(above)])
+    assert (set(ref.tolist()) - above) <= set(tied)
+    return True
+
+
 @pytest.mark.parametrize("ties", [False, True])
 def test_recall_selection_matches_reference(ties):
     """orc_arm_select against the reference's sp_arm_select (core/arm/arm.c:
-    110-160): the same positions in the same order, including the
-    quickselect's arrangement when projected scores tie (duplicated sidecar
-    rows), for budgets below and above the context, windows and sinks."""
+    110-160): the same positions in the same order for budgets below and above
+    the context, windows and sinks.  With duplicated sidecar rows (tied
+    projected scores) the lists are identical unless the tie straddles the
+    k-th score; there the oracle (like the device) keeps the lowest tied
+    positions, where the reference keeps its quickselect's arrangement."""
     R = _ref(); L = orc.lib()
     rng = np.random.default_rng(8 + ties)
+    straddled = 0
     for trial in range(40):
         hd, r, nkv = (64, 16, 2) if trial % 2 else (128, 8, 4)
         P_, layer = 300, int(rng.integers(0, 3))
@@ -367,8 +404,38 @@ def test_recall_selection_matches_reference(ties):
         base = flat.ctypes.data + ((layer * P_ * nkv + kvh) * r) * 4
         ma = L.orc_arm_select(P(Rm), r, hd, P(q), ctypes.c_void_p(base), nkv, B, W, sink, pos, P(cand_a), P(ri_a))
         mb = R.sp_arm_select(P(Rm), r, hd, P(q), P(flat), layer, P_, nkv, kvh, B, W, sink, pos, P(cand_b), P(ri_b))
-        assert ma == mb and np.array_equal(ri_a[:ma], ri_b[:mb]), trial
+        straddled += _check_selection(ri_a, ma, ri_b, mb, cand_a, B, W, sink, pos)
         assert pk.shape == (P_, r)
+    if not ties:
+        assert straddled == 0
+
+
+def test_recall_selection_tie_rule_on_zero_scores():
+    """A zero query projects every candidate to the score +0.0 (and a score of
+    -0.0 equals it): the top-k slots take the lowest candidate positions, the
+    sinks and the window stay where they are."""
+    R = _ref(); L = orc.lib()
+    hd, r, nkv, P_ = 64, 16, 2, 200
+    Rm = np.zeros(r * hd, np.int8); L.orc_arm_build_R(P(Rm), r, hd)
+    rng = np.random.default_rng(3)
+    flat = np.ascontiguousarray(rng.standard_normal((1, P_, nkv, r)).astype(np.float32))
+    q = np.zeros(hd, np.float32)
+    for B, W, sink, pos in ((40, 8, 4, 150), (64, 16, 0, 199), (20, 4, 2, 60)):
+        cand_a = np.zeros(2 * P_, np.int32); ri_a = np.zeros(P_, np.int32)
+        cand_b = np.zeros(2 * P_, np.int32); ri_b = np.zeros(P_, np.int32)
+        ma = L.orc_arm_select(P(Rm), r, hd, P(q), P(flat), nkv, B, W, sink, pos, P(cand_a), P(ri_a))
+        mb = R.sp_arm_select(P(Rm), r, hd, P(q), P(flat), 0, P_, nkv, 0, B, W, sink, pos, P(cand_b), P(ri_b))
+        _, sk, hi, topk = _sel_geom(B, W, sink, pos)
+        want = list(range(sk)) + list(range(sk, sk + topk)) + list(range(hi, pos + 1))
+        assert ri_a[:ma].tolist() == want, (B, W, sink, pos)
+        _check_selection(ri_a, ma, ri_b, mb, cand_a, B, W, sink, pos)
+    # -0.0 and +0.0 are one score: a sidecar of negative zeros ties with positive ones
+    z = np.zeros((1, P_, nkv, r), np.float32)
+    z[0, ::2] = -0.0
+    q1 = rng.standard_normal(hd).astype(np.float32)
+    cand_a = np.zeros(2 * P_, np.int32); ri_a = np.zeros(P_, np.int32)
+    ma = L.orc_arm_select(P(Rm), r, hd, P(q1), P(z), nkv, 40, 8, 4, 150, P(cand_a), P(ri_a))
+    assert ri_a[:ma].tolist() == list(range(4)) + list(range(4, 32)) + list(range(143, 151))
 
 
 @pytest.mark.parametrize("cfg", [(0, 64, 4, 16), (16, 8, 2, 16), (24, 4, 3, 8), (12, 4, 0, 32)])
