@@ -51,8 +51,10 @@ KERNEL_NAMES = {
     "embed_rope_argmax": ["kvd::k_embed", "kvd::k_rope_table", "kvd::k_argmax"],
 }
 # committed rocprofv3 --pmc summaries (FETCH_SIZE / WRITE_SIZE per dispatch) of the
-# decode kernels at this model shape, with the 1 GiB calibration copy they hold
-PMC_SUMMARY = os.path.join(ROOT, "profiles", "gemma3-12b_decode_pmc_fetch_write.txt")
+# decode kernels at this model shape and context, with the 1 GiB calibration copy they hold
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "gemma3-12b_32k_decode_pmc_fetch_write.txt")
+# committed rocprofv3 --kernel-trace --stats summary of this workload (kernel durations)
+KERNEL_STATS = os.path.join(ROOT, "profiles", "gemma3-12b_32k_kernel_stats.csv.txt")
 
 
 def pmc_traffic(kernel, path=PMC_SUMMARY):
@@ -73,8 +75,8 @@ def pmc_traffic(kernel, path=PMC_SUMMARY):
             parts = ln.split()
             name = " ".join(parts[:-3])
             mean, mx = float(parts[-2]), float(parts[-1])
-            if "copyBuffer" in name:
-                cal[sec] = mx
+            if "copyBuffer" in name:                  # the 1 GiB copy: the largest copy dispatch
+                cal[sec] = max(cal.get(sec, 0.0), mx)
             if name.startswith("void " + kernel + "(") or name.startswith(kernel + "("):
                 val[sec] = mean
     if len(val) < 2 or len(cal) < 2 or not cal["FETCH_SIZE"] or not cal["WRITE_SIZE"]:
@@ -84,6 +86,31 @@ def pmc_traffic(kernel, path=PMC_SUMMARY):
     w = val["WRITE_SIZE"] * gib_kib / cal["WRITE_SIZE"]
     return {"bytes": (f + w) * 1024.0, "fetch_scale": round(gib_kib / cal["FETCH_SIZE"], 4),
             "write_scale": round(gib_kib / cal["WRITE_SIZE"], 4), "source": os.path.relpath(path, ROOT)}
+
+
+def rocprof_fields(names, launch_bytes, headline):
+    """The dominant kernel's average duration in the committed rocprof summary of
+    this workload (the headline workload only) and the roofline fraction it gives."""
+    us = rocprof_avg_us(names[0]) if headline and len(names) == 1 else None
+    if not us:
+        return {"rocprof_avg_us": None}
+    gbs = launch_bytes / (us * 1e-6) / 1e9
+    return {"rocprof_avg_us": round(us, 3), "rocprof_achieved": round(gbs, 1),
+            "rocprof_frac": round(gbs / PEAK_GBS, 4), "rocprof_source": os.path.relpath(KERNEL_STATS, ROOT)}
+
+
+def rocprof_avg_us(kernel, path=KERNEL_STATS):
+    """Average duration (us) of `kernel` in the committed rocprofv3 kernel-stats
+    summary, or None."""
+    import csv
+    try:
+        rows = [ln for ln in open(path).read().splitlines() if ln and not ln.startswith("#")]
+    except OSError:
+        return None
+    for r in csv.DictReader(rows):
+        if r["Name"].startswith("void " + kernel + "(") or r["Name"].startswith(kernel + "("):
+            return float(r["AverageNs"]) / 1e3
+    return None
 
 
 WORKLOADS = {
@@ -134,6 +161,10 @@ def main():
                     help="ARM recall on the global layers (sp_hipkv_set_recall): budget, window, sinks, projection rows")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="run one device-to-device copy of this many MiB first (HBM counter calibration)")
+    ap.add_argument("--kv-import", action="store_true",
+                    help="build the context by writing synthetic K/V rows (sp_hipkv_write_kv) instead of the "
+                         "prefill: the decode reads the same bytes, and a counter run sees a few dispatches "
+                         "before it instead of the prefill's ~150k")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("CSV", "COUNTER"), default=None,
                     help="summarize a rocprofv3 --pmc counter_collection.csv per kernel and exit")
     args = ap.parse_args()
@@ -188,11 +219,16 @@ def main():
         prompt = splitmix_tokens(ctx, V, seed=1)
         logits = np.zeros(V, np.float32)
         t0 = time.time()
-        chunk = 4096
-        for c0 in range(0, ctx, chunk):
-            rc = sess.prefill(prompt[c0:c0 + chunk], logits)
-            spkv.check(rc, "sp_prefill_chunk")
-            log(f"prefill {c0 + min(chunk, ctx - c0)}/{ctx} ({time.time()-t0:.1f}s)")
+        if args.kv_import:
+            import_kv(be, shape, ctx, exact)
+            log(f"synthetic K/V of {ctx} positions written ({time.time()-t0:.1f}s)")
+            spkv.check(sess.decode(int(prompt[-1]), logits), "sp_decode_step")
+        else:
+            chunk = 4096
+            for c0 in range(0, ctx, chunk):
+                rc = sess.prefill(prompt[c0:c0 + chunk], logits)
+                spkv.check(rc, "sp_prefill_chunk")
+                log(f"prefill {c0 + min(chunk, ctx - c0)}/{ctx} ({time.time()-t0:.1f}s)")
         prefill_s = time.time() - t0
         tok = int(np.argmax(logits))
 
@@ -251,8 +287,10 @@ def main():
         for c in cls:
             log(f"  {c['kernel']:26s} launches {c['launches']:6d} avg {c['avg_us']:8.2f} us  {c['gbs'] or 0:8.1f} GB/s")
 
+        headline = (args.workload == "gemma3-12b-32k" and ctx == 32768 and not recall and exact
+                    and args.kv == "plain")
         cpu = None
-        if not args.no_cpu_baseline:
+        if not args.no_cpu_baseline and not args.kv_import:
             cpu = cpu_baseline(spm, be, info, shape, exact, args.cpu_steps, tok, sess, args.kv == "spinor", recall)
 
         rec = {
@@ -277,6 +315,9 @@ def main():
                          "frac": round(dom["gbs"] / PEAK_GBS, 4),
                          "algorithmic_bytes_per_launch": round(dom_launch_bytes),
                          "avg_launch_us": round(dom["avg_us"], 3),
+                         "timing": "HIP events around every launch of the class on the backend's stream "
+                                   "(the event pair adds about 1.8 us per launch)",
+                         **rocprof_fields(dom_names, dom_launch_bytes, headline),
                          "traffic": round(traffic["bytes"]) if traffic else None,
                          "traffic_source": traffic},
             "kv_read": {"gbs": round(kv_gb / (kv_ms * 1e-3), 1), "frac": round(kv_gb / (kv_ms * 1e-3) / PEAK_GBS, 4),
@@ -287,7 +328,7 @@ def main():
             "step_hbm_frac": round(step_bytes / (wall / args.steps) / 1e9 / PEAK_GBS, 4),
             "device_ms_per_step": round(dev_ms / args.steps, 4),
             "pcie_inclusive_tokens_per_s": round(n_abi / abi_s, 2),
-            "prefill_tokens_per_s": round(ctx / prefill_s, 1),
+            "prefill_tokens_per_s": None if args.kv_import else round(ctx / prefill_s, 1),
             "kernels": cls,
             "cpu_baseline": cpu,
         }
@@ -297,6 +338,36 @@ def main():
     finally:
         if not args.workdir:
             shutil.rmtree(work, ignore_errors=True)
+
+
+def import_kv(be, shape, ctx, exact):
+    """Synthetic K/V for positions [0, ctx - 1) through sp_hipkv_write_kv: every
+    position of the full-attention layers, the last window of the window
+    layers (the positions a decode step reads).  Values: exact mode int32 grid
+    values below 2^17 (|k|, |v| < 2), float mode N(0, 1); one 64-position block
+    of rows reused.  The resident position ends at ctx - 1, so the next decode
+    step is position ctx - 1 as after a ctx-token prefill."""
+    import spkv
+    NL, NKV, HD, SW = shape["n_layers"], shape["n_kv_heads"], shape["head_dim"], shape.get("swa_window", 0)
+    gemma = shape["arch_id"] == spkv.ARCH_GEMMA3
+    rng = np.random.default_rng(5)
+    if exact:
+        blk = rng.integers(-(1 << 17), 1 << 17, size=(2, 64, NKV * HD), dtype=np.int32).view(np.float32)
+    else:
+        blk = rng.standard_normal((2, 64, NKV * HD)).astype(np.float32)
+    n = ctx - 1
+    glob = [l for l in range(NL) if not (gemma and SW > 0 and l % 6 != 5)]      # Gemma-3: L % 6 == 5 is global
+    for p0 in range(0, n, 64):
+        m = min(64, n - p0)
+        for l in glob:
+            be.write_kv(l, p0, blk[0, :m], blk[1, :m])
+    for l in range(NL):
+        if l in glob:
+            continue
+        lo = max(0, n - SW)
+        for p0 in range(lo, n, 64):
+            m = min(64, n - p0)
+            be.write_kv(l, p0, blk[0, :m], blk[1, :m])
 
 
 def run_sessions(args, wl):
@@ -450,17 +521,24 @@ def pmc_summary(path, counter):
     FETCH_SIZE / WRITE_SIZE) from a rocprofv3 --pmc counter_collection.csv."""
     import csv
     from collections import defaultdict
-    agg = defaultdict(lambda: [0, 0.0, 0.0, set()])
-    for r in csv.DictReader(open(path)):
-        if r.get("Counter_Name") != counter:
-            continue
-        a = agg[r["Kernel_Name"]]
+    rows = [r for r in csv.DictReader(open(path)) if r.get("Counter_Name") == counter]
+    grids = defaultdict(set)
+    for r in rows:
+        grids[r["Kernel_Name"]].add(r.get("Grid_Size", ""))
+    agg = defaultdict(lambda: [0, 0.0, 0.0])
+    for r in rows:
+        k = r["Kernel_Name"]
+        # a kernel launched with several grid sizes (the same attention kernel on
+        # window and full-attention layers) is listed per grid size
+        if len(grids[k]) > 1:
+            k = f"{k} [grid {r.get('Grid_Size', '')}]"
+        a = agg[k]
         v = float(r["Counter_Value"])
-        a[0] += 1; a[1] += v; a[2] = max(a[2], v); a[3].add(r.get("Grid_Size", ""))
+        a[0] += 1; a[1] += v; a[2] = max(a[2], v)
     print(f"# {counter} per dispatch (KiB), from {os.path.basename(path)}")
     print(f"{'kernel':100s} {'dispatches':>10s} {'mean':>14s} {'max':>14s}")
-    for k, (n, sm, mx, _) in sorted(agg.items(), key=lambda kv: -kv[1][1]):
-        print(f"{k[:100]:100s} {n:10d} {sm / n:14.1f} {mx:14.1f}")
+    for k, (n, sm, mx) in sorted(agg.items(), key=lambda kv: -kv[1][1]):
+        print(f"{k:100s} {n:10d} {sm / n:14.1f} {mx:14.1f}")
 
 
 def calib_copy(nbytes):

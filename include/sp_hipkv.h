@@ -146,6 +146,15 @@ int  sp_hipkv_decode_batch_times(sp_kvdecode_handle *const *hs, int n, const int
 /* Read K/V of one layer for positions [p0, p0+n) in the reference slab layout
  * ([n][n_kv_heads*head_dim] floats, or int32 grid values in exact mode). */
 int  sp_hipkv_read_kv(const sp_kvdecode_handle *h, int layer, int p0, int n, float *k, float *v);
+/* Write K/V of one layer for positions [p0, p0+n) from the reference slab
+ * layout (the inverse of sp_hipkv_read_kv: [n][n_kv_heads*head_dim] floats, or
+ * int32 grid values in exact mode) and make them resident: p0 <= dpos, and
+ * dpos becomes max(dpos, p0+n), as if those positions had been prefilled.
+ * Pages shared with a fork are copied first.  Plain K/V rows only (not float
+ * mode with the Spinor codec), recall off.  Restores a session's K/V kept on
+ * the host (the oracle's set_kv counterpart); no counterpart in the reference,
+ * whose host KV slab is the session's own memory (core/session/sp_session.c:240-245). */
+int  sp_hipkv_write_kv(sp_kvdecode_handle *h, int layer, int p0, int n, const float *k, const float *v);
 /* Use a captured HIP graph for each step body (1, default) or plain launches (0). */
 int  sp_hipkv_set_graph(sp_kvdecode_handle *h, int on);
 /* Prefill through the batched path (1, default: 128 tokens per pass, int8-MFMA

@@ -1831,6 +1831,55 @@ int sp_hipkv_read_kv(const sp_kvdecode_handle *h, int layer, int p0, int n, floa
     return 0;
 }
 
+int sp_hipkv_write_kv(sp_kvdecode_handle *h, int layer, int p0, int n, const float *k, const float *v) {
+    if (!h || !k || !v || layer < 0 || layer >= h->m->NL || p0 < 0 || n < 0 || p0 > h->dpos || n > h->pmax - p0)
+        return fail("sp_hipkv_write_kv: bad argument (positions must start at or below the resident position "
+                    "and end within pmax)%s");
+    if (kv_row_bytes(h->m, h->mode, h->kvc) != (size_t)h->m->HD * 4)
+        return fail("sp_hipkv_write_kv: the handle stores Spinor code rows (float mode with SP_KV_SPINOR)%s");
+    if (h->rec.B > 0) return fail("sp_hipkv_write_kv: recall is on (the K sidecar is formed by the step itself)%s");
+    if (n == 0) return 0;
+    const DevModel *m = h->m;
+    const int HD = m->HD, NKV = m->NKV, S = h->slots[layer], KVD = NKV * HD;
+    if (ensure_pages(h, p0, p0 + n)) return 1;
+    // each touched page goes through one pinned page image: read back first
+    // when the write covers only part of it, then one copy to the device
+    const size_t RB = (size_t)HD * 4, half = (size_t)NKV * PAGE * RB, img = 2 * half;
+    uint8_t *stage = nullptr;
+    HIPCHK(hipHostMalloc((void **)&stage, img, hipHostMallocDefault), "kv write staging alloc");
+    int rc = 0;
+    for (int lp = p0 / PAGE; lp <= (p0 + n - 1) / PAGE && !rc; lp++) {
+        const int slot = S == h->full_pages ? lp : lp % S;
+        uint8_t *page = (uint8_t *)h->pool->ptr[h->pt[layer][slot]];
+        const int a = std::max(p0, lp * PAGE), b = std::min(p0 + n, (lp + 1) * PAGE);
+        hipError_t e = hipSuccess;
+        if (b - a < PAGE) {
+            e = hipMemcpyAsync(stage, page, img, hipMemcpyDeviceToHost, h->stream);
+            if (e == hipSuccess) e = hipStreamSynchronize(h->stream);
+        }
+        for (int p = a; p < b && e == hipSuccess; p++)
+            for (int hh = 0; hh < NKV; hh++) {
+                const size_t src = (size_t)(p - p0) * KVD + (size_t)hh * HD;
+                const size_t dst = ((size_t)hh * PAGE + (p & (PAGE - 1))) * RB;
+                memcpy(stage + dst, k + src, RB);
+                memcpy(stage + half + dst, v + src, RB);
+            }
+        if (e == hipSuccess) e = hipMemcpyAsync(page, stage, img, hipMemcpyHostToDevice, h->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(h->stream);       // the image is reused by the next page
+        if (e != hipSuccess) {
+            char b_[300];
+            snprintf(b_, sizeof b_, "sp_hipkv_write_kv: page copy: %s", hipGetErrorString(e));
+            sp_set_error(b_);
+            rc = 1;
+        }
+    }
+    hipHostFree(stage);
+    if (rc) return rc;
+    h->dpos = std::max(h->dpos, p0 + n);
+    h->hwm = std::max(h->hwm, h->dpos);
+    return 0;
+}
+
 int sp_hipkv_v_clamps(const sp_kvdecode_handle *h, long long *count) {
     if (!h || !count) return fail("sp_hipkv_v_clamps: null argument%s");
     int c = 0;

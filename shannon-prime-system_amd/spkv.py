@@ -114,6 +114,7 @@ def kv():
         _sig(lib, "sp_hipkv_set_max_rewind", c_int, [c_void_p, c_int])
         _sig(lib, "sp_hipkv_set_graph", c_int, [c_void_p, c_int])
         _sig(lib, "sp_hipkv_set_pool_growth", c_int, [c_void_p, c_int])
+        _sig(lib, "sp_hipkv_write_kv", c_int, [c_void_p, c_int, c_int, c_int, c_void_p, c_void_p])
         _sig(lib, "sp_hipkv_set_batch_prefill", c_int, [c_void_p, c_int])
         _sig(lib, "sp_hipkv_fork", c_int, [c_void_p, ctypes.POINTER(c_void_p)])
         _sig(lib, "sp_hipkv_attach", c_int, [c_void_p, c_int, c_int])
@@ -365,6 +366,12 @@ class Backend:
         v = np.zeros((n, kvd), np.float32)
         check(kv().sp_hipkv_read_kv(self.h, layer, p0, n, ptr(k), ptr(v)), "sp_hipkv_read_kv")
         return k, v
+
+    def write_kv(self, layer, p0, k, v):
+        import numpy as np
+        k = np.ascontiguousarray(k, dtype=np.float32); v = np.ascontiguousarray(v, dtype=np.float32)
+        assert k.shape == v.shape and k.ndim == 2
+        check(kv().sp_hipkv_write_kv(self.h, layer, p0, k.shape[0], ptr(k), ptr(v)), "sp_hipkv_write_kv")
 
     def set_recall(self, B, W=64, sink=4, r=16):
         """ARM recall on the global layers (decode steps route, prefill is dense)."""

@@ -347,6 +347,50 @@ def test_decode_batch_across_chunks(tmpdir_models, name, exact):
     close_all(s, m)
 
 
+@pytest.mark.parametrize("name", ["qwen3-hd128", "gemma3-hd256"])
+@pytest.mark.parametrize("exact", [True, False])
+def test_write_kv_restores_a_session(tmpdir_models, name, exact):
+    """sp_hipkv_write_kv, the inverse of read_kv: the K/V of a prefilled handle,
+    written layer by layer into a fresh handle in uneven pieces, read back
+    identical, the position follows, and the next decode step equals the
+    original handle's bit for bit (same kernels, same K/V) and the oracle's
+    given the same K/V (exact mode bit for bit, float mode within 1e-3).
+    Writes past the resident position are refused."""
+    pmax, n = 512, 300
+    spm, spt = model_files(tmpdir_models, name)
+    m = spkv.Model(spm, spt); s = spkv.Session(m, pmax)
+    qm = spkv.l1().sp_session_qwen3_model(s.h)
+    o = orc.Oracle(spm, pmax, orc.EXACT if exact else orc.FLOAT)
+    kvd = o.NKV * o.HD
+    pr = prompt(n + 1, o.V, seed=17)
+    a = spkv.Backend(qm, pmax, exact=exact)
+    a.prefill(pr[:n])
+    b = spkv.Backend(qm, pmax, exact=exact)
+    with pytest.raises(RuntimeError):
+        b.write_kv(0, 1, *a.read_kv(0, 0, 1, kvd))          # p0 beyond the resident position
+    kv_all = [a.read_kv(layer, 0, n, kvd) for layer in range(o.NL)]
+    for lo, hi in ((0, 37), (37, 200), (200, n)):
+        for layer in range(o.NL):
+            k, v = kv_all[layer]
+            b.write_kv(layer, lo, k[lo:hi], v[lo:hi])
+    assert b.position() == n
+    for layer in range(o.NL):
+        kb, vb = b.read_kv(layer, 0, n, kvd)
+        assert same_bits(kb, kv_all[layer][0]) and same_bits(vb, kv_all[layer][1]), f"layer {layer}"
+        assert o.set_kv(layer, 0, kv_all[layer][0], kv_all[layer][1]) == 0
+    assert o.set_pos(n) == 0
+    la, lb = np.zeros(o.V, np.float32), np.zeros(o.V, np.float32)
+    a.decode(int(pr[n]), la)
+    b.decode(int(pr[n]), lb)
+    ol = o.step(int(pr[n]))
+    assert same_bits(la, lb)
+    if exact:
+        assert same_bits(lb, ol)
+    else:
+        assert rel(lb, ol) < FLOAT_TOL and int(lb.argmax()) == int(ol.argmax())
+    close_all(a, b, o, s, m)
+
+
 def test_decode_batch_errors(tmpdir_models):
     spm, spt = model_files(tmpdir_models, "qwen3-hd128")
     m = spkv.Model(spm, spt); s = spkv.Session(m, 64)
