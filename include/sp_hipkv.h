@@ -97,6 +97,12 @@ int  sp_hipkv_set_kv_codec(sp_kvdecode_handle *h, int codec);
  * not with Spinor code rows in float mode.  Only before the first token
  * (dpos == 0).  Forks inherit it; batched decodes step such handles one by one. */
 int  sp_hipkv_set_recall(sp_kvdecode_handle *h, int B, int W, int sink, int r);
+/* SP_RECALL_KVSEL (core/forward/decode.c:53-63, :600-629, :738-757): route
+ * and select once per kv head with the group-centroid query (the float sum of
+ * the group's rotated q heads, in head order) instead of once per q head; the
+ * group's q heads then attend over that shared set with their own q.  Off by
+ * default (per-q-head selection).  Any time; forks inherit it. */
+int  sp_hipkv_set_recall_kvsel(sp_kvdecode_handle *h, int on);
 /* The recall sidecar of a global layer for positions [p0, p0+n): [n][n_kv_heads][r]
  * floats (the reference's projk rows, include/sp/arm.h:60-67). */
 int  sp_hipkv_read_recall_sidecar(const sp_kvdecode_handle *h, int layer, int p0, int n, float *out);

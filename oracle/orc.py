@@ -65,6 +65,7 @@ def lib():
             ("orc_set_recall", c_int, [c_void_p, c_int, c_int, c_int, c_int]),
             ("orc_recall_sidecar", c_int, [c_void_p, c_int, c_int, c_int, c_void_p]),
             ("orc_set_recall_dense", None, [c_void_p, c_int]),
+            ("orc_set_recall_kvsel", c_int, [c_void_p, c_int]),
             ("orc_recall_sidecar_set", c_int, [c_void_p, c_int, c_int, c_int, c_void_p]),
         ]:
             f = getattr(L, name); f.restype = res; f.argtypes = args
@@ -103,6 +104,8 @@ def ref_lib():
         L.refh_generate_recall.restype = c_int
         L.refh_generate_recall.argtypes = [ctypes.c_char_p, ctypes.c_char_p, c_void_p, c_int, c_int, c_int, c_int,
                                            c_int, c_int, c_int]
+        L.refh_set_kvsel.restype = None
+        L.refh_set_kvsel.argtypes = [c_int]
         L.sp_arm_build_R.restype = None
         L.sp_arm_build_R.argtypes = [c_void_p, c_int, c_int]
         L.sp_arm_select.restype = c_int
@@ -168,6 +171,11 @@ class Oracle:
         if lib().orc_set_recall(self.s, B, W, sink, r):
             raise RuntimeError("orc_set_recall failed")
         self.rec_r = r
+
+    def set_recall_kvsel(self, on):
+        """SP_RECALL_KVSEL: one recall set per kv head from the group-centroid query."""
+        if lib().orc_set_recall_kvsel(self.s, 1 if on else 0):
+            raise RuntimeError("orc_set_recall_kvsel failed")
 
     def set_recall_dense(self, on):
         lib().orc_set_recall_dense(self.s, 1 if on else 0)

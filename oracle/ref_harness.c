@@ -70,6 +70,10 @@ int refh_qwen3_fixture_sha(uint8_t out[32], size_t *len) {
     return 0;
 }
 
+/* SP_RECALL_KVSEL for the recall calls below (0: off, the default) */
+static int g_refh_kvsel = 0;
+void refh_set_kvsel(int on) { g_refh_kvsel = on ? 1 : 0; }
+
 /* The reference's decode-path perplexity (core/forward/decode.c
  * qwen3_ppl_decode) on a Qwen3 .sp-model with the ARM recall knobs
  * SP_RECALL_B / _W / _SINK / _R set for the call (B = 0: recall off); the
@@ -85,6 +89,7 @@ int refh_ppl_recall(const char *spm, const char *spt, const int32_t *toks, int n
     snprintf(b, sizeof b, "%d", W); setenv("SP_RECALL_W", b, 1);
     snprintf(b, sizeof b, "%d", sink); setenv("SP_RECALL_SINK", b, 1);
     snprintf(b, sizeof b, "%d", r); setenv("SP_RECALL_R", b, 1);
+    if (g_refh_kvsel) setenv("SP_RECALL_KVSEL", "1", 1);
     sp_model *m = NULL;
     if (sp_model_load(spm, spt, &m) != SP_OK) return -1;
     struct qwen3_model *qm = sp_model_to_qwen3(m);
@@ -97,7 +102,7 @@ int refh_ppl_recall(const char *spm, const char *spt, const int32_t *toks, int n
         qwen3_free(qm);
     }
     sp_model_unload(m);
-    unsetenv("SP_RECALL_B");
+    unsetenv("SP_RECALL_B"); unsetenv("SP_RECALL_KVSEL");
     return rc;
 }
 
@@ -117,6 +122,7 @@ int refh_generate_recall(const char *spm, const char *spt, int32_t *seq, int n_p
     snprintf(b, sizeof b, "%d", sink); setenv("SP_RECALL_SINK", b, 1);
     snprintf(b, sizeof b, "%d", r); setenv("SP_RECALL_R", b, 1);
     if (decode_only) setenv("SP_RECALL_DECODE_ONLY", "1", 1);
+    if (g_refh_kvsel) setenv("SP_RECALL_KVSEL", "1", 1);
     sp_model *m = NULL;
     if (sp_model_load(spm, spt, &m) != SP_OK) return -1;
     struct qwen3_model *qm = sp_model_to_qwen3(m);
@@ -126,6 +132,6 @@ int refh_generate_recall(const char *spm, const char *spt, int32_t *seq, int n_p
         qwen3_free(qm);
     }
     sp_model_unload(m);
-    unsetenv("SP_RECALL_B"); unsetenv("SP_RECALL_DECODE_ONLY");
+    unsetenv("SP_RECALL_B"); unsetenv("SP_RECALL_DECODE_ONLY"); unsetenv("SP_RECALL_KVSEL");
     return rc;
 }

@@ -759,6 +759,9 @@ struct orc_sess {
      * selection scratch ri / cand [NH][P] */
     int rec_B, rec_W, rec_sink, rec_r;
     int rec_dense;                    /* orc_set_recall_dense: effective budget 0 (identity lists) */
+    int rec_kvsel;                    /* orc_set_recall_kvsel: one selection per kv head (SP_RECALL_KVSEL) */
+    int rec_mm[256];                  /* KVSEL: each kv head's set size this step */
+    float *rec_qg;                    /* KVSEL: the group-centroid query [HD] */
     signed char *rec_R;
     float *projk;
     int *rec_ri;
@@ -790,12 +793,12 @@ void orc_sess_free(orc_sess *s) {
     if (!s) return;
     free(s->kc); free(s->vc); free(s->x); free(s->nx); free(s->q); free(s->kn); free(s->vn);
     free(s->ao); free(s->ap); free(s->gg); free(s->up); free(s->dn); free(s->sc); free(s->pd);
-    free(s->rec_R); free(s->projk); free(s->rec_ri); free(s->rec_cand); free(s);
+    free(s->rec_R); free(s->projk); free(s->rec_ri); free(s->rec_cand); free(s->rec_qg); free(s);
 }
 int orc_set_recall(orc_sess *s, int B, int W, int sink, int r) {
     if (!s || B < 0 || W < 0 || sink < 0 || r < 1 || r > 64) return 1;
-    free(s->rec_R); free(s->projk); free(s->rec_ri); free(s->rec_cand);
-    s->rec_R = NULL; s->projk = NULL; s->rec_ri = NULL; s->rec_cand = NULL;
+    free(s->rec_R); free(s->projk); free(s->rec_ri); free(s->rec_cand); free(s->rec_qg);
+    s->rec_R = NULL; s->projk = NULL; s->rec_ri = NULL; s->rec_cand = NULL; s->rec_qg = NULL;
     s->rec_B = B; s->rec_W = W; s->rec_sink = sink; s->rec_r = r;
     if (!B) return 0;
     const orc_model *m = s->m;
@@ -803,11 +806,36 @@ int orc_set_recall(orc_sess *s, int B, int W, int sink, int r) {
     s->projk = (float *)calloc((size_t)m->NL * s->P * m->NKV * r, sizeof(float));
     s->rec_ri = (int *)malloc((size_t)m->NH * s->P * sizeof(int));
     s->rec_cand = malloc((size_t)m->NH * s->P * sizeof(orc_sidx));
-    if (!s->rec_R || !s->projk || !s->rec_ri || !s->rec_cand) return 1;
+    s->rec_qg = (float *)malloc((size_t)m->HD * sizeof(float));
+    if (!s->rec_R || !s->projk || !s->rec_ri || !s->rec_cand || !s->rec_qg) return 1;
     orc_arm_build_R(s->rec_R, r, (int)m->HD);
     return 0;
 }
 void orc_set_recall_dense(orc_sess *s, int on) { s->rec_dense = on ? 1 : 0; }
+/* SP_RECALL_KVSEL (core/forward/decode.c:53-63, :600-629, :738-757): the
+ * group leader selects once per kv head with the group-centroid query
+ * qg = ((0 + q_0) + q_1) + ... (float, in head order) and every q head of the
+ * group attends over that shared set with its own q. */
+int orc_set_recall_kvsel(orc_sess *s, int on) {
+    if (on && s->m->NKV > 256) return 1;
+    s->rec_kvsel = on ? 1 : 0;
+    return 0;
+}
+/* the KVSEL lists of one layer at pos: list kvh at rec_ri + kvh * P */
+static void kvsel_select(orc_sess *s, int L, const float *q, int pos, float *qg) {
+    const orc_model *m = s->m;
+    const int HD = (int)m->HD, NKV = (int)m->NKV, group = (int)(m->NH / m->NKV), P = s->P;
+    for (int kvh = 0; kvh < NKV; kvh++) {
+        for (int i = 0; i < HD; i++) qg[i] = 0.0f;
+        for (int g2 = 0; g2 < group; g2++) {
+            const float *qx = q + (size_t)(kvh * group + g2) * HD;
+            for (int i = 0; i < HD; i++) qg[i] += qx[i];
+        }
+        s->rec_mm[kvh] = orc_arm_select(s->rec_R, s->rec_r, HD, qg, s->projk + ((size_t)L * P * NKV + kvh) * s->rec_r,
+                                        NKV, s->rec_dense ? 0 : s->rec_B, s->rec_W, s->rec_sink, pos,
+                                        (orc_sidx *)s->rec_cand + (size_t)kvh * P, s->rec_ri + (size_t)kvh * P);
+    }
+}
 int orc_recall_sidecar_set(orc_sess *s, int layer, int p0, int n, const float *in) {
     if (!s || !s->projk || layer < 0 || layer >= (int)s->m->NL || p0 < 0 || n < 0 || p0 + n > s->P) return 1;
     const size_t row = (size_t)s->m->NKV * s->rec_r;
@@ -843,6 +871,7 @@ orc_sess *orc_clone(const orc_sess *s) {
         memcpy(c->projk, s->projk, (size_t)s->m->NL * s->P * s->m->NKV * s->rec_r * sizeof(float));
     }
     c->rec_dense = s->rec_dense;
+    c->rec_kvsel = s->rec_kvsel;
     return c;
 }
 int orc_kv_get(const orc_sess *s, int layer, int p0, int n, float *k, float *v) {
@@ -969,11 +998,14 @@ static int step_any(orc_sess *s, int32_t tok, int pos, float *logits) {
                     for (int i = h * HD; i < (h + 1) * HD; i++) { kd[i] = (int32_t)rintf(kn[i] * 65536.0f); vd[i] = vq_of(vn[i], &cl); }
                     s->vclamp += cl;
                 }
+            const int kvsel = s->rec_B > 0 && win < 0 && s->rec_kvsel;
+            if (kvsel) kvsel_select(s, L, q, pos, s->rec_qg);
             #pragma omp parallel for schedule(static, 1) num_threads(g_threads) if (g_threads > 1 && pos >= 256)
             for (int h = 0; h < NH; h++) {
                 if (s->rec_B > 0 && win < 0) {           /* recall: the head's selected positions */
-                    int *ri = s->rec_ri + (size_t)h * P;
-                    const int mm = orc_arm_select(s->rec_R, s->rec_r, HD, q + (size_t)h * HD,
+                    int *ri = s->rec_ri + (size_t)(kvsel ? h / group : h) * P;
+                    const int mm = kvsel ? s->rec_mm[h / group]
+                                         : orc_arm_select(s->rec_R, s->rec_r, HD, q + (size_t)h * HD,
                                                   s->projk + ((size_t)L * P * NKV + h / group) * s->rec_r, NKV,
                                                   s->rec_dense ? 0 : s->rec_B, s->rec_W, s->rec_sink, pos,
                                                   (orc_sidx *)s->rec_cand + (size_t)h * P, ri);
@@ -989,11 +1021,14 @@ static int step_any(orc_sess *s, int32_t tok, int pos, float *logits) {
                 memcpy(kcl + (size_t)pos * KVD, kn, (size_t)KVD * sizeof(float));
                 memcpy(vcl + (size_t)pos * KVD, vn, (size_t)KVD * sizeof(float));
             }
+            const int kvsel = s->rec_B > 0 && win < 0 && s->rec_kvsel;
+            if (kvsel) kvsel_select(s, L, q, pos, s->rec_qg);
             #pragma omp parallel for schedule(static, 1) num_threads(g_threads) if (g_threads > 1 && pos >= 256)
             for (int h = 0; h < NH; h++) {
                 if (s->rec_B > 0 && win < 0) {           /* recall: decode.c:740-790 */
-                    int *ri = s->rec_ri + (size_t)h * P;
-                    const int mm = orc_arm_select(s->rec_R, s->rec_r, HD, q + (size_t)h * HD,
+                    int *ri = s->rec_ri + (size_t)(kvsel ? h / group : h) * P;
+                    const int mm = kvsel ? s->rec_mm[h / group]
+                                         : orc_arm_select(s->rec_R, s->rec_r, HD, q + (size_t)h * HD,
                                                   s->projk + ((size_t)L * P * NKV + h / group) * s->rec_r, NKV,
                                                   s->rec_dense ? 0 : s->rec_B, s->rec_W, s->rec_sink, pos,
                                                   (orc_sidx *)s->rec_cand + (size_t)h * P, ri);

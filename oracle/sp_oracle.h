@@ -109,6 +109,7 @@ int   orc_set_recall(orc_sess *s, int B, int W, int sink, int r);
  * the effective budget is 0, so each q head attends every position through the
  * identity list) while on; the sidecar is still written.  Off by default. */
 void  orc_set_recall_dense(orc_sess *s, int on);
+int   orc_set_recall_kvsel(orc_sess *s, int on);     /* SP_RECALL_KVSEL */
 /* sidecar rows [p0, p0+n) of a layer: NKV*r floats per position */
 int   orc_recall_sidecar(const orc_sess *s, int layer, int p0, int n, float *out);
 /* overwrite sidecar rows [p0, p0+n) of a layer (a state loaded from elsewhere) */

@@ -409,6 +409,7 @@ struct sp_kvdecode_handle {
     int use_batch = 1;                       // batched (MFMA) prefill where the shapes allow it
     int max_rewind = 0;                      // 0: full tables for window layers
     int pool_growth = 0;                     // pages per pool growth (0: ~1 GiB)
+    int recall_kvsel = 0;                    // SP_RECALL_KVSEL: one recall selection per kv head
     int full_pages = 0, ring_pages = 0;
     std::vector<std::vector<int>> pt;        // [NL][slots] page ids (-1 = unmapped)
     std::vector<int> slots;                  // per layer: number of slots
@@ -822,6 +823,7 @@ RecallArgs recall_args(const sp_kvdecode_handle *h, float *const *pages, VecStat
     rc.score_blocks = std::min(RECALL_SCORE_BLOCKS, (h->pmax + 255) / 256);
     rc.NH = m->NH; rc.NKV = m->NKV; rc.HD = m->HD; rc.r = R.r; rc.B = R.B; rc.W = R.W; rc.sink = R.sink;
     rc.mode = h->mode; rc.ascale = 1.0f / sqrtf((float)m->HD);
+    rc.Rb = R.Rb; rc.kvsel = h->recall_kvsel;
     return rc;
 }
 
@@ -1234,6 +1236,7 @@ int sp_hipkv_open(const void *qm_opaque, int pmax, sp_kvdecode_handle **out) {
         set_handle_mode(sh, FLOAT);
         if (sh->kvc != KVC_PLAIN) { sh->kvc = KVC_PLAIN; free_graphs(sh); }   // graphs bake in the codec
         sh->use_graph = 1; sh->use_batch = 1; sh->dpos = 0; sh->hwm = 0; sh->pool_growth = 0;
+        if (sh->recall_kvsel) { sh->recall_kvsel = 0; free_graphs(sh); }
         if (sh->rec.B) { free_recall(sh); free_graphs(sh); }
         sh->pool = new_pool();
         if (hipMemsetAsync(sh->vclamp, 0, sizeof(int), sh->stream) != hipSuccess) {
@@ -1605,6 +1608,15 @@ int sp_hipkv_set_recall(sp_kvdecode_handle *h, int B, int W, int sink, int r) {
     return repage(h, "sp_hipkv_set_recall");
 }
 
+int sp_hipkv_set_recall_kvsel(sp_kvdecode_handle *h, int on) {
+    if (!h) return fail("sp_hipkv_set_recall_kvsel: null handle%s");
+    if ((on ? 1 : 0) == h->recall_kvsel) return 0;
+    if (on && h->m->HD > 256) return fail("sp_hipkv_set_recall_kvsel: head_dim above 256%s");
+    h->recall_kvsel = on ? 1 : 0;
+    free_graphs(h);                          // the captured steps bake the router's arguments
+    return 0;
+}
+
 int sp_hipkv_read_recall_sidecar(const sp_kvdecode_handle *h, int layer, int p0, int n, float *out) {
     if (!h || !out || layer < 0 || layer >= h->m->NL || p0 < 0 || n < 0 || p0 + n > h->dpos)
         return fail("sp_hipkv_read_recall_sidecar: bad argument%s");
@@ -1662,6 +1674,7 @@ int sp_hipkv_fork(const sp_kvdecode_handle *p, sp_kvdecode_handle **out) {
         sp_hipkv_close(h.release()); return fail("sp_hipkv_fork: clamp counter reset failed%s");
     }
     h->use_batch = p->use_batch; h->use_graph = p->use_graph; h->pool_growth = p->pool_growth;
+    if (h->recall_kvsel != p->recall_kvsel) { h->recall_kvsel = p->recall_kvsel; free_graphs(h.get()); }
     hipStreamSynchronize(p->stream);
     // share every mapped page (copy-on-write on the next append into it)
     {

@@ -132,6 +132,8 @@ struct RecallArgs {
     int kstride, lstride, mchunks, score_blocks;   // kstride: a multiple of 4, >= pmax
     int NH, NKV, HD, r, B, W, sink, mode;
     float ascale;
+    const uint32_t *Rb;      // KVSEL: the projection's sign bits [r][HD/32]
+    int kvsel;               // SP_RECALL_KVSEL: one selection per kv head from the group-centroid query
 };
 void launch_recall_attention(const RecallArgs &rc, hipStream_t s);
 // exact-mode attention of one session's batched prefill on global layers

@@ -70,14 +70,36 @@ __device__ __forceinline__ SelGeom sel_geom(const RecallArgs &rc, int pos) {
 // One thread per candidate position: its sidecar row (r floats, contiguous in
 // the page) is read once for all G q heads of the kv head; each head's score
 // sum_p pq[p] * side[p] is sequential in p with separate multiply and add.
+// With KVSEL (SP_RECALL_KVSEL, core/forward/decode.c:738-757) the kv head
+// scores once, with the projection of its group-centroid query
+// qg = ((0 + q_0) + q_1) + ... (float, in head order), formed here from the
+// rotated q heads; its keys go to the group leader's row (kvh * G).
 template <int RT>
 __global__ __launch_bounds__(256) void k_recall_score(RecallArgs rc) {
-    const int pos = rc.st->pos, kvh = blockIdx.y, G = rc.NH / rc.NKV;
+    const int pos = rc.st->pos, kvh = blockIdx.y, G0 = rc.NH / rc.NKV;
     const SelGeom g = sel_geom(rc, pos);
     if (g.ident || g.topk == 0) return;
     const int r = RT ? RT : rc.r, HD = rc.HD;
+    const int G = rc.kvsel ? 1 : G0;                     // heads scored here
     __shared__ float pq[RECALL_MAX_GROUP * 64];
-    for (int i = threadIdx.x; i < G * r; i += 256) pq[i] = rc.pq[(size_t)kvh * G * r + i];
+    if (rc.kvsel) {
+        __shared__ float qg[256];
+        for (int i = threadIdx.x; i < HD; i += 256) {
+            float a = 0.0f;
+            for (int gh = 0; gh < G0; gh++) a = __fadd_rn(a, rc.qr[(size_t)(kvh * G0 + gh) * HD + i]);
+            qg[i] = a;
+        }
+        __syncthreads();
+        if ((int)threadIdx.x < r) {                      // sequential +-1 sum over d, as the sidecar's
+            const int p = threadIdx.x, NW = HD / 32;
+            float a = 0.0f;
+            for (int d = 0; d < HD; d++)
+                a = __fadd_rn(a, ((rc.Rb[(size_t)p * NW + (d >> 5)] >> (d & 31)) & 1u) ? qg[d] : -qg[d]);
+            pq[p] = a;
+        }
+    } else {
+        for (int i = threadIdx.x; i < G * r; i += 256) pq[i] = rc.pq[(size_t)kvh * G * r + i];
+    }
     __syncthreads();
     for (int s = g.sink + blockIdx.x * 256 + threadIdx.x; s < g.cand_hi; s += gridDim.x * 256) {
         const float *side = rc_page(rc, s) + (size_t)2 * rc.NKV * PAGE * HD + ((size_t)kvh * PAGE + (s & (PAGE - 1))) * r;
@@ -97,7 +119,7 @@ __global__ __launch_bounds__(256) void k_recall_score(RecallArgs rc) {
             } else {
                 for (int p = 0; p < r; p++) a = __fadd_rn(a, __fmul_rn(pq[gh * r + p], gmem(side)[p]));
             }
-            rc.keys[(size_t)(kvh * G + gh) * rc.kstride + s] = order_key(a);
+            rc.keys[(size_t)(kvh * G0 + gh) * rc.kstride + s] = order_key(a);
         }
     }
 }
@@ -181,6 +203,7 @@ __global__ __launch_bounds__(SEL_T) void k_recall_select(RecallArgs rc) {
     const SelGeom g = sel_geom(rc, pos);
     int *list = rc.lists + (size_t)h * rc.lstride;
     if (tid == 0) rc.counts[h] = g.m;
+    if (rc.kvsel && h % (rc.NH / rc.NKV)) return;       // KVSEL: the group leader's list serves the group
     if (g.ident) {
         for (int s = tid; s <= pos; s += SEL_T) list[s] = s;
         return;
@@ -352,6 +375,11 @@ __global__ __launch_bounds__(SEL_T) void k_recall_select(RecallArgs rc) {
     }
 }
 
+// the row of rc.lists that q head h attends over (KVSEL: its group leader's)
+__device__ __forceinline__ int list_row(const RecallArgs &rc, int h) {
+    return rc.kvsel ? h - h % (rc.NH / rc.NKV) : h;
+}
+
 // ---- attention pass 1: scores of a chunk of the list + the chunk maximum
 // (grid: mchunks x NH).  Row-quad layout: a wave scores 16 list entries at a
 // time, lane = 4 * entry + quarter, a quarter reads 16 B at byte 64 i + 16
@@ -381,7 +409,7 @@ __global__ __launch_bounds__(256) void k_recall_scores(RecallArgs rc) {
     int64_t ai = 0;
     float af = 0.0f;
     if (live) {
-        const int s = rc.lists[(size_t)h * rc.lstride + j];
+        const int s = rc.lists[(size_t)list_row(rc, h) * rc.lstride + j];
         const int32_t *row = rc_row(rc, kvh, s, 0) + 4 * k4;
         #pragma unroll
         for (int i = 0; i < 4 * EPL; i++) {
@@ -468,7 +496,7 @@ __global__ __launch_bounds__(256) void k_recall_vsum_exact(RecallArgs rc) {
         cm = lane < nact ? x : INT32_MIN;
     }
     const int jl = jw + lane < m ? jw + lane : m - 1;
-    const int s_l = rc.lists[(size_t)h * rc.lstride + jl], z_l = rc.zs[(size_t)h * rc.lstride + jl];
+    const int s_l = rc.lists[(size_t)list_row(rc, h) * rc.lstride + jl], z_l = rc.zs[(size_t)h * rc.lstride + jl];
     int32_t v[16][EPL];
     #pragma unroll
     for (int u = 0; u < 16; u++) rc_vrow<EPL>(rc, kvh, __builtin_amdgcn_readlane(s_l, u), lane, v[u]);
@@ -553,7 +581,7 @@ __global__ __launch_bounds__(256) void k_recall_vsum_float(RecallArgs rc) {
         cm = lane < nact ? x : -INFINITY;
     }
     const int jl = jw + lane < m ? jw + lane : m - 1;
-    const int s_l = rc.lists[(size_t)h * rc.lstride + jl];
+    const int s_l = rc.lists[(size_t)list_row(rc, h) * rc.lstride + jl];
     const float z_l = __int_as_float(rc.zs[(size_t)h * rc.lstride + jl]);
     int32_t v[16][EPL];
     #pragma unroll
@@ -628,7 +656,7 @@ void launch_recall_attention(const RecallArgs &rc, hipStream_t s) {
     // multiple of 4 for the select's 16-byte loads)
     if (rc.r < 1 || rc.r > 64 || rc.NH < 1 || rc.NKV < 1 || rc.NH % rc.NKV || rc.NH / rc.NKV > RECALL_MAX_GROUP ||
         rc.mchunks < 1 || !rc.stat_out || !rc.pq || rc.mchunks * RECALL_CHUNK < rc.lstride || rc.score_blocks < 1 ||
-        rc.kstride < 4 || rc.kstride % 4)
+        rc.kstride < 4 || rc.kstride % 4 || (rc.kvsel && (!rc.Rb || !rc.qr || rc.HD > 256)))
         return launch_fail("recall attention: arguments outside the kernels' limits");
     if (rc.HD != 64 && rc.HD != 128 && rc.HD != 256)
         return launch_fail("recall attention serves head_dim 64, 128 and 256");

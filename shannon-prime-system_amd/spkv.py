@@ -114,6 +114,7 @@ def kv():
         _sig(lib, "sp_hipkv_set_max_rewind", c_int, [c_void_p, c_int])
         _sig(lib, "sp_hipkv_set_graph", c_int, [c_void_p, c_int])
         _sig(lib, "sp_hipkv_set_pool_growth", c_int, [c_void_p, c_int])
+        _sig(lib, "sp_hipkv_set_recall_kvsel", c_int, [c_void_p, c_int])
         _sig(lib, "sp_hipkv_write_kv", c_int, [c_void_p, c_int, c_int, c_int, c_void_p, c_void_p])
         _sig(lib, "sp_hipkv_set_batch_prefill", c_int, [c_void_p, c_int])
         _sig(lib, "sp_hipkv_fork", c_int, [c_void_p, ctypes.POINTER(c_void_p)])
@@ -376,6 +377,10 @@ class Backend:
     def set_recall(self, B, W=64, sink=4, r=16):
         """ARM recall on the global layers (decode steps route, prefill is dense)."""
         check(kv().sp_hipkv_set_recall(self.h, B, W, sink, r), "sp_hipkv_set_recall")
+
+    def set_recall_kvsel(self, on):
+        """SP_RECALL_KVSEL: one recall set per kv head (group-centroid query)."""
+        check(kv().sp_hipkv_set_recall_kvsel(self.h, 1 if on else 0), "sp_hipkv_set_recall_kvsel")
 
     def recall_sidecar(self, layer, p0, n, nkv, r):
         import numpy as np

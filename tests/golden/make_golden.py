@@ -16,7 +16,8 @@ core/session/sp_session.c sp_prefill_chunk :154-212 + sp_decode_step :725-770):
     (one Qwen3-0.6B layer, vocab 151936, 512-token prompt, 64 decode steps).
 Recall: the reference's decode-path perplexity (core/forward/decode.c
 qwen3_ppl_decode, through oracle/ref_harness.c refh_ppl_recall) with the ARM
-recall knobs SP_RECALL_B/W/SINK/R, as the exact double (hex).
+recall knobs SP_RECALL_B/W/SINK/R, as the exact double (hex), also with
+SP_RECALL_KVSEL=1 (recall_kvsel).
 Recall generation: the reference's greedy decode (qwen3_generate_kv through
 oracle/ref_harness.c refh_generate_recall) with the recall knobs, with and
 without SP_RECALL_DECODE_ONLY=1 (dense prompt, router at the generated
@@ -137,6 +138,33 @@ def main():
                 out["recall_generate"].append({
                     "model": name, "max_context": 64, "n_prompt": n_prompt, "prompt_seed": 1, "B": B, "W": W,
                     "sink": sink, "r": r, "decode_only": dec_only, "generated": [int(t) for t in seq[n_prompt:]]})
+
+    # SP_RECALL_KVSEL (one selection per kv head, group-centroid query)
+    out["recall_kvsel"] = []
+    out["recall_generate_kvsel"] = []
+    R.refh_set_kvsel(1)
+    with tempfile.TemporaryDirectory() as d:
+        for name in ("qwen3-tiny", "qwen3-g4"):
+            spm, spt = model(d, name, 64)
+            V = int(SMALL[name]["vocab"])
+            toks = spkv.splitmix_tokens(48, V, seed=1)
+            for B, W, sink, r in RECALL[1:]:
+                ppl = ctypes.c_double()
+                if R.refh_ppl_recall(spm.encode(), spt.encode(), P(toks), len(toks), 4, B, W, sink, r, ctypes.byref(ppl)):
+                    sys.exit(f"reference KVSEL recall decode failed for {name}")
+                out["recall_kvsel"].append({"model": name, "max_context": 64, "n": 48, "n_warm": 4, "prompt_seed": 1,
+                                            "B": B, "W": W, "sink": sink, "r": r, "ppl_hex": ppl.value.hex()})
+            for B, W, sink, r, dec_only in RECALL_GEN[1:]:
+                n_prompt, n_gen = 24, 32
+                seq = np.zeros(n_prompt + n_gen, np.int32)
+                seq[:n_prompt] = spkv.splitmix_tokens(n_prompt, V, seed=1)
+                if R.refh_generate_recall(spm.encode(), spt.encode(), P(seq), n_prompt, n_gen, B, W, sink, r,
+                                          dec_only) != n_prompt + n_gen:
+                    sys.exit(f"reference KVSEL recall generation failed for {name}")
+                out["recall_generate_kvsel"].append({
+                    "model": name, "max_context": 64, "n_prompt": n_prompt, "prompt_seed": 1, "B": B, "W": W,
+                    "sink": sink, "r": r, "decode_only": dec_only, "generated": [int(t) for t in seq[n_prompt:]]})
+    R.refh_set_kvsel(0)
 
     x, w, z, g = island_inputs()
     a = np.zeros_like(x); R.sp_rmsnorm_exact(P(x), P(w), x.size, P(a))

@@ -130,6 +130,52 @@ def test_oracle_recall_generation_matches_reference_golden(tmpdir_models, case):
     o.close()
 
 
+@pytest.mark.parametrize("case", GOLDEN["recall_kvsel"],
+                         ids=lambda c: f'{c["model"]}-B{c["B"]}-W{c["W"]}-s{c["sink"]}-r{c["r"]}')
+def test_oracle_recall_kvsel_decode_matches_reference_golden(tmpdir_models, case):
+    """SP_RECALL_KVSEL: one selection per kv head from the group-centroid query
+    (core/forward/decode.c:53-63, :738-757); the reference's perplexity as the
+    exact double."""
+    c = dict(case, seed=0, flags=0)
+    spm, _ = _files(tmpdir_models, c)
+    o = orc.Oracle(spm, case["max_context"])
+    o.set_recall(case["B"], case["W"], case["sink"], case["r"])
+    o.set_recall_kvsel(True)
+    toks = spkv.splitmix_tokens(case["n"], o.V, seed=case["prompt_seed"])
+    assert oracle_ppl(o, toks, case["n_warm"]).hex() == case["ppl_hex"]
+    o.close()
+
+
+@pytest.mark.parametrize("case", GOLDEN["recall_generate_kvsel"],
+                         ids=lambda c: f'{c["model"]}-B{c["B"]}-W{c["W"]}-s{c["sink"]}-r{c["r"]}-d{c["decode_only"]}')
+def test_oracle_recall_kvsel_generation_matches_reference_golden(tmpdir_models, case):
+    c = dict(case, seed=0, flags=0)
+    spm, _ = _files(tmpdir_models, c)
+    o = orc.Oracle(spm, case["max_context"])
+    o.set_recall(case["B"], case["W"], case["sink"], case["r"])
+    o.set_recall_kvsel(True)
+    o.set_recall_dense(case["decode_only"])
+    pr = spkv.splitmix_tokens(case["n_prompt"], o.V, seed=case["prompt_seed"])
+    for t in pr:
+        lg = o.step(int(t))
+    o.set_recall_dense(0)
+    out = []
+    for k in range(len(case["generated"])):
+        out.append(int(lg.argmax()))
+        if k + 1 < len(case["generated"]):
+            lg = o.step(out[-1])
+    assert out == case["generated"]
+    o.close()
+
+
+def test_kvsel_goldens_differ_from_per_head_selection():
+    """KVSEL changes the recalled sets: its perplexities differ from the
+    per-q-head selection's for every case."""
+    per_head = {(c["model"], c["B"], c["W"], c["sink"], c["r"]): c["ppl_hex"] for c in GOLDEN["recall"]}
+    for c in GOLDEN["recall_kvsel"]:
+        assert c["ppl_hex"] != per_head[(c["model"], c["B"], c["W"], c["sink"], c["r"])], c
+
+
 def test_recall_generation_goldens_see_the_router():
     plain = {c["model"]: c["generated"] for c in GOLDEN["recall_generate"] if c["B"] == 0}
     for c in GOLDEN["recall_generate"]:

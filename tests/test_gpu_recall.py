@@ -133,6 +133,53 @@ def test_recall_exact_bitexact(tmpdir_models, name, rec, n_pre, n_gen):
     p.close()
 
 
+KVSEL_CASES = [
+    ("qwen3-tiny", (48, 16, 4, 16), 150, 30, True),
+    ("qwen3-g4", (40, 12, 3, 8), 170, 30, True),        # GQA 4: one selection serves four q heads
+    ("gemma3-hd256", (64, 16, 4, 32), 180, 30, True),
+    ("qwen3-hd128", (100, 8, 0, 64), 180, 20, True),
+    ("qwen3-g4", (40, 12, 3, 8), 170, 20, False),
+]
+
+
+@pytest.mark.parametrize("name,rec,n_pre,n_gen,exact", KVSEL_CASES,
+                         ids=[f"{c[0]}-B{c[1][0]}-{'exact' if c[4] else 'float'}" for c in KVSEL_CASES])
+def test_recall_kvsel(tmpdir_models, name, rec, n_pre, n_gen, exact):
+    """SP_RECALL_KVSEL on the device (sp_hipkv_set_recall_kvsel) against the
+    oracle's KVSEL decode, which reproduces the compiled reference's KVSEL
+    perplexities and greedy sequences (committed goldens): exact mode bit for
+    bit, float mode within 1e-3; a fork inherits the setting; the shared sets
+    change the logits against per-q-head selection."""
+    spm, spt = model_files(tmpdir_models, name, 256)
+    p = Pair(spm, spt, exact, 256, rec)
+    p.be.set_recall_kvsel(True)
+    p.o.set_recall_kvsel(True)
+    per_head = orc.Oracle(spm, 256, orc.EXACT if exact else orc.FLOAT)   # the same steps, per-q-head sets
+    per_head.set_recall(*rec)
+    pr = prompt(n_pre + 1, p.V, seed=3)
+    p.prefill(pr[:-1])
+    per_head.set_recall_dense(1)
+    for t in pr[:-1]:
+        per_head.step(int(t), False)
+    per_head.set_recall_dense(0)
+    g, c = p.step(pr[-1])
+    check_step(g, c, exact, "first routed step")
+    t = int(pr[-1])
+    differs = not same_bits(c, per_head.step(t))
+    for k in range(n_gen):
+        t = int(c.argmax())
+        if k == n_gen // 2:                                 # continue on a fork
+            f = p.be.fork(); p.be.close(); p.be = f
+        g, c = p.step(t)
+        check_step(g, c, exact, f"step {k}")
+        differs |= not same_bits(c, per_head.step(t))
+    assert differs, "KVSEL changed no logits: the case does not exercise the shared selection"
+    if exact:
+        check_resident(p, p.be.position())
+    per_head.close()
+    p.close()
+
+
 def test_recall_float_within_tolerance(tmpdir_models):
     spm, spt = model_files(tmpdir_models, "qwen3-hd128", 256)
     p = Pair(spm, spt, False, 256, (64, 16, 4, 16))
