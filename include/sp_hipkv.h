@@ -103,6 +103,22 @@ int  sp_hipkv_set_recall(sp_kvdecode_handle *h, int B, int W, int sink, int r);
  * group's q heads then attend over that shared set with their own q.  Off by
  * default (per-q-head selection).  Any time; forks inherit it. */
 int  sp_hipkv_set_recall_kvsel(sp_kvdecode_handle *h, int on);
+/* Ring-2 (SP_RING2 with the SP_RECALL_FUSE boundary, core/forward/decode.c:
+ * 117-131, 233-237, 408-440, 518-556; include/sp/arm.h:196-256): with recall
+ * on, before each decode step (and each device greedy run) the full-context
+ * layers' pages that hold neither a sink position nor a position of the recall
+ * window move to pinned host memory (the Ring-2 store), so HBM keeps the
+ * Ring-1 set (sinks + W-window, by 64-position page) plus the page being
+ * written; the recalled rows of spilled pages are read over the bus, the same
+ * bytes, so results are bit-identical to recall without Ring-2.  A page written
+ * again after a rewind comes back to HBM first.  Pages shared with a fork stay
+ * in HBM.  Spilled pages return to the pool's free list (later positions reuse
+ * them), so a long session's HBM footprint stops growing with its context.
+ * Any time; forks inherit it.  No effect while recall is off. */
+int  sp_hipkv_set_ring2(sp_kvdecode_handle *h, int on);
+/* This handle's page-table entries in host memory and in HBM, and the pool's
+ * spills and fetch-backs so far. */
+int  sp_hipkv_ring2_stats(const sp_kvdecode_handle *h, long long out[4]);
 /* The recall sidecar of a global layer for positions [p0, p0+n): [n][n_kv_heads][r]
  * floats (the reference's projk rows, include/sp/arm.h:60-67). */
 int  sp_hipkv_read_recall_sidecar(const sp_kvdecode_handle *h, int layer, int p0, int n, float *out);

@@ -354,6 +354,13 @@ void model_put(DevModel *m) {
 }
 
 // ------------------------------------------------------------ KV page pool
+// Device pages have ids >= 0.  With Ring-2 (sp_hipkv_set_ring2) a page that
+// left the attention window moves to pinned host memory: a host page, named in
+// the page tables by id HOST_ID(hid) <= -2 (-1 is an unmapped slot).  Device
+// and host pages are both refcounted (forks share them).
+constexpr int NO_PAGE = -1;
+constexpr int HOST_ID(int hid) { return -2 - hid; }
+constexpr int HID_OF(int id) { return -2 - id; }
 struct KvPool {
     std::mutex mu;                            // shared by a handle and its forks
     size_t page_bytes = 0;
@@ -361,7 +368,42 @@ struct KvPool {
     std::vector<float *> ptr;
     std::vector<int> refc, free_ids;
     int pages_per_chunk = 0;
-    ~KvPool() { for (void *c : chunks) hipFree(c); }
+    // host pages (Ring-2): pinned chunks, device-visible pointers
+    std::vector<void *> hchunks;
+    std::vector<float *> hptr;
+    std::vector<int> hrefc, hfree;
+    long long spills = 0, fetches = 0;
+    ~KvPool() {
+        for (void *c : chunks) hipFree(c);
+        for (void *c : hchunks) hipHostFree(c);
+    }
+    float *page_ptr(int id) const { return id >= 0 ? ptr[id] : (id <= -2 ? hptr[HID_OF(id)] : nullptr); }
+    void retain(int id) { if (id >= 0) refc[id]++; else if (id <= -2) hrefc[HID_OF(id)]++; }
+    void release(int id) {
+        if (id >= 0) unref(id);
+        else if (id <= -2 && --hrefc[HID_OF(id)] == 0) hfree.push_back(HID_OF(id));
+    }
+    int refcount(int id) const { return id >= 0 ? refc[id] : (id <= -2 ? hrefc[HID_OF(id)] : 0); }
+    // one host page (growing the host store by about 256 MiB), or -1
+    int host_alloc() {
+        if (hfree.empty()) {
+            const int n = (int)std::max<size_t>(4, ((size_t)256 << 20) / page_bytes);
+            void *c = nullptr;
+            if (hipHostMalloc(&c, (size_t)n * page_bytes, hipHostMallocDefault) != hipSuccess) return -1;
+            void *dc = nullptr;
+            if (hipHostGetDevicePointer(&dc, c, 0) != hipSuccess) { hipHostFree(c); return -1; }
+            hchunks.push_back(c);
+            for (int i = 0; i < n; i++) {
+                hptr.push_back((float *)((uint8_t *)dc + (size_t)i * page_bytes));
+                hrefc.push_back(0);
+                hfree.push_back((int)hptr.size() - 1);
+            }
+            std::reverse(hfree.end() - n, hfree.end());
+        }
+        const int hid = hfree.back(); hfree.pop_back();
+        hrefc[hid] = 1;
+        return hid;
+    }
     int grow(int min_pages) {
         const int n = std::max(min_pages, pages_per_chunk);
         void *c = nullptr;
@@ -410,6 +452,7 @@ struct sp_kvdecode_handle {
     int max_rewind = 0;                      // 0: full tables for window layers
     int pool_growth = 0;                     // pages per pool growth (0: ~1 GiB)
     int recall_kvsel = 0;                    // SP_RECALL_KVSEL: one recall selection per kv head
+    int ring2 = 0;                           // Ring-2: spill full-context pages outside sinks + window to host
     int full_pages = 0, ring_pages = 0;
     std::vector<std::vector<int>> pt;        // [NL][slots] page ids (-1 = unmapped)
     std::vector<int> slots;                  // per layer: number of slots
@@ -441,6 +484,8 @@ struct sp_kvdecode_handle {
     struct Recall {
         int B = 0, W = 0, sink = 0, r = 0;
         void *buf = nullptr;
+        float *side = nullptr;               // K sidecar [global layers][pmax][NKV][r] (zeroed at allocation)
+        size_t side_layer = 0;               // floats per global layer
         uint32_t *Rb = nullptr, *keys = nullptr;
         int *lists = nullptr, *counts = nullptr, *zs = nullptr, *cmax = nullptr, *counter = nullptr;
         int64_t *vacc = nullptr, *vs = nullptr;
@@ -494,19 +539,18 @@ size_t kv_row_bytes(const DevModel *m, int mode, int kvc) {
 double kv_row_payload(const DevModel *m, int mode, int kvc) {
     return mode == FLOAT && kvc == KVC_SPINOR ? (double)(m->HD + 4 * spn_blocks(m->HD)) : 4.0 * m->HD;
 }
-// A page: K and V rows of PAGE positions of every kv head, then with recall
-// (r > 0) the K sidecar [NKV][PAGE][r] floats.
-size_t page_bytes_of(const DevModel *m, int mode, int kvc, int r) {
-    return (size_t)2 * m->NKV * PAGE * kv_row_bytes(m, mode, kvc) + (size_t)recall_page_floats(m->NKV, r) * 4;
+// A page: K and V rows of PAGE positions of every kv head.
+size_t page_bytes_of(const DevModel *m, int mode, int kvc) {
+    return (size_t)2 * m->NKV * PAGE * kv_row_bytes(m, mode, kvc);
 }
 // growth: pages per device allocation when the pool grows (0: about 1 GiB of
 // pages, at least 16)
 int pool_growth_pages(size_t page_bytes, int growth) {
     return growth > 0 ? growth : (int)std::max<size_t>(16, ((size_t)1 << 30) / page_bytes);
 }
-std::shared_ptr<KvPool> make_pool(const DevModel *m, int mode, int kvc, int r, int growth) {
+std::shared_ptr<KvPool> make_pool(const DevModel *m, int mode, int kvc, int growth) {
     auto pool = std::make_shared<KvPool>();
-    pool->page_bytes = page_bytes_of(m, mode, kvc, r);
+    pool->page_bytes = page_bytes_of(m, mode, kvc);
     pool->pages_per_chunk = pool_growth_pages(pool->page_bytes, growth);
     return pool;
 }
@@ -556,7 +600,7 @@ int ensure_pages(sp_kvdecode_handle *h, int p0, int p1, bool may_grow = true) {
         for (int i = 0; i < n; i++) {
             const int lp = lp0 + i, slot = (S == h->full_pages) ? lp : lp % S;
             const int id = h->pt[l][slot];
-            if (id < 0 || pool.refc[id] > 1) need++;
+            if (id < 0 || pool.refc[id] > 1) need++;     // unmapped, host (Ring-2) or shared with a fork
         }
     }
     if (need > pool.free_ids.size()) {
@@ -576,10 +620,11 @@ int ensure_pages(sp_kvdecode_handle *h, int p0, int p1, bool may_grow = true) {
             int &id = h->pt[l][slot];
             if (id >= 0 && pool.refc[id] <= 1) continue;
             const int nid = pool.alloc(false);   // reserved above: cannot fail
-            if (id >= 0) {                       // shared with a fork: copy, then drop this handle's reference
-                err = hipMemcpyAsync(pool.ptr[nid], pool.ptr[id], pool.page_bytes, hipMemcpyDeviceToDevice, h->stream);
+            if (id != NO_PAGE) {                 // shared with a fork, or in host memory: copy, then drop this reference
+                err = hipMemcpyAsync(pool.ptr[nid], pool.page_ptr(id), pool.page_bytes, hipMemcpyDefault, h->stream);
                 if (err != hipSuccess) { pool.unref(nid); break; }
-                pool.unref(id);
+                if (id <= -2) pool.fetches++;
+                pool.release(id);
             }
             id = nid;
             h->h_pt[h->pt_off[l] + slot] = pool.ptr[nid];
@@ -595,6 +640,59 @@ int ensure_pages(sp_kvdecode_handle *h, int p0, int p1, bool may_grow = true) {
         HIPCHK(hipStreamSynchronize(h->stream), "page table update sync");
     }
     HIPCHK(err, "copy-on-write page copy");
+    return 0;
+}
+
+// Ring-2 (the reference's SP_RING2 with the SP_RECALL_FUSE boundary,
+// core/forward/decode.c:117-131, 233-237, 408-440, 518-556): with recall on,
+// the full-context (global) layers keep in HBM only the pages that hold a sink
+// position or reach into the recall window of the position about to be
+// decoded (the Ring-1 set, sp_arm_r1slot's sinks + W-window by page); every
+// other page this handle owns alone moves to pinned host memory and its
+// table entry points there.  The recall attention reads the recalled rows of
+// such pages over the bus, the same bytes, so results are bit-identical; a
+// page written again (after a rewind) comes back first (ensure_pages).
+// Pages shared with a fork stay in HBM.  Best effort: when the host store
+// cannot grow, the remaining pages stay where they are.
+int ring2_spill(sp_kvdecode_handle *h, int pos) {
+    if (!h->ring2 || h->rec.B <= 0) return 0;
+    const DevModel *m = h->m;
+    const int lo = pos + 1 - h->rec.W;                 // the window's first position
+    if (lo <= 0) return 0;
+    const int lp_begin = (h->rec.sink + PAGE - 1) / PAGE, lp_end = lo / PAGE;
+    if (lp_begin >= lp_end) return 0;
+    std::lock_guard<std::mutex> lk(h->pool->mu);
+    KvPool &pool = *h->pool;
+    std::vector<int> moved;                            // device ids whose pages were copied out
+    size_t lo_i = SIZE_MAX, hi_i = 0;
+    hipError_t err = hipSuccess;
+    for (int l = 0; l < m->NL && err == hipSuccess; l++) {
+        if (!is_global(m, l) || h->slots[l] != h->full_pages) continue;
+        for (int lp = lp_begin; lp < lp_end; lp++) {
+            int &id = h->pt[l][lp];
+            if (id < 0 || pool.refc[id] != 1) continue;
+            const int hid = pool.host_alloc();
+            if (hid < 0) { l = m->NL; break; }         // the host store is full: stop here
+            err = hipMemcpyAsync(pool.hptr[hid], pool.ptr[id], pool.page_bytes, hipMemcpyDefault, h->stream);
+            if (err != hipSuccess) { pool.release(HOST_ID(hid)); break; }
+            moved.push_back(id);
+            const size_t ti = h->pt_off[l] + lp;
+            id = HOST_ID(hid);
+            h->h_pt[ti] = pool.hptr[hid];
+            lo_i = std::min(lo_i, ti); hi_i = std::max(hi_i, ti + 1);
+        }
+    }
+    if (hi_i > lo_i) {
+        // the copies complete before their device pages can be reused, and the
+        // device table is updated before the step's kernels read it
+        hipError_t e2 = hipMemcpyAsync(h->d_pt + lo_i, h->h_pt + lo_i, (hi_i - lo_i) * sizeof(float *),
+                                       hipMemcpyHostToDevice, h->stream);
+        const hipError_t e3 = hipStreamSynchronize(h->stream);
+        if (e2 == hipSuccess) e2 = e3;
+        if (e2 != hipSuccess) err = e2;
+        else for (int id : moved) { pool.unref(id); pool.spills++; }
+    }
+    HIPCHK(err, "Ring-2 page spill");
     return 0;
 }
 
@@ -658,11 +756,11 @@ void set_handle_mode(sp_kvdecode_handle *h, int mode) {
 // A fresh pool when the stored row format changes (mode or codec, only before
 // the first token): unmaps every page and rebuilds the empty tables.
 int repage(sp_kvdecode_handle *h, const char *who) {
-    const size_t want = page_bytes_of(h->m, h->mode, h->kvc, h->rec.r);
+    const size_t want = page_bytes_of(h->m, h->mode, h->kvc);
     if (h->pool->page_bytes == want) return 0;
     if (h->pool.use_count() > 1) return fail("%s: the KV pages are shared with a fork", who);
-    { std::lock_guard<std::mutex> pl(h->pool->mu); for (auto &v : h->pt) for (int id : v) h->pool->unref(id); }
-    h->pool = make_pool(h->m, h->mode, h->kvc, h->rec.r, h->pool_growth);
+    { std::lock_guard<std::mutex> pl(h->pool->mu); for (auto &v : h->pt) for (int id : v) h->pool->release(id); }
+    h->pool = make_pool(h->m, h->mode, h->kvc, h->pool_growth);
     free_graphs(h);
     return build_tables(h);
 }
@@ -701,7 +799,11 @@ int alloc_recall(sp_kvdecode_handle *h, int B, int W, int sink, int r) {
     R.kstride = (int)align_up((size_t)P, 64);
     const size_t NH = m->NH, HD = m->HD, mc = R.mchunks, ls = R.lstride;
     struct Item { void **p; size_t n; };
+    int ng = 0;
+    for (int l = 0; l < m->NL; l++) ng += is_global(m, l) ? 1 : 0;
+    R.side_layer = (size_t)P * m->NKV * r;
     Item items[] = {
+        {(void **)&R.side, (size_t)ng * R.side_layer * 4},
         {(void **)&R.Rb, (size_t)r * HD / 8}, {(void **)&R.keys, NH * R.kstride * 4}, {(void **)&R.pq, NH * r * 4},
         {(void **)&R.lists, NH * ls * 4},
         {(void **)&R.zs, NH * ls * 4}, {(void **)&R.counts, NH * 4}, {(void **)&R.cmax, NH * mc * 4},
@@ -721,6 +823,14 @@ int alloc_recall(sp_kvdecode_handle *h, int B, int W, int sink, int r) {
     HIPCHK(hipStreamSynchronize(h->stream), "recall buffers");
     R.B = B; R.W = W; R.sink = sink; R.r = r;
     return 0;
+}
+
+// layer l's K sidecar array [pmax][NKV][r] (global layers; null otherwise)
+float *side_of(const sp_kvdecode_handle *h, int l) {
+    if (!h->rec.side || !is_global(h->m, l)) return nullptr;
+    int g = 0;
+    for (int i = 0; i < l; i++) g += is_global(h->m, i) ? 1 : 0;
+    return h->rec.side + (size_t)g * h->rec.side_layer;
 }
 
 // The recall set's geometry at position pos (the device router's sel_geom,
@@ -812,11 +922,12 @@ int attn_chunks(const sp_kvdecode_handle *h, int pos_hi, StepShape &sh) {
 
 typedef void (*TimeCb)(void *ctx, int cls, bool begin);
 
-RecallArgs recall_args(const sp_kvdecode_handle *h, float *const *pages, VecStat *stat_out) {
+RecallArgs recall_args(const sp_kvdecode_handle *h, int layer, float *const *pages, VecStat *stat_out) {
     const DevModel *m = h->m;
     const auto &R = h->rec;
     RecallArgs rc{};
     rc.pq = R.pq; rc.qr = h->qr; rc.pages = pages; rc.st = h->d_st; rc.ao = h->ao; rc.stat_out = stat_out;
+    rc.side = side_of(h, layer);
     rc.keys = R.keys; rc.lists = R.lists; rc.counts = R.counts; rc.zs = R.zs; rc.cmax = R.cmax;
     rc.vacc = R.vacc; rc.vs = R.vs; rc.part = R.part; rc.psum = R.psum; rc.counter = R.counter;
     rc.kstride = R.kstride; rc.lstride = R.lstride; rc.mchunks = R.mchunks;
@@ -874,12 +985,12 @@ void enqueue_body(sp_kvdecode_handle *h, const StepShape &sh, TimeCb cb, void *c
         a.chunk = glob ? sh.chunk_global : sh.chunk_local;
         a.vchunk = glob ? sh.vchunk_global : 0;
         a.stat_out = st(l, STAT_AO);
-        if (h->rec.B > 0 && a.win < 0) { a.rec_R = h->rec.Rb; a.rec_r = h->rec.r; }
+        if (h->rec.B > 0 && a.win < 0) { a.rec_R = h->rec.Rb; a.rec_r = h->rec.r; a.rec_side = side_of(h, l); }
         const int cls = (glob || a.win < 0) ? 5 : 6, grid = glob ? sh.grid_global : sh.grid_local;
         if (sh.route && a.rec_r) {
             a.rec_pq = h->rec.pq;                       // the router's query projections
             T(7, true); launch_qk_prep(a, s); T(7, false);
-            T(cls, true); launch_recall_attention(recall_args(h, a.pages, a.stat_out), s); T(cls, false);
+            T(cls, true); launch_recall_attention(recall_args(h, l, a.pages, a.stat_out), s); T(cls, false);
         } else if (attention_fuses_prep(a)) {
             T(cls, true); launch_prep_attention(a, grid, s); T(cls, false);
         } else {
@@ -1041,7 +1152,9 @@ int run_batch(sp_kvdecode_handle *h, int T, int pos0, int pos_hi, bool multi, Ti
             a.tpos = b.tpos; a.tpages = b.tpages + (size_t)l * b.TB;
             if (glob || a.win < 0) { a.work = b.work; a.nwork = b.nwork; }
         }
-        else if (h->rec.B > 0 && a.win < 0) { a.rec_R = h->rec.Rb; a.rec_r = h->rec.r; }   // prefill: the sidecar
+        else if (h->rec.B > 0 && a.win < 0) {                   // prefill: the sidecar
+            a.rec_R = h->rec.Rb; a.rec_r = h->rec.r; a.rec_side = side_of(h, l);
+        }
         // batched decode over sessions: the longest chunks the kernels take,
         // so that the many sessions' rows make fewer, longer workgroups
         a.chunk = (glob || a.win < 0) ? (multi ? ATTN_MAXCH : 256) : 64;
@@ -1157,7 +1270,7 @@ int check_tok(const sp_kvdecode_handle *h, int32_t tok) {
 int step_one(sp_kvdecode_handle *h, int32_t tok, int want_logits) {
     if (check_tok(h, tok)) return 1;
     if (h->dpos >= h->pmax) return fail("sp_hipkv: context full (dpos == pmax %s%lld)", "", (long long)h->pmax);
-    if (ensure_pages(h, h->dpos, h->dpos + 1)) return 1;
+    if (ensure_pages(h, h->dpos, h->dpos + 1) || ring2_spill(h, h->dpos)) return 1;
     if (set_state(h, h->dpos, tok, DRIVE_HOST)) return 1;
     StepShape sh = shape_for(h, h->dpos, want_logits, 0);
     if (run_body(h, sh)) return 1;
@@ -1230,13 +1343,14 @@ int sp_hipkv_open(const void *qm_opaque, int pmax, sp_kvdecode_handle **out) {
         return fail("sp_hipkv_open: no HIP device visible (this backend runs on MI355X / gfx950)%s");
     DevModel *m = model_get(qm);
     if (!m) return 1;
-    auto new_pool = [m]() { return make_pool(m, FLOAT, KVC_PLAIN, 0, 0); };
+    auto new_pool = [m]() { return make_pool(m, FLOAT, KVC_PLAIN, 0); };
     if (sp_kvdecode_handle *sh = take_shell(m, pmax, 0)) {
         // a kept shell: reset to the open defaults, unmapped tables
         set_handle_mode(sh, FLOAT);
         if (sh->kvc != KVC_PLAIN) { sh->kvc = KVC_PLAIN; free_graphs(sh); }   // graphs bake in the codec
         sh->use_graph = 1; sh->use_batch = 1; sh->dpos = 0; sh->hwm = 0; sh->pool_growth = 0;
         if (sh->recall_kvsel) { sh->recall_kvsel = 0; free_graphs(sh); }
+        sh->ring2 = 0;
         if (sh->rec.B) { free_recall(sh); free_graphs(sh); }
         sh->pool = new_pool();
         if (hipMemsetAsync(sh->vclamp, 0, sizeof(int), sh->stream) != hipSuccess) {
@@ -1264,7 +1378,7 @@ void sp_hipkv_close(sp_kvdecode_handle *h) {
     if (!h) return;
     std::lock_guard<std::mutex> lk(g_mu);
     const bool idle = !h->stream || hipStreamSynchronize(h->stream) == hipSuccess;
-    if (h->pool) { std::lock_guard<std::mutex> pl(h->pool->mu); for (auto &v : h->pt) for (int id : v) h->pool->unref(id); }
+    if (h->pool) { std::lock_guard<std::mutex> pl(h->pool->mu); for (auto &v : h->pt) for (int id : v) h->pool->release(id); }
     h->pool.reset();
     for (auto &v : h->pt) std::fill(v.begin(), v.end(), -1);
     DevModel *m = h->m;
@@ -1562,7 +1676,7 @@ int sp_hipkv_set_kv_codec(sp_kvdecode_handle *h, int codec) {
 int sp_hipkv_set_max_rewind(sp_kvdecode_handle *h, int max_rewind) {
     if (!h || max_rewind < 0) return fail("sp_hipkv_set_max_rewind: bad argument%s");
     if (h->dpos != 0) return fail("sp_hipkv_set_max_rewind: only before the first token%s");
-    { std::lock_guard<std::mutex> pl(h->pool->mu); for (auto &v : h->pt) for (int id : v) h->pool->unref(id); }
+    { std::lock_guard<std::mutex> pl(h->pool->mu); for (auto &v : h->pt) for (int id : v) h->pool->release(id); }
     h->max_rewind = max_rewind;
     free_graphs(h);
     return build_tables(h);
@@ -1617,6 +1731,22 @@ int sp_hipkv_set_recall_kvsel(sp_kvdecode_handle *h, int on) {
     return 0;
 }
 
+int sp_hipkv_set_ring2(sp_kvdecode_handle *h, int on) {
+    if (!h) return fail("sp_hipkv_set_ring2: null handle%s");
+    h->ring2 = on ? 1 : 0;
+    return 0;
+}
+
+int sp_hipkv_ring2_stats(const sp_kvdecode_handle *h, long long out[4]) {
+    if (!h || !out) return fail("sp_hipkv_ring2_stats: null argument%s");
+    std::lock_guard<std::mutex> lk(h->pool->mu);
+    long long host = 0, dev = 0;
+    for (const auto &v : h->pt)
+        for (int id : v) { host += id <= -2; dev += id >= 0; }
+    out[0] = host; out[1] = dev; out[2] = h->pool->spills; out[3] = h->pool->fetches;
+    return 0;
+}
+
 int sp_hipkv_read_recall_sidecar(const sp_kvdecode_handle *h, int layer, int p0, int n, float *out) {
     if (!h || !out || layer < 0 || layer >= h->m->NL || p0 < 0 || n < 0 || p0 + n > h->dpos)
         return fail("sp_hipkv_read_recall_sidecar: bad argument%s");
@@ -1624,20 +1754,10 @@ int sp_hipkv_read_recall_sidecar(const sp_kvdecode_handle *h, int layer, int p0,
     const DevModel *m = h->m;
     if (!is_global(m, layer)) return fail("sp_hipkv_read_recall_sidecar: window layers keep no sidecar%s");
     const int NKV = m->NKV, r = h->rec.r;
-    const size_t side0 = page_bytes_of(m, h->mode, h->kvc, 0);          // the sidecar follows K and V
     HIPCHK(hipStreamSynchronize(h->stream), "sidecar read sync");
-    std::vector<float> side((size_t)recall_page_floats(NKV, r));
-    for (int lp = p0 / PAGE; lp <= (p0 + n - 1) / PAGE && n > 0; lp++) {
-        const int id = h->pt[layer][lp];
-        if (id < 0) return fail("sp_hipkv_read_recall_sidecar: position not resident%s");
-        HIPCHK(hipMemcpy(side.data(), (const uint8_t *)h->pool->ptr[id] + side0, side.size() * 4, hipMemcpyDeviceToHost),
-               "sidecar page read");
-        const int a = std::max(p0, lp * PAGE), b = std::min(p0 + n, (lp + 1) * PAGE);
-        for (int p = a; p < b; p++)
-            for (int kh = 0; kh < NKV; kh++)
-                memcpy(out + ((size_t)(p - p0) * NKV + kh) * r, side.data() + ((size_t)kh * PAGE + p % PAGE) * r,
-                       (size_t)r * 4);
-    }
+    if (n > 0)
+        HIPCHK(hipMemcpy(out, side_of(h, layer) + (size_t)p0 * NKV * r, (size_t)n * NKV * r * 4, hipMemcpyDeviceToHost),
+               "sidecar read");
     return 0;
 }
 
@@ -1670,11 +1790,22 @@ int sp_hipkv_fork(const sp_kvdecode_handle *p, sp_kvdecode_handle **out) {
         }
     }
     h->pool = p->pool; h->dpos = p->dpos; h->hwm = p->hwm;
+    if (p->rec.side && p->dpos > 0) {
+        // the sidecar array is per handle: the child starts with the parent's
+        hipStreamSynchronize(p->stream);
+        int ng = 0;
+        for (int l = 0; l < h->m->NL; l++) ng += is_global(h->m, l) ? 1 : 0;
+        if (hipMemcpyAsync(h->rec.side, p->rec.side, (size_t)ng * p->rec.side_layer * 4, hipMemcpyDeviceToDevice,
+                           h->stream) != hipSuccess) {
+            sp_hipkv_close(h.release()); return fail("sp_hipkv_fork: sidecar copy failed%s");
+        }
+    }
     if (hipMemsetAsync(h->vclamp, 0, sizeof(int), h->stream) != hipSuccess) {
         sp_hipkv_close(h.release()); return fail("sp_hipkv_fork: clamp counter reset failed%s");
     }
     h->use_batch = p->use_batch; h->use_graph = p->use_graph; h->pool_growth = p->pool_growth;
     if (h->recall_kvsel != p->recall_kvsel) { h->recall_kvsel = p->recall_kvsel; free_graphs(h.get()); }
+    h->ring2 = p->ring2;
     hipStreamSynchronize(p->stream);
     // share every mapped page (copy-on-write on the next append into it)
     {
@@ -1683,8 +1814,8 @@ int sp_hipkv_fork(const sp_kvdecode_handle *p, sp_kvdecode_handle **out) {
             for (int s = 0; s < h->slots[l]; s++) {
                 const int id = p->pt[l][s];
                 h->pt[l][s] = id;
-                if (id >= 0) h->pool->refc[id]++;
-                h->h_pt[h->pt_off[l] + s] = id >= 0 ? h->pool->ptr[id] : nullptr;
+                h->pool->retain(id);
+                h->h_pt[h->pt_off[l] + s] = h->pool->page_ptr(id);
             }
         }
     }
@@ -1724,7 +1855,7 @@ int sp_hipkv_greedy(sp_kvdecode_handle *h, int32_t first_token, int n, int32_t *
     if (check_tok(h, first_token)) return 1;
     if (n > h->pmax - h->dpos) return fail("sp_hipkv_greedy: context full%s");
     if (n == 0) { if (device_ms) *device_ms = 0; return 0; }
-    if (ensure_pages(h, h->dpos, h->dpos + n)) return 1;
+    if (ensure_pages(h, h->dpos, h->dpos + n) || ring2_spill(h, h->dpos)) return 1;
     if (set_state(h, h->dpos, first_token, DRIVE_GREEDY)) return 1;
     hipEvent_t e0, e1;
     HIPCHK(hipEventCreate(&e0), "event"); HIPCHK(hipEventCreate(&e1), "event");
@@ -1758,7 +1889,7 @@ int sp_hipkv_kernel_times(sp_kvdecode_handle *h, int32_t first_token, int n, dou
     if (!h || n <= 0 || !ms || !launches || !bytes) return fail("sp_hipkv_kernel_times: bad argument%s");
     if (check_tok(h, first_token)) return 1;
     if (n > h->pmax - h->dpos) return fail("sp_hipkv_kernel_times: context full%s");
-    if (ensure_pages(h, h->dpos, h->dpos + n)) return 1;
+    if (ensure_pages(h, h->dpos, h->dpos + n) || ring2_spill(h, h->dpos)) return 1;
     if (set_state(h, h->dpos, first_token, DRIVE_GREEDY)) return 1;
     struct Ctx { hipStream_t s; std::vector<std::pair<int, std::pair<hipEvent_t, hipEvent_t>>> ev; hipEvent_t cur; };
     Ctx c; c.s = h->stream;
@@ -1831,8 +1962,8 @@ int sp_hipkv_read_kv(const sp_kvdecode_handle *h, int layer, int p0, int n, floa
     for (int lp = p0 / PAGE; lp <= (p0 + n - 1) / PAGE && n > 0; lp++) {
         const int slot = S == h->full_pages ? lp : lp % S;
         const int id = h->pt[layer][slot];
-        if (id < 0) return fail("sp_hipkv_read_kv: position not resident%s");
-        HIPCHK(hipMemcpy(page.data(), h->pool->ptr[id], h->pool->page_bytes, hipMemcpyDeviceToHost), "kv page read");
+        if (id == NO_PAGE) return fail("sp_hipkv_read_kv: position not resident%s");
+        HIPCHK(hipMemcpy(page.data(), h->pool->page_ptr(id), h->pool->page_bytes, hipMemcpyDefault), "kv page read");
         const int a = std::max(p0, lp * PAGE), b = std::min(p0 + n, (lp + 1) * PAGE);
         for (int p = a; p < b; p++)
             for (int hh = 0; hh < NKV; hh++) {

@@ -106,9 +106,11 @@ struct AttnArgs {
     const int2 *work;
     int nwork;
     // recall sidecar: rec_r > 0 writes each new K head's projection on the
-    // frozen +-1 matrix (sign bits rec_R [rec_r][HD/32]) into its page
+    // frozen +-1 matrix (sign bits rec_R [rec_r][HD/32]) into the layer's
+    // sidecar array rec_side [pmax][NKV][rec_r] at its position
     const uint32_t *rec_R;
     int rec_r;
+    float *rec_side;
     float *rec_pq;           // routed step: each q head's projection [NH][rec_r] (NULL: not needed)
 };
 
@@ -118,6 +120,7 @@ struct RecallArgs {
     const float *pq;         // each q head's projection [NH][r] (written by the head preparation)
     const float *qr;         // rotated, normed q [NH*HD]
     float *const *pages;     // this layer's page table (full: no ring)
+    const float *side;       // this layer's K sidecar [pmax][NKV][r]
     const DState *st;
     float *ao;               // output [NH*HD]
     VecStat *stat_out;       // statistics of ao for the O GEMV
@@ -143,7 +146,6 @@ void launch_prefill_attention(const AttnArgs &a, hipStream_t s);
 constexpr int RECALL_CHUNK = 64;        // recalled positions per attention workgroup
 constexpr int RECALL_SCORE_BLOCKS = 64; // router scoring workgroups per kv head (grid-stride)
 constexpr int RECALL_MAX_GROUP = 8;     // q heads per kv head the router serves
-int recall_page_floats(int NKV, int r); // sidecar floats per page
 
 struct Seg { DevW w; float *out; };
 enum Act { ACT_NONE = 0, ACT_GELU = 1, ACT_SILU = 2 };

@@ -23,6 +23,7 @@ struct HeadPrep {
     int *vclamp;              // exact mode: count of V heads stored with a clamped element
     const uint32_t *rec_R;    // recall sidecar projection sign bits [rec_r][HD/32]
     int rec_r;                // 0: no sidecar
+    float *rec_side;          // the layer's sidecar array [pmax][NKV][rec_r]
     float *rec_pq;            // routed step: q heads' projections [NH][rec_r]
 };
 __device__ __forceinline__ HeadPrep head_prep_of(const AttnArgs &a) {
@@ -30,7 +31,7 @@ __device__ __forceinline__ HeadPrep head_prep_of(const AttnArgs &a) {
     p.q = a.q; p.k = a.k; p.v = a.v; p.q_norm = a.q_norm; p.k_norm = a.k_norm; p.rope_cs = a.rope_cs;
     p.qr = a.qr; p.pages = a.pages; p.ring_pages = a.ring_pages; p.NH = a.NH; p.NKV = a.NKV; p.HD = a.HD;
     p.mode = a.mode; p.kvc = a.kvc; p.eps = a.eps; p.vclamp = a.vclamp;
-    p.rec_R = a.rec_R; p.rec_r = a.rec_r; p.rec_pq = a.rec_pq;
+    p.rec_R = a.rec_R; p.rec_r = a.rec_r; p.rec_pq = a.rec_pq; p.rec_side = a.rec_side;
     return p;
 }
 
@@ -258,8 +259,7 @@ __device__ __forceinline__ void qk_prep_head_t(const HeadPrep a, int hb, int pos
         return;
     }
     if (a.rec_r)                                                // sidecar from the K before any codec
-        recall_sidecar<PER>(a.rec_R, a.rec_r, out,
-                            page + (size_t)2 * a.NKV * PAGE * HD + ((size_t)h * PAGE + slot) * a.rec_r, lane);
+        recall_sidecar<PER>(a.rec_R, a.rec_r, out, a.rec_side + ((size_t)pos * a.NKV + h) * a.rec_r, lane);
     if (a.kvc == KVC_SPINOR && a.mode == FLOAT) {
         constexpr int RB = spn_row_bytes(HD);
         spinor_head<PER>(out, lane, true, (uint8_t *)page + ((size_t)h * PAGE + slot) * RB);

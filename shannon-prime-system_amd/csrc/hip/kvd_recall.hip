@@ -26,8 +26,6 @@
 
 namespace kvd {
 
-int recall_page_floats(int NKV, int r) { return NKV * PAGE * r; }
-
 namespace {
 
 __device__ __forceinline__ const float *rc_page(const RecallArgs &rc, int pos) { return gmem(rc.pages)[pos / PAGE]; }
@@ -102,7 +100,7 @@ __global__ __launch_bounds__(256) void k_recall_score(RecallArgs rc) {
     }
     __syncthreads();
     for (int s = g.sink + blockIdx.x * 256 + threadIdx.x; s < g.cand_hi; s += gridDim.x * 256) {
-        const float *side = rc_page(rc, s) + (size_t)2 * rc.NKV * PAGE * HD + ((size_t)kvh * PAGE + (s & (PAGE - 1))) * r;
+        const float *side = rc.side + ((size_t)s * rc.NKV + kvh) * r;
         float row[RT ? RT : 64];
         if constexpr (RT) {
             #pragma unroll
@@ -654,7 +652,7 @@ void launch_recall_attention(const RecallArgs &rc, hipStream_t s) {
     // lstride must hold every list (mchunks chunks of RECALL_CHUNK entries
     // cover it) and the keys every candidate position (kstride >= pmax, a
     // multiple of 4 for the select's 16-byte loads)
-    if (rc.r < 1 || rc.r > 64 || rc.NH < 1 || rc.NKV < 1 || rc.NH % rc.NKV || rc.NH / rc.NKV > RECALL_MAX_GROUP ||
+    if (!rc.side || rc.r < 1 || rc.r > 64 || rc.NH < 1 || rc.NKV < 1 || rc.NH % rc.NKV || rc.NH / rc.NKV > RECALL_MAX_GROUP ||
         rc.mchunks < 1 || !rc.stat_out || !rc.pq || rc.mchunks * RECALL_CHUNK < rc.lstride || rc.score_blocks < 1 ||
         rc.kstride < 4 || rc.kstride % 4 || (rc.kvsel && (!rc.Rb || !rc.qr || rc.HD > 256)))
         return launch_fail("recall attention: arguments outside the kernels' limits");

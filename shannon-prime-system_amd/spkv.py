@@ -115,6 +115,8 @@ def kv():
         _sig(lib, "sp_hipkv_set_graph", c_int, [c_void_p, c_int])
         _sig(lib, "sp_hipkv_set_pool_growth", c_int, [c_void_p, c_int])
         _sig(lib, "sp_hipkv_set_recall_kvsel", c_int, [c_void_p, c_int])
+        _sig(lib, "sp_hipkv_set_ring2", c_int, [c_void_p, c_int])
+        _sig(lib, "sp_hipkv_ring2_stats", c_int, [c_void_p, c_void_p])
         _sig(lib, "sp_hipkv_write_kv", c_int, [c_void_p, c_int, c_int, c_int, c_void_p, c_void_p])
         _sig(lib, "sp_hipkv_set_batch_prefill", c_int, [c_void_p, c_int])
         _sig(lib, "sp_hipkv_fork", c_int, [c_void_p, ctypes.POINTER(c_void_p)])
@@ -381,6 +383,17 @@ class Backend:
     def set_recall_kvsel(self, on):
         """SP_RECALL_KVSEL: one recall set per kv head (group-centroid query)."""
         check(kv().sp_hipkv_set_recall_kvsel(self.h, 1 if on else 0), "sp_hipkv_set_recall_kvsel")
+
+    def set_ring2(self, on):
+        """Ring-2: spill full-context pages outside sinks + recall window to host memory."""
+        check(kv().sp_hipkv_set_ring2(self.h, 1 if on else 0), "sp_hipkv_set_ring2")
+
+    def ring2_stats(self):
+        """(host entries, device entries, pool spills, pool fetch-backs)"""
+        import numpy as np
+        o = np.zeros(4, np.int64)
+        check(kv().sp_hipkv_ring2_stats(self.h, ptr(o)), "sp_hipkv_ring2_stats")
+        return [int(x) for x in o]
 
     def recall_sidecar(self, layer, p0, n, nkv, r):
         import numpy as np

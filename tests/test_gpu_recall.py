@@ -180,6 +180,74 @@ def test_recall_kvsel(tmpdir_models, name, rec, n_pre, n_gen, exact):
     p.close()
 
 
+RING2_CASES = [
+    ("qwen3-tiny", (48, 16, 4, 16), True),
+    ("gemma3-tiny", (40, 16, 4, 16), True),             # the global layer among window layers
+    ("qwen3-g4", (40, 70, 0, 8), True),                 # no sinks, a window over two pages
+    ("qwen3-hd128", (64, 16, 4, 16), False),
+]
+
+
+@pytest.mark.parametrize("name,rec,exact", RING2_CASES,
+                         ids=[f"{c[0]}-B{c[1][0]}-{'exact' if c[2] else 'float'}" for c in RING2_CASES])
+def test_recall_ring2_is_bit_identical(tmpdir_models, name, rec, exact):
+    """Ring-2 (sp_hipkv_set_ring2): the full-context layers' pages outside the
+    sinks and the recall window move to host memory before each decode step.
+    Against a twin without Ring-2 fed the same tokens: every step's logits bit
+    for bit (both modes: the same bytes reach the same kernels), every resident
+    K/V row read back identical, pages actually spilled, a rewind into spilled
+    pages (they come back to HBM when written), a fork and the device greedy
+    loop."""
+    pmax, n_pre = 1024, 600
+    spm, spt = model_files(tmpdir_models, name, pmax)
+    m = spkv.Model(spm, spt); s = spkv.Session(m, pmax)
+    qm = spkv.l1().sp_session_qwen3_model(s.h)
+    o = orc.Oracle(spm, 64, orc.EXACT)
+    V, NL, kvd = o.V, o.NL, o.NKV * o.HD
+    glob = global_layers(o)
+    o.close()
+    a = spkv.Backend(qm, pmax, exact=exact); a.set_recall(*rec)
+    b = spkv.Backend(qm, pmax, exact=exact); b.set_recall(*rec); b.set_ring2(True)
+    pr = prompt(n_pre, V, seed=11)
+    a.prefill(pr); b.prefill(pr)
+    la, lb = np.zeros(V, np.float32), np.zeros(V, np.float32)
+
+    def both(tok, what):
+        a.decode(int(tok), la); b.decode(int(tok), lb)
+        assert same_bits(la, lb), what
+        return int(la.argmax())
+
+    t = int(pr[-1])
+    for k in range(24):
+        t = both(t, f"step {k}")
+    host, dev, spills, _ = b.ring2_stats()
+    W, sink = rec[1], rec[2]
+    lo = b.position() - W
+    expect = len(glob) * max(0, lo // 64 - (sink + 63) // 64)
+    assert spills >= expect > 0 and host >= expect, (host, dev, spills, expect)
+    for l in range(NL):
+        ka, va = a.read_kv(l, 0, a.position(), kvd); kb, vb = b.read_kv(l, 0, b.position(), kvd)
+        assert same_bits(ka, kb) and same_bits(va, vb), f"layer {l}: K/V read back"
+    # rewind into spilled pages: the next writes bring them back
+    assert a.rewind(300) == 0 and b.rewind(300) == 0
+    for k in range(12):
+        t = both(t, f"after the rewind, step {k}")
+    assert b.ring2_stats()[3] > 0, "no page came back from host memory"
+    # a fork reads the shared (host) history and writes its own pages
+    fa, fb = a.fork(), b.fork()
+    for k in range(6):
+        fa.decode(t, la); fb.decode(t, lb)
+        assert same_bits(la, lb), f"fork step {k}"
+        t = int(la.argmax())
+    # the device greedy loop
+    ga, _ = a.greedy(t, 20)
+    gb, _ = b.greedy(t, 20)
+    assert list(ga) == list(gb)
+    for x in (fa, fb, a, b):
+        x.close()
+    s.close(); m.close()
+
+
 def test_recall_float_within_tolerance(tmpdir_models):
     spm, spt = model_files(tmpdir_models, "qwen3-hd128", 256)
     p = Pair(spm, spt, False, 256, (64, 16, 4, 16))
