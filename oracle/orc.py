@@ -20,7 +20,7 @@ def ptr(a):
 def lib():
     global _orc
     if _orc is None:
-        path = os.path.join(HERE, "lib", "liboracle.so")
+        path = os.path.join(os.environ.get("ORC_LIB_DIR") or os.path.join(HERE, "lib"), "liboracle.so")
         if not os.path.exists(path):
             raise RuntimeError(f"{path} not built (make -C oracle)")
         L = ctypes.CDLL(path)

@@ -421,7 +421,9 @@ int orc_q4b_gemv_exact(const uint8_t *codes, const uint16_t *bs, int rows, int c
             int32_t a = 0;
             for (int i = i0; i < i1; i++) a += nib(rc, i) * xq[i];
             int64_t M; int e; f16_parts(b[blk], &M, &e);
-            acc += (i128)((int64_t)a * M) << (e + 24);
+            /* (d * M) * 2^(e + 24): shifted as the unsigned image (a signed left
+             * shift of a negative value is undefined in C; the bits are the same) */
+            acc += (i128)((u128)(i128)((int64_t)a * M) << (e + 24));
         }
         y[j] = i128_scaled_to_float(acc, -24 - sh);
     }
@@ -512,7 +514,7 @@ static i128 log2_q62(float v) {
         y = (y * y) >> 62;
         if (y >= ((u128)2 << 62)) { y >>= 1; frac |= (i128)1 << b; }
     }
-    return ((i128)e << 62) + frac;
+    return (i128)((u128)(i128)e << 62) + frac;      /* e < 0 for v < 1: shifted unsigned */
 }
 /* base^(-2i/d) in Q60: t = (2i/d)*log2(base) = n + r, result = 2^-r >> n with
  * 2^-r = prod over the set bits j of r of 2^(-2^-j). */

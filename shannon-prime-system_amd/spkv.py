@@ -11,7 +11,8 @@ import ctypes
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_DIR = os.path.join(HERE, "lib")
+# SPKV_LIB_DIR: another build of the two libraries (the sanitizer build, lib-asan)
+LIB_DIR = os.environ.get("SPKV_LIB_DIR") or os.path.join(HERE, "lib")
 
 SP_OK, SP_EBADARG, SP_EBADSTATE, SP_EUNSUPPORTED = 0, -3, -4, -5
 SP_ECANCEL, SP_ECONTEXT_FULL, SP_EBACKEND_OOM = -2, -33, -43
