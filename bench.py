@@ -562,11 +562,12 @@ def calib_copy(nbytes):
 def cpu_baseline(spm, be, info, shape, exact, n_steps, tok, sess, spinor=False, recall=None):
     """The oracle's decode steps on the host at the same context, the K/V state
     loaded from the device.  Rows: float mode (the reference's arithmetic) and
-    exact mode, each n_steps steps on all host cores (the row-parallel oracle:
-    GEMV rows and attention heads over threads, bit-identical to one thread)
-    and one step on one core.  In the GPU's mode every threaded oracle step is
-    compared with the GPU's logits for the same token (exact mode: bit for
-    bit).  The first row (float, all cores) is the reported value."""
+    exact mode, each n_steps greedy steps on one core (the reference decode is
+    single-threaded by contract) and the same steps on all host cores (the
+    row-parallel oracle: GEMV rows and attention heads over threads,
+    bit-identical to one thread).  In the GPU's mode every threaded oracle step
+    is compared with the GPU's logits for the same token (exact mode: bit for
+    bit).  The reported value is the float row on one core."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import orc
     spkv = __import__("spkv")
@@ -607,10 +608,13 @@ def cpu_baseline(spm, be, info, shape, exact, n_steps, tok, sess, spinor=False, 
         if recall:
             o.set_recall(*recall)
         load(o, mode)
-        L.orc_set_threads(1)                                  # one core, one step
-        t0 = time.time(); o.step(tok); one_s = time.time() - t0
-        assert o.rewind(1) == 0
-        L.orc_set_threads(threads)                            # all cores, n_steps steps
+        L.orc_set_threads(1)                                  # one core, n_steps greedy steps
+        t_tok, one_s = tok, 0.0
+        for i in range(n_steps):
+            t0 = time.time(); ol = o.step(t_tok); one_s += time.time() - t0
+            t_tok = int(ol.argmax())
+        assert o.rewind(n_steps) == 0
+        L.orc_set_threads(threads)                            # all cores, the same n_steps steps
         t_tok, cpu_s, same, worst = tok, 0.0, True, 0.0
         for i in range(n_steps):
             t0 = time.time(); ol = o.step(t_tok); cpu_s += time.time() - t0
@@ -620,18 +624,19 @@ def cpu_baseline(spm, be, info, shape, exact, n_steps, tok, sess, spinor=False, 
                 worst = max(worst, float(np.abs(ol - glog).max() / max(np.abs(ol).max(), 1e-30)))
             t_tok = int(ol.argmax())
         o.close()
-        row = {"mode": mode, "cores": threads, "steps": n_steps, "value": round(n_steps / cpu_s, 5),
-               "single_core_value": round(1.0 / one_s, 5)}
+        row = {"mode": mode, "steps": n_steps, "single_core_value": round(n_steps / one_s, 5),
+               "cores": threads, "value": round(n_steps / cpu_s, 5)}
         if gpu_mode:
             row.update(gpu_logits_bitexact=same, gpu_logits_max_rel=worst)
-        log(f"cpu baseline {mode}: {n_steps} steps on {threads} threads {cpu_s:.1f}s ({row['value']} tok/s), "
-            f"1 step on 1 core {one_s:.1f}s" + (f"; gpu==cpu bit-exact {same}, max rel {worst:.2e}" if gpu_mode else ""))
+        log(f"cpu baseline {mode}: {n_steps} steps on 1 core {one_s:.1f}s ({row['single_core_value']} tok/s), "
+            f"on {threads} threads {cpu_s:.1f}s ({row['value']} tok/s)"
+            + (f"; gpu==cpu bit-exact {same}, max rel {worst:.2e}" if gpu_mode else ""))
         rows.append(row)
     first = rows[0]
-    return {"value": first["value"], "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"{n_steps} decode steps of the same model at ctx {pos} (float-mode oracle, the reference's "
-                      f"arithmetic, row-parallel on {threads} threads; K/V loaded from the device), {cpu_model()}, "
-                      f"nproc {os.cpu_count()}",
+    return {"value": first["single_core_value"], "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"{n_steps} greedy decode steps of the same model at ctx {pos} (float-mode oracle, the "
+                      f"reference's arithmetic, one core; K/V loaded from the device), {cpu_model()}, "
+                      f"nproc {os.cpu_count()}; rows: float and exact mode on 1 core and on {threads} threads",
             "rows": rows,
             "gpu_logits_bitexact": next((r.get("gpu_logits_bitexact") for r in rows if "gpu_logits_bitexact" in r), None),
             "gpu_logits_max_rel": next((r.get("gpu_logits_max_rel") for r in rows if "gpu_logits_max_rel" in r), None)}
