@@ -542,8 +542,8 @@ __global__ __launch_bounds__(256) void k_attn_float(AttnArgs a_in) {
 // The step's head preparation inside the exact score pass (decode): wave g < G
 // normalizes and rotates q head h*G + g into qs; in the workgroup holding pos,
 // wave G % 4 prepares the new K row (paged store + kn) and wave (G + 1) % 4
-// appends the new V row.  prep_load requests the inputs, prep_finish computes
-// and stores.
+// appends the new V row (and keeps a copy in vn when given).  prep_load
+// requests the inputs, prep_finish computes and stores.
 template <int EPL> struct PrepIn { HeadIn q, k; float v[EPL]; };
 template <int EPL, int G>
 __device__ __forceinline__ void prep_load(const AttnArgs &a, int h, int pos, int wave, int lane, bool holds_pos, PrepIn<EPL> &in) {
@@ -559,7 +559,7 @@ __device__ __forceinline__ void prep_load(const AttnArgs &a, int h, int pos, int
 }
 template <int EPL, int G>
 __device__ __forceinline__ void prep_finish(const AttnArgs &a, int h, int pos, int wave, int lane, bool holds_pos,
-                                            const PrepIn<EPL> &in, int4 (*qs)[EPL * 16], int4 *kn) {
+                                            const PrepIn<EPL> &in, int4 (*qs)[EPL * 16], int4 *kn, int32_t *vn = nullptr) {
     constexpr int HD = EPL * 64;
     const HeadPrep hp = head_prep_of(a);
     float out[8];
@@ -589,7 +589,11 @@ __device__ __forceinline__ void prep_finish(const AttnArgs &a, int h, int pos, i
             if (a.kvc == KVC_SPINOR) spinor_head<EPL>(x, lane, false, nullptr);
             bool cl = false;
             #pragma unroll
-            for (int j = 0; j < EPL; j++) gmem(dst)[lane + 64 * j] = kv_code_v(x[j], cl);
+            for (int j = 0; j < EPL; j++) {
+                const int32_t vi = kv_code_v(x[j], cl);
+                gmem(dst)[lane + 64 * j] = vi;
+                if (vn) vn[lane + 64 * j] = vi;
+            }
             count_v_clamp(a.vclamp, cl);
         }
     }
@@ -696,6 +700,66 @@ __global__ __launch_bounds__(256) void k_attn_exact_scores(AttnArgs a_in) {
     }
 }
 
+// ---- exact mode: the join of a kv head's chunks ----
+// The chunk's V-sums (ored: one row per wave, summed here) join the kv head's
+// totals, exactly and in any order, in VREP replicas (chunk c adds into
+// replica c % VREP, where its softmax denominators were added too); the last
+// of the head's nch workgroups to arrive reads and clears the totals, divides
+// and writes ao, and resets the head's counter.  Every thread of the
+// workgroup calls this, last.
+template <int EPL, int G>
+__device__ __forceinline__ void exact_join(const AttnArgs &a, int h, int c, int nch, int64_t (*ored)[G][EPL * 64]) {
+    constexpr int HD = EPL * 64;
+    const size_t QDh = (size_t)a.NH * HD;
+    int64_t *vrep = a.vacc + (size_t)(c % VREP) * QDh;
+    for (int i = threadIdx.x; i < G * HD; i += 256) {
+        const int g = i / HD, d = i % HD;
+        const int64_t t = ored[0][g][d] + ored[1][g][d] + ored[2][g][d] + ored[3][g][d];
+        atomicAdd((unsigned long long *)&vrep[(size_t)(h * G + g) * HD + d], (unsigned long long)t);
+    }
+    mem_complete();
+    __syncthreads();
+    __shared__ int is_last;
+    if (threadIdx.x == 0) is_last = (arrive(&a.counter[h]) == nch - 1);
+    __syncthreads();
+    if (!is_last) return;
+    // the totals are read and cleared for the next launch in one atomic step;
+    // every exchange (denominators and V-sums) is issued before any total is
+    // used: one round trip
+    __shared__ int64_t Sg[G];
+    int64_t S = 0;
+    if (threadIdx.x < G)
+        #pragma unroll
+        for (int r = 0; r < VREP; r++)
+            S += (int64_t)__hip_atomic_exchange((unsigned long long *)&a.vacc_s[(size_t)r * a.NH + h * G + threadIdx.x], 0ull,
+                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    constexpr int PT = (G * EPL * 64 + 255) / 256;   // elements per thread
+    int64_t tot[PT];
+    #pragma unroll
+    for (int k = 0; k < PT; k++) {
+        const int i = threadIdx.x + 256 * k;
+        tot[k] = 0;
+        if (i < G * HD)
+            #pragma unroll
+            for (int r = 0; r < VREP; r++)
+                tot[k] += (int64_t)__hip_atomic_exchange((unsigned long long *)&a.vacc[(size_t)r * QDh + (size_t)h * G * HD + i], 0ull,
+                                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (threadIdx.x < G) Sg[threadIdx.x] = S;
+    __syncthreads();
+    StatAcc sacc;
+    #pragma unroll
+    for (int k = 0; k < PT; k++) {
+        const int i = threadIdx.x + 256 * k;
+        if (i >= G * HD) break;
+        const float o = rne_div_to_float((i128)tot[k], Sg[i / HD], 16);
+        a.ao[(size_t)h * G * HD + i] = o;
+        sacc.add(o);
+    }
+    if (a.stat_out) stat_flush_block(a.stat_out, sacc);      // max |ao| for the O GEMV
+    if (threadIdx.x == 0) reset_counter(&a.counter[h]);
+}
+
 // ---- exact mode: pass 2, exp weights on the island grid, exact V-sum ----
 template <int EPL, int G, bool BATCH, int UV>
 __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a_in) {
@@ -716,7 +780,6 @@ __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a_in) {
     __shared__ int64_t ored[4][G][EPL * 64];
     __shared__ int redi[4][G];
     __shared__ int64_t redl[4][G];
-    __shared__ int is_last;
     const int n = ce - cs;
     // This chunk's scores and the chunk maxima are requested first, then the
     // first UV V rows of each wave: the global-max reduction and the weights
@@ -808,18 +871,6 @@ __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a_in) {
     for (int g = 0; g < G; g++)
         #pragma unroll
         for (int e = 0; e < EPL; e++) ored[wave][g][lane * EPL + e] = (int64_t)o[g][e];
-    __syncthreads();
-    // exact, order-free accumulation of this chunk into the kv-head's totals
-    // (VREP replicas, chunk c adding into replica c % VREP); the last
-    // workgroup sums them
-    const size_t QDh = (size_t)a.NH * HD;
-    int64_t *vrep = a.vacc + (size_t)(c % VREP) * QDh;
-    int64_t *srep = a.vacc_s + (size_t)(c % VREP) * a.NH;
-    for (int i = threadIdx.x; i < G * HD; i += 256) {
-        const int g = i / HD, d = i % HD;
-        const int64_t t = ored[0][g][d] + ored[1][g][d] + ored[2][g][d] + ored[3][g][d];
-        atomicAdd((unsigned long long *)&vrep[(size_t)(h * G + g) * HD + d], (unsigned long long)t);
-    }
     // the chunk's softmax denominators, all heads of the group in one round
     #pragma unroll
     for (int g = 0; g < G; g++) {
@@ -831,48 +882,242 @@ __global__ __launch_bounds__(256) void k_attn_exact_vsum(AttnArgs a_in) {
     __syncthreads();
     if (threadIdx.x < G) {
         const int g = threadIdx.x;
-        atomicAdd((unsigned long long *)&srep[h * G + g], (unsigned long long)(redl[0][g] + redl[1][g] + redl[2][g] + redl[3][g]));
+        atomicAdd((unsigned long long *)&a.vacc_s[(size_t)(c % VREP) * a.NH + h * G + g],
+                  (unsigned long long)(redl[0][g] + redl[1][g] + redl[2][g] + redl[3][g]));
     }
-    mem_complete();
+    exact_join<EPL, G>(a, h, c, nch, ored);
+}
+
+// ---- exact mode, window layers (decode): both passes in one launch ----
+// A window layer attends over at most (W-1)/64 + 2 64-position chunks per kv
+// head (at most WIN_MAXCH here), and the host launches this kernel only when
+// its whole grid fits the device at once, four times over (one launch per
+// hardware queue).  Workgroup (c, h) scores chunk c of kv head h into LDS and
+// hands data to the head's other workgroups through tagged slots in a.wslot:
+// each value is stored with a non-zero tag (WTAG added: the values are far
+// below 2^52), its single reader polls until every value it needs is
+// non-zero, then clears them.  Every slot is zero when a launch starts (zeroed
+// with the buffer, cleared by its reader in every launch), so there are no
+// counters, fences or resets: one store and one poll per hand-off.
+//   1. chunk maxima: workgroup c stores its G maxima into every reader's row
+//      (mx[h][r][g][c], r < nch); wave g of workgroup r polls mx[h][r][g][*]
+//      for the window maximum of head g;
+//   2. V partials: workgroup c stores its G*HD exact V-sums and its G softmax
+//      denominators (one copy per reader) into pv[h][c][*]; workgroup s
+//      finishes slice s of the head's G*HD outputs (ceil(G*HD / nch) each):
+//      sums the slice over the chunks, divides by the summed denominators
+//      (RNE) and writes ao.
+// The arithmetic is that of k_attn_exact_scores (PREP, 4 lanes per row)
+// followed by k_attn_exact_vsum, bit for bit: the sums are exact integers.
+// The polls are bounded (2^20 rounds), so every wave exits whatever happens;
+// with the grid resident the bound is never reached.
+constexpr int WIN_MAXCH = WIN_MAXCH_HOST;
+constexpr int64_t WTAG = (int64_t)1 << 62;
+template <int EPL, int G> constexpr size_t win_slots_per_head() {
+    return (size_t)WIN_MAXCH * G * WIN_MAXCH + (size_t)WIN_MAXCH * (G * EPL * 64 + WIN_MAXCH * G);
+}
+size_t window_slot_bytes(int NKV, int HD, int G) {
+    return (size_t)NKV * WIN_MAXCH * G * (2 * WIN_MAXCH + HD) * sizeof(int64_t);
+}
+
+template <int EPL, int G>
+__global__ __launch_bounds__(256) void k_attn_exact_window(AttnArgs a_in) {
+    constexpr int HD = EPL * 64, LPR = 4, RPW = 64 / LPR, NLD = EPL * 16 / LPR, UV = 2 * UNR;
+    constexpr int PVROW = G * HD + WIN_MAXCH * G;    // partial row: G*HD V-sums, then G denominators per reader
+    constexpr int PPT = (G * HD + WIN_MAXCH * (1 + G) + 255) / 256;   // polled values per thread (finisher)
+    static_assert(8 * UV == 64, "two V row groups per wave cover a 64-position chunk");
+    static_assert(G * HD + WIN_MAXCH * (1 + G) <= 4 * G * HD, "the finisher's values fit the V-sum LDS");
+    static_assert(win_slots_per_head<EPL, G>() == (size_t)WIN_MAXCH * G * (2 * WIN_MAXCH + HD), "slot layout");
+    AttnArgs a = a_in;
+    const int pos = a.st->pos, c = blockIdx.x, h = blockIdx.y;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    int cs, ce, nch;
+    chunk_range(a, pos, c, cs, ce, nch);
+    if (c >= nch) return;
+    __shared__ int4 qs[G][EPL * 16];
+    __shared__ int4 kn[EPL * 16];
+    __shared__ int32_t vn[HD];
+    __shared__ int32_t zs[G][64];
+    __shared__ int32_t ew[G][64];
+    __shared__ int zmax[4][G];
+    __shared__ int64_t Sl[G];
+    __shared__ int64_t ored[4][G][EPL * 64];
+    const int r = lane / LPR, k4 = lane % LPR, n = ce - cs;
+    const bool holds_pos = c == nch - 1;             // chunk ranges end at pos
+    int64_t *mxh = a.wslot + (size_t)h * win_slots_per_head<EPL, G>();      // [reader][g][chunk]
+    int64_t *pvh = mxh + (size_t)WIN_MAXCH * G * WIN_MAXCH;                 // [chunk][PVROW]
+    // requests: the preparation's inputs, the wave's K rows, then its first V
+    // row group (rows wave*UV.., clamped like every load); the second group
+    // ((wave+4)*UV..) follows the scores, in the K rows' registers
+    PrepIn<EPL> pin;
+    prep_load<EPL, G>(a, h, pos, wave, lane, holds_pos, pin);
+    __builtin_amdgcn_sched_barrier(0);
+    int4 kv[NLD];
+    load_kgroup<EPL, LPR>(a, h, cs, n, wave * RPW, r, k4, kv);
+    int32_t va[UV][EPL], vb[UV][EPL];
+    load_rows_c<EPL, UV>(a, h, cs, n, wave * UV, true, lane, va);
+    __builtin_amdgcn_sched_barrier(0);
+    prep_finish<EPL, G>(a, h, pos, wave, lane, holds_pos, pin, qs, kn, vn);
     __syncthreads();
-    if (threadIdx.x == 0) is_last = (arrive(&a.counter[h]) == nch - 1);
-    __syncthreads();
-    if (!is_last) return;
-    // the totals are read and cleared for the next launch in one atomic step;
-    // every exchange (denominators and V-sums) is issued before any total is
-    // used: one round trip
-    __shared__ int64_t Sg[G];
-    int64_t S = 0;
-    if (threadIdx.x < G)
+    // scores on the softmax grid: row wave*RPW + r, one pass covers the chunk
+    int mx = INT32_MIN;                              // lane with k4 == g tracks head g
+    {
+        const int j = wave * RPW + r;
+        int64_t acc[G];
         #pragma unroll
-        for (int r = 0; r < VREP; r++)
-            S += (int64_t)__hip_atomic_exchange((unsigned long long *)&a.vacc_s[(size_t)r * a.NH + h * G + threadIdx.x], 0ull,
-                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    constexpr int PT = (G * EPL * 64 + 255) / 256;   // elements per thread
-    int64_t tot[PT];
-    #pragma unroll
-    for (int k = 0; k < PT; k++) {
-        const int i = threadIdx.x + 256 * k;
-        tot[k] = 0;
-        if (i < G * HD)
+        for (int g = 0; g < G; g++) acc[g] = 0;
+        if (j < n) {
+            if (holds_pos && cs + j == pos) {
+                #pragma unroll
+                for (int i = 0; i < NLD; i++) kv[i] = kn[LPR * i + k4];
+            }
             #pragma unroll
-            for (int r = 0; r < VREP; r++)
-                tot[k] += (int64_t)__hip_atomic_exchange((unsigned long long *)&a.vacc[(size_t)r * QDh + (size_t)h * G * HD + i], 0ull,
-                                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (int i = 0; i < NLD; i++)
+                #pragma unroll
+                for (int g = 0; g < G; g++) {
+                    const int4 q = qs[g][LPR * i + k4];
+                    acc[g] += (int64_t)q.x * kv[i].x + (int64_t)q.y * kv[i].y + (int64_t)q.z * kv[i].z + (int64_t)q.w * kv[i].w;
+                }
+        }
+        #pragma unroll
+        for (int g = 0; g < G; g++) acc[g] = group_sum<LPR>(acc[g]);
+        if (j < n && k4 < G) {
+            int64_t tot = acc[0];
+            #pragma unroll
+            for (int g = 1; g < G; g++) if (k4 == g) tot = acc[g];
+            const float scv = (float)((double)tot / 4294967296.0) * a.ascale;
+            const int32_t z = (int32_t)llround_pow2<14>(scv);
+            zs[k4][j] = z;
+            mx = z;
+        }
     }
-    if (threadIdx.x < G) Sg[threadIdx.x] = S;
+    #pragma unroll
+    for (int g = 0; g < G; g++) {
+        const int t = wave_allmax_i(k4 == g ? mx : INT32_MIN);
+        if (lane == 0) zmax[wave][g] = t;
+    }
+    __syncthreads();
+    // 1. this chunk's maxima into every reader's row, then the second V group
+    if ((int)threadIdx.x < nch * G) {
+        const int rd = threadIdx.x / G, g = threadIdx.x % G;
+        int t = zmax[0][g];
+        for (int w = 1; w < 4; w++) t = zmax[w][g] > t ? zmax[w][g] : t;
+        st_agent(&mxh[((size_t)rd * G + g) * WIN_MAXCH + c], WTAG | (int64_t)(uint32_t)t);
+    }
+    load_rows_c<EPL, UV>(a, h, cs, n, (wave + 4) * UV, true, lane, vb);
+    // wave g < G: the window maximum of head g from this reader's row (lane k:
+    // chunk k, nch <= WIN_MAXCH <= 64), the row cleared; the island weights
+    // (0 past the chunk) and the chunk's softmax denominator
+    if (wave < G) {
+        const int g = wave;
+        int64_t *row = mxh + ((size_t)c * G + g) * WIN_MAXCH;
+        const bool mine = lane < nch;
+        int64_t v = WTAG;
+        for (int spins = 0; spins < (1 << 20); spins++) {
+            if (mine) v = ld_agent(&row[lane]);
+            if (__ballot(v == 0) == 0) break;
+            __builtin_amdgcn_s_sleep(1);
+        }
+        if (mine) st_agent(&row[lane], (int64_t)0);
+        const int M = wave_allmax_i(mine ? (int)(uint32_t)v : INT32_MIN);
+        const int32_t w = lane < n ? (int32_t)(exp_fixed((((int64_t)zs[g][lane] - (int64_t)M) * ONE) >> 14) >> 8) : 0;
+        ew[g][lane] = w;
+        const int64_t S = wsuml((int64_t)w);
+        if (lane == 0) Sl[g] = S;
+    }
+    // the workgroup holding pos sums the new V row from LDS (its own loads of
+    // that row predate the append)
+    if (holds_pos) {
+        const int jp = pos - cs, u0 = jp % UV;
+        #pragma unroll
+        for (int u = 0; u < UV; u++)
+            if (u == u0) {
+                #pragma unroll
+                for (int e = 0; e < EPL; e++) {
+                    if (jp / UV == wave) va[u][e] = vn[lane * EPL + e];
+                    if (jp / UV == wave + 4) vb[u][e] = vn[lane * EPL + e];
+                }
+            }
+    }
+    __syncthreads();
+    // the exact FP64 V-sum of k_attn_exact_vsum over the wave's 2 * UV rows
+    double o[G][EPL];
+    #pragma unroll
+    for (int g = 0; g < G; g++)
+        #pragma unroll
+        for (int e = 0; e < EPL; e++) o[g][e] = 0.0;
+    auto vsum = [&](const int32_t (&v)[UV][EPL], int j0) {
+        #pragma unroll
+        for (int u = 0; u < UV; u++) {
+            #pragma unroll
+            for (int g = 0; g < G; g++) {
+                const double w = (double)ew[g][j0 + u];
+                #pragma unroll
+                for (int e = 0; e < EPL; e++) o[g][e] = fma(w, (double)v[u][e], o[g][e]);
+            }
+        }
+    };
+    vsum(va, wave * UV);
+    vsum(vb, (wave + 4) * UV);
+    #pragma unroll
+    for (int g = 0; g < G; g++)
+        #pragma unroll
+        for (int e = 0; e < EPL; e++) ored[wave][g][lane * EPL + e] = (int64_t)o[g][e];
+    __syncthreads();
+    // 2. this chunk's V-sums and (one copy per reader) denominators
+    int64_t *prow = pvh + (size_t)c * PVROW;
+    for (int i = threadIdx.x; i < G * HD; i += 256) {
+        const int g = i / HD, d = i % HD;
+        st_agent(&prow[i], ored[0][g][d] + ored[1][g][d] + ored[2][g][d] + ored[3][g][d] + WTAG);
+    }
+    if ((int)threadIdx.x < nch * G) st_agent(&prow[G * HD + threadIdx.x], Sl[threadIdx.x % G] + WTAG);
+    // this workgroup's slice [e0, e0 + nl) of the head's G*HD outputs: value p
+    // of the nch x (nl + G) it needs is element e0 + j (j < nl) or
+    // denominator j - nl of chunk p / (nl + G)
+    const int L = (G * HD + nch - 1) / nch, e0 = c * L;
+    const int nl = e0 >= G * HD ? 0 : (G * HD - e0 < L ? G * HD - e0 : L), pw = nl + G, P = nch * pw;
+    int64_t pv[PPT];
+    int64_t *addr[PPT];
+    #pragma unroll
+    for (int k = 0; k < PPT; k++) {
+        const int p = threadIdx.x + 256 * k, ck = p / pw, j = p % pw;
+        addr[k] = pvh + (size_t)ck * PVROW + (j < nl ? e0 + j : G * HD + c * G + (j - nl));
+        pv[k] = p < P ? 0 : WTAG;
+    }
+    for (int spins = 0; spins < (1 << 20); spins++) {
+        bool ok = true;
+        #pragma unroll
+        for (int k = 0; k < PPT; k++)
+            if (pv[k] == 0) pv[k] = ld_agent(addr[k]);
+        #pragma unroll
+        for (int k = 0; k < PPT; k++) ok &= pv[k] != 0;
+        if (__syncthreads_and(ok)) break;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    int64_t *vals = &ored[0][0][0];                  // [nch][pw], untagged
+    #pragma unroll
+    for (int k = 0; k < PPT; k++) {
+        const int p = threadIdx.x + 256 * k;
+        if (p < P) { vals[p] = pv[k] - WTAG; st_agent(addr[k], (int64_t)0); }
+    }
+    __syncthreads();
+    __shared__ int64_t Sg[G];
+    if ((int)threadIdx.x < G) {
+        int64_t S = 0;
+        for (int ck = 0; ck < nch; ck++) S += vals[ck * pw + nl + threadIdx.x];
+        Sg[threadIdx.x] = S;
+    }
     __syncthreads();
     StatAcc sacc;
-    #pragma unroll
-    for (int k = 0; k < PT; k++) {
-        const int i = threadIdx.x + 256 * k;
-        if (i >= G * HD) break;
-        const float o = rne_div_to_float((i128)tot[k], Sg[i / HD], 16);
-        a.ao[(size_t)h * G * HD + i] = o;
+    for (int j = threadIdx.x; j < nl; j += 256) {
+        int64_t tot = 0;
+        for (int ck = 0; ck < nch; ck++) tot += vals[ck * pw + j];
+        const int e = e0 + j;
+        const float o = rne_div_to_float((i128)tot, Sg[e / HD], 16);
+        a.ao[(size_t)h * G * HD + e] = o;
         sacc.add(o);
     }
     if (a.stat_out) stat_flush_block(a.stat_out, sacc);      // max |ao| for the O GEMV
-    if (threadIdx.x == 0) reset_counter(&a.counter[h]);
 }
 
 // decode (B = false: position from the step state) and batched prefill
@@ -883,6 +1128,10 @@ template <int EPL, int G, bool B> static void attn_dispatch_b(const AttnArgs &a,
     else if (a.mode == FLOAT) hipLaunchKernelGGL((k_attn_float<EPL, G, B, false>), grid, dim3(256), 0, s, a);
     else {
         const bool wide = a.chunk > 64;
+        if (!B && prep && a.one_launch && a.wslot && a.chunk == 64 && grid_chunks <= WIN_MAXCH) {
+            hipLaunchKernelGGL((k_attn_exact_window<EPL, G>), grid, dim3(256), 0, s, a);
+            return;
+        }
         if (!B && prep) {
             if (wide) hipLaunchKernelGGL((k_attn_exact_scores<EPL, G, B, !B, 8>), grid, dim3(256), 0, s, a);
             else hipLaunchKernelGGL((k_attn_exact_scores<EPL, G, B, !B, 4>), grid, dim3(256), 0, s, a);
@@ -931,6 +1180,23 @@ template <int EPL, int G> static int attn_cap_t() {
         hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, k_attn_exact_vsum<EPL, G, false, 2 * UNR>, 256, 0) != hipSuccess)
         return 0;
     return a < b ? a : b;
+}
+template <int EPL, int G> static int window_cap_t() {
+    int a = 0;
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(&a, k_attn_exact_window<EPL, G>, 256, 0) == hipSuccess ? a : 0;
+}
+int window_capacity(int HD, int G) {
+    int nb = 0, dev = 0, ncu = 0;
+    if (HD == 256 && G == 2) nb = window_cap_t<4, 2>();
+    else if (HD == 128 && G == 2) nb = window_cap_t<2, 2>();
+    else if (HD == 128 && G == 4) nb = window_cap_t<2, 4>();
+    else if (HD == 64 && G == 2) nb = window_cap_t<1, 2>();
+    else if (HD == 256 && G == 4) nb = window_cap_t<4, 4>();
+    else if (HD == 64 && G == 4) nb = window_cap_t<1, 4>();
+    if (nb <= 0 || hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return 0;
+    return nb * ncu;
 }
 int attn_capacity(int HD, int G) {
     int nb = 0, dev = 0, ncu = 0;

@@ -438,6 +438,7 @@ struct StepScratch {
     int *counter = nullptr, *zscratch = nullptr;
     int64_t *vacc = nullptr, *vacc_s = nullptr;
     VecStat *stats = nullptr;
+    int64_t *wslot = nullptr;                // one-launch window attention slots (NULL: two-kernel path)
 };
 
 }  // namespace
@@ -493,6 +494,7 @@ struct sp_kvdecode_handle {
         int lstride = 0, mchunks = 0, kstride = 0;
     } rec;
     int attn_cap = 0;                        // exact decode attention workgroups resident at once
+    int win_cap = 0;                         // one-launch window attention workgroups resident at once
     void *scratch = nullptr;
     int built = 0;                           // tables and scratch allocated (reusable as a shell)
     // batched prefill buffers ([TB][...] per token), allocated on first use
@@ -696,11 +698,19 @@ int ring2_spill(sp_kvdecode_handle *h, int pos) {
     return 0;
 }
 
+// Bytes of the one-launch window attention's slots: models with window
+// layers whose window spans at most WIN_MAXCH_HOST chunks (0: none).
+size_t window_slots(const DevModel *m) {
+    if (!m->gemma || m->SW <= 0 || (m->SW - 1) / 64 + 2 > WIN_MAXCH_HOST) return 0;
+    return window_slot_bytes(m->NKV, m->HD, m->NH / m->NKV);
+}
+
 int alloc_scratch(sp_kvdecode_handle *h) {
     const DevModel *m = h->m;
     const int QD = m->NH * m->HD, KVD = m->NKV * m->HD;
     h->max_chunks = (h->pmax + 15) / 16 + 2;
     h->attn_cap = attn_capacity(m->HD, m->NH / m->NKV);
+    h->win_cap = window_capacity(m->HD, m->NH / m->NKV);
     struct Item { void **p; size_t n; };
     const size_t part_bytes = (size_t)m->NH * h->max_chunks * m->HD * 8;
     const size_t ml_bytes = (size_t)m->NH * h->max_chunks * 16;
@@ -720,6 +730,7 @@ int alloc_scratch(sp_kvdecode_handle *h) {
         {(void **)&h->vacc, (size_t)QD * 8 * VREP}, {(void **)&h->vacc_s, (size_t)m->NH * 8 * VREP},
         {(void **)&h->d_st, sizeof(DState) * 4}, {(void **)&h->vclamp, 64},
         {(void **)&h->stats, (size_t)m->NL * STAT_PER_LAYER * STAT_REP * sizeof(VecStat)},
+        {(void **)&h->ss.wslot, window_slots(m)},
     };
     size_t tot = 0;
     for (auto &it : items) tot = align_up(tot + it.n, 256);
@@ -732,6 +743,7 @@ int alloc_scratch(sp_kvdecode_handle *h) {
     h->ss.gacc = h->gacc; h->ss.gcnt = h->gcnt; h->ss.acc_rows = h->acc_rows;
     h->ss.part = h->part; h->ss.part_ml = h->part_ml; h->ss.counter = h->counter; h->ss.zscratch = h->zscratch;
     h->ss.vacc = h->vacc; h->ss.vacc_s = h->vacc_s; h->ss.stats = h->stats;
+    if (!window_slots(m)) h->ss.wslot = nullptr;
     HIPCHK(hipHostMalloc(&h->h_st, sizeof(DState) * 4, hipHostMallocDefault), "pinned state alloc");
     HIPCHK(hipHostMalloc(&h->h_logits, (size_t)m->V * 4, hipHostMallocDefault), "pinned logits alloc");
     h->built = 1;
@@ -985,6 +997,11 @@ void enqueue_body(sp_kvdecode_handle *h, const StepShape &sh, TimeCb cb, void *c
         a.chunk = glob ? sh.chunk_global : sh.chunk_local;
         a.vchunk = glob ? sh.vchunk_global : 0;
         a.stat_out = st(l, STAT_AO);
+        // window layers in exact mode: one launch when its grid, 4 times over
+        // (one per hardware queue), fits the device at once
+        a.wslot = ss.wslot;
+        a.one_launch = a.win >= 0 && h->mode == EXACT && ss.wslot && sh.grid_local <= WIN_MAXCH_HOST &&
+                       (size_t)sh.grid_local * m->NKV * 4 <= (size_t)h->win_cap;
         if (h->rec.B > 0 && a.win < 0) { a.rec_R = h->rec.Rb; a.rec_r = h->rec.r; a.rec_side = side_of(h, l); }
         const int cls = (glob || a.win < 0) ? 5 : 6, grid = glob ? sh.grid_global : sh.grid_local;
         if (sh.route && a.rec_r) {
@@ -1312,9 +1329,11 @@ bool carve_noalloc(const sp_kvdecode_handle *h, uint8_t *base, StepScratch &ss, 
         {(void **)&ss.zscratch, exact ? (size_t)m->NH * mc * 16 * 4 : 256}, {(void **)&ss.counter, 256},
         {(void **)&ss.vacc, QD * 8 * VREP}, {(void **)&ss.vacc_s, (size_t)m->NH * 8 * VREP},
         {(void **)&ss.stats, (size_t)m->NL * STAT_PER_LAYER * STAT_REP * sizeof(VecStat)},
+        {(void **)&ss.wslot, exact ? window_slots(m) : 0},
     };
     size_t off = 0;
     for (auto &it : items) { *it.p = base + off; off = align_up(off + it.n, 256); }
+    if (!exact || !window_slots(m)) ss.wslot = nullptr;
     ss.acc_rows = h->acc_rows;
     *used = off;
     return off <= NOALLOC_SCRATCH_BYTES;

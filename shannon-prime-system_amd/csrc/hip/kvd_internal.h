@@ -112,6 +112,12 @@ struct AttnArgs {
     int rec_r;
     float *rec_side;
     float *rec_pq;           // routed step: each q head's projection [NH][rec_r] (NULL: not needed)
+    // exact decode, window layer: scores and V-sum in one launch, whose grid
+    // the host has checked fits the device at once (window_capacity), handing
+    // data between workgroups through tagged slots (window_slot_bytes, zero
+    // between launches)
+    int one_launch;
+    int64_t *wslot;
 };
 
 // ARM recall over one global layer's pages (decode): the router picks each q
@@ -261,6 +267,9 @@ void launch_rope_table(const DState *st, int HD, int mode, float base_g, float b
                        const int64_t *fq_g, const int64_t *fq_l, float *out, hipStream_t s);
 void launch_attention(const AttnArgs &a, int grid_chunks, hipStream_t s);
 int  attn_capacity(int HD, int G);
+int  window_capacity(int HD, int G);   // workgroups of the one-launch window attention resident at once (0: none)
+size_t window_slot_bytes(int NKV, int HD, int G);   // its tagged slots (zeroed once, kept zero by the kernel)
+constexpr int WIN_MAXCH_HOST = 32;      // chunks per kv head it takes (the window of at most 1 922 positions)
 constexpr int ATTN_MAXCH = 512;         // largest chunk of the two-kernel attention
 void launch_prep_attention(const AttnArgs &a, int grid_chunks, hipStream_t s);   // qk_prep + attention, fused where possible
 bool attention_fuses_prep(const AttnArgs &a);

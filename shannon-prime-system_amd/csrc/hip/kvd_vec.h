@@ -197,10 +197,23 @@ __device__ __forceinline__ void stat_reduce(int64_t q, float m, int64_t &ss, flo
     mx = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 63));
 }
 // The exact-mode RMS scale of a vector whose sum of squares a producer accumulated
-__device__ __forceinline__ NormScale stat_scale(int64_t ss, int n) {
-    NormScale s; s.f = 0.0f; s.inv = 0; s.invd = 0.0; s.zero = 0;
-    if (ss == 0) { s.zero = 1; return s; }
-    s.inv = rms_inv_q72(n, ss);
+// rms_inv_q72 of a workgroup-uniform sum of squares (0 for ss == 0), formed by
+// wave 0 alone and handed to the other waves through the LDS slot: the exact
+// inverse (double divide and square root, 128-bit corrections: a few hundred
+// instructions) would otherwise run once per wave, on SIMDs that several
+// waves share.  Every thread of the workgroup calls this (it has a barrier);
+// each call site has a slot of its own.
+__device__ __forceinline__ int64_t rms_inv_wg(int n, int64_t ss, int64_t *slot) {
+    if (threadIdx.x < 64) {
+        const int64_t v = ss ? rms_inv_q72(n, ss) : 0;
+        if (threadIdx.x == 0) *slot = v;
+    }
+    __syncthreads();
+    return *slot;
+}
+__device__ __forceinline__ NormScale stat_scale(int64_t ss, int n, int64_t *slot) {
+    NormScale s; s.f = 0.0f; s.inv = 0; s.invd = 0.0; s.zero = ss == 0;
+    s.inv = rms_inv_wg(n, ss, slot);
     s.invd = (double)s.inv;
     return s;
 }
@@ -210,15 +223,16 @@ __device__ __forceinline__ int sh_of_max(float m) {
     return 22 - e;
 }
 
-__device__ NormScale norm_finish(const SumSq &p, int n, float eps, int mode, void *red) {
+// slot: an LDS int64 of the call site's own (exact mode's broadcast inverse)
+__device__ NormScale norm_finish(const SumSq &p, int n, float eps, int mode, void *red, int64_t *slot) {
     NormScale s; s.f = 0.0f; s.inv = 0; s.invd = 0.0; s.zero = 0;
     if (mode == FLOAT) {
         const double ss = block_sum<double>(p.f, (double *)red);
         s.f = 1.0f / sqrtf((float)(ss / n) + eps);
     } else {
         const int64_t ss = block_sum<int64_t>(p.i, (int64_t *)red);
-        if (ss == 0) { s.zero = 1; return s; }
-        s.inv = rms_inv_q72(n, ss);
+        s.zero = ss == 0;
+        s.inv = rms_inv_wg(n, ss, slot);
         s.invd = (double)s.inv;                       // inv < 2^43: exact
     }
     return s;
@@ -304,6 +318,7 @@ template <int PRO>
 __device__ int input_transform(const ProArgs &p, int mode, const ProLoads &L, float *xf, void *red, bool write_x,
                                int c_lo = 0, int c_hi = 0x7FFFFFFF) {
     const int n = p.n, T = blockDim.x, tid = threadIdx.x;
+    __shared__ int64_t bcs[2];                       // broadcast RMS inverses: branch norm, pre-norm
     float m = 0.0f;
     if constexpr (PRO == PRO_PLAIN) {
         // the producer's maximum: no pass over the vector here (callers read
@@ -334,7 +349,7 @@ __device__ int input_transform(const ProArgs &p, int mode, const ProLoads &L, fl
             if (pro_uses_stat<PRO>(p, mode)) {
                 int64_t ss; float mx;
                 stat_reduce(L.sq, L.sm, ss, mx);             // the producer's exact sum of squares
-                sd = stat_scale(ss, n);
+                sd = stat_scale(ss, n, &bcs[0]);
             } else if (p.post_w) {
                 SumSq q;
                 #pragma unroll
@@ -342,7 +357,7 @@ __device__ int input_transform(const ProArgs &p, int mode, const ProLoads &L, fl
                     if (4 * (k * T + tid) < n)
                         #pragma unroll
                         for (int c = 0; c < 4; c++) q.add(f4c(dv[k], c), mode);
-                sd = norm_finish(q, n, p.eps, mode, red_slot(red, 0));
+                sd = norm_finish(q, n, p.eps, mode, red_slot(red, 0), &bcs[0]);
             }
             const bool wr = write_x && p.x_out;
             if (mode == EXACT) {
@@ -417,8 +432,9 @@ __device__ int input_transform(const ProArgs &p, int mode, const ProLoads &L, fl
                 __syncthreads();
                 ss = rs[0]; pm = rm[0];
                 for (int w = 1; w < (T >> 6); w++) { ss += rs[w]; pm = fmax(pm, rm[w]); }
-                NormScale s; s.f = 0.0f; s.inv = 0; s.invd = 0.0; s.zero = ss == 0;
-                if (!s.zero) { s.inv = rms_inv_q72(n, ss); s.invd = (double)s.inv; }
+                NormScale s; s.f = 0.0f; s.zero = ss == 0;
+                s.inv = rms_inv_wg(n, ss, &bcs[1]);
+                s.invd = (double)s.inv;
                 const double pmx = pm * s.invd;
                 if (s.zero || (pm < 9007199254740992.0 && pmx < 4611686018427387904.0)) {
                     m = s.zero ? 0.0f : (float)(pmx * 2.220446049250313e-16);
@@ -472,7 +488,7 @@ __device__ int input_transform(const ProArgs &p, int mode, const ProLoads &L, fl
             if (4 * (k * T + tid) < n)
                 #pragma unroll
                 for (int c = 0; c < 4; c++) q.add(f4c(xv[k], c), mode);
-        const NormScale s = norm_finish(q, n, p.eps, mode, red_slot(red, 1));
+        const NormScale s = norm_finish(q, n, p.eps, mode, red_slot(red, 1), &bcs[1]);
         #pragma unroll
         for (int k = 0; k < PB4; k++) {
             const int i = 4 * (k * T + tid);
@@ -500,13 +516,13 @@ __device__ int input_transform(const ProArgs &p, int mode, const ProLoads &L, fl
                 #pragma unroll
                 for (int k = 0; k < PB; k++) { const int i = base + k * T + tid; if (i < n) xf[i] = a[k]; }
             }
-            s = norm_finish(q, n, p.eps, mode, red_slot(red, 1));
+            s = norm_finish(q, n, p.eps, mode, red_slot(red, 1), &bcs[1]);
         } else {
             NormScale sd; sd.f = 0.0f; sd.inv = 0; sd.invd = 0.0; sd.zero = 0;
             if (pro_uses_stat<PRO>(p, mode)) {
                 int64_t ss; float mx;
                 stat_reduce(L.sq, L.sm, ss, mx);
-                sd = stat_scale(ss, n);
+                sd = stat_scale(ss, n, &bcs[0]);
             } else if (p.post_w) {
                 SumSq q;
                 for (int base = 0; base < n; base += PB * T) {
@@ -516,7 +532,7 @@ __device__ int input_transform(const ProArgs &p, int mode, const ProLoads &L, fl
                     #pragma unroll
                     for (int k = 0; k < PB; k++) q.add(a[k], mode);
                 }
-                sd = norm_finish(q, n, p.eps, mode, red_slot(red, 0));
+                sd = norm_finish(q, n, p.eps, mode, red_slot(red, 0), &bcs[0]);
             }
             // residual add (+ sandwich norm of the branch), sum of squares of the result
             SumSq q;
@@ -537,7 +553,7 @@ __device__ int input_transform(const ProArgs &p, int mode, const ProLoads &L, fl
                     if (i < n) { xf[i] = r; if (wr) p.x_out[i] = r; q.add(r, mode); }
                 }
             }
-            s = norm_finish(q, n, p.eps, mode, red_slot(red, 1));
+            s = norm_finish(q, n, p.eps, mode, red_slot(red, 1), &bcs[1]);
         }
         // xf <- norm(xf) * w; running max
         for (int base = 0; base < n; base += PB * T) {

@@ -24,6 +24,11 @@ SMALL = {
                        head_dim=128, n_ff=4352, vocab=3000),
     "gemma3-wide": dict(arch_id=spkv.ARCH_GEMMA3, n_layers=6, hidden=2304, n_heads=8, n_kv_heads=4,
                         head_dim=256, n_ff=4352, vocab=3000, swa_window=16),
+    # windows over several 64-position chunks (the one-launch window attention)
+    "gemma3-w200": dict(arch_id=spkv.ARCH_GEMMA3, n_layers=6, hidden=512, n_heads=4, n_kv_heads=2,
+                        head_dim=256, n_ff=1024, vocab=2048, swa_window=200),
+    "gemma3-g4w130": dict(arch_id=spkv.ARCH_GEMMA3, n_layers=6, hidden=512, n_heads=8, n_kv_heads=2,
+                          head_dim=128, n_ff=1024, vocab=2048, swa_window=130),
 }
 
 

@@ -455,6 +455,40 @@ def test_window_ring_rewind(tmpdir_models):
     be.close(); close_all(s, o, m)
 
 
+@pytest.mark.parametrize("name", ["gemma3-w200", "gemma3-g4w130"])
+@pytest.mark.parametrize("ring", [False, True])
+def test_window_layers_one_launch(tmpdir_models, name, ring):
+    """Exact decode on window layers scores and sums V in one launch whose
+    workgroups meet on a per-kv-head barrier.  Windows of 200 and 130 positions
+    span 3 to 5 64-position chunks (the first and last ragged); decoding from
+    position 179 to 399 crosses the point where the window starts to slide and,
+    on a ring of window + 8 positions (plain launches), wraps it.  Logits every
+    step and the last 100 positions' K/V of every layer bit-exact."""
+    spm, spt = model_files(tmpdir_models, name)
+    m = spkv.Model(spm, spt); s = spkv.Session(m, 512)
+    be = spkv.Backend(spkv.l1().sp_session_qwen3_model(s.h), 512, exact=True, graph=not ring)
+    if ring:
+        spkv.check(spkv.kv().sp_hipkv_set_max_rewind(be.h, 8), "set_max_rewind")
+    o = orc.Oracle(spm, 512, orc.EXACT)
+    lg = np.zeros(o.V, np.float32)
+    toks = prompt(180, o.V, seed=11)
+    be.prefill(toks[:-1])
+    for t in toks[:-1]:
+        o.step(int(t), False)
+    t = int(toks[-1])
+    for k in range(220):
+        be.decode(t, lg)
+        ol = o.step(t)
+        assert same_bits(lg, ol), f"step {k}: max rel {rel(lg, ol):.3e}"
+        t = int(ol.argmax())
+    pos, kvd = be.position(), o.NKV * o.HD
+    for layer in range(o.NL):
+        kg, vg = be.read_kv(layer, pos - 100, 100, kvd)
+        kc, vc = o.kv(layer, pos - 100, 100)
+        assert same_bits(kg, kc) and same_bits(vg, vc), f"layer {layer}"
+    be.close(); close_all(s, o, m)
+
+
 def test_greedy_device_loop_matches_abi(tmpdir_models):
     """The device-resident greedy loop (argmax on the GPU) generates the same tokens
     as host-driven sp_decode_step + argmax, and as the oracle (exact mode)."""
