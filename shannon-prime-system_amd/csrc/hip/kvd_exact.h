@@ -110,13 +110,18 @@ __device__ __forceinline__ int64_t tanh_fixed(int64_t t) {
     int64_t num = (2 * e2) << FB;                  // <= 2^61, quotient <= 2^31
     return (int64_t)s * (ONE - udiv_small(num, ONE + e2));
 }
+// roundf (half away from zero) in three instructions instead of six: adding
+// the float just below 1/2, with v's sign, and truncating gives roundf(v)
+// bit for bit for every float (checked over all 2^32 bit patterns by the
+// tests: no carry of the sum can round up a value below a half).
+__device__ __forceinline__ float round_away(float v) { return truncf(v + copysignf(0x1.fffffep-2f, v)); }
 // round half away from zero of a double to int64 (llround)
 __device__ __forceinline__ int64_t llround_d(double d) { return (int64_t)round(d); }
 // llround(x * 2^SH) of a float: x * 2^SH is exact in float short of overflow,
 // roundf is exact, and results below 2^31 convert in 32 bits; anything else
 // takes the double route.  The same value either way.
 template <int SH> __device__ __forceinline__ int64_t llround_pow2(float x) {
-    const float r = roundf(x * (float)(1 << SH));
+    const float r = round_away(x * (float)(1 << SH));
     if (fabsf(r) < 2147483648.0f) return (int64_t)(int32_t)r;
     return llround_d((double)x * (double)(1 << SH));
 }

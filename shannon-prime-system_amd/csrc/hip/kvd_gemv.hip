@@ -63,7 +63,7 @@ __device__ __forceinline__ void gemv_pro_load(const ProArgs &p, int mode, GemvLo
 }
 
 template <int PRO>
-__device__ int gemv_prologue(const ProArgs &p, int mode, const GemvLoads &L, float *xf, uint4 *dig, int b_lo, int b_hi, void *red) {
+__device__ __forceinline__ int gemv_prologue(const ProArgs &p, int mode, const GemvLoads &L, float *xf, uint4 *dig, int b_lo, int b_hi, void *red) {
     const int T = blockDim.x, tid = threadIdx.x;
     const int sh = input_transform<PRO>(p, mode, L.pro, xf, red, blockIdx.x == 0, b_lo * 32, b_hi * 32);
     if (sh == SH_ZERO) return SH_ZERO;
@@ -221,8 +221,10 @@ __device__ __forceinline__ int eb_of(uint64_t ebw, int r) { return (int)(int8_t)
 // for the next launch.  The first weights are requested before the prologue
 // (after the prologue's own loads), and each task requests the next task's
 // weights before its own epilogue.
+// PAIRED (gate/up: one workgroup per CU, the plan sees to it) may use 256
+// registers; the others run up to 4 waves per SIMD, two workgroups per CU.
 template <int PRO, bool PAIRED, bool WIDE>
-__global__ __launch_bounds__(512, 4) void k_gemv(GemvArgs a) {   // 4 waves per SIMD: two workgroups per CU
+__global__ __launch_bounds__(512, PAIRED ? 2 : 4) void k_gemv(GemvArgs a) {
     extern __shared__ uint4 smem4[];
     const int nblk = (a.cols + 31) / 32, nsplit = a.nsplit, bps = a.bps;
     const int split = blockIdx.x % nsplit;
@@ -252,6 +254,12 @@ __global__ __launch_bounds__(512, 4) void k_gemv(GemvArgs a) {   // 4 waves per 
     const int sh = gemv_prologue<PRO>(a.pro, a.mode, L, xf, dig, b_lo, b_hi, red);
     const int nit = (nb + 63) / 64;
     StatAcc sacc;                                          // this thread's outputs, for stat_out
+    // PAIRED: the exact activation (a few hundred instructions on the holder
+    // lanes) runs once per two tasks: a task's (gate, up, row) waits parked in
+    // lanes 32.. until the next task's gate rows (lanes 0..31) join it
+    bool parked = false;                                   // wave-uniform
+    float pg = 0.0f, pu = 0.0f;
+    int pj = -1;
 
     for (; grp < a.groups; grp += gstride) {
         const uint64_t ebw = ebn;                          // this task's (ebn is reloaded for the next)
@@ -337,26 +345,37 @@ __global__ __launch_bounds__(512, 4) void k_gemv(GemvArgs a) {   // 4 waves per 
                 const float y = sh == SH_ZERO ? 0.0f : rne_i64_scaled(tot, ebm - sh);
                 // lane (myrow*8) owns row myrow's total; paired rows fetch their up partner
                 const float partner = __shfl_xor(y, 32, 64);          // row myrow^4
-                bool wrote = false;
-                float sv = 0.0f;                                      // the statistic's input
-                if (holder) {
-                    if (PAIRED) {
-                        if (myrow < HR) {
-                            const int j = t.row0 + myrow;
-                            a.seg[0].out[j] = y; a.seg[1].out[j] = partner;
-                            sv = act_apply(y, partner, a.act, a.mode);
-                            a.act_out[j] = sv;
-                            wrote = true;
+                if (PAIRED) {
+                    // lanes 0, 8, 16, 24 hold this task's gate rows (partner:
+                    // the up row); lanes 32.. the parked task's
+                    const int j = holder && myrow < HR ? t.row0 + myrow : -1;
+                    if (j >= 0) { a.seg[0].out[j] = y; a.seg[1].out[j] = partner; }
+                    if (parked) {
+                        const float g = lane < 32 ? y : pg, u = lane < 32 ? partner : pu;
+                        const int jj = lane < 32 ? j : pj;
+                        if (jj >= 0) {
+                            const float sv = act_apply(g, u, a.act, a.mode);
+                            a.act_out[jj] = sv;
+                            sacc.add(sv);
                         }
                     } else {
-                        a.seg[t.seg].out[t.row0 + myrow] = y;
-                        sv = y; wrote = true;
+                        // park: lane l + 32 takes lane l's gate value (its own y is the up value)
+                        pg = __shfl_xor(y, 32, 64); pu = y; pj = __shfl_xor(j, 32, 64);
+                        if (lane < 32) pj = -1;
                     }
+                    parked = !parked;
+                } else if (holder) {
+                    a.seg[t.seg].out[t.row0 + myrow] = y;
+                    sacc.add(y);
                 }
-                if (wrote) sacc.add(sv);
             }
         }
         t = tn;
+    }
+    if (PAIRED && !WIDE && parked && pj >= 0) {       // the last parked task
+        const float sv = act_apply(pg, pu, a.act, a.mode);
+        a.act_out[pj] = sv;
+        sacc.add(sv);
     }
     if (a.stat_out) stat_flush_block(a.stat_out, sacc);
 }
@@ -380,7 +399,7 @@ GemvPlan gemv_plan(int nrows_total, int cols, int paired, int wide) {
     GemvPlan p;
     const int nblk = (cols + 31) / 32;
     p.groups = paired ? (nrows_total + GEMV_R / 2 - 1) / (GEMV_R / 2) : (nrows_total + GEMV_R - 1) / GEMV_R;
-    int cap = 2 * num_cu();                             // workgroups
+    int cap = (paired ? 1 : 2) * num_cu();              // workgroups (paired instances hold one per CU)
     const int max_split = (nblk + 63) / 64;
     int want = (cap * GEMV_WAVES + p.groups - 1) / p.groups;
     // a split costs every task an atomic hand-off; it only pays when whole

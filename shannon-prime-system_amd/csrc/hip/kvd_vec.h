@@ -137,7 +137,7 @@ struct SumSq {
         if (mode == FLOAT) { f += (double)v * (double)v; return; }
         // llround(v * 2^16): roundf of the exact float product is that integer;
         // below 2^31 its square is one 32 x 32 -> 64 multiply
-        const float r = roundf(v * 65536.0f);
+        const float r = round_away(v * 65536.0f);
         if (fabsf(r) < 2147483648.0f) { const int32_t q = (int32_t)r; i += (int64_t)q * q; }
         else { const int64_t q = llround_q16(v); i += q * q; }
     }
@@ -152,7 +152,7 @@ struct StatAcc {
     int64_t q2 = 0;
     float mx = 0.0f;
     __device__ __forceinline__ void add(float v) {
-        const float r = roundf(v * 65536.0f);
+        const float r = round_away(v * 65536.0f);
         if (fabsf(r) < 2147483648.0f) { const int32_t q = (int32_t)r; q2 += (int64_t)q * q; }
         else { const int64_t q = llround_q16(v); q2 += q * q; }
         mx = fmaxf(mx, fabsf(v));
@@ -246,7 +246,7 @@ __device__ NormScale norm_finish(const SumSq &p, int n, float eps, int mode, voi
 __device__ __forceinline__ float norm_apply(float x, float w, const NormScale &s, int mode) {
     if (mode == FLOAT) return x * s.f * w;
     if (s.zero) return 0.0f;
-    const double dx = (double)roundf(x * 65536.0f) * (double)roundf(w * 65536.0f);
+    const double dx = (double)round_away(x * 65536.0f) * (double)round_away(w * 65536.0f);
     if (fabs(dx) < 9007199254740992.0) {              // 2^53
         const double pr = dx * s.invd;
         if (fabs(pr) < 4611686018427387904.0)          // 2^62
@@ -379,14 +379,14 @@ __device__ int input_transform(const ProArgs &p, int mode, const ProLoads &L, fl
                         const float d = f4c(dv[k], c);
                         float nd = d;
                         if (pn) {
-                            const double dx = (double)roundf(d * 65536.0f) * (double)roundf(f4c(pw[k], c) * 65536.0f);
+                            const double dx = (double)round_away(d * 65536.0f) * (double)round_away(f4c(pw[k], c) * 65536.0f);
                             const double pr = dx * sd.invd;
                             bad |= !(fabs(dx) < 9007199254740992.0) | !(fabs(pr) < 4611686018427387904.0);
                             nd = sd.zero ? 0.0f : (float)(pr * 2.220446049250313e-16);
                         }
                         const float r = f4c(xv[k], c) + nd;
                         f4s(xv[k], c, r);
-                        const float r16 = roundf(r * 65536.0f), w16 = roundf(f4c(nw[k], c) * 65536.0f);
+                        const float r16 = round_away(r * 65536.0f), w16 = round_away(f4c(nw[k], c) * 65536.0f);
                         bad |= !(fabsf(r16) < 2147483648.0f);
                         const int32_t q = (int32_t)r16;
                         ss += (int64_t)q * q;
@@ -405,10 +405,10 @@ __device__ int input_transform(const ProArgs &p, int mode, const ProLoads &L, fl
                         const float d = p.delta[i];
                         const float r = p.x[i] + (pn ? norm_apply(d, p.post_w[i], sd, mode) : d);
                         xf[i] = r;
-                        const float r16 = roundf(r * 65536.0f);
+                        const float r16 = round_away(r * 65536.0f);
                         if (fabsf(r16) < 2147483648.0f) { const int32_t q = (int32_t)r16; ss += (int64_t)q * q; }
                         else { const int64_t q = llround_q16(r); ss += q * q; }
-                        const double dx2 = fabs((double)r16 * (double)roundf(p.norm_w[i] * 65536.0f));
+                        const double dx2 = fabs((double)r16 * (double)round_away(p.norm_w[i] * 65536.0f));
                         pm = dx2 < 9007199254740992.0 ? fmax(pm, dx2) : INFINITY;     // NaN too
                     }
                     #pragma unroll
@@ -445,8 +445,8 @@ __device__ int input_transform(const ProArgs &p, int mode, const ProLoads &L, fl
                             float4 y;
                             #pragma unroll
                             for (int c = 0; c < 4; c++)
-                                f4s(y, c, s.zero ? 0.0f : (float)(((double)roundf(f4c(xv[k], c) * 65536.0f) *
-                                                                   (double)roundf(f4c(nw[k], c) * 65536.0f) * s.invd) *
+                                f4s(y, c, s.zero ? 0.0f : (float)(((double)round_away(f4c(xv[k], c) * 65536.0f) *
+                                                                   (double)round_away(f4c(nw[k], c) * 65536.0f) * s.invd) *
                                                                   2.220446049250313e-16));
                             *(float4 *)(xf + i) = y;
                         }
