@@ -92,6 +92,7 @@ __device__ __forceinline__ int gemv_prologue(const ProArgs &p, int mode, const G
 }
 
 // ------------------------------------------------------- main kernel
+constexpr int64_t SPLIT_TAG = (int64_t)1 << 62;          // marks a parked split partial
 __device__ __forceinline__ int32_t dot_digits(const uint4 c, const uint4 *D) {
     // sum over the 32 codes of code * xq, xq = sum_k 16^k digit_k, Horner form
     // folded into the dot accumulator: a = 16 a + dots of plane k (|a| < 2^30
@@ -218,7 +219,8 @@ __device__ __forceinline__ int eb_of(uint64_t ebw, int r) { return (int)(int8_t)
 // With nsplit > 1 every task adds its exact int64 row partials atomically into
 // accbuf (order-free, so still bit-exact); the wave that completes a group's
 // last split converts the totals, writes the outputs and clears accbuf/gcnt
-// for the next launch.  The first weights are requested before the prologue
+// for the next launch.  Two splits of unpaired rows need no counter: each row's
+// partials meet through one atomic exchange on its accbuf slot.  The first weights are requested before the prologue
 // (after the prologue's own loads), and each task requests the next task's
 // weights before its own epilogue.
 // PAIRED (gate/up: one workgroup per CU, the plan sees to it) may use 256
@@ -326,8 +328,21 @@ __global__ __launch_bounds__(512, PAIRED ? 2 : 4) void k_gemv(GemvArgs a) {
             const int myrow = ((lane >> 5) & 1) * 4 + ((lane >> 4) & 1) * 2 + ((lane >> 3) & 1);
             const int rr = myrow % per;
             const bool holder = (lane & 7) == 0 && rr < t.nvalid;
-            bool finish = true;
-            if (nsplit > 1) {
+            bool finish = true;                                // per lane on the two-split path
+            if (!PAIRED && nsplit == 2) {
+                // one atomic exchange per row: the first split to arrive
+                // leaves its partial, tagged with 2^62 (|partial| < 2^62: at
+                // most 2^lg blocks of |d| <= 2^30 times Ms < 2^(32-lg)), and
+                // is done; the second takes it, finishes the row and clears
+                // the slot
+                int64_t *slot = a.accbuf + t.grow0 + myrow;
+                int64_t other = 0;
+                if (holder)
+                    other = (int64_t)__hip_atomic_exchange((unsigned long long *)slot, (unsigned long long)(tot + SPLIT_TAG),
+                                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                finish = other != 0;
+                if (finish) { tot += other - SPLIT_TAG; st_agent(slot, (int64_t)0); }
+            } else if (nsplit > 1) {
                 int64_t *slot = a.accbuf + (PAIRED ? (myrow >= HR ? a.seg[0].w.rows : 0) + t.row0 + rr : t.grow0 + myrow);
                 if (holder) atomicAdd((unsigned long long *)slot, (unsigned long long)tot);
                 mem_complete();
