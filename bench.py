@@ -44,7 +44,7 @@ KERNEL_NAMES = {
     "lm_head_gemv_q4b": ["kvd::k_gemv<2, false, false>"],
     "gqa_decode_attn_global": ["kvd::k_attn_exact_scores<EPL, G, false, true, 8> + kvd::k_attn_exact_vsum<EPL, G, false, 8>",
                                "[kvd::k_qk_prep<false> + kvd::k_attn_float<EPL, G, false, SPINOR>]"],
-    "gqa_decode_attn_window": ["kvd::k_attn_exact_scores<EPL, G, false, true, 4> + kvd::k_attn_exact_vsum<EPL, G, false, 8>",
+    "gqa_decode_attn_window": ["kvd::k_attn_exact_window<EPL, G>",
                                "[kvd::k_qk_prep<false> + kvd::k_attn_float<EPL, G, false, SPINOR>]"],
     # float mode only: exact-mode decode prepares the heads inside the score pass
     "qk_norm_rope_append": ["[kvd::k_qk_prep<false>]"],
