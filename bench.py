@@ -613,6 +613,7 @@ def cpu_baseline(spm, be, info, shape, exact, n_steps, tok, sess, spinor=False, 
         for i in range(n_steps):
             t0 = time.time(); ol = o.step(t_tok); one_s += time.time() - t0
             t_tok = int(ol.argmax())
+            log(f"cpu baseline {mode}: 1-core step {i + 1}/{n_steps} ({one_s:.1f}s)")   # long contexts: minutes
         assert o.rewind(n_steps) == 0
         L.orc_set_threads(threads)                            # all cores, the same n_steps steps
         t_tok, cpu_s, same, worst = tok, 0.0, True, 0.0
