@@ -649,23 +649,24 @@ __global__ __launch_bounds__(256) void k_attn_exact_scores(AttnArgs a_in) {
     }
     __syncthreads();
     int mx = INT32_MIN;                              // lane with k4 == g tracks head g
-    for (int j0 = wave * RPW; j0 < n; j0 += 4 * RPW) {
+    // one row group's scores (rows j0 + r): the new K row of pos from LDS in
+    // the workgroup that holds it
+    auto score = [&](int4 (&kr)[NLD], int j0) {
         const int j = j0 + r;
-        if (j0 != wave * RPW) load_kgroup<EPL, LPR>(a, h, cs, n, j0, r, k4, kv);
         int64_t acc[G];
         #pragma unroll
         for (int g = 0; g < G; g++) acc[g] = 0;
         if (j < n) {
             if (holds_pos && cs + j == pos) {
                 #pragma unroll
-                for (int i = 0; i < NLD; i++) kv[i] = kn[LPR * i + k4];
+                for (int i = 0; i < NLD; i++) kr[i] = kn[LPR * i + k4];
             }
             #pragma unroll
             for (int i = 0; i < NLD; i++)
                 #pragma unroll
                 for (int g = 0; g < G; g++) {
                     const int4 q = qs[g][LPR * i + k4];
-                    acc[g] += (int64_t)q.x * kv[i].x + (int64_t)q.y * kv[i].y + (int64_t)q.z * kv[i].z + (int64_t)q.w * kv[i].w;
+                    acc[g] += (int64_t)q.x * kr[i].x + (int64_t)q.y * kr[i].y + (int64_t)q.z * kr[i].z + (int64_t)q.w * kr[i].w;
                 }
         }
         #pragma unroll
@@ -681,6 +682,18 @@ __global__ __launch_bounds__(256) void k_attn_exact_scores(AttnArgs a_in) {
             a.zscratch[(size_t)(h * G + k4) * a.zstride + (size_t)(cs + j)] = z;
             mx = z > mx ? z : mx;
         }
+    };
+    // the next row group is requested before the current one is scored, into
+    // the other buffer (every load issued, clamped past the chunk)
+    int4 kw[NLD];
+    for (int j0 = wave * RPW; j0 < n; j0 += 8 * RPW) {
+        load_kgroup<EPL, LPR>(a, h, cs, n, j0 + 4 * RPW, r, k4, kw);
+        __builtin_amdgcn_sched_barrier(0);
+        score(kv, j0);
+        if (j0 + 4 * RPW >= n) break;
+        load_kgroup<EPL, LPR>(a, h, cs, n, j0 + 8 * RPW, r, k4, kv);
+        __builtin_amdgcn_sched_barrier(0);
+        score(kw, j0 + 4 * RPW);
     }
     // per-head maximum over this wave
     int mxg[G];

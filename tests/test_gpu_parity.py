@@ -489,6 +489,31 @@ def test_window_layers_one_launch(tmpdir_models, name, ring):
     be.close(); close_all(s, o, m)
 
 
+@pytest.mark.parametrize("name,n_prompt,pmax", [("gemma3-w1", 70, 256), ("gemma3-w2100", 2150, 2304)])
+def test_window_edges(tmpdir_models, name, n_prompt, pmax):
+    """Window edge cases, exact mode, bit for bit every step: a one-position
+    window (one chunk: one workgroup finishes the whole head) and a window of
+    2 100 positions (over 32 chunks: the two-kernel path), decoding across a
+    64-position boundary and, for 2 100, past the point where the window starts
+    to slide."""
+    spm, spt = model_files(tmpdir_models, name, max_context=pmax)
+    m = spkv.Model(spm, spt); s = spkv.Session(m, pmax)
+    be = spkv.Backend(spkv.l1().sp_session_qwen3_model(s.h), pmax, exact=True)
+    o = orc.Oracle(spm, pmax, orc.EXACT)
+    lg = np.zeros(o.V, np.float32)
+    toks = prompt(n_prompt, o.V, seed=13)
+    be.prefill(toks[:-1])
+    for t in toks[:-1]:
+        o.step(int(t), False)
+    t = int(toks[-1])
+    for k in range(pmax - n_prompt - 8):
+        be.decode(t, lg)
+        ol = o.step(t)
+        assert same_bits(lg, ol), f"step {k}: max rel {rel(lg, ol):.3e}"
+        t = int(ol.argmax())
+    be.close(); close_all(s, o, m)
+
+
 def test_greedy_device_loop_matches_abi(tmpdir_models):
     """The device-resident greedy loop (argmax on the GPU) generates the same tokens
     as host-driven sp_decode_step + argmax, and as the oracle (exact mode)."""
