@@ -261,6 +261,12 @@ DevModel *model_get(const qwen3_model *qm, bool upload = true) {
     std::vector<std::pair<const float *, size_t>> norms;   // (host src, len)
     std::vector<const float **> norm_slots;
     std::vector<size_t> norm_off;
+    // every norm weight vector goes up as [w (n) | roundf(w * 2^16) (n)]: the
+    // exact mode's input transforms read the Q16 half instead of rounding the
+    // weights in every workgroup (roundf of the exact float product, the value
+    // the device's own rounding gives)
+    std::vector<std::vector<float>> nq;
+    nq.reserve((size_t)m->NL * 6 + 2);
     auto addn = [&](const gguf_tensor *t, int n, const float **slot) -> int {
         const float *src = t ? sp_as_f32(qm, t) : nullptr;
         if (!src) return fail("sp_hipkv_open: missing norm tensor %s", t ? t->name : "(null)");
@@ -270,7 +276,10 @@ DevModel *model_get(const qwen3_model *qm, bool upload = true) {
         for (uint32_t d = 0; d < t->n_dims && d < GGUF_MAX_DIMS; d++) ne *= t->dims[d];
         if (t->n_dims > GGUF_MAX_DIMS || ne != (uint64_t)n)
             return fail("sp_hipkv_open: norm tensor %s has the wrong length", t->name);
-        norm_off.push_back(up.add(src, (size_t)n * 4));
+        nq.emplace_back(2 * (size_t)n);
+        std::vector<float> &v = nq.back();
+        for (int i = 0; i < n; i++) { v[i] = src[i]; v[(size_t)n + i] = roundf(src[i] * 65536.0f); }
+        norm_off.push_back(up.add(v.data(), (size_t)n * 8));
         norm_slots.push_back(slot);
         return 0;
     };

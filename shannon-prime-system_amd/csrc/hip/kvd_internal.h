@@ -47,6 +47,8 @@ enum ProKind { PRO_PLAIN = 0, PRO_NORM = 1, PRO_RESID = 2 };
 struct ProArgs {
     const float *x;        // residual stream (or plain input)
     const float *delta;    // PRO_RESID: branch output added into x
+    // norm weights are [w (n floats) | roundf(w * 2^16) (n floats)]: exact mode
+    // reads the second half where it needs the Q16 integers
     const float *post_w;   // PRO_RESID: sandwich norm weight on delta (NULL = add raw)
     const float *norm_w;   // PRO_NORM / PRO_RESID: pre-norm weight
     float       *x_out;    // PRO_RESID: updated residual (written by workgroup 0)

@@ -255,6 +255,23 @@ __device__ __forceinline__ float norm_apply(float x, float w, const NormScale &s
     const int64_t xi = llround_q16(x), wi = llround_q16(w);
     return (float)((double)mul3_lo64(xi, s.inv, wi) / 4503599627370496.0);   // 2^52
 }
+// norm_apply with the weight given as its Q16 integer w16 = round_away(w * 2^16)
+// (exact mode; the same value: llround_q16(w) is that integer)
+__device__ __forceinline__ float norm_apply_q16(float x, float w16, const NormScale &s) {
+    if (s.zero) return 0.0f;
+    const double dx = (double)round_away(x * 65536.0f) * (double)w16;
+    if (fabs(dx) < 9007199254740992.0) {              // 2^53
+        const double pr = dx * s.invd;
+        if (fabs(pr) < 4611686018427387904.0)          // 2^62
+            return (float)(pr * 2.220446049250313e-16);  // 2^-52
+    }
+    const int64_t xi = llround_q16(x), wi = llround_d((double)w16);
+    return (float)((double)mul3_lo64(xi, s.inv, wi) / 4503599627370496.0);   // 2^52
+}
+// a weight pro_load loaded: the Q16 half in exact mode, w itself in float mode
+__device__ __forceinline__ float norm_apply_loaded(float x, float wl, const NormScale &s, int mode) {
+    return mode == EXACT ? norm_apply_q16(x, wl, s) : norm_apply(x, wl, s, mode);
+}
 
 // ------------------------------------------------------- input transform
 // Latency matters more than work here (every GEMV workgroup runs it before its
@@ -289,13 +306,15 @@ __device__ __forceinline__ void pro_load(const ProArgs &p, int mode, ProLoads &L
     // 0, a missing post_w reads x); input_transform masks the values when it
     // uses them -- masking here would wait for the loads at once, and a select
     // between loads would become a load through a selected pointer
-    const float *pwp = p.post_w ? p.post_w : p.x;
+    // exact mode: the weights' Q16 halves (round_away(w * 2^16) as floats)
+    const int wq = mode == EXACT ? n : 0;
+    const float *pwp = p.post_w ? p.post_w + wq : p.x;
     #pragma unroll
     for (int k = 0; k < PB4; k++) {
         const int i = 4 * (k * T + tid);
         const int ic = i < n ? i : 0;                    // n is a multiple of 4
         L.xv[k] = *(const float4 *)(p.x + ic);
-        L.nw[k] = *(const float4 *)(p.norm_w + ic);
+        L.nw[k] = *(const float4 *)(p.norm_w + wq + ic);
         if constexpr (PRO == PRO_RESID) {
             L.dv[k] = *(const float4 *)(p.delta + ic);
             L.pw[k] = *(const float4 *)(pwp + ic);
@@ -379,14 +398,14 @@ __device__ int input_transform(const ProArgs &p, int mode, const ProLoads &L, fl
                         const float d = f4c(dv[k], c);
                         float nd = d;
                         if (pn) {
-                            const double dx = (double)round_away(d * 65536.0f) * (double)round_away(f4c(pw[k], c) * 65536.0f);
+                            const double dx = (double)round_away(d * 65536.0f) * (double)f4c(pw[k], c);
                             const double pr = dx * sd.invd;
                             bad |= !(fabs(dx) < 9007199254740992.0) | !(fabs(pr) < 4611686018427387904.0);
                             nd = sd.zero ? 0.0f : (float)(pr * 2.220446049250313e-16);
                         }
                         const float r = f4c(xv[k], c) + nd;
                         f4s(xv[k], c, r);
-                        const float r16 = round_away(r * 65536.0f), w16 = round_away(f4c(nw[k], c) * 65536.0f);
+                        const float r16 = round_away(r * 65536.0f), w16 = f4c(nw[k], c);
                         bad |= !(fabsf(r16) < 2147483648.0f);
                         const int32_t q = (int32_t)r16;
                         ss += (int64_t)q * q;
@@ -446,7 +465,7 @@ __device__ int input_transform(const ProArgs &p, int mode, const ProLoads &L, fl
                             #pragma unroll
                             for (int c = 0; c < 4; c++)
                                 f4s(y, c, s.zero ? 0.0f : (float)(((double)round_away(f4c(xv[k], c) * 65536.0f) *
-                                                                   (double)round_away(f4c(nw[k], c) * 65536.0f) * s.invd) *
+                                                                   (double)f4c(nw[k], c) * s.invd) *
                                                                   2.220446049250313e-16));
                             *(float4 *)(xf + i) = y;
                         }
@@ -461,7 +480,7 @@ __device__ int input_transform(const ProArgs &p, int mode, const ProLoads &L, fl
                         float4 y;
                         #pragma unroll
                         for (int c = 0; c < 4; c++) {
-                            const float v = norm_apply(f4c(xv[k], c), f4c(nw[k], c), s, mode);
+                            const float v = norm_apply_loaded(f4c(xv[k], c), f4c(nw[k], c), s, mode);
                             f4s(y, c, v);
                             m = fmaxf(m, fabsf(v));
                         }
@@ -496,7 +515,7 @@ __device__ int input_transform(const ProArgs &p, int mode, const ProLoads &L, fl
                 float4 y;
                 #pragma unroll
                 for (int c = 0; c < 4; c++) {
-                    const float v = norm_apply(f4c(xv[k], c), f4c(nw[k], c), s, mode);
+                    const float v = norm_apply_loaded(f4c(xv[k], c), f4c(nw[k], c), s, mode);
                     f4s(y, c, v);
                     m = fmaxf(m, fabsf(v));
                 }
