@@ -269,25 +269,39 @@ __global__ __launch_bounds__(512, PAIRED ? 2 : 4) void k_gemv(GemvArgs a) {
         acc_t acc[GEMV_R];
         #pragma unroll
         for (int r = 0; r < GEMV_R; r++) acc[r] = 0;
-        for (int it = 0; it < nit; it++) {
-            const int b = b_lo + it * 64 + lane;
-            if (it > 0) load_iter<PAIRED>(a, t, b, b_lo, b_hi, c, h);
+        auto iter = [&](int b, const uint4 (&cc)[GEMV_R], const uint32_t (&hh)[GEMV_R]) {
             if (b < b_hi && sh != SH_ZERO) {
                 uint4 D[NDIG];
                 #pragma unroll
                 for (int k = 0; k < NDIG; k++) D[k] = dig[k * nb + (b - b_lo)];
                 #pragma unroll
                 for (int r = 0; r < GEMV_R; r++) {
-                    const int32_t d = dot_digits(c[r], D);
+                    const int32_t d = dot_digits(cc[r], D);
                     if constexpr (WIDE) {
-                        int32_t M; int e; f16_parts(h[r], M, e);
+                        int32_t M; int e; f16_parts(hh[r], M, e);
                         const int64_t p = (int64_t)d * (int64_t)M;
                         acc[r] += (i128)((u128)(i128)p << (e + 24));
                     } else {
                         // (d * M) << (e - ebase) == d * Ms: one 32 x 32 + 64 multiply-add
-                        acc[r] += (int64_t)d * (int64_t)block_mult(h[r], eb_of(ebw, r));
+                        acc[r] += (int64_t)d * (int64_t)block_mult(hh[r], eb_of(ebw, r));
                     }
                 }
+            }
+        };
+        if (PAIRED && !WIDE && nit == 2) {
+            // the second unit is requested before the first is used (the
+            // paired instance has the registers for both)
+            uint4 c2[GEMV_R];
+            uint32_t h2[GEMV_R];
+            load_iter<PAIRED>(a, t, b_lo + 64 + lane, b_lo, b_hi, c2, h2);
+            __builtin_amdgcn_sched_barrier(0);
+            iter(b_lo + lane, c, h);
+            iter(b_lo + 64 + lane, c2, h2);
+        } else {
+            for (int it = 0; it < nit; it++) {
+                const int b = b_lo + it * 64 + lane;
+                if (it > 0) load_iter<PAIRED>(a, t, b, b_lo, b_hi, c, h);
+                iter(b, c, h);
             }
         }
         // request the next task's first weights before this task's epilogue
