@@ -37,18 +37,21 @@ __constant__ int64_t g_kinv_q62;
 constexpr int64_t TWO_PI_Q60 = 7244019458077122842LL;     // round(2*pi * 2^60)
 constexpr int64_t HALF_PI_Q60 = 1811004864519280711LL;    // round(pi/2 * 2^60)
 
-__device__ void cordic_q62(int64_t th, int64_t &co, int64_t &si) {
+// atan: the 62 Q60 arctangents, staged in LDS by the caller (unrolled, the
+// reads are issued ahead of the dependent steps instead of one constant-cache
+// round trip per step)
+__device__ void cordic_q62(int64_t th, int64_t &co, int64_t &si, const int64_t *atan) {
     int quad = 0;
     while (th >= HALF_PI_Q60 && quad < 3) { th -= HALF_PI_Q60; quad++; }
     int64_t x = g_kinv_q62, y = 0, z = th;
     // branch-free rotation direction: sm = -1 where z < 0, and (v ^ sm) - sm
     // is v or -v; the same integer steps as the two-sided update
-    #pragma unroll 2
+    #pragma unroll
     for (int i = 0; i < 62; i++) {
         const int64_t xs = x >> i, ys = y >> i, sm = z >> 63;
         x -= (ys ^ sm) - sm;
         y += (xs ^ sm) - sm;
-        z -= (g_atan_q60[i] ^ sm) - sm;
+        z -= (atan[i] ^ sm) - sm;
     }
     switch (quad) {
         case 0: co = x;  si = y;  break;
@@ -156,6 +159,9 @@ __global__ __launch_bounds__(256) void k_rope_table(const DState *st, int pos0, 
     // tpos[t] (several sessions) or pos0 + t (one session's prefill)
     const int half = HD / 2, pos = st ? st->pos : (tpos ? tpos[blockIdx.x] : pos0 + (int)blockIdx.x);
     out += (size_t)blockIdx.x * 2 * HD;
+    __shared__ int64_t atan_s[64];
+    if (threadIdx.x < 64) atan_s[threadIdx.x] = g_atan_q60[threadIdx.x];
+    __syncthreads();
     for (int idx = threadIdx.x; idx < 2 * half; idx += blockDim.x) {
         const int t = idx / half, i = idx % half;
         float c, s;
@@ -166,7 +172,7 @@ __global__ __launch_bounds__(256) void k_rope_table(const DState *st, int pos0, 
             c = cosf(theta); s = sinf(theta);
         } else {
             const i128 th = (i128)pos * (t ? fq_l : fq_g)[i];
-            int64_t co, si; cordic_q62(umod128_64(th, TWO_PI_Q60), co, si);
+            int64_t co, si; cordic_q62(umod128_64(th, TWO_PI_Q60), co, si, atan_s);
             c = rne_i64_scaled(co, -62); s = rne_i64_scaled(si, -62);
         }
         out[(size_t)t * HD + i] = c;
