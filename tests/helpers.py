@@ -29,6 +29,13 @@ SMALL = {
                         head_dim=256, n_ff=1024, vocab=2048, swa_window=200),
     "gemma3-g4w130": dict(arch_id=spkv.ARCH_GEMMA3, n_layers=6, hidden=512, n_heads=8, n_kv_heads=2,
                           head_dim=128, n_ff=1024, vocab=2048, swa_window=130),
+    # the other head_dim x group instances of the one-launch window attention
+    "gemma3-hd128w100": dict(arch_id=spkv.ARCH_GEMMA3, n_layers=6, hidden=512, n_heads=4, n_kv_heads=2,
+                             head_dim=128, n_ff=1024, vocab=2048, swa_window=100),
+    "gemma3-g4hd256w150": dict(arch_id=spkv.ARCH_GEMMA3, n_layers=6, hidden=512, n_heads=8, n_kv_heads=2,
+                               head_dim=256, n_ff=1024, vocab=2048, swa_window=150),
+    "gemma3-g4hd64w150": dict(arch_id=spkv.ARCH_GEMMA3, n_layers=6, hidden=512, n_heads=8, n_kv_heads=2,
+                              head_dim=64, n_ff=1024, vocab=2048, swa_window=150),
     # one-position window (a single chunk); a window over more than 32 chunks (the two-kernel path)
     "gemma3-w1": dict(arch_id=spkv.ARCH_GEMMA3, n_layers=6, hidden=512, n_heads=4, n_kv_heads=2,
                       head_dim=64, n_ff=1024, vocab=2048, swa_window=1),

@@ -455,15 +455,17 @@ def test_window_ring_rewind(tmpdir_models):
     be.close(); close_all(s, o, m)
 
 
-@pytest.mark.parametrize("name", ["gemma3-w200", "gemma3-g4w130"])
+@pytest.mark.parametrize("name", ["gemma3-w200", "gemma3-g4w130", "gemma3-hd128w100", "gemma3-g4hd256w150",
+                                  "gemma3-g4hd64w150"])
 @pytest.mark.parametrize("ring", [False, True])
 def test_window_layers_one_launch(tmpdir_models, name, ring):
     """Exact decode on window layers scores and sums V in one launch whose
-    workgroups meet on a per-kv-head barrier.  Windows of 200 and 130 positions
-    span 3 to 5 64-position chunks (the first and last ragged); decoding from
-    position 179 to 399 crosses the point where the window starts to slide and,
-    on a ring of window + 8 positions (plain launches), wraps it.  Logits every
-    step and the last 100 positions' K/V of every layer bit-exact."""
+    workgroups hand off through tagged slots.  Windows of 100 to 200 positions
+    span 2 to 5 64-position chunks (the first and last ragged), at every
+    head_dim x group instance (256/128/64 x 2/4); decoding from position 179 to
+    399 crosses the point where the window starts to slide and, on a ring of
+    window + 8 positions (plain launches), wraps it.  Logits every step and the
+    last 100 positions' K/V of every layer bit-exact."""
     spm, spt = model_files(tmpdir_models, name)
     m = spkv.Model(spm, spt); s = spkv.Session(m, 512)
     be = spkv.Backend(spkv.l1().sp_session_qwen3_model(s.h), 512, exact=True, graph=not ring)
