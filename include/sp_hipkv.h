@@ -179,6 +179,14 @@ int  sp_hipkv_read_kv(const sp_kvdecode_handle *h, int layer, int p0, int n, flo
 int  sp_hipkv_write_kv(sp_kvdecode_handle *h, int layer, int p0, int n, const float *k, const float *v);
 /* Use a captured HIP graph for each step body (1, default) or plain launches (0). */
 int  sp_hipkv_set_graph(sp_kvdecode_handle *h, int on);
+/* Exact-mode window layers (sliding window of at most 1 922 positions) run
+ * their attention in one launch (1, default) whose workgroups hand data to each
+ * other through the handle's slots, or in the score + V-sum launches of the
+ * full-context layers (0).  Both give bit-identical results; 0 is the fallback
+ * should a deployment run so many concurrent handles that a launch of up to
+ * 32 x n_kv_heads workgroups could not be resident at once.  No counterpart in
+ * the reference (a CPU attention). */
+int  sp_hipkv_set_window_one_launch(sp_kvdecode_handle *h, int on);
 /* Prefill through the batched path (1, default: 128 tokens per pass, int8-MFMA
  * GEMMs, token-batched attention) or one decode step per token (0).  Both
  * leave the same K/V (bit-identical in exact mode). */

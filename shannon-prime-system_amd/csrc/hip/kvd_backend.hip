@@ -462,6 +462,7 @@ struct sp_kvdecode_handle {
     int max_rewind = 0;                      // 0: full tables for window layers
     int pool_growth = 0;                     // pages per pool growth (0: ~1 GiB)
     int recall_kvsel = 0;                    // SP_RECALL_KVSEL: one recall selection per kv head
+    int win_one = 1;                         // exact window layers in one launch (0: the two-kernel path)
     int ring2 = 0;                           // Ring-2: spill full-context pages outside sinks + window to host
     int full_pages = 0, ring_pages = 0;
     std::vector<std::vector<int>> pt;        // [NL][slots] page ids (-1 = unmapped)
@@ -1009,7 +1010,7 @@ void enqueue_body(sp_kvdecode_handle *h, const StepShape &sh, TimeCb cb, void *c
         // window layers in exact mode: one launch when its grid, 4 times over
         // (one per hardware queue), fits the device at once
         a.wslot = ss.wslot;
-        a.one_launch = a.win >= 0 && h->mode == EXACT && ss.wslot && sh.grid_local <= WIN_MAXCH_HOST &&
+        a.one_launch = h->win_one && a.win >= 0 && h->mode == EXACT && ss.wslot && sh.grid_local <= WIN_MAXCH_HOST &&
                        (size_t)sh.grid_local * m->NKV * 4 <= (size_t)h->win_cap;
         if (h->rec.B > 0 && a.win < 0) { a.rec_R = h->rec.Rb; a.rec_r = h->rec.r; a.rec_side = side_of(h, l); }
         const int cls = (glob || a.win < 0) ? 5 : 6, grid = glob ? sh.grid_global : sh.grid_local;
@@ -1378,6 +1379,7 @@ int sp_hipkv_open(const void *qm_opaque, int pmax, sp_kvdecode_handle **out) {
         if (sh->kvc != KVC_PLAIN) { sh->kvc = KVC_PLAIN; free_graphs(sh); }   // graphs bake in the codec
         sh->use_graph = 1; sh->use_batch = 1; sh->dpos = 0; sh->hwm = 0; sh->pool_growth = 0;
         if (sh->recall_kvsel) { sh->recall_kvsel = 0; free_graphs(sh); }
+        if (!sh->win_one) { sh->win_one = 1; free_graphs(sh); }
         sh->ring2 = 0;
         if (sh->rec.B) { free_recall(sh); free_graphs(sh); }
         sh->pool = new_pool();
@@ -1725,6 +1727,14 @@ int sp_hipkv_set_graph(sp_kvdecode_handle *h, int on) {
     return 0;
 }
 
+int sp_hipkv_set_window_one_launch(sp_kvdecode_handle *h, int on) {
+    if (!h) return fail("sp_hipkv_set_window_one_launch: null handle%s");
+    if ((on ? 1 : 0) == h->win_one) return 0;
+    h->win_one = on ? 1 : 0;
+    free_graphs(h);                          // the captured steps bake the attention launches
+    return 0;
+}
+
 int sp_hipkv_set_batch_prefill(sp_kvdecode_handle *h, int on) {
     if (!h) return fail("sp_hipkv_set_batch_prefill: null handle%s");
     h->use_batch = on ? 1 : 0;
@@ -1833,6 +1843,7 @@ int sp_hipkv_fork(const sp_kvdecode_handle *p, sp_kvdecode_handle **out) {
     }
     h->use_batch = p->use_batch; h->use_graph = p->use_graph; h->pool_growth = p->pool_growth;
     if (h->recall_kvsel != p->recall_kvsel) { h->recall_kvsel = p->recall_kvsel; free_graphs(h.get()); }
+    if (h->win_one != p->win_one) { h->win_one = p->win_one; free_graphs(h.get()); }
     h->ring2 = p->ring2;
     hipStreamSynchronize(p->stream);
     // share every mapped page (copy-on-write on the next append into it)

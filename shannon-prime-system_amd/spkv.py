@@ -114,6 +114,7 @@ def kv():
         _sig(lib, "sp_hipkv_set_kv_codec", c_int, [c_void_p, c_int])
         _sig(lib, "sp_hipkv_set_max_rewind", c_int, [c_void_p, c_int])
         _sig(lib, "sp_hipkv_set_graph", c_int, [c_void_p, c_int])
+        _sig(lib, "sp_hipkv_set_window_one_launch", c_int, [c_void_p, c_int])
         _sig(lib, "sp_hipkv_set_pool_growth", c_int, [c_void_p, c_int])
         _sig(lib, "sp_hipkv_set_recall_kvsel", c_int, [c_void_p, c_int])
         _sig(lib, "sp_hipkv_set_ring2", c_int, [c_void_p, c_int])
@@ -380,6 +381,10 @@ class Backend:
     def set_recall(self, B, W=64, sink=4, r=16):
         """ARM recall on the global layers (decode steps route, prefill is dense)."""
         check(kv().sp_hipkv_set_recall(self.h, B, W, sink, r), "sp_hipkv_set_recall")
+
+    def set_window_one_launch(self, on):
+        """Exact window layers in one launch (default) or the two-kernel path."""
+        check(kv().sp_hipkv_set_window_one_launch(self.h, 1 if on else 0), "sp_hipkv_set_window_one_launch")
 
     def set_recall_kvsel(self, on):
         """SP_RECALL_KVSEL: one recall set per kv head (group-centroid query)."""

@@ -18,7 +18,7 @@ import pytest
 
 import orc
 import spkv
-from helpers import model_files, prompt
+from helpers import SMALL, model_files, prompt
 
 pytestmark = pytest.mark.gpu
 FLOAT_TOL = 1e-3
@@ -489,6 +489,29 @@ def test_window_layers_one_launch(tmpdir_models, name, ring):
         kc, vc = o.kv(layer, pos - 100, 100)
         assert same_bits(kg, kc) and same_bits(vg, vc), f"layer {layer}"
     be.close(); close_all(s, o, m)
+
+
+def test_window_one_launch_switch(tmpdir_models):
+    """sp_hipkv_set_window_one_launch(0) sends exact window layers through the
+    score + V-sum launches: the same bits as the one-launch kernel, step by
+    step, on a fork of the same handle (graphs recaptured at each switch)."""
+    name = "gemma3-w200"
+    spm, spt = model_files(tmpdir_models, name)
+    m = spkv.Model(spm, spt); s = spkv.Session(m, 512)
+    a = spkv.Backend(spkv.l1().sp_session_qwen3_model(s.h), 512, exact=True)
+    V = SMALL[name]["vocab"]
+    a.prefill(prompt(230, V, seed=17))
+    b = a.fork()
+    b.set_window_one_launch(False)
+    la, lb = np.zeros(V, np.float32), np.zeros(V, np.float32)
+    t = 5
+    for k in range(40):
+        if k == 20:
+            b.set_window_one_launch(True); a.set_window_one_launch(False)
+        a.decode(t, la); b.decode(t, lb)
+        assert same_bits(la, lb), f"step {k}"
+        t = int(la.argmax())
+    a.close(); b.close(); s.close(); m.close()
 
 
 @pytest.mark.parametrize("name,n_prompt,pmax", [("gemma3-w1", 70, 256), ("gemma3-w2100", 2150, 2304)])
