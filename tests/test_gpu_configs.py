@@ -252,6 +252,54 @@ def test_config3_gemma3_12b_32k(gemma12b):
     s.close(); m.close()
 
 
+def test_gemma3_12b_concurrent_window_launches(gemma12b):
+    """The Gemma-3-12B shape's one-launch window attention (17 chunks x 8 kv
+    heads = 136 workgroups per launch) from three handles decoding at once on
+    three threads and streams, contexts 1 500-2 300: every step's logits equal
+    a fresh handle's fed the same tokens afterwards, alone (exact mode)."""
+    import threading
+    spm, spt = gemma12b
+    pmax, V = 2560, 262144
+    m = spkv.Model(spm, spt); s = spkv.Session(m, pmax)
+    qm = spkv.l1().sp_session_qwen3_model(s.h)
+    prompts = [prompt(n, V, seed=60 + i) for i, n in enumerate((1500, 1900, 2300))]
+    feeds = [prompt(12, V, seed=70 + i) for i in range(3)]
+    hs = []
+    for pr in prompts:
+        b = spkv.Backend(qm, pmax, exact=True)
+        b.prefill(pr)
+        hs.append(b)
+    out = [[None] * 12 for _ in range(3)]
+    errs = []
+
+    def run(i):
+        try:
+            for k in range(12):
+                lg = np.zeros(V, np.float32)
+                hs[i].decode(int(feeds[i][k]), lg)
+                out[i][k] = lg
+        except Exception as e:                       # reported below
+            errs.append((i, repr(e)))
+
+    th = [threading.Thread(target=run, args=(i,)) for i in range(3)]
+    for t in th:
+        t.start()
+    for t in th:
+        t.join()
+    assert not errs, errs
+    for b in hs:
+        b.close()
+    for i in range(3):
+        c = spkv.Backend(qm, pmax, exact=True)
+        c.prefill(prompts[i])
+        lg = np.zeros(V, np.float32)
+        for k in range(12):
+            c.decode(int(feeds[i][k]), lg)
+            assert same_bits(out[i][k], lg), (i, k)
+        c.close()
+    s.close(); m.close()
+
+
 def test_config3_gemma3_12b_32k_float(gemma12b):
     """C3 in float mode: the 32768-token prefill; the oracle, given the device's
     f32 K/V before the last prompt position (window layers: the last 1024

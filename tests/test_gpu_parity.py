@@ -615,3 +615,54 @@ def test_exact_v_clamp_is_counted(tmp_path):
         assert be.v_clamps() == o.v_clamps()
         assert (o.v_clamps() > 0) == want_clamps
         close_all(s, o, m)
+
+
+def test_concurrent_handles_window_layers(tmpdir_models):
+    """Three handles of one model decode from three threads at once (each on
+    its own stream, graph replay), windows of 200 positions over 4-5 chunks:
+    every step's logits equal those of a fresh handle fed the same tokens
+    afterwards, alone (exact mode, bit for bit).  The one-launch window kernel
+    polls for its sibling workgroups; concurrent launches from the other
+    handles' streams must not change that."""
+    import threading
+    name, pmax = "gemma3-w200", 512
+    spm, spt = model_files(tmpdir_models, name)
+    m = spkv.Model(spm, spt); s = spkv.Session(m, pmax)
+    qm = spkv.l1().sp_session_qwen3_model(s.h)
+    V = SMALL[name]["vocab"]
+    prompts = [prompt(n, V, seed=40 + i) for i, n in enumerate((230, 260, 300))]
+    feeds = [prompt(40, V, seed=50 + i) for i in range(3)]
+    hs = []
+    for pr in prompts:
+        b = spkv.Backend(qm, pmax, exact=True)
+        b.prefill(pr)
+        hs.append(b)
+    out = [[None] * 40 for _ in range(3)]
+    errs = []
+
+    def run(i):
+        try:
+            for k in range(40):
+                lg = np.zeros(V, np.float32)
+                hs[i].decode(int(feeds[i][k]), lg)
+                out[i][k] = lg
+        except Exception as e:                       # reported below
+            errs.append((i, repr(e)))
+
+    th = [threading.Thread(target=run, args=(i,)) for i in range(3)]
+    for t in th:
+        t.start()
+    for t in th:
+        t.join()
+    assert not errs, errs
+    for i in range(3):
+        c = spkv.Backend(qm, pmax, exact=True)
+        c.prefill(prompts[i])
+        lg = np.zeros(V, np.float32)
+        for k in range(40):
+            c.decode(int(feeds[i][k]), lg)
+            assert same_bits(out[i][k], lg), (i, k)
+        c.close()
+    for b in hs:
+        b.close()
+    s.close(); m.close()
