@@ -48,7 +48,7 @@ KERNEL_NAMES = {
                                "[kvd::k_qk_prep<false> + kvd::k_attn_float<EPL, G, false, SPINOR>]"],
     # float mode only: exact-mode decode prepares the heads inside the score pass
     "qk_norm_rope_append": ["[kvd::k_qk_prep<false>]"],
-    "embed_rope_argmax": ["kvd::k_embed", "kvd::k_rope_table", "kvd::k_argmax"],
+    "embed_rope_argmax": ["kvd::k_embed_rope", "kvd::k_argmax"],
 }
 # committed rocprofv3 --pmc summaries (FETCH_SIZE / WRITE_SIZE per dispatch) of the
 # decode kernels at this model shape and context, with the 1 GiB calibration copy they hold

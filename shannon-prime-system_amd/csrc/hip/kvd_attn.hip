@@ -153,12 +153,12 @@ __global__ __launch_bounds__(64) void k_qk_prep(AttnArgs a_in) {
 // out[t][0..half) = cos, out[t][half..HD) = sin, t = 0 global base, 1 window base.
 // Float mode: freq = powf(base, -2i/d), theta = (float)p*freq, cosf/sinf
 // (forward_kernels.c:31-41); exact mode: p*F_i mod 2*pi (Q60) by CORDIC, RNE.
-__global__ __launch_bounds__(256) void k_rope_table(const DState *st, int pos0, const int *tpos, int HD, int mode, float base_g,
-                                                     float base_l, const int64_t *fq_g, const int64_t *fq_l, float *out) {
-    // decode: one workgroup at the step's position; batched: workgroup t at
-    // tpos[t] (several sessions) or pos0 + t (one session's prefill)
-    const int half = HD / 2, pos = st ? st->pos : (tpos ? tpos[blockIdx.x] : pos0 + (int)blockIdx.x);
-    out += (size_t)blockIdx.x * 2 * HD;
+// table t of a launch (decode: t = 0 at the step's position; batched: table t
+// at tpos[t] or pos0 + t); every thread of the workgroup calls this
+__device__ __forceinline__ void rope_table_body(int t_idx, const DState *st, int pos0, const int *tpos, int HD, int mode,
+                                                const int64_t *fq_g, const int64_t *fq_l, float *out) {
+    const int half = HD / 2, pos = st ? st->pos : (tpos ? tpos[t_idx] : pos0 + t_idx);
+    out += (size_t)t_idx * 2 * HD;
     __shared__ int64_t atan_s[64];
     if (threadIdx.x < 64) atan_s[threadIdx.x] = g_atan_q60[threadIdx.x];
     __syncthreads();
@@ -179,13 +179,17 @@ __global__ __launch_bounds__(256) void k_rope_table(const DState *st, int pos0, 
         out[(size_t)t * HD + half + i] = s;
     }
 }
+__global__ __launch_bounds__(256) void k_rope_table(const DState *st, int pos0, const int *tpos, int HD, int mode,
+                                                     const int64_t *fq_g, const int64_t *fq_l, float *out) {
+    rope_table_body((int)blockIdx.x, st, pos0, tpos, HD, mode, fq_g, fq_l, out);
+}
 void launch_rope_table(const DState *st, int HD, int mode, float base_g, float base_l,
                        const int64_t *fq_g, const int64_t *fq_l, float *out, hipStream_t s) {
-    hipLaunchKernelGGL(k_rope_table, dim3(1), dim3(256), 0, s, st, 0, nullptr, HD, mode, base_g, base_l, fq_g, fq_l, out);
+    hipLaunchKernelGGL(k_rope_table, dim3(1), dim3(256), 0, s, st, 0, nullptr, HD, mode, fq_g, fq_l, out);
 }
 void launch_rope_table_batch(int pos0, int T, int HD, int mode, float base_g, float base_l,
                              const int64_t *fq_g, const int64_t *fq_l, float *out, hipStream_t s, const int *tpos) {
-    hipLaunchKernelGGL(k_rope_table, dim3(T), dim3(256), 0, s, nullptr, pos0, tpos, HD, mode, base_g, base_l, fq_g, fq_l, out);
+    hipLaunchKernelGGL(k_rope_table, dim3(T), dim3(256), 0, s, nullptr, pos0, tpos, HD, mode, fq_g, fq_l, out);
 }
 void launch_qk_prep(const AttnArgs &a, hipStream_t s) {
     if (a.nt) hipLaunchKernelGGL(k_qk_prep<true>, dim3(a.NH + 2 * a.NKV, a.nt), dim3(64), 0, s, a);
@@ -1242,8 +1246,8 @@ void launch_prep_attention(const AttnArgs &a, int grid_chunks, hipStream_t s) {
 }
 
 // ------------------------------------------------------------------ embedding
-__global__ __launch_bounds__(256) void k_embed(DevW w, const DState *st, const int *tokbuf, int pos0, const int *toks,
-                                                float *x, float scale, VecStat *stats, int nstats) {
+__device__ __forceinline__ void embed_body(int t_idx, DevW w, const DState *st, const int *tokbuf, int pos0, const int *toks,
+                                           float *x, float scale, VecStat *stats, int nstats) {
     // a decode step starts here: clear the step's vector statistics (plain
     // stores; the step's later kernels accumulate into them)
     static_assert(sizeof(VecStat) == 16, "one 16-byte store per statistic replica");
@@ -1251,8 +1255,8 @@ __global__ __launch_bounds__(256) void k_embed(DevW w, const DState *st, const i
     // decode: the step's token; batched: workgroup t embeds toks[t] (several
     // sessions) or tokbuf[pos0 + t] (one session's prefill) into row t
     const int tok = st ? (st->drive == DRIVE_STREAM ? tokbuf[st->pos] : st->tok)
-                       : (toks ? toks[blockIdx.x] : tokbuf[pos0 + blockIdx.x]), E = w.cols;
-    x += (size_t)blockIdx.x * E;
+                       : (toks ? toks[t_idx] : tokbuf[pos0 + t_idx]), E = w.cols;
+    x += (size_t)t_idx * E;
     const uint8_t *rc = w.codes + (size_t)tok * ((E + 1) / 2);
     const uint16_t *bs = w.bs + (size_t)tok * w.nblk;
     if ((E & 7) == 0) {
@@ -1283,9 +1287,26 @@ __global__ __launch_bounds__(256) void k_embed(DevW w, const DState *st, const i
         }
     }
 }
+__global__ __launch_bounds__(256) void k_embed(DevW w, const DState *st, const int *tokbuf, int pos0, const int *toks,
+                                                float *x, float scale, VecStat *stats, int nstats) {
+    embed_body((int)blockIdx.x, w, st, tokbuf, pos0, toks, x, scale, stats, nstats);
+}
+// decode: the step's embedding (workgroup 0) and its rotation tables
+// (workgroup 1, independent of it) in one launch
+__global__ __launch_bounds__(256) void k_embed_rope(DevW w, const DState *st, const int *tokbuf, float *x, float scale,
+                                                     VecStat *stats, int nstats, int HD, int mode, const int64_t *fq_g,
+                                                     const int64_t *fq_l, float *rope) {
+    if (blockIdx.x == 0) embed_body(0, w, st, tokbuf, 0, nullptr, x, scale, stats, nstats);
+    else rope_table_body(0, st, 0, nullptr, HD, mode, fq_g, fq_l, rope);
+}
 void launch_embed(const DevW &embd, const DState *st, const int *tokbuf, float *x, float scale, hipStream_t s,
                   VecStat *stats, int nstats) {
     hipLaunchKernelGGL(k_embed, dim3(1), dim3(256), 0, s, embd, st, tokbuf, 0, nullptr, x, scale, stats, nstats);
+}
+void launch_embed_rope(const DevW &embd, const DState *st, const int *tokbuf, float *x, float scale, VecStat *stats,
+                       int nstats, int HD, int mode, const int64_t *fq_g, const int64_t *fq_l, float *rope, hipStream_t s) {
+    hipLaunchKernelGGL(k_embed_rope, dim3(2), dim3(256), 0, s, embd, st, tokbuf, x, scale, stats, nstats, HD, mode,
+                       fq_g, fq_l, rope);
 }
 void launch_embed_batch(const DevW &embd, const int *tokbuf, int pos0, int T, float *x, float scale, hipStream_t s,
                         const int *toks) {

@@ -970,9 +970,9 @@ void enqueue_body(sp_kvdecode_handle *h, const StepShape &sh, TimeCb cb, void *c
     // writes the vector and read by the GEMV that consumes it
     VecStat *stat = ss.stats;
     auto st = [&](int l, int k) { return stat + ((size_t)l * STAT_PER_LAYER + k) * STAT_REP; };
-    launch_embed(m->embd, h->d_st, h->tokbuf, h->x1, m->gemma ? sqrtf((float)m->E) : 0.0f, s,
-                 stat, m->NL * STAT_PER_LAYER * STAT_REP);
-    launch_rope_table(h->d_st, m->HD, h->mode, m->base, m->gemma ? 10000.0f : m->base,
+    // the embedding and the step's rotation tables (independent) in one launch
+    launch_embed_rope(m->embd, h->d_st, h->tokbuf, h->x1, m->gemma ? sqrtf((float)m->E) : 0.0f,
+                      stat, m->NL * STAT_PER_LAYER * STAT_REP, m->HD, h->mode,
                       m->freq_global, m->gemma ? m->freq_local : m->freq_global, h->rope, s);
     T(8, false);
     for (int l = 0; l < m->NL; l++) {

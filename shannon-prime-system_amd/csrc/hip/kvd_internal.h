@@ -265,6 +265,8 @@ bool gemm_supported(const DevW &w);
 void launch_advance(DState *st, hipStream_t s);
 void launch_gemv(const GemvArgs &a, int nrows_total, hipStream_t s);
 void launch_qk_prep(const AttnArgs &a, hipStream_t s);
+void launch_embed_rope(const DevW &embd, const DState *st, const int *tokbuf, float *x, float scale, VecStat *stats,
+                       int nstats, int HD, int mode, const int64_t *fq_g, const int64_t *fq_l, float *rope, hipStream_t s);
 void launch_rope_table(const DState *st, int HD, int mode, float base_g, float base_l,
                        const int64_t *fq_g, const int64_t *fq_l, float *out, hipStream_t s);
 void launch_attention(const AttnArgs &a, int grid_chunks, hipStream_t s);
