@@ -33,6 +33,7 @@ from spkv import splitmix_tokens, splitmix_u64  # noqa: E402  (seeded synthetic 
 
 METRIC = "kvdecode tokens/s + KV-read HBM GB/s (% of peak), Gemma-12B shape 32k ctx"
 PEAK_GBS = 8000.0
+GEMV_CLASSES = ("qkv_gemv_q4b", "o_gemv_q4b", "gate_up_gemv_q4b", "down_gemv_q4b", "lm_head_gemv_q4b")
 CLASSES = ["qkv_gemv_q4b", "o_gemv_q4b", "gate_up_gemv_q4b", "down_gemv_q4b", "lm_head_gemv_q4b",
            "gqa_decode_attn_global", "gqa_decode_attn_window", "qk_norm_rope_append", "embed_rope_argmax"]
 # the rocprofv3 kernel names of each class's launches (exact mode; float mode in brackets)
@@ -315,8 +316,10 @@ def main():
                          "frac": round(dom["gbs"] / PEAK_GBS, 4),
                          "algorithmic_bytes_per_launch": round(dom_launch_bytes),
                          "avg_launch_us": round(dom["avg_us"], 3),
-                         "timing": "HIP events around every launch of the class on the backend's stream "
-                                   "(the event pair adds about 1.8 us per launch)",
+                         "timing": ("HIP events recorded by each launch of the class at the kernel's start and end "
+                                    "(hipExtLaunchKernelGGL)" if dom["kernel"] in GEMV_CLASSES else
+                                    "HIP events around every launch of the class on the backend's stream "
+                                    "(the event pair adds about 2 us per launch)"),
                          **rocprof_fields(dom_names, dom_launch_bytes, headline),
                          "traffic": round(traffic["bytes"]) if traffic else None,
                          "traffic_source": traffic},

@@ -1930,10 +1930,23 @@ int sp_hipkv_kernel_times(sp_kvdecode_handle *h, int32_t first_token, int n, dou
     if (n > h->pmax - h->dpos) return fail("sp_hipkv_kernel_times: context full%s");
     if (ensure_pages(h, h->dpos, h->dpos + n) || ring2_spill(h, h->dpos)) return 1;
     if (set_state(h, h->dpos, first_token, DRIVE_GREEDY)) return 1;
-    struct Ctx { hipStream_t s; std::vector<std::pair<int, std::pair<hipEvent_t, hipEvent_t>>> ev; hipEvent_t cur; };
+    // the GEMV classes (0-4, one launch each) are timed by events the launch
+    // itself records at the kernel's start and end; the others (several
+    // kernels, or not GEMVs) by events recorded on the stream around them
+    struct Ctx { hipStream_t s; std::vector<std::pair<int, std::pair<hipEvent_t, hipEvent_t>>> ev; hipEvent_t cur, cur2; };
     Ctx c; c.s = h->stream;
     auto cb = [](void *vp, int cls, bool begin) {
         Ctx *cc = (Ctx *)vp;
+        if (cls <= 4) {
+            if (begin) {
+                hipEventCreate(&cc->cur); hipEventCreate(&cc->cur2);
+                gemv_time_next(cc->cur, cc->cur2);
+            } else {
+                gemv_time_next(nullptr, nullptr);    // (already consumed unless the launch failed)
+                cc->ev.push_back({cls, {cc->cur, cc->cur2}});
+            }
+            return;
+        }
         hipEvent_t e; hipEventCreate(&e); hipEventRecord(e, cc->s);
         if (begin) cc->cur = e; else cc->ev.push_back({cls, {cc->cur, e}});
     };

@@ -23,6 +23,7 @@
 #include "kvd_internal.h"
 #include "kvd_exact.h"
 #include "kvd_vec.h"
+#include <hip/hip_ext.h>
 #include <cstdio>
 #include <cstdlib>
 
@@ -452,8 +453,21 @@ GemvPlan gemv_plan(int nrows_total, int cols, int paired, int wide) {
     return p;
 }
 
+// Kernel-tight timing: the next GEMV launch on this thread records these
+// events at its own start and end (hipExtLaunchKernelGGL), instead of events
+// recorded on the stream around it (two more queue packets, ~2 us).
+static thread_local hipEvent_t g_t_start = nullptr, g_t_stop = nullptr;
+void gemv_time_next(hipEvent_t start, hipEvent_t stop) { g_t_start = start; g_t_stop = stop; }
+
 template <int PRO, bool PAIRED>
 static void launch_pro(const GemvArgs &a, bool wide, int grid, int waves, size_t lds, hipStream_t s) {
+    hipEvent_t e0 = g_t_start, e1 = g_t_stop;
+    g_t_start = g_t_stop = nullptr;
+    if (e0) {
+        if (wide) hipExtLaunchKernelGGL((k_gemv<PRO, PAIRED, true>), dim3(grid), dim3(waves * 64), lds, s, e0, e1, 0, a);
+        else      hipExtLaunchKernelGGL((k_gemv<PRO, PAIRED, false>), dim3(grid), dim3(waves * 64), lds, s, e0, e1, 0, a);
+        return;
+    }
     if (wide) hipLaunchKernelGGL((k_gemv<PRO, PAIRED, true>), dim3(grid), dim3(waves * 64), lds, s, a);
     else      hipLaunchKernelGGL((k_gemv<PRO, PAIRED, false>), dim3(grid), dim3(waves * 64), lds, s, a);
 }

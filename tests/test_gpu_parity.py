@@ -666,3 +666,27 @@ def test_concurrent_handles_window_layers(tmpdir_models):
     for b in hs:
         b.close()
     s.close(); m.close()
+
+
+def test_kernel_times_are_greedy_steps(tmpdir_models):
+    """sp_hipkv_kernel_times runs n greedy steps with every kernel class timed:
+    the GEMV classes by events their launches record at the kernel's start and
+    end, the attention classes by events on the stream; every class of the
+    model gets launches and positive time, and the handle goes on bit-identically
+    to a fork that ran the same steps untimed through the device greedy loop."""
+    name = "gemma3-w200"
+    spm, spt = model_files(tmpdir_models, name)
+    m = spkv.Model(spm, spt); s = spkv.Session(m, 512)
+    a = spkv.Backend(spkv.l1().sp_session_qwen3_model(s.h), 512, exact=True)
+    V = SMALL[name]["vocab"]
+    a.prefill(prompt(240, V, seed=19))
+    b = a.fork()
+    ms, nl, by = a.kernel_times(7, 4)
+    for c in range(7):                          # QKV, O, gate/up, down, LM head, global, window attention
+        assert nl[c] > 0 and ms[c] > 0 and by[c] > 0, (c, nl[c], ms[c], by[c])
+    toks, _ = b.greedy(7, 4)
+    assert a.position() == b.position()
+    la, lb = np.zeros(V, np.float32), np.zeros(V, np.float32)
+    a.decode(int(toks[-1]), la); b.decode(int(toks[-1]), lb)
+    assert same_bits(la, lb)
+    a.close(); b.close(); s.close(); m.close()
