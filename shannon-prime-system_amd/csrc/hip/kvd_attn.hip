@@ -21,6 +21,7 @@
 // of the group, so every K/V byte is read once per step.  The last workgroup to
 // finish a kv-head merges the chunk partials (arrival counter, self-resetting).
 #include "kvd_internal.h"
+#include <hip/hip_ext.h>
 #include "kvd_exact.h"
 #include "kvd_qkprep.h"
 #include "kvd_vec.h"
@@ -1143,30 +1144,42 @@ __global__ __launch_bounds__(256) void k_attn_exact_window(AttnArgs a_in) {
     if (a.stat_out) stat_flush_block(a.stat_out, sacc);      // max |ao| for the O GEMV
 }
 
+// Kernel-tight timing of the calling thread's next attention dispatch: its
+// first launch records `start` at the kernel's start, its last `stop` at the
+// last kernel's end (hipExtLaunchKernelGGL).
+static thread_local hipEvent_t g_at_start = nullptr, g_at_stop = nullptr;
+void attn_time_next(hipEvent_t start, hipEvent_t stop) { g_at_start = start; g_at_stop = stop; }
+template <typename K> static void launch_ev(K kernel, dim3 grid, hipStream_t s, hipEvent_t e0, hipEvent_t e1, const AttnArgs &a) {
+    if (e0 || e1) hipExtLaunchKernelGGL(kernel, grid, dim3(256), 0, s, e0, e1, 0, a);
+    else hipLaunchKernelGGL(kernel, grid, dim3(256), 0, s, a);
+}
+
 // decode (B = false: position from the step state) and batched prefill
 // (B = true: token grid dimension) are separate instances
 template <int EPL, int G, bool B> static void attn_dispatch_b(const AttnArgs &a, int grid_chunks, bool prep, hipStream_t s) {
     const dim3 grid = B ? (a.work ? dim3(a.nwork, a.NKV, 1) : dim3(a.nt, grid_chunks, a.NKV)) : dim3(grid_chunks, a.NKV, 1);
-    if (a.mode == FLOAT && a.kvc == KVC_SPINOR) hipLaunchKernelGGL((k_attn_float<EPL, G, B, true>), grid, dim3(256), 0, s, a);
-    else if (a.mode == FLOAT) hipLaunchKernelGGL((k_attn_float<EPL, G, B, false>), grid, dim3(256), 0, s, a);
+    const hipEvent_t e0 = g_at_start, e1 = g_at_stop;
+    g_at_start = g_at_stop = nullptr;
+    if (a.mode == FLOAT && a.kvc == KVC_SPINOR) launch_ev(k_attn_float<EPL, G, B, true>, grid, s, e0, e1, a);
+    else if (a.mode == FLOAT) launch_ev(k_attn_float<EPL, G, B, false>, grid, s, e0, e1, a);
     else {
         const bool wide = a.chunk > 64;
         if (!B && prep && a.one_launch && a.wslot && a.chunk == 64 && grid_chunks <= WIN_MAXCH) {
-            hipLaunchKernelGGL((k_attn_exact_window<EPL, G>), grid, dim3(256), 0, s, a);
+            launch_ev(k_attn_exact_window<EPL, G>, grid, s, e0, e1, a);
             return;
         }
         if (!B && prep) {
-            if (wide) hipLaunchKernelGGL((k_attn_exact_scores<EPL, G, B, !B, 8>), grid, dim3(256), 0, s, a);
-            else hipLaunchKernelGGL((k_attn_exact_scores<EPL, G, B, !B, 4>), grid, dim3(256), 0, s, a);
+            if (wide) launch_ev(k_attn_exact_scores<EPL, G, B, !B, 8>, grid, s, e0, nullptr, a);
+            else launch_ev(k_attn_exact_scores<EPL, G, B, !B, 4>, grid, s, e0, nullptr, a);
         } else {
-            if (wide) hipLaunchKernelGGL((k_attn_exact_scores<EPL, G, B, false, 8>), grid, dim3(256), 0, s, a);
-            else hipLaunchKernelGGL((k_attn_exact_scores<EPL, G, B, false, 4>), grid, dim3(256), 0, s, a);
+            if (wide) launch_ev(k_attn_exact_scores<EPL, G, B, false, 8>, grid, s, e0, nullptr, a);
+            else launch_ev(k_attn_exact_scores<EPL, G, B, false, 4>, grid, s, e0, nullptr, a);
         }
         dim3 gv = grid;
         // V-sum chunks of vchunk positions: the span of grid_chunks score
         // chunks meets at most grid_chunks * chunk / vchunk + 2 of them
         if (!B && a.vchunk > a.chunk) gv.x = grid_chunks * a.chunk / a.vchunk + 2;
-        hipLaunchKernelGGL((k_attn_exact_vsum<EPL, G, B, 2 * UNR>), gv, dim3(256), 0, s, a);
+        launch_ev(k_attn_exact_vsum<EPL, G, B, 2 * UNR>, gv, s, nullptr, e1, a);
     }
 }
 template <int EPL, int G> static void attn_dispatch(const AttnArgs &a, int grid_chunks, bool prep, hipStream_t s) {

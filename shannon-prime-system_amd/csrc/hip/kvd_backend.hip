@@ -1933,16 +1933,19 @@ int sp_hipkv_kernel_times(sp_kvdecode_handle *h, int32_t first_token, int n, dou
     // the GEMV classes (0-4, one launch each) are timed by events the launch
     // itself records at the kernel's start and end; the others (several
     // kernels, or not GEMVs) by events recorded on the stream around them
-    struct Ctx { hipStream_t s; std::vector<std::pair<int, std::pair<hipEvent_t, hipEvent_t>>> ev; hipEvent_t cur, cur2; };
-    Ctx c; c.s = h->stream;
+    struct Ctx { hipStream_t s; bool routed; std::vector<std::pair<int, std::pair<hipEvent_t, hipEvent_t>>> ev; hipEvent_t cur, cur2; };
+    Ctx c; c.s = h->stream; c.routed = h->rec.B > 0;
     auto cb = [](void *vp, int cls, bool begin) {
         Ctx *cc = (Ctx *)vp;
-        if (cls <= 4) {
+        // GEMVs (0-4) and the score/V-sum or one-launch attention (5, 6; not
+        // the routed recall kernels): events recorded by the launches
+        const bool gemv = cls <= 4, attn = (cls == 5 && !cc->routed) || cls == 6;
+        if (gemv || attn) {
             if (begin) {
                 hipEventCreate(&cc->cur); hipEventCreate(&cc->cur2);
-                gemv_time_next(cc->cur, cc->cur2);
+                if (gemv) gemv_time_next(cc->cur, cc->cur2); else attn_time_next(cc->cur, cc->cur2);
             } else {
-                gemv_time_next(nullptr, nullptr);    // (already consumed unless the launch failed)
+                gemv_time_next(nullptr, nullptr); attn_time_next(nullptr, nullptr);   // consumed unless a launch failed
                 cc->ev.push_back({cls, {cc->cur, cc->cur2}});
             }
             return;

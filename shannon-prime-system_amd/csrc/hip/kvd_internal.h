@@ -265,6 +265,7 @@ bool gemm_supported(const DevW &w);
 void launch_advance(DState *st, hipStream_t s);
 void launch_gemv(const GemvArgs &a, int nrows_total, hipStream_t s);
 void gemv_time_next(hipEvent_t start, hipEvent_t stop);   // events of the calling thread's next GEMV launch
+void attn_time_next(hipEvent_t start, hipEvent_t stop);   // ... and of its next (score/V-sum or one-launch) attention
 void launch_qk_prep(const AttnArgs &a, hipStream_t s);
 void launch_embed_rope(const DevW &embd, const DState *st, const int *tokbuf, float *x, float scale, VecStat *stats,
                        int nstats, int HD, int mode, const int64_t *fq_g, const int64_t *fq_l, float *rope, hipStream_t s);
