@@ -66,31 +66,6 @@ __device__ void cordic_q62(int64_t th, int64_t &co, int64_t &si, const int64_t *
 __device__ __forceinline__ float wsum(float v) { return wave_allsum(v); }
 __device__ __forceinline__ double wsumd(double v) { return wave_allsum(v); }
 __device__ __forceinline__ int64_t wsuml(int64_t v) { return wave_allsum(v); }
-// Transposed butterfly over P per-lane int64 values (P a power of two, 2..64):
-// each exchange round halves the values a lane carries; afterwards every lane
-// holds the wave total of value treduce_index<P>(lane).
-template <int P> __device__ __forceinline__ int treduce_index(int lane) {
-    int idx = 0;
-    #pragma unroll
-    for (int r = 0, S = P; S > 1; r++, S >>= 1) idx += ((lane >> (5 - r)) & 1) * (S >> 1);
-    return idx;
-}
-template <int P, typename T> __device__ __forceinline__ T treduce(T v[P], int lane) {
-    int o = 32;
-    #pragma unroll
-    for (int S = P; S > 1; S >>= 1, o >>= 1) {
-        const bool hi = lane & o;
-        #pragma unroll
-        for (int i = 0; i < S / 2; i++) {
-            const T send = hi ? v[i] : v[i + S / 2];
-            const T keep = hi ? v[i + S / 2] : v[i];
-            v[i] = keep + __shfl_xor(send, o, 64);
-        }
-    }
-    T t = v[0];
-    for (; o > 0; o >>= 1) t += __shfl_xor(t, o, 64);
-    return t;
-}
 __device__ __forceinline__ float wmax(float v) { return wave_allmax(v); }
 
 // K/V rows are streamed once per step: nontemporal 16-byte loads (measured

@@ -119,28 +119,55 @@ __device__ __forceinline__ int32_t block_mult(uint32_t h, int ebase) {
     return (int32_t)ldexpf((float)__builtin_bit_cast(_Float16, (unsigned short)h), -ebase);
 }
 
-// Sum GEMV_R = 8 per-lane int64 partials over the wave with 10 exchanges
-// instead of 48: each step halves the rows a lane carries.  Afterwards lane l
-// holds the total of row ((l>>5)&1)*4 + ((l>>4)&1)*2 + ((l>>3)&1) (all lanes
-// of an aligned group of 8 agree).
+// Cross-lane moves without LDS round trips (CDNA4 VALU lane permutes):
+// v_permlane32_swap swaps the upper half of its first operand with the lower
+// half of its second; v_permlane16_swap the odd 16-lane rows of the first with
+// the even rows of the second.
+struct U32Pair { uint32_t a, b; };
+__device__ __forceinline__ U32Pair swap32(uint32_t x, uint32_t y) {
+    const auto r = __builtin_amdgcn_permlane32_swap(x, y, false, false);
+    return {r[0], r[1]};
+}
+__device__ __forceinline__ U32Pair swap16(uint32_t x, uint32_t y) {
+    const auto r = __builtin_amdgcn_permlane16_swap(x, y, false, false);
+    return {r[0], r[1]};
+}
+// x from lane l ^ 32
+__device__ __forceinline__ uint32_t xor32_u(uint32_t x, int lane) {
+    const U32Pair p = swap32(x, x);          // a: lanes 0..31 of x twice, b: lanes 32..63 twice
+    return lane < 32 ? p.b : p.a;
+}
+__device__ __forceinline__ float xor32_f(float x, int lane) { return __uint_as_float(xor32_u(__float_as_uint(x), lane)); }
+__device__ __forceinline__ int xor32_i(int x, int lane) { return (int)xor32_u((uint32_t)x, lane); }
+// lanes 0..31: x(l) + x(l + 32); lanes 32..63: y(l - 32) + y(l)
+__device__ __forceinline__ int64_t fold32(int64_t x, int64_t y) {
+    const U32Pair lo = swap32((uint32_t)x, (uint32_t)y), hi = swap32((uint32_t)((uint64_t)x >> 32), (uint32_t)((uint64_t)y >> 32));
+    return (int64_t)(((uint64_t)hi.a << 32) | lo.a) + (int64_t)(((uint64_t)hi.b << 32) | lo.b);
+}
+// rows 0, 2: x(row) + x(row + 1); rows 1, 3: y(row - 1) + y(row)
+__device__ __forceinline__ int64_t fold16(int64_t x, int64_t y) {
+    const U32Pair lo = swap16((uint32_t)x, (uint32_t)y), hi = swap16((uint32_t)((uint64_t)x >> 32), (uint32_t)((uint64_t)y >> 32));
+    return (int64_t)(((uint64_t)hi.a << 32) | lo.a) + (int64_t)(((uint64_t)hi.b << 32) | lo.b);
+}
+
+// Sum GEMV_R = 8 per-lane int64 partials over the wave: each step halves the
+// rows a lane carries (lane halves, then 16-lane rows, then half rows), and
+// the last three sum within groups of 8 lanes.  Afterwards lane l holds the
+// total of row ((l>>5)&1)*4 + ((l>>4)&1)*2 + ((l>>3)&1) (all lanes of an
+// aligned group of 8 agree).
 __device__ __forceinline__ int64_t transpose_reduce8(const int64_t v[8], int lane) {
-    const bool hi32 = lane & 32, hi16 = lane & 16, hi8 = lane & 8;
+    const bool hi8 = lane & 8;
     int64_t w[4], x[2];
     #pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const int64_t send = hi32 ? v[r] : v[r + 4];
-        w[r] = (hi32 ? v[r + 4] : v[r]) + __shfl_xor(send, 32, 64);
-    }
+    for (int r = 0; r < 4; r++) w[r] = fold32(v[r], v[r + 4]);      // lanes >= 32 carry rows 4..7
     #pragma unroll
-    for (int r = 0; r < 2; r++) {
-        const int64_t send = hi16 ? w[r] : w[r + 2];
-        x[r] = (hi16 ? w[r + 2] : w[r]) + __shfl_xor(send, 16, 64);
-    }
-    const int64_t send = hi8 ? x[0] : x[1];
-    int64_t y = (hi8 ? x[1] : x[0]) + __shfl_xor(send, 8, 64);
-    y += __shfl_xor(y, 4, 64);
-    y += __shfl_xor(y, 2, 64);
-    y += __shfl_xor(y, 1, 64);
+    for (int r = 0; r < 2; r++) x[r] = fold16(w[r], w[r + 2]);      // odd rows carry rows +2
+    // half rows: lane l keeps its row (bit 3) and takes the other row from l ^ 8
+    const uint64_t keep = (uint64_t)(hi8 ? x[1] : x[0]), send = (uint64_t)(hi8 ? x[0] : x[1]);
+    int64_t y = (int64_t)(keep + dpp64<0x128, 0xF>(send, 0));        // row_ror:8
+    y += (int64_t)dpp64<0xB1, 0xF>((uint64_t)y, 0);                  // quad_perm 1,0,3,2
+    y += (int64_t)dpp64<0x4E, 0xF>((uint64_t)y, 0);                  // quad_perm 2,3,0,1
+    y += (int64_t)dpp64<0x141, 0xF>((uint64_t)y, 0);                 // row_half_mirror
     return y;
 }
 
@@ -363,7 +390,7 @@ __global__ __launch_bounds__(512, PAIRED ? 2 : 4) void k_gemv(GemvArgs a) {
                 mem_complete();
                 int prev = 0;
                 if (lane == 0) prev = arrive(&a.gcnt[grp]);
-                prev = __shfl(prev, 0, 64);
+                prev = __builtin_amdgcn_readlane(prev, 0);
                 finish = prev == nsplit - 1;
                 if (finish) {
                     if (holder) tot = (int64_t)__hip_atomic_exchange((unsigned long long *)slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -374,7 +401,7 @@ __global__ __launch_bounds__(512, PAIRED ? 2 : 4) void k_gemv(GemvArgs a) {
                 const int ebm = eb_of(ebw, myrow);
                 const float y = sh == SH_ZERO ? 0.0f : rne_i64_scaled(tot, ebm - sh);
                 // lane (myrow*8) owns row myrow's total; paired rows fetch their up partner
-                const float partner = __shfl_xor(y, 32, 64);          // row myrow^4
+                const float partner = xor32_f(y, lane);               // row myrow^4
                 if (PAIRED) {
                     // lanes 0, 8, 16, 24 hold this task's gate rows (partner:
                     // the up row); lanes 32.. the parked task's
@@ -390,7 +417,7 @@ __global__ __launch_bounds__(512, PAIRED ? 2 : 4) void k_gemv(GemvArgs a) {
                         }
                     } else {
                         // park: lane l + 32 takes lane l's gate value (its own y is the up value)
-                        pg = __shfl_xor(y, 32, 64); pu = y; pj = __shfl_xor(j, 32, 64);
+                        pg = xor32_f(y, lane); pu = y; pj = xor32_i(j, lane);
                         if (lane < 32) pj = -1;
                     }
                     parked = !parked;

@@ -86,11 +86,17 @@ template <typename T> __device__ __forceinline__ T quad_sum(T v) {
     v = v + sw(v, std::integral_constant<int, 0xB1>{});      // quad_perm 1,0,3,2
     return v + sw(v, std::integral_constant<int, 0x4E>{});   // quad_perm 2,3,0,1
 }
-// Sum over aligned groups of N = 4 or 8 lanes (all lanes of a group get it).
+// Sum over aligned groups of N = 4 or 8 lanes (all lanes of a group get it):
+// after the quad sums, the half-row mirror pairs each quad with the other
+// quad of its 8 lanes.
 template <int N, typename T> __device__ __forceinline__ T group_sum(T v) {
     static_assert(N == 4 || N == 8, "groups of 4 or 8 lanes");
+    typedef typename std::conditional<sizeof(T) == 8, uint64_t, uint32_t>::type B;
     v = quad_sum(v);
-    if constexpr (N == 8) v += __shfl_xor(v, 4, 64);
+    if constexpr (N == 8) {
+        if constexpr (sizeof(T) == 8) v = v + __builtin_bit_cast(T, dpp64<0x141, 0xF>(__builtin_bit_cast(B, v), 0));
+        else v = v + __builtin_bit_cast(T, dpp32<0x141, 0xF>(__builtin_bit_cast(B, v), 0));
+    }
     return v;
 }
 
