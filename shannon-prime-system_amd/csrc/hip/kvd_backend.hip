@@ -173,7 +173,8 @@ struct Uploader {                         // one allocation, arrays carved at 25
 };
 
 int load_weight(const qwen3_model *qm, const gguf_tensor *t, int rows, int cols, Uploader &up,
-                std::vector<std::vector<int8_t>> &ebase_store, DevW &w, size_t offs[3]) {
+                std::vector<std::vector<int8_t>> &ebase_store, std::vector<std::vector<uint16_t>> &bs8_store,
+                DevW &w, size_t offs[4]) {
     if (!t) return fail("sp_hipkv_open: model lacks a weight tensor%s", "");
     const sp_arena_tensor *at = sp_arena_find(qm->arena, t->name);
     if (!at) return fail("sp_hipkv_open: weight %s not in the packed arena", t->name);
@@ -208,9 +209,18 @@ int load_weight(const qwen3_model *qm, const gguf_tensor *t, int rows, int cols,
         eb[r] = (int8_t)emin;
         if (emax - emin > max_spread) wide = 1;
     }
+    // the GEMV's copy of the scales, 8 rows interleaved per block
+    bs8_store.emplace_back((size_t)(rows + 7) / 8 * 8 * nb, (uint16_t)0);
+    std::vector<uint16_t> &b8 = bs8_store.back();
+    for (int r = 0; r < rows; r++) {
+        const uint16_t *bs = p.bscale + (size_t)r * nb;
+        uint16_t *dst = b8.data() + (size_t)(r / 8) * nb * 8 + r % 8;
+        for (size_t b = 0; b < nb; b++) dst[b * 8] = bs[b];
+    }
     offs[0] = up.add(p.codes, rb * rows);
     offs[1] = up.add(p.bscale, nb * 2 * rows);
     offs[2] = up.add(eb.data(), (size_t)rows + 8);
+    offs[3] = up.add(b8.data(), b8.size() * 2);
     w.rows = rows; w.cols = cols; w.nblk = (int)nb; w.wide = wide;
     return 0;
 }
@@ -249,12 +259,14 @@ DevModel *model_get(const qwen3_model *qm, bool upload = true) {
     const int QD = m->NH * HD, KVD = m->NKV * HD;
     Uploader up;
     std::vector<std::vector<int8_t>> ebs;
+    std::vector<std::vector<uint16_t>> b8s;
     ebs.reserve((size_t)m->NL * 7 + 2);
-    struct Pending { DevW *w; size_t o[3]; };
+    b8s.reserve((size_t)m->NL * 7 + 2);
+    struct Pending { DevW *w; size_t o[4]; };
     std::vector<Pending> pend;
     auto addw = [&](const gguf_tensor *t, int rows, int cols, DevW &w) -> int {
         Pending pd; pd.w = &w;
-        if (load_weight(qm, t, rows, cols, up, ebs, w, pd.o)) return 1;
+        if (load_weight(qm, t, rows, cols, up, ebs, b8s, w, pd.o)) return 1;
         pend.push_back(pd);
         return 0;
     };
@@ -336,6 +348,7 @@ DevModel *model_get(const qwen3_model *qm, bool upload = true) {
         pd.w->codes = base + pd.o[0];
         pd.w->bs = (const uint16_t *)(base + pd.o[1]);
         pd.w->ebase = (const int8_t *)(base + pd.o[2]);
+        pd.w->bs8 = (const uint16_t *)(base + pd.o[3]);
     }
     for (size_t i = 0; i < norm_slots.size(); i++) *norm_slots[i] = (const float *)(base + norm_off[i]);
     if (tied) m->out = m->embd;

@@ -37,17 +37,32 @@ namespace kvd {
 // plane.  u = xq + 0x888888 has the digits + 8 as its plain nibbles (|xq| <=
 // 2^22 keeps 0 <= u < 16^6), so digit & 15 = nibble ^ 8.  x * 2^sh is exact in
 // float for every result that can round to a non-zero integer.
+// The 6 x 8 nibble transpose runs on bytes: v_perm_b32 gathers byte b of the
+// even columns (D0[b]) and of the odd columns (D1[b]); the low nibbles of
+// D0[b] | D1[b] << 4 are then plane 2b in column order, the high nibbles plane
+// 2b + 1 (one bitfield insert each).
 __device__ __forceinline__ void digits8(const float v[8], int sh, uint32_t dw[NDIG]) {
+    uint32_t u[8];
     #pragma unroll
-    for (int k = 0; k < NDIG; k++) dw[k] = 0;
+    for (int j = 0; j < 8; j++) u[j] = (uint32_t)((int32_t)rintf(ldexpf(v[j], sh)) + 0x888888);
+    // bytes 0..2 of columns a, b, c, d, in that order, one dword per byte
+    auto gather = [](uint32_t a, uint32_t b, uint32_t c, uint32_t d, uint32_t (&D)[3]) {
+        const uint32_t p01 = __builtin_amdgcn_perm(b, a, 0x05010400u);   // a.0 b.0 a.1 b.1
+        const uint32_t p2 = __builtin_amdgcn_perm(b, a, 0x0C0C0602u);    // a.2 b.2 0 0
+        const uint32_t q01 = __builtin_amdgcn_perm(d, c, 0x05010400u);
+        const uint32_t q2 = __builtin_amdgcn_perm(d, c, 0x0C0C0602u);
+        D[0] = __builtin_amdgcn_perm(q01, p01, 0x05040100u);
+        D[1] = __builtin_amdgcn_perm(q01, p01, 0x07060302u);
+        D[2] = __builtin_amdgcn_perm(q2, p2, 0x05040100u);
+    };
+    uint32_t D0[3], D1[3];
+    gather(u[0], u[2], u[4], u[6], D0);
+    gather(u[1], u[3], u[5], u[7], D1);
     #pragma unroll
-    for (int j = 0; j < 8; j++) {
-        const uint32_t u = (uint32_t)((int32_t)rintf(ldexpf(v[j], sh)) + 0x888888);
-        #pragma unroll
-        for (int k = 0; k < NDIG; k++) dw[k] |= ((u >> (4 * k)) & 15u) << (4 * j);
+    for (int b = 0; b < 3; b++) {
+        dw[2 * b] = ((D0[b] & 0x0F0F0F0Fu) | ((D1[b] << 4) & 0xF0F0F0F0u)) ^ 0x88888888u;
+        dw[2 * b + 1] = (((D0[b] >> 4) & 0x0F0F0F0Fu) | (D1[b] & 0xF0F0F0F0u)) ^ 0x88888888u;
     }
-    #pragma unroll
-    for (int k = 0; k < NDIG; k++) dw[k] ^= 0x88888888u;
 }
 
 // The prologue's global loads (pro_load, plus for PRO_PLAIN this thread's
@@ -223,7 +238,19 @@ __device__ __forceinline__ void load_iter(const GemvArgs &a, const Task &t, int 
         const uint8_t *cp = w.codes + (size_t)row * rb + (size_t)bc * 16;
         const u32x4 v = __builtin_nontemporal_load((const u32x4 *)cp);
         c[r] = make_uint4(v.x, v.y, v.z, v.w);
-        h[r] = w.bs[(size_t)row * nblk + bc];
+    }
+    // the scales from the 8-row interleaved copy: one load per matrix (paired:
+    // the 4 rows at row0 & 7 of the gate and of the up group; rows past the end
+    // are zero padding)
+    const size_t gi = ((size_t)(t.row0 >> 3) * nblk + bc) * 8 + (t.row0 & 7);
+    if constexpr (PAIRED) {
+        const uint2 ga = *(const uint2 *)(wa.bs8 + gi), gb = *(const uint2 *)(wb.bs8 + gi);
+        h[0] = ga.x & 0xffffu; h[1] = ga.x >> 16; h[2] = ga.y & 0xffffu; h[3] = ga.y >> 16;
+        h[4] = gb.x & 0xffffu; h[5] = gb.x >> 16; h[6] = gb.y & 0xffffu; h[7] = gb.y >> 16;
+    } else {
+        const uint4 g = *(const uint4 *)(wa.bs8 + gi);
+        h[0] = g.x & 0xffffu; h[1] = g.x >> 16; h[2] = g.y & 0xffffu; h[3] = g.y >> 16;
+        h[4] = g.z & 0xffffu; h[5] = g.z >> 16; h[6] = g.w & 0xffffu; h[7] = g.w >> 16;
     }
 }
 
