@@ -81,8 +81,10 @@ __device__ __forceinline__ void gemv_pro_load(const ProArgs &p, int mode, GemvLo
 template <int PRO>
 __device__ __forceinline__ int gemv_prologue(const ProArgs &p, int mode, const GemvLoads &L, float *xf, uint4 *dig, int b_lo, int b_hi, void *red) {
     const int T = blockDim.x, tid = threadIdx.x;
-    const int sh = input_transform<PRO>(p, mode, L.pro, xf, red, blockIdx.x == 0, b_lo * 32, b_hi * 32);
-    if (sh == SH_ZERO) return SH_ZERO;
+    DigOut dout{dig, b_lo, b_hi - b_lo, false};
+    const int sh = input_transform<PRO>(p, mode, L.pro, xf, red, blockIdx.x == 0, b_lo * 32, b_hi * 32,
+                                        PRO == PRO_PLAIN ? nullptr : &dout);
+    if (sh == SH_ZERO || dout.done) return sh;
     // digits: one thread per 8 consecutive columns (one nibble-dword per plane);
     // the column count is a multiple of 32, so a group never runs past n
     const float *src = PRO == PRO_PLAIN ? p.x : xf;

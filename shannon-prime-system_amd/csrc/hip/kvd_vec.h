@@ -339,9 +339,31 @@ __device__ __forceinline__ void f4s(float4 &v, int c, float x) { if (c == 0) v.x
 // L: what pro_load<PRO> loaded for the same p and mode.
 // [c_lo, c_hi): the columns of xf the caller reads (the exact residual path
 // forms only those; every other path writes the whole vector).
+// The GEMV's digit planes (six balanced base-16 planes of rne(y 2^sh), 8
+// columns per dword, dig[plane * nb + block - b_lo]): the exact residual path
+// writes them itself, straight from its registers, when a caller passes one
+// (and sets done); the caller forms them otherwise.
+struct DigOut { uint4 *dig; int b_lo, nb; bool done; };
+// 4 consecutive columns' planes as 16-bit halves (nibble j = column j): byte
+// b of the even and of the odd columns gathered by v_perm_b32, then the low
+// nibbles of E | O << 4 are plane 2b and the high nibbles plane 2b + 1;
+// h[k] = plane k.
+__device__ __forceinline__ void digits4(const float y[4], int sh, uint32_t h[6]) {
+    uint32_t u[4];
+    #pragma unroll
+    for (int j = 0; j < 4; j++) u[j] = (uint32_t)((int32_t)rintf(ldexpf(y[j], sh)) + 0x888888);
+    const uint32_t e01 = __builtin_amdgcn_perm(u[2], u[0], 0x05010400u), o01 = __builtin_amdgcn_perm(u[3], u[1], 0x05010400u);
+    const uint32_t e2 = __builtin_amdgcn_perm(u[2], u[0], 0x0C0C0602u), o2 = __builtin_amdgcn_perm(u[3], u[1], 0x0C0C0602u);
+    const uint32_t l01 = ((e01 & 0x0F0F0F0Fu) | ((o01 << 4) & 0xF0F0F0F0u)) ^ 0x88888888u;
+    const uint32_t h01 = (((e01 >> 4) & 0x0F0F0F0Fu) | (o01 & 0xF0F0F0F0u)) ^ 0x88888888u;
+    const uint32_t l2 = ((e2 & 0x0F0F0F0Fu) | ((o2 << 4) & 0xF0F0F0F0u)) ^ 0x88888888u;
+    const uint32_t h2 = (((e2 >> 4) & 0x0F0F0F0Fu) | (o2 & 0xF0F0F0F0u)) ^ 0x88888888u;
+    h[0] = l01 & 0xFFFFu; h[1] = h01 & 0xFFFFu; h[2] = l01 >> 16; h[3] = h01 >> 16; h[4] = l2 & 0xFFFFu; h[5] = h2 & 0xFFFFu;
+}
+
 template <int PRO>
 __device__ int input_transform(const ProArgs &p, int mode, const ProLoads &L, float *xf, void *red, bool write_x,
-                               int c_lo = 0, int c_hi = 0x7FFFFFFF) {
+                               int c_lo = 0, int c_hi = 0x7FFFFFFF, DigOut *dout = nullptr) {
     const int n = p.n, T = blockDim.x, tid = threadIdx.x;
     __shared__ int64_t bcs[2];                       // broadcast RMS inverses: branch norm, pre-norm
     float m = 0.0f;
@@ -407,7 +429,9 @@ __device__ int input_transform(const ProArgs &p, int mode, const ProLoads &L, fl
                             const double dx = (double)round_away(d * 65536.0f) * (double)f4c(pw[k], c);
                             const double pr = dx * sd.invd;
                             bad |= !(fabs(dx) < 9007199254740992.0) | !(fabs(pr) < 4611686018427387904.0);
-                            nd = sd.zero ? 0.0f : (float)(pr * 2.220446049250313e-16);
+                            // (a zero sum of squares has inverse 0: pr is then
+                            // +-0 and x + nd = x, as with the island's zero)
+                            nd = (float)(pr * 2.220446049250313e-16);
                         }
                         const float r = f4c(xv[k], c) + nd;
                         f4s(xv[k], c, r);
@@ -463,16 +487,45 @@ __device__ int input_transform(const ProArgs &p, int mode, const ProLoads &L, fl
                 const double pmx = pm * s.invd;
                 if (s.zero || (pm < 9007199254740992.0 && pmx < 4611686018427387904.0)) {
                     m = s.zero ? 0.0f : (float)(pmx * 2.220446049250313e-16);
+                    if (dout) {
+                        // the digit planes from the registers: no pass through xf
+                        const int sh = sh_of_max(m);
+                        if (sh != SH_ZERO) {
+                            #pragma unroll
+                            for (int k = 0; k < PB4; k++) {
+                                const int i = 4 * (k * T + tid);
+                                if (i < n && i + 3 >= c_lo && i < c_hi) {
+                                    float y[4];
+                                    #pragma unroll
+                                    for (int c = 0; c < 4; c++)
+                                        y[c] = (float)(((double)round_away(f4c(xv[k], c) * 65536.0f) * (double)f4c(nw[k], c) *
+                                                        s.invd) * 2.220446049250313e-16);
+                                    uint32_t h[6];
+                                    digits4(y, sh, h);
+                                    // column i: block i / 32, dword (i % 32) / 8, half (i % 8) / 4
+                                    const int rel = i - dout->b_lo * 32;
+                                    uint16_t *d16 = (uint16_t *)(dout->dig + (rel >> 5)) + ((rel & 31) >> 2);
+                                    #pragma unroll
+                                    for (int pl = 0; pl < 6; pl++) d16[(size_t)pl * dout->nb * 8] = (uint16_t)h[pl];
+                                }
+                            }
+                        }
+                        __syncthreads();                               // orders the plane writes
+                        dout->done = true;
+                        return sh;
+                    }
                     #pragma unroll
                     for (int k = 0; k < PB4; k++) {
                         const int i = 4 * (k * T + tid);
                         if (i < n && i + 3 >= c_lo && i < c_hi) {
+                            // (straight-line: for a zero vector, inverse 0, the
+                            // values are +-0 and sh is SH_ZERO, so nobody reads them)
                             float4 y;
                             #pragma unroll
                             for (int c = 0; c < 4; c++)
-                                f4s(y, c, s.zero ? 0.0f : (float)(((double)round_away(f4c(xv[k], c) * 65536.0f) *
-                                                                   (double)f4c(nw[k], c) * s.invd) *
-                                                                  2.220446049250313e-16));
+                                f4s(y, c, (float)(((double)round_away(f4c(xv[k], c) * 65536.0f) *
+                                                   (double)f4c(nw[k], c) * s.invd) *
+                                                  2.220446049250313e-16));
                             *(float4 *)(xf + i) = y;
                         }
                     }
