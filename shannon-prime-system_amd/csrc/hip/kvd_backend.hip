@@ -174,7 +174,7 @@ struct Uploader {                         // one allocation, arrays carved at 25
 
 int load_weight(const qwen3_model *qm, const gguf_tensor *t, int rows, int cols, Uploader &up,
                 std::vector<std::vector<int8_t>> &ebase_store, std::vector<std::vector<uint16_t>> &bs8_store,
-                DevW &w, size_t offs[4]) {
+                DevW &w, size_t offs[4], int il) {
     if (!t) return fail("sp_hipkv_open: model lacks a weight tensor%s", "");
     const sp_arena_tensor *at = sp_arena_find(qm->arena, t->name);
     if (!at) return fail("sp_hipkv_open: weight %s not in the packed arena", t->name);
@@ -209,19 +209,19 @@ int load_weight(const qwen3_model *qm, const gguf_tensor *t, int rows, int cols,
         eb[r] = (int8_t)emin;
         if (emax - emin > max_spread) wide = 1;
     }
-    // the GEMV's copy of the scales, 8 rows interleaved per block
-    bs8_store.emplace_back((size_t)(rows + 7) / 8 * 8 * nb, (uint16_t)0);
+    // the GEMV's copy of the scales, il rows interleaved per block
+    bs8_store.emplace_back((size_t)(rows + il - 1) / il * il * nb, (uint16_t)0);
     std::vector<uint16_t> &b8 = bs8_store.back();
     for (int r = 0; r < rows; r++) {
         const uint16_t *bs = p.bscale + (size_t)r * nb;
-        uint16_t *dst = b8.data() + (size_t)(r / 8) * nb * 8 + r % 8;
-        for (size_t b = 0; b < nb; b++) dst[b * 8] = bs[b];
+        uint16_t *dst = b8.data() + (size_t)(r / il) * nb * il + r % il;
+        for (size_t b = 0; b < nb; b++) dst[b * il] = bs[b];
     }
     offs[0] = up.add(p.codes, rb * rows);
     offs[1] = up.add(p.bscale, nb * 2 * rows);
     offs[2] = up.add(eb.data(), (size_t)rows + 8);
     offs[3] = up.add(b8.data(), b8.size() * 2);
-    w.rows = rows; w.cols = cols; w.nblk = (int)nb; w.wide = wide;
+    w.rows = rows; w.cols = cols; w.nblk = (int)nb; w.wide = wide; w.il = il;
     return 0;
 }
 
@@ -264,9 +264,9 @@ DevModel *model_get(const qwen3_model *qm, bool upload = true) {
     b8s.reserve((size_t)m->NL * 7 + 2);
     struct Pending { DevW *w; size_t o[4]; };
     std::vector<Pending> pend;
-    auto addw = [&](const gguf_tensor *t, int rows, int cols, DevW &w) -> int {
+    auto addw = [&](const gguf_tensor *t, int rows, int cols, DevW &w, int il = 8) -> int {
         Pending pd; pd.w = &w;
-        if (load_weight(qm, t, rows, cols, up, ebs, b8s, w, pd.o)) return 1;
+        if (load_weight(qm, t, rows, cols, up, ebs, b8s, w, pd.o, il)) return 1;
         pend.push_back(pd);
         return 0;
     };
@@ -303,8 +303,8 @@ DevModel *model_get(const qwen3_model *qm, bool upload = true) {
         const qwen3_layer &y = qm->layers[l];
         DevLayer &d = m->L[l];
         if (addw(y.attn_q, QD, m->E, d.q) || addw(y.attn_k, KVD, m->E, d.k) || addw(y.attn_v, KVD, m->E, d.v) ||
-            addw(y.attn_output, m->E, QD, d.o) || addw(y.ffn_gate, m->FF, m->E, d.gate) ||
-            addw(y.ffn_up, m->FF, m->E, d.up) || addw(y.ffn_down, m->E, m->FF, d.down)) return nullptr;
+            addw(y.attn_output, m->E, QD, d.o) || addw(y.ffn_gate, m->FF, m->E, d.gate, 4) ||
+            addw(y.ffn_up, m->FF, m->E, d.up, 4) || addw(y.ffn_down, m->E, m->FF, d.down)) return nullptr;
         if (addn(y.attn_norm, m->E, &d.attn_norm) || addn(y.attn_q_norm, HD, &d.q_norm) ||
             addn(y.attn_k_norm, HD, &d.k_norm) || addn(y.ffn_norm, m->E, &d.ffn_norm)) return nullptr;
         d.post_attn = d.post_ffw = nullptr;

@@ -241,16 +241,15 @@ __device__ __forceinline__ void load_iter(const GemvArgs &a, const Task &t, int 
         const u32x4 v = __builtin_nontemporal_load((const u32x4 *)cp);
         c[r] = make_uint4(v.x, v.y, v.z, v.w);
     }
-    // the scales from the 8-row interleaved copy: one load per matrix (paired:
-    // the 4 rows at row0 & 7 of the gate and of the up group; rows past the end
-    // are zero padding)
-    const size_t gi = ((size_t)(t.row0 >> 3) * nblk + bc) * 8 + (t.row0 & 7);
+    // the scales from the interleaved copy: one load per matrix (paired: the
+    // 4-row groups of gate and up; rows past the end are zero padding)
     if constexpr (PAIRED) {
+        const size_t gi = ((size_t)(t.row0 >> 2) * nblk + bc) * 4;
         const uint2 ga = *(const uint2 *)(wa.bs8 + gi), gb = *(const uint2 *)(wb.bs8 + gi);
         h[0] = ga.x & 0xffffu; h[1] = ga.x >> 16; h[2] = ga.y & 0xffffu; h[3] = ga.y >> 16;
         h[4] = gb.x & 0xffffu; h[5] = gb.x >> 16; h[6] = gb.y & 0xffffu; h[7] = gb.y >> 16;
     } else {
-        const uint4 g = *(const uint4 *)(wa.bs8 + gi);
+        const uint4 g = *(const uint4 *)(wa.bs8 + ((size_t)(t.row0 >> 3) * nblk + bc) * 8);
         h[0] = g.x & 0xffffu; h[1] = g.x >> 16; h[2] = g.y & 0xffffu; h[3] = g.y >> 16;
         h[4] = g.z & 0xffffu; h[5] = g.z >> 16; h[6] = g.w & 0xffffu; h[7] = g.w >> 16;
     }
@@ -536,6 +535,8 @@ void launch_gemv(const GemvArgs &a_in, int nrows_total, hipStream_t s) {
     bool wide = false;
     for (int i = 0; i < a.nseg; i++) wide |= a.seg[i].w.wide != 0;
     const bool paired = a.act != ACT_NONE;
+    for (int i = 0; i < a.nseg; i++)
+        if (a.seg[i].w.il != (paired ? 4 : 8)) { launch_fail("GEMV scale interleave does not match the row pairing"); return; }
     GemvPlan p = gemv_plan(nrows_total, a.cols, paired, wide);
     // A plan that leaves over half of the CUs without a workgroup runs the
     // same waves in half-size workgroups on twice as many CUs (plain inputs

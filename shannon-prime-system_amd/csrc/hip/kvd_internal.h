@@ -22,14 +22,17 @@ enum Mode { FLOAT = 0, EXACT = 1 };
 // codes [rows][cols/2] nibbles (low = even column), scales [rows][cols/32] f16,
 // plus ebase[rows + 8] = smallest block exponent of the row (for the int64 fast path;
 // 8 bytes of padding: the GEMV reads 8 rows at a time), and the scales again
-// interleaved by 8 rows, bs8[ceil(rows/8)][nblk][8] (zero-padded rows): one
-// 16-byte load gives a GEMV lane a block's scales for its 8 rows.
+// interleaved by il rows, bs8[ceil(rows/il)][nblk][il] (zero-padded rows): one
+// load gives a GEMV lane a block's scales for the rows of its task in this
+// matrix -- il = 8 for the GEMV's unpaired rows, 4 for the gate and up
+// matrices, which it reads 4 rows each per task.
 struct DevW {
     const uint8_t  *codes;
     const uint16_t *bs;
     const int8_t   *ebase;
     const uint16_t *bs8;
     int rows, cols, nblk, wide;   // wide: a row's exponent spread needs the int128 path
+    int il;
 };
 
 // Whole-vector statistics that the kernel producing a vector accumulates while
