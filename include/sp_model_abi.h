@@ -232,8 +232,14 @@ void sp_q4b_quantize_row(const float *w, int cols, uint8_t *codes, uint16_t *bsc
 
 /* Synthetic random-init OK_Q4B model writer.  Weights N(0, 0.02) from one
  * SplitMix64 stream (seed) through Box-Muller in double; every norm vector 1.0;
- * tied LM head unless `untied`.  `n_threads` <= 0 picks the machine's count.
- * Writes `model_path` and its paired `tok_path`.  SP_OK or an error code. */
+ * tied LM head unless `untied`.  The first `spread_rows` rows of the weight
+ * matrices that `spread_mask` selects (bit 0 token_embd, 1 output, 2 attn_q,
+ * 3 attn_k, 4 attn_v, 5 attn_output, 6 ffn_gate, 7 ffn_up, 8 ffn_down; 0: all)
+ * have their odd blocks' weights scaled by 2^13 and their even blocks' by 2^-7
+ * before quantization: block scales about 2^20 apart, rows whose exact
+ * accumulation needs more than 64 bits; 0 rows leaves every row plain.
+ * `n_threads` <= 0 picks the machine's count.  Writes `model_path` and its
+ * paired `tok_path`.  SP_OK or an error code. */
 typedef struct {
     uint32_t arch_id;          /* SP_ARCH_ID_QWEN3 or SP_ARCH_ID_GEMMA3 */
     uint32_t n_layers, hidden, n_heads, n_kv_heads, head_dim, n_ff, vocab;
@@ -241,6 +247,7 @@ typedef struct {
     float    rope_base, rms_eps;
     int      untied;
     uint64_t seed;
+    uint32_t spread_rows, spread_mask;
 } sp_synth_spec;
 sp_status sp_write_synthetic_q4b(const sp_synth_spec *spec, const char *model_path,
                                  const char *tok_path, int n_threads);

@@ -79,6 +79,7 @@ typedef struct {
     uint8_t *data;            /* mapped data region */
     int      w;               /* weight currently generated */
     int      codes_i, scale_i;
+    uint64_t spread_rows;     /* rows of the current weight with spread block scales */
     uint64_t row_next;        /* work cursor */
     int      digest_next;
     pthread_mutex_t mu;
@@ -110,6 +111,8 @@ static void *gen_rows(void *arg) {
             } else {
                 for (uint64_t c = 0; c < cols; c++) row[c] = synth_normal(g->sp->seed, e0 + c);
             }
+            if (r < g->spread_rows)                    /* odd blocks x 2^13, even blocks x 2^-7 */
+                for (uint64_t c = 0; c < cols; c++) row[c] = ldexpf(row[c], ((c / 32u) & 1u) ? 13 : -7);
             sp_q4b_quantize_row(row, (int)cols, g->data + pc->offset + r * rb,
                                 (uint16_t *)(g->data + ps->offset) + r * nb);
         }
@@ -252,9 +255,15 @@ sp_status sp_write_synthetic_q4b(const sp_synth_spec *sp, const char *model_path
     pthread_mutex_init(&g.mu, NULL);
     for (int i = 0; i < np; i++)
         if (P[i].kind == 2) { float *f = (float *)(g.data + P[i].offset); for (uint64_t j = 0; j < P[i].dims[0]; j++) f[j] = 1.0f; }
+    static const char *const kinds[9] = {"token_embd.", "output.", ".attn_q.", ".attn_k.", ".attn_v.",
+                                         ".attn_output.", ".ffn_gate.", ".ffn_up.", ".ffn_down."};
     for (int w = 0; w < n_w; w++) {
         g.codes_i = g.scale_i = -1;
         for (int i = 0; i < np; i++) if (P[i].weight == w) { if (P[i].kind == 0) g.codes_i = i; else g.scale_i = i; }
+        const char *wn = P[g.codes_i].name;
+        int kind = 0;                       /* the first two are prefixes ("attn_output." holds "output.") */
+        while (kind < 9 && !(kind < 2 ? strncmp(wn, kinds[kind], strlen(kinds[kind])) == 0 : strstr(wn, kinds[kind]) != NULL)) kind++;
+        g.spread_rows = (!sp->spread_mask || (kind < 9 && (sp->spread_mask >> kind) & 1u)) ? sp->spread_rows : 0;
         g.row_next = 0;
         run_threads(gen_rows, &g, n_threads);
     }

@@ -29,7 +29,7 @@ class SynthSpec(ctypes.Structure):
                 ("n_heads", c_uint32), ("n_kv_heads", c_uint32), ("head_dim", c_uint32),
                 ("n_ff", c_uint32), ("vocab", c_uint32), ("max_context", c_uint32),
                 ("swa_window", c_uint32), ("rope_base", c_float), ("rms_eps", c_float),
-                ("untied", c_int), ("seed", c_uint64)]
+                ("untied", c_int), ("seed", c_uint64), ("spread_rows", c_uint32), ("spread_mask", c_uint32)]
 
 
 class SessionConfig(ctypes.Structure):
@@ -191,7 +191,8 @@ def write_model(path_prefix, shape=None, seed=0, max_context=4096, threads=0, **
     d.update(kw)
     spec = SynthSpec(d["arch_id"], d["n_layers"], d["hidden"], d["n_heads"], d["n_kv_heads"],
                      d["head_dim"], d["n_ff"], d["vocab"], max_context, d.get("swa_window", 0),
-                     d.get("rope_base", 1e6), d.get("rms_eps", 1e-6), d.get("untied", 0), seed)
+                     d.get("rope_base", 1e6), d.get("rms_eps", 1e-6), d.get("untied", 0), seed,
+                     d.get("spread_rows", 0), d.get("spread_mask", 0))
     spm, spt = path_prefix + ".spm", path_prefix + ".spt"
     check(l1().sp_write_synthetic_q4b(ctypes.byref(spec), spm.encode(), spt.encode(), threads),
           "sp_write_synthetic_q4b")

@@ -41,6 +41,19 @@ SMALL = {
                       head_dim=64, n_ff=1024, vocab=2048, swa_window=1),
     "gemma3-w2100": dict(arch_id=spkv.ARCH_GEMMA3, n_layers=6, hidden=512, n_heads=4, n_kv_heads=2,
                          head_dim=64, n_ff=1024, vocab=2048, swa_window=2100),
+    # rows whose block scales span about 20 binary exponents: the GEMVs' int128
+    # accumulation (and the per-token prefill: no batched GEMM).  Spread in every
+    # matrix, the activations outgrow exact mode's 64-bit sums of squares (float
+    # mode only); in the embedding/LM head, q, k, v and gate (SPREAD_EXACT) the
+    # norms, the V clamp and the activation keep them in range.
+    "qwen3-spread": dict(arch_id=spkv.ARCH_QWEN3, n_layers=2, hidden=256, n_heads=4, n_kv_heads=2,
+                         head_dim=64, n_ff=512, vocab=1000, spread_rows=8),
+    "gemma3-spread": dict(arch_id=spkv.ARCH_GEMMA3, n_layers=7, hidden=256, n_heads=4, n_kv_heads=2,
+                          head_dim=64, n_ff=512, vocab=1000, swa_window=16, spread_rows=8),
+    "qwen3-spread-x": dict(arch_id=spkv.ARCH_QWEN3, n_layers=2, hidden=256, n_heads=4, n_kv_heads=2,
+                           head_dim=64, n_ff=512, vocab=1000, spread_rows=8, spread_mask=0x5D),
+    "gemma3-spread-x": dict(arch_id=spkv.ARCH_GEMMA3, n_layers=7, hidden=256, n_heads=4, n_kv_heads=2,
+                            head_dim=64, n_ff=512, vocab=1000, swa_window=16, spread_rows=8, spread_mask=0x5D),
 }
 
 

@@ -99,6 +99,23 @@ def test_decode_parity(tmpdir_models, name, exact):
     close_all(s, o, m)
 
 
+@pytest.mark.parametrize("name,exact", [("qwen3-spread", False),
+                                        ("qwen3-spread-x", True), ("qwen3-spread-x", False),
+                                        ("gemma3-spread-x", True), ("gemma3-spread-x", False)])
+def test_decode_parity_int128_rows(tmpdir_models, name, exact):
+    """Rows whose block scales span about 2^20 (their exact sums need more than
+    64 bits): every GEMV of the model runs its int128 instance, prefill goes
+    token by token.  Spread in every matrix (Qwen3, float mode: the
+    activations outgrow exact mode's 64-bit sums of squares, as in the
+    reference's islands, and through Gemma-3's seven layers the reference's
+    float sums drift past 1e-3 of the exact ones); spread in the embedding/LM
+    head, q, k, v and gate: both modes, both architectures."""
+    spm, spt = model_files(tmpdir_models, name)
+    m, s, o, be, res = run_pair(spm, spt, exact, n_prompt=24, n_gen=12)
+    check(res, exact)
+    close_all(s, o, m)
+
+
 @pytest.mark.parametrize("exact", [True, False])
 def test_plain_launches_and_direct_table(tmpdir_models, exact):
     spm, spt = model_files(tmpdir_models, "gemma3-tiny")

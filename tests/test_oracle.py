@@ -182,9 +182,11 @@ def test_rope_exact_vs_libm():
         assert np.abs(n0 - n1).max() < 1e-5 * n0.max()
 
 
-def _q4b_tensor(rows, cols, seed):
+def _q4b_tensor(rows, cols, seed, spread=False):
     rng = np.random.default_rng(seed)
     w = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
+    if spread:   # odd blocks x 2^13, even blocks x 2^-7, as the synthetic writer's spread rows
+        w *= np.repeat(np.ldexp(1.0, np.where(np.arange(cols // 32) & 1, 13, -7)), 32).astype(np.float32)
     codes = np.zeros((rows, cols // 2), np.uint8); bs = np.zeros((rows, cols // 32), np.uint16)
     for r in range(rows):
         spkv.l1().sp_q4b_quantize_row(P(w[r]), cols, P(codes[r]), P(bs[r]))
@@ -203,12 +205,16 @@ def _f16_frac(h):
     return -v if h & 0x8000 else v
 
 
-@pytest.mark.parametrize("cols", [64, 256, 1024])
-def test_exact_gemv_is_rne_of_rational(cols):
+@pytest.mark.parametrize("cols,spread", [(64, False), (256, False), (1024, False), (256, True), (1024, True)])
+def test_exact_gemv_is_rne_of_rational(cols, spread):
     """y = RNE( sum_b f16(s_b) sum_i code_i * xq_i / 2^sh ) exactly, with xq the
-    per-vector power-of-two grid of x (max |xq| < 2^22)."""
+    per-vector power-of-two grid of x (max |xq| < 2^22); also for rows whose
+    block scales span about 20 binary exponents (sums beyond 64 bits)."""
     rows = 24
-    codes, bs = _q4b_tensor(rows, cols, cols)
+    codes, bs = _q4b_tensor(rows, cols, cols, spread)
+    if spread:   # every row past the int64 bound: exponent spread > 21 - ceil(log2 nblk)
+        e = ((bs.astype(np.int64) >> 10) & 31)
+        assert (e.max(axis=1) - e.min(axis=1)).min() > 21 - math.ceil(math.log2(cols // 32))
     x = (np.random.default_rng(9).standard_normal(cols) * np.float32(0.7)).astype(np.float32)
     x[3] = 0.0
     y = np.zeros(rows, np.float32)
