@@ -279,10 +279,12 @@ __device__ __forceinline__ int eb_of(uint64_t ebw, int r) { return (int)(int8_t)
 // partials meet through one atomic exchange on its accbuf slot.  The first weights are requested before the prologue
 // (after the prologue's own loads), and each task requests the next task's
 // weights before its own epilogue.
-// PAIRED (gate/up: one workgroup per CU, the plan sees to it) may use 256
-// registers; the others run up to 4 waves per SIMD, two workgroups per CU.
+// PAIRED (gate/up) and the plain-input instances (O, down) hold one workgroup
+// per CU (the plan sees to it) and may use 256 registers: a task over two
+// 64-block units keeps both in flight; the residual and norm instances (QKV,
+// LM head) run up to 4 waves per SIMD, two workgroups per CU.
 template <int PRO, bool PAIRED, bool WIDE>
-__global__ __launch_bounds__(512, PAIRED ? 2 : 4) void k_gemv(GemvArgs a) {
+__global__ __launch_bounds__(512, (PAIRED || PRO == PRO_PLAIN) ? 2 : 4) void k_gemv(GemvArgs a) {
     extern __shared__ uint4 smem4[];
     const int nblk = (a.cols + 31) / 32, nsplit = a.nsplit, bps = a.bps;
     const int split = blockIdx.x % nsplit;
@@ -344,9 +346,9 @@ __global__ __launch_bounds__(512, PAIRED ? 2 : 4) void k_gemv(GemvArgs a) {
                 }
             }
         };
-        if (PAIRED && !WIDE && nit == 2) {
-            // the second unit is requested before the first is used (the
-            // paired instance has the registers for both)
+        if ((PAIRED || PRO == PRO_PLAIN) && !WIDE && nit == 2) {
+            // the second unit is requested before the first is used (these
+            // instances have the registers for both)
             uint4 c2[GEMV_R];
             uint32_t h2[GEMV_R];
             load_iter<PAIRED>(a, t, b_lo + 64 + lane, b_lo, b_hi, c2, h2);
@@ -480,11 +482,11 @@ static int num_cu() {
 // Work decomposition: row groups x column splits of 64-block multiples, so
 // that about two 8-wave workgroups per CU have work; the grid is a multiple
 // of nsplit so that a workgroup keeps one split (and builds only its digits).
-GemvPlan gemv_plan(int nrows_total, int cols, int paired, int wide) {
+GemvPlan gemv_plan(int nrows_total, int cols, int paired, int wide, int one_per_cu) {
     GemvPlan p;
     const int nblk = (cols + 31) / 32;
     p.groups = paired ? (nrows_total + GEMV_R / 2 - 1) / (GEMV_R / 2) : (nrows_total + GEMV_R - 1) / GEMV_R;
-    int cap = (paired ? 1 : 2) * num_cu();              // workgroups (paired instances hold one per CU)
+    int cap = (one_per_cu ? 1 : 2) * num_cu();          // workgroups resident at once
     const int max_split = (nblk + 63) / 64;
     int want = (cap * GEMV_WAVES + p.groups - 1) / p.groups;
     // a split costs every task an atomic hand-off; it only pays when whole
@@ -537,7 +539,7 @@ void launch_gemv(const GemvArgs &a_in, int nrows_total, hipStream_t s) {
     const bool paired = a.act != ACT_NONE;
     for (int i = 0; i < a.nseg; i++)
         if (a.seg[i].w.il != (paired ? 4 : 8)) { launch_fail("GEMV scale interleave does not match the row pairing"); return; }
-    GemvPlan p = gemv_plan(nrows_total, a.cols, paired, wide);
+    GemvPlan p = gemv_plan(nrows_total, a.cols, paired, wide, paired || a.pro.kind == PRO_PLAIN);
     // A plan that leaves over half of the CUs without a workgroup runs the
     // same waves in half-size workgroups on twice as many CUs (plain inputs
     // only: the norm prologues keep the whole vector in registers of 8 waves)

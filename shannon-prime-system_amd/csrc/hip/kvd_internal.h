@@ -289,6 +289,6 @@ void set_rope_tables(const int64_t atan_q60[64], int64_t kinv_q62);
 void launch_argmax(const float *logits, int V, float *pval, int *pidx, int *counter,
                    DState *st, int *gen_log, int nblocks, hipStream_t s);
 int  argmax_blocks(int V);
-GemvPlan gemv_plan(int nrows_total, int cols, int paired, int wide);
+GemvPlan gemv_plan(int nrows_total, int cols, int paired, int wide, int one_per_cu);
 
 }  // namespace kvd
