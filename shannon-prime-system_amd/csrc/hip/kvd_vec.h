@@ -429,9 +429,7 @@ __device__ int input_transform(const ProArgs &p, int mode, const ProLoads &L, fl
                             const double dx = (double)round_away(d * 65536.0f) * (double)f4c(pw[k], c);
                             const double pr = dx * sd.invd;
                             bad |= !(fabs(dx) < 9007199254740992.0) | !(fabs(pr) < 4611686018427387904.0);
-                            // (a zero sum of squares has inverse 0: pr is then
-                            // +-0 and x + nd = x, as with the island's zero)
-                            nd = (float)(pr * 2.220446049250313e-16);
+                            nd = sd.zero ? 0.0f : (float)(pr * 2.220446049250313e-16);
                         }
                         const float r = f4c(xv[k], c) + nd;
                         f4s(xv[k], c, r);
