@@ -51,6 +51,11 @@ KERNEL_NAMES = {
     "qk_norm_rope_append": ["[kvd::k_qk_prep<false>]"],
     "embed_rope_argmax": ["kvd::k_embed_rope", "kvd::k_argmax"],
 }
+# a routed global layer's launches (--recall), exact and float mode
+RECALL_NAMES = {True: "kvd::k_recall_score<RT> + kvd::k_recall_select + kvd::k_recall_scores<EPL, true>"
+                      " + kvd::k_recall_vsum_exact<EPL>",
+                False: "kvd::k_recall_score<RT> + kvd::k_recall_select + kvd::k_recall_scores<EPL, false>"
+                       " + kvd::k_recall_vsum_float<EPL>"}
 # committed rocprofv3 --pmc summaries (FETCH_SIZE / WRITE_SIZE per dispatch) of the
 # decode kernels at this model shape and context, with the 1 GiB calibration copy they hold
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "gemma3-12b_32k_decode_pmc_fetch_write.txt")
@@ -278,6 +283,8 @@ def main():
                                 gbs=float(by[i] / (ms[i] * 1e-3) / 1e9) if ms[i] > 0 else None))
         dom = max(cls, key=lambda c: c["total_ms"])             # the class with the most device time per step
         dom_names = KERNEL_NAMES.get(dom["kernel"], [])
+        if recall and dom["kernel"] == "gqa_decode_attn_global":
+            dom_names = [RECALL_NAMES[exact]]
         dom_launch_bytes = dom["bytes"] / dom["launches"]
         traffic = pmc_traffic(dom_names[0]) if len(dom_names) == 1 else None
         kv_gb = sum(c["bytes"] for c in cls if c["kernel"].startswith("gqa")) / 1e9
