@@ -179,7 +179,7 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
-              "multi-GPU sharding is a design in DESIGN.md, not a measured path", file=sys.stderr)
+              "sharding the path over several GPUs is designed but not built or measured", file=sys.stderr)
         sys.exit(2)
 
     import spkv

@@ -2,7 +2,7 @@
 reference (oracle/_ref/libspref.so, built from the reference's own C sources
 under /root/reference by oracle/ref.mk) on this repository's synthetic OK_Q4B
 models, so that the oracle stays pinned where the compiled reference is absent
-(the GPU box, a fresh checkout).
+(a GPU host, a fresh checkout).
 
 Recorded per decode case (float decode through the reference's own session:
 core/session/sp_session.c sp_prefill_chunk :154-212 + sp_decode_step :725-770):
