@@ -43,7 +43,7 @@ KERNEL_NAMES = {
     "gate_up_gemv_q4b": ["kvd::k_gemv<2, true, false>"],
     "down_gemv_q4b": ["kvd::k_gemv<0, false, false>"],
     "lm_head_gemv_q4b": ["kvd::k_gemv<2, false, false>"],
-    "gqa_decode_attn_global": ["kvd::k_attn_exact_scores<EPL, G, false, true, 8> + kvd::k_attn_exact_vsum<EPL, G, false, 8>",
+    "gqa_decode_attn_global": ["kvd::k_attn_exact_scores<EPL, G, false, true, 8> + kvd::k_attn_exact_vsum<EPL, G, false, 12>",
                                "[kvd::k_qk_prep<false> + kvd::k_attn_float<EPL, G, false, SPINOR>]"],
     "gqa_decode_attn_window": ["kvd::k_attn_exact_window<EPL, G>",
                                "[kvd::k_qk_prep<false> + kvd::k_attn_float<EPL, G, false, SPINOR>]"],
@@ -484,7 +484,7 @@ def run_sessions(args, wl):
         kv = [c for c in cls if c["kernel"].startswith("gqa")]
         kv_gb, kv_ms = sum(c["bytes"] for c in kv) / 1e9, sum(c["total_ms"] for c in kv)
         step_bytes = sum(c["bytes"] for c in cls)
-        names = {"gqa_decode_attn_global": ["kvd::k_attn_exact_scores<2, 4, true, false, 8> + kvd::k_attn_exact_vsum<2, 4, true, 8>"
+        names = {"gqa_decode_attn_global": ["kvd::k_attn_exact_scores<2, 4, true, false, 8> + kvd::k_attn_exact_vsum<2, 4, true, 12>"
                                             if exact else "kvd::k_attn_float<2, 4, true, false>"]}
         rec = {
             "metric": BATCH_METRIC, "value": round(value, 3), "unit": "tokens/s", "n_gpus": 1,
