@@ -51,6 +51,10 @@ KERNEL_NAMES = {
     "qk_norm_rope_append": ["[kvd::k_qk_prep<false>]"],
     "embed_rope_argmax": ["kvd::k_embed_rope", "kvd::k_argmax"],
 }
+# the batched multi-session decode's global attention (Qwen3-8B shape: head_dim
+# 128, 4 q heads per kv head), exact and float mode
+BATCH_ATTN_NAMES = {True: "kvd::k_attn_exact_scores<2, 4, true, false, 8> + kvd::k_attn_exact_vsum<2, 4, true, 12>",
+                    False: "kvd::k_attn_float<2, 4, true, false>"}
 # a routed global layer's launches (--recall), exact and float mode
 RECALL_NAMES = {True: "kvd::k_recall_score<RT> + kvd::k_recall_select + kvd::k_recall_scores<EPL, true>"
                       " + kvd::k_recall_vsum_exact<EPL>",
@@ -484,8 +488,7 @@ def run_sessions(args, wl):
         kv = [c for c in cls if c["kernel"].startswith("gqa")]
         kv_gb, kv_ms = sum(c["bytes"] for c in kv) / 1e9, sum(c["total_ms"] for c in kv)
         step_bytes = sum(c["bytes"] for c in cls)
-        names = {"gqa_decode_attn_global": ["kvd::k_attn_exact_scores<2, 4, true, false, 8> + kvd::k_attn_exact_vsum<2, 4, true, 12>"
-                                            if exact else "kvd::k_attn_float<2, 4, true, false>"]}
+        names = {"gqa_decode_attn_global": [BATCH_ATTN_NAMES[exact]]}
         rec = {
             "metric": BATCH_METRIC, "value": round(value, 3), "unit": "tokens/s", "n_gpus": 1,
             "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(1e3 * wall / args.steps, 4),
